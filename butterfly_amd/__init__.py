@@ -1,0 +1,50 @@
+"""butterfly_amd: Butterfly compressed attention for AMD MI355X (gfx950).
+
+PyTorch-ROCm host code over hand-written HIP kernels reached through a C ABI
+(``include/butterfly_amd.h``, ``butterfly_amd/_lib/libbutterfly_amd.so``).
+"""
+from .attention import (
+    block_mean_summaries,
+    butterfly_compressed_attention,
+    butterfly_compressed_attention_active,
+    compressed_butterfly_active_index_tensors,
+    compressed_butterfly_attention,
+    compressed_butterfly_attention_active,
+    compressed_butterfly_attention_cached,
+    compressed_butterfly_attention_from_cache,
+    compressed_butterfly_block_index_tensors,
+)
+from .compressed_cache import CompressedKVCache
+from .layout import BlockButterflyLayout, build_block_butterfly_layout, clear_layout_cache
+from .topology import (
+    ButterflyLayoutMetadata,
+    block_neighbor_table,
+    butterfly_layout_metadata,
+    butterfly_partner_bits,
+    butterfly_stage_count,
+    butterfly_stage_meta,
+    butterfly_width,
+)
+
+__all__ = [
+    "BlockButterflyLayout",
+    "ButterflyLayoutMetadata",
+    "CompressedKVCache",
+    "block_mean_summaries",
+    "block_neighbor_table",
+    "build_block_butterfly_layout",
+    "butterfly_compressed_attention",
+    "butterfly_compressed_attention_active",
+    "butterfly_layout_metadata",
+    "butterfly_partner_bits",
+    "butterfly_stage_count",
+    "butterfly_stage_meta",
+    "butterfly_width",
+    "clear_layout_cache",
+    "compressed_butterfly_active_index_tensors",
+    "compressed_butterfly_attention",
+    "compressed_butterfly_attention_active",
+    "compressed_butterfly_attention_cached",
+    "compressed_butterfly_attention_from_cache",
+    "compressed_butterfly_block_index_tensors",
+]

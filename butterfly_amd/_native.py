@@ -1,0 +1,93 @@
+"""ctypes binding of ``libbutterfly_amd.so`` (the C ABI in ``include/butterfly_amd.h``).
+
+The library is built in-tree by ``butterfly_amd.build``.  There is no fallback:
+if the library is missing every product entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libbutterfly_amd.so"
+
+OK = 0
+ERR_INVALID = -1
+ERR_UNSUPPORTED = -2
+ERR_HIP = -3
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+RULES = {
+    "xor": 0,
+    "bit_reversal": 1,
+    "benes": 2,
+    "causal_shift": 3,
+    "fixed_stride": 4,
+    "random": 5,
+}
+
+_i32, _i64, _f32, _vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
+_int = C.c_int
+_pi32 = C.POINTER(C.c_int32)
+
+# name -> (restype, argtypes); mirrors include/butterfly_amd.h
+SIGNATURES = {
+    "bfly_last_error": (C.c_char_p, []),
+    "bfly_abi_version": (_int, []),
+    "bfly_stage_meta": (_int, [_i64, _i64, _int, _pi32, _pi32, _pi32]),
+    "bfly_partner_bits": (_int, [_int, _int, _int, _int, _int, _pi32]),
+    "bfly_block_neighbors": (_int, [_i64, _i64, _int, _int, _int, _int, _vp, _int, _vp, _vp]),
+    "bfly_prefill_tables": (_int, [_vp, _i64, _int, _int, _i64, _int, _vp, _vp, _vp, _vp, _vp]),
+    "bfly_active_tables": (_int, [_vp, _i64, _int, _int, _i64, _int, _vp, _i64, _i64, _i64, _i64,
+                                  _vp, _vp, _vp, _vp, _vp]),
+    "bfly_block_mean": (_int, [_vp, _vp, _vp, _vp, _int, _i64, _i64, _int, _int, _i64, _vp]),
+    "bfly_prefill": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _i64, _int, _int, _i64, _int, _vp, _i64,
+                            _int, _int, _int, _f32, _vp, _vp]),
+    "bfly_attend_cache": (_int, [_vp, _int, _i64, _int, _int, _i64, _int, _vp, _i64, _vp, _vp, _i64,
+                                 _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _int, _int, _int, _f32,
+                                 _vp, _vp]),
+    "bfly_cache_append": (_int, [_vp, _vp, _int, _i64, _int, _i64, _int, _vp, _vp, _i64, _i64, _vp]),
+    "bfly_cache_compress": (_int, [_vp, _vp, _int, _i64, _int, _int, _i64, _i64, _i64, _int, _vp, _vp,
+                                   _i64, _i64, _vp]),
+}
+
+_lib = None
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def lib() -> C.CDLL:
+    """Load (once) and return the native library; raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise NativeLibraryMissing(
+                f"{LIB_PATH} not found; build it with `python -m butterfly_amd.build`")
+        handle = C.CDLL(os.fspath(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    """Map a BFLY_ERR_* code to the reference's exception types."""
+    if rc == OK:
+        return
+    msg = lib().bfly_last_error().decode(errors="replace")
+    text = f"{what}: {msg}" if what else msg
+    if rc == ERR_INVALID:
+        raise ValueError(text)
+    if rc == ERR_UNSUPPORTED:
+        raise NotImplementedError(text)
+    raise RuntimeError(text)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)

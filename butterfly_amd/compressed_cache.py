@@ -1,0 +1,248 @@
+"""Two-pool KV cache for compressed Butterfly attention, resident in HBM.
+
+Contract: the reference's ``CompressedKVCache`` (bna/mlx/compressed_cache.py:9-302):
+constructor arguments, capacity formulas, the counters ``offset``,
+``tail_size``, ``summary_count``, ``summary_offset`` and their update rules,
+the logical views (``keys``/``values`` = the tail, ``k_summary``/``v_summary``
+= completed block means), ``get_compressed_state``, ``nbytes``, ``state`` /
+``meta_state`` round trip and the capacity ``RuntimeError``s.
+
+Physical layout (MI355X-specific): the tail is a ring of
+``tail_capacity = W + 2*max_chunk + 2*BS`` slots per (batch, kv head) in which
+position ``p`` lives at slot ``p mod tail_capacity``; trimming the tail is a
+counter update (no data moves).  The summary pool is
+``[B, H, summary_capacity, d]``.  Appends and block means run as HIP kernels
+(``bfly_cache_append``, ``bfly_cache_compress``); the host only does the
+reference's integer bookkeeping.  The logical tail always fits the ring because
+``tail_size <= tail_capacity`` (the reference's own capacity check).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Optional
+
+import torch
+
+from . import _native
+from .attention import _c, _dtype_code, _stream
+
+
+@dataclass(frozen=True)
+class RingState:
+    ring_k: torch.Tensor
+    ring_v: torch.Tensor
+    ring_capacity: int
+    tail_start: int
+    offset: int
+    pool_k: torch.Tensor
+    pool_v: torch.Tensor
+    summary_count: int
+
+
+class CompressedKVCache:
+    def __init__(self, *, block_size: int = 128, local_window_tokens: int = 128,
+                 max_kv_size: Optional[int] = None, max_chunk_size: int = 512) -> None:
+        self.block_size = int(block_size)
+        self.local_window_tokens = int(local_window_tokens)
+        self.max_kv_size = int(max_kv_size) if max_kv_size else None
+        self.max_chunk_size = int(max_chunk_size)
+        self._ring_k: Optional[torch.Tensor] = None
+        self._ring_v: Optional[torch.Tensor] = None
+        self._pool_k: Optional[torch.Tensor] = None
+        self._pool_v: Optional[torch.Tensor] = None
+        self._realign = False   # tail stored at slots [0, tail_size) by the state setter
+        self.tail_capacity = 0
+        self.summary_capacity = 0
+        self.tail_size = 0
+        self.summary_count = 0
+        self.offset = 0
+        self.summary_offset = 0
+
+    # ------------------------------------------------------------------ allocation
+    def _allocate(self, b: int, h: int, d: int, dtype: torch.dtype, device) -> None:
+        # compressed_cache.py:69-92 (same capacity formulas)
+        self.tail_capacity = self.local_window_tokens + 2 * self.max_chunk_size + 2 * self.block_size
+        self.summary_capacity = (self.max_kv_size // self.block_size + 4) if self.max_kv_size is not None else 2048
+        self._ring_k = torch.zeros((b, h, self.tail_capacity, d), dtype=dtype, device=device)
+        self._ring_v = torch.zeros_like(self._ring_k)
+        self._pool_k = torch.zeros((b, h, self.summary_capacity, d), dtype=dtype, device=device)
+        self._pool_v = torch.zeros_like(self._pool_k)
+
+    def _apply_realign(self) -> None:
+        if self._realign and self._ring_k is not None:
+            shift = (self.offset - self.tail_size) % self.tail_capacity
+            if shift:
+                self._ring_k = torch.roll(self._ring_k, shifts=shift, dims=2).contiguous()
+                self._ring_v = torch.roll(self._ring_v, shifts=shift, dims=2).contiguous()
+        self._realign = False
+
+    # ------------------------------------------------------------------ update
+    def update(self, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """Append, summarise completed blocks, trim (compressed_cache.py:94-172)."""
+        if not keys.is_cuda or keys.shape != values.shape or keys.dtype != values.dtype:
+            raise ValueError("keys/values must be matching GPU tensors [B, H, step, d]")
+        step = int(keys.shape[2])
+        b, h, d = int(keys.shape[0]), int(keys.shape[1]), int(keys.shape[3])
+        if self._ring_k is None:
+            self._allocate(b, h, d, keys.dtype, keys.device)
+        self._apply_realign()
+        if tuple(self._ring_k.shape[:2]) != (b, h) or self._ring_k.shape[3] != d or keys.dtype != self._ring_k.dtype:
+            raise ValueError("keys do not match the cache's batch/head/dim/dtype")
+        bs, lw = self.block_size, self.local_window_tokens
+        if self.tail_size + step > self.tail_capacity:
+            raise RuntimeError(
+                f"CompressedKVCache.tail_capacity={self.tail_capacity} too small to fit "
+                f"tail_size={self.tail_size} + step={step}; raise max_chunk_size or "
+                f"local_window_tokens to make room.")
+        keys, values = _c(keys), _c(values)
+        dt = _dtype_code(keys)
+        st = _stream(keys)
+        with torch.cuda.device(keys.device):
+            _native.call("bfly_cache_append", keys.data_ptr(), values.data_ptr(), dt, b, h, step, d,
+                         self._ring_k.data_ptr(), self._ring_v.data_ptr(), self.tail_capacity, self.offset, st)
+        self.tail_size += step
+        self.offset += step
+        first_pos, first_slot, n_new = self.summary_offset, self.summary_count, 0
+        overflow = False
+        while self.summary_offset + bs <= self.offset - lw:
+            tail_start = self.offset - self.tail_size
+            block_start = self.summary_offset - tail_start
+            if block_start < 0 or block_start + bs > self.tail_size:
+                break
+            if self.summary_count + n_new >= self.summary_capacity:
+                overflow = True
+                break
+            n_new += 1
+            self.summary_offset += bs
+        if n_new:
+            with torch.cuda.device(keys.device):
+                _native.call("bfly_cache_compress", self._ring_k.data_ptr(), self._ring_v.data_ptr(), dt, b, h, d,
+                             self.tail_capacity, first_pos, n_new, bs, self._pool_k.data_ptr(),
+                             self._pool_v.data_ptr(), self.summary_capacity, first_slot, st)
+            self.summary_count += n_new
+        if overflow:
+            raise RuntimeError(
+                f"CompressedKVCache.summary_capacity={self.summary_capacity} exhausted "
+                f"at offset={self.offset}; raise max_kv_size at construction time.")
+        target = max(lw, step + lw - 1)
+        while self.tail_size - bs >= target:
+            self.tail_size -= bs
+
+    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
+        self.update(keys, values)
+        return self.keys, self.values
+
+    # ------------------------------------------------------------------ views
+    def _tail_view(self, ring: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+        if ring is None:
+            return None
+        if self._realign:
+            return ring[:, :, : self.tail_size]
+        start = self.offset - self.tail_size
+        idx = (torch.arange(start, self.offset, device=ring.device) % self.tail_capacity)
+        return ring.index_select(2, idx)
+
+    @property
+    def keys(self) -> Optional[torch.Tensor]:
+        return self._tail_view(self._ring_k)
+
+    @property
+    def values(self) -> Optional[torch.Tensor]:
+        return self._tail_view(self._ring_v)
+
+    @property
+    def k_summary(self) -> Optional[torch.Tensor]:
+        return None if self._pool_k is None else self._pool_k[:, :, : self.summary_count]
+
+    @property
+    def v_summary(self) -> Optional[torch.Tensor]:
+        return None if self._pool_v is None else self._pool_v[:, :, : self.summary_count]
+
+    def get_compressed_state(self):
+        if self._ring_k is None:
+            raise ValueError("CompressedKVCache is empty")
+        return (self.keys, self.values, self.k_summary, self.v_summary,
+                int(self.offset - self.tail_size), int(self.offset))
+
+    def ring_state(self) -> RingState:
+        """Device buffers and counters for the attention kernel (no copies)."""
+        if self._ring_k is None:
+            raise ValueError("CompressedKVCache is empty")
+        self._apply_realign()
+        return RingState(self._ring_k, self._ring_v, self.tail_capacity, self.offset - self.tail_size,
+                         self.offset, self._pool_k, self._pool_v, self.summary_count)
+
+    # ------------------------------------------------------------------ mlx_lm cache protocol
+    def size(self) -> int:
+        return int(self.offset)
+
+    def is_trimmable(self) -> bool:
+        return False
+
+    def trim(self, n: int) -> int:
+        return 0
+
+    def make_mask(self, N: int, window_size: Optional[int] = None, return_array: bool = False):
+        """Causal mask for N new queries (mlx_lm ``create_causal_mask`` semantics)."""
+        if N == 1 and window_size is None:
+            return None
+        if return_array or N > 1:
+            dev = self._ring_k.device if self._ring_k is not None else None
+            r = torch.arange(self.offset + N, device=dev)
+            l = torch.arange(self.offset, self.offset + N, device=dev)[:, None]
+            mask = l >= r[None]
+            if window_size is not None:
+                mask = mask & (l < r[None] + window_size)
+            return mask
+        return None
+
+    def empty(self) -> bool:
+        return self._ring_k is None or self.tail_size == 0
+
+    @property
+    def nbytes(self) -> int:
+        """Bytes of the valid slices only (compressed_cache.py:231-244)."""
+        if self._ring_k is None:
+            return 0
+        b, h, _, d = self._ring_k.shape
+        e = self._ring_k.element_size()
+        return 2 * b * h * d * e * (self.tail_size + self.summary_count)
+
+    @property
+    def state(self) -> tuple[Any, Any, Any, Any]:
+        return self.keys, self.values, self.k_summary, self.v_summary
+
+    @state.setter
+    def state(self, v) -> None:
+        keys, values, k_summary, v_summary = v
+        if keys is None or values is None:
+            self._ring_k = self._ring_v = None
+            self.tail_size = 0
+        else:
+            b, h, t, d = keys.shape
+            if self._ring_k is None or self._ring_k.shape[2] < t:
+                self._allocate(int(b), int(h), int(d), keys.dtype, keys.device)
+            self._ring_k[:, :, :t] = keys
+            self._ring_v[:, :, :t] = values
+            self.tail_size = int(t)
+            self._realign = True
+        if k_summary is None or v_summary is None:
+            self.summary_count = 0
+        else:
+            b, h, s, d = k_summary.shape
+            if self._pool_k is None or self._pool_k.shape[2] < s:
+                cap = max(int(s), self.summary_capacity)
+                self._pool_k = torch.zeros((b, h, cap, d), dtype=k_summary.dtype, device=k_summary.device)
+                self._pool_v = torch.zeros_like(self._pool_k)
+                self.summary_capacity = cap
+            self._pool_k[:, :, :s] = k_summary
+            self._pool_v[:, :, :s] = v_summary
+            self.summary_count = int(s)
+
+    @property
+    def meta_state(self) -> tuple[str, str, str, str]:
+        return tuple(map(str, (self.block_size, self.local_window_tokens, self.offset, self.summary_offset)))
+
+    @meta_state.setter
+    def meta_state(self, v) -> None:
+        self.block_size, self.local_window_tokens, self.offset, self.summary_offset = map(int, v)

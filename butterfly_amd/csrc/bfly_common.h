@@ -1,0 +1,58 @@
+// Shared helpers for the Butterfly compressed-attention HIP library (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/butterfly_amd.h"
+
+namespace bfly {
+
+// Per-thread last-error string returned by bfly_last_error().
+void set_error(const char* fmt, ...);
+
+#define BFLY_CHECK_ARG(cond, ...)          \
+  do {                                     \
+    if (!(cond)) {                         \
+      ::bfly::set_error(__VA_ARGS__);      \
+      return BFLY_ERR_INVALID;             \
+    }                                      \
+  } while (0)
+
+#define BFLY_CHECK_LAUNCH(what)                                              \
+  do {                                                                       \
+    hipError_t e_ = hipGetLastError();                                       \
+    if (e_ != hipSuccess) {                                                  \
+      ::bfly::set_error("%s: launch failed: %s", what, hipGetErrorString(e_)); \
+      return BFLY_ERR_HIP;                                                   \
+    }                                                                        \
+  } while (0)
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(__bf16 x) { return (float)x; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ __bf16 from_f32<__bf16>(float x) { return (__bf16)x; }
+
+// Vectorised paths issue 16-byte loads/stores: tensor base pointers must be 16-byte aligned.
+__host__ __forceinline__ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Floor division / modulo for possibly negative positions.
+__host__ __device__ __forceinline__ int64_t floordiv(int64_t a, int64_t b) {
+  int64_t q = a / b;
+  return (a % b != 0 && ((a < 0) != (b < 0))) ? q - 1 : q;
+}
+__host__ __device__ __forceinline__ int64_t posmod(int64_t a, int64_t b) {
+  int64_t r = a % b;
+  return r < 0 ? r + b : r;
+}
+
+}  // namespace bfly

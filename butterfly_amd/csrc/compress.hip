@@ -1,0 +1,197 @@
+// Mean-pool block compressor and two-pool cache maintenance on gfx950.
+//
+// Reference semantics: _block_mean_summaries_torch
+// (bna/torch/attention_wayfinder_permute.py:1022-1043), the summarise and
+// append steps of CompressedKVCache.update_and_fetch
+// (bna/mlx/compressed_cache.py:104-149).
+//
+// These kernels are HBM-bound: every input byte is read once with 16-byte
+// vector loads, accumulated in fp32 registers and reduced through LDS.
+// Fixed summation order (documented so results are reproducible): thread slot
+// s (of RS slots) sums tokens s, s+RS, s+2RS, ... sequentially; the RS partial
+// sums are then added in slot order 0..RS-1; the total is divided by the
+// valid-token count and rounded (RNE) to the storage type.
+#include "bfly_common.h"
+
+namespace bfly {
+
+struct PoolJob {
+  const void* src;      // [rows, src_rows_per_seq, d]
+  void* dst;            // [rows, dst_rows_per_seq, d]
+  int64_t src_rows;     // rows per sequence in src (T, or ring capacity)
+  int64_t dst_rows;     // rows per sequence in dst
+  int64_t ring;         // 0: linear source; else position p lives at p mod ring
+  int64_t base_pos;     // position of token 0 of block 0
+  int64_t dst_slot0;    // dst row of block 0
+  int64_t seq_len;      // valid tokens are positions < base_pos + seq_len
+};
+
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256) block_mean_kernel(PoolJob j0, PoolJob j1, int d, int bs) {
+  const PoolJob& job = blockIdx.z == 0 ? j0 : j1;
+  const int64_t n = blockIdx.x;          // block index
+  const int64_t row = blockIdx.y;        // sequence (b*h)
+  const int lpr = d / VEC;               // lanes per token row
+  const int rs = 256 / lpr;              // token slots
+  const int t = threadIdx.x;
+  const int c = t % lpr, s = t / lpr;
+  const int64_t first = n * bs;
+  int64_t cnt = job.seq_len - first;
+  cnt = cnt < bs ? cnt : bs;
+  if (cnt < 0) cnt = 0;
+  const T* src = reinterpret_cast<const T*>(job.src) + row * job.src_rows * d;
+  float acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+  if (s < rs) {
+    for (int64_t tok = s; tok < cnt; tok += rs) {
+      int64_t p = job.base_pos + first + tok;
+      int64_t r = job.ring ? posmod(p, job.ring) : p;
+      const T* ptr = src + r * d + c * VEC;
+      if constexpr (VEC * sizeof(T) == 16) {
+        uint4 raw = *reinterpret_cast<const uint4*>(ptr);
+        const T* v = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += to_f32(v[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += to_f32(ptr[e]);
+      }
+    }
+  }
+  __shared__ float part[256 * 8];
+  if (s < rs) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) part[s * d + c * VEC + e] = acc[e];
+  }
+  __syncthreads();
+  T* dst = reinterpret_cast<T*>(job.dst) + (row * job.dst_rows + job.dst_slot0 + n) * d;
+  const float denom = cnt > 0 ? (float)cnt : 1.f;
+  for (int col = t; col < d; col += 256) {
+    float tot = 0.f;
+    for (int k = 0; k < rs; ++k) tot += part[k * d + col];
+    dst[col] = from_f32<T>(tot / denom);
+  }
+}
+
+template <typename T>
+static int launch_pool(const PoolJob& a, const PoolJob* b, int64_t rows, int d, int bs,
+                       int64_t nblocks, hipStream_t stream) {
+  dim3 grid((unsigned)nblocks, (unsigned)rows, b ? 2 : 1);
+  const PoolJob& bj = b ? *b : a;
+  constexpr int V16 = 16 / sizeof(T);
+  if (d % V16 == 0 && d / V16 <= 256 && 256 * V16 <= 256 * 8) {
+    hipLaunchKernelGGL((block_mean_kernel<T, V16>), grid, dim3(256), 0, stream, a, bj, d, bs);
+  } else if (d <= 256) {
+    hipLaunchKernelGGL((block_mean_kernel<T, 1>), grid, dim3(256), 0, stream, a, bj, d, bs);
+  } else {
+    set_error("head_dim=%d unsupported by the compressor", d);
+    return BFLY_ERR_UNSUPPORTED;
+  }
+  return BFLY_OK;
+}
+
+template <typename T>
+__global__ void append_kernel(const T* __restrict__ kn, const T* __restrict__ vn, T* __restrict__ rk,
+                              T* __restrict__ rv, int64_t step, int d, int64_t ring,
+                              int64_t offset, int64_t total_vec, int vec) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool isv = blockIdx.y == 1;
+  if (i >= total_vec) return;
+  const int64_t per_row = d / vec;
+  const int64_t e = (i % per_row) * vec;
+  const int64_t rowi = i / per_row;          // (bh, t) flattened
+  const int64_t t = rowi % step, bh = rowi / step;
+  const int64_t slot = posmod(offset + t, ring);
+  const T* src = (isv ? vn : kn) + rowi * d + e;
+  T* dst = (isv ? rv : rk) + (bh * ring + slot) * d + e;
+  if (vec * sizeof(T) == 16) {
+    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+  } else {
+    for (int k = 0; k < vec; ++k) dst[k] = src[k];
+  }
+}
+
+}  // namespace bfly
+
+using namespace bfly;
+
+static bool dtype_ok(int dtype) { return dtype == BFLY_DTYPE_F32 || dtype == BFLY_DTYPE_BF16; }
+
+extern "C" int bfly_block_mean(const void* x, void* out, const void* x2, void* out2, int dtype,
+                               int64_t rows, int64_t seq_len, int head_dim, int block_size,
+                               int64_t num_blocks, hipStream_t stream) {
+  BFLY_CHECK_ARG(dtype_ok(dtype), "unsupported dtype %d", dtype);
+  BFLY_CHECK_ARG(x && out, "null pointer");
+  BFLY_CHECK_ARG((x2 == nullptr) == (out2 == nullptr), "x2/out2 must both be given or both NULL");
+  BFLY_CHECK_ARG(aligned16(x) && aligned16(out) && aligned16(x2) && aligned16(out2),
+                 "tensor pointers must be 16-byte aligned");
+  BFLY_CHECK_ARG(rows > 0 && rows <= 65535, "rows=%lld out of range", (long long)rows);
+  BFLY_CHECK_ARG(seq_len > 0 && head_dim > 0 && block_size > 0, "non-positive shape");
+  BFLY_CHECK_ARG(num_blocks * block_size >= seq_len && num_blocks <= INT32_MAX,
+                 "num_blocks*block_size must cover seq_len");
+  PoolJob a{x, out, seq_len, num_blocks, 0, 0, 0, seq_len};
+  PoolJob b{x2, out2, seq_len, num_blocks, 0, 0, 0, seq_len};
+  int rc = dtype == BFLY_DTYPE_F32
+               ? launch_pool<float>(a, x2 ? &b : nullptr, rows, head_dim, block_size, num_blocks, stream)
+               : launch_pool<__bf16>(a, x2 ? &b : nullptr, rows, head_dim, block_size, num_blocks, stream);
+  if (rc) return rc;
+  BFLY_CHECK_LAUNCH("bfly_block_mean");
+  return BFLY_OK;
+}
+
+extern "C" int bfly_cache_append(const void* k_new, const void* v_new, int dtype, int64_t batch,
+                                 int hkv, int64_t step, int head_dim, void* ring_k, void* ring_v,
+                                 int64_t ring_capacity, int64_t offset, hipStream_t stream) {
+  BFLY_CHECK_ARG(dtype_ok(dtype), "unsupported dtype %d", dtype);
+  BFLY_CHECK_ARG(k_new && v_new && ring_k && ring_v, "null pointer");
+  BFLY_CHECK_ARG(aligned16(k_new) && aligned16(v_new) && aligned16(ring_k) && aligned16(ring_v),
+                 "tensor pointers must be 16-byte aligned");
+  BFLY_CHECK_ARG(batch > 0 && hkv > 0 && head_dim > 0 && step >= 0, "bad shape");
+  BFLY_CHECK_ARG(ring_capacity > 0 && step <= ring_capacity, "step=%lld exceeds ring capacity %lld",
+                 (long long)step, (long long)ring_capacity);
+  BFLY_CHECK_ARG(offset >= 0, "negative offset");
+  if (step == 0) return BFLY_OK;
+  const int esz = dtype == BFLY_DTYPE_F32 ? 4 : 2;
+  const int vec = (head_dim * esz) % 16 == 0 ? 16 / esz : 1;
+  const int64_t total = batch * hkv * step * (head_dim / vec);
+  const int threads = 256;
+  dim3 grid((unsigned)((total + threads - 1) / threads), 2);
+  if (dtype == BFLY_DTYPE_F32)
+    hipLaunchKernelGGL(append_kernel<float>, grid, dim3(threads), 0, stream, (const float*)k_new,
+                       (const float*)v_new, (float*)ring_k, (float*)ring_v, step, head_dim,
+                       ring_capacity, offset, total, vec);
+  else
+    hipLaunchKernelGGL(append_kernel<__bf16>, grid, dim3(threads), 0, stream, (const __bf16*)k_new,
+                       (const __bf16*)v_new, (__bf16*)ring_k, (__bf16*)ring_v, step, head_dim,
+                       ring_capacity, offset, total, vec);
+  BFLY_CHECK_LAUNCH("bfly_cache_append");
+  return BFLY_OK;
+}
+
+extern "C" int bfly_cache_compress(const void* ring_k, const void* ring_v, int dtype,
+                                   int64_t batch, int hkv, int head_dim, int64_t ring_capacity,
+                                   int64_t first_block_pos, int64_t n_blocks, int block_size,
+                                   void* pool_k, void* pool_v, int64_t pool_capacity,
+                                   int64_t first_slot, hipStream_t stream) {
+  BFLY_CHECK_ARG(dtype_ok(dtype), "unsupported dtype %d", dtype);
+  BFLY_CHECK_ARG(ring_k && ring_v && pool_k && pool_v, "null pointer");
+  BFLY_CHECK_ARG(aligned16(ring_k) && aligned16(ring_v) && aligned16(pool_k) && aligned16(pool_v),
+                 "tensor pointers must be 16-byte aligned");
+  BFLY_CHECK_ARG(batch > 0 && hkv > 0 && head_dim > 0 && block_size > 0, "bad shape");
+  BFLY_CHECK_ARG(batch * hkv <= 65535, "batch*hkv too large");
+  BFLY_CHECK_ARG(ring_capacity >= block_size, "ring smaller than a block");
+  BFLY_CHECK_ARG(n_blocks >= 0 && first_slot >= 0 && first_slot + n_blocks <= pool_capacity,
+                 "summary pool overflow: slots [%lld, %lld) of %lld", (long long)first_slot,
+                 (long long)(first_slot + n_blocks), (long long)pool_capacity);
+  if (n_blocks == 0) return BFLY_OK;
+  const int64_t seq = n_blocks * (int64_t)block_size;
+  PoolJob a{ring_k, pool_k, ring_capacity, pool_capacity, ring_capacity, first_block_pos, first_slot, seq};
+  PoolJob b{ring_v, pool_v, ring_capacity, pool_capacity, ring_capacity, first_block_pos, first_slot, seq};
+  int rc = dtype == BFLY_DTYPE_F32
+               ? launch_pool<float>(a, &b, batch * hkv, head_dim, block_size, n_blocks, stream)
+               : launch_pool<__bf16>(a, &b, batch * hkv, head_dim, block_size, n_blocks, stream);
+  if (rc) return rc;
+  BFLY_CHECK_LAUNCH("bfly_cache_compress");
+  return BFLY_OK;
+}

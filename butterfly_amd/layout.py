@@ -1,0 +1,116 @@
+"""Block Butterfly layout (the reference's ``build_block_butterfly_layout``).
+
+Reference: bna/torch/attention_wayfinder_permute.py:568-682 (Torch,
+``BlockHamiltonianLayout`` :382-405) and bna/mlx/attention.py:196-301 (MLX,
+``BlockSparseButterflyLayout`` :105-141).  The layout holds the device
+neighbour table once ([N, K] int32); ``block_neighbors`` exposes it as the
+reference's [Hq, N, K] tensor (identical across heads) without copying.
+
+Tables are shared across layouts with the same block count and topology
+(the reference shares layouts across layers through a keyed cache,
+bna/integrations/qwen_mlx.py:47-48, 790-820): during decode the sequence
+length grows by one token per step but the table only changes when the block
+count does.
+"""
+from __future__ import annotations
+
+from collections import OrderedDict
+from dataclasses import dataclass
+
+import torch
+
+from .topology import ButterflyLayoutMetadata, block_neighbor_table, butterfly_layout_metadata
+
+_TABLE_CACHE: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+_TABLE_CACHE_MAX = 256
+
+
+@dataclass(frozen=True)
+class BlockButterflyLayout:
+    seq_len: int
+    block_size: int
+    num_blocks: int
+    num_query_heads: int
+    neighbors: torch.Tensor          # device int32 [N, K], -1 padded
+    metadata: ButterflyLayoutMetadata
+    topology_name: str = "butterfly"
+
+    @property
+    def block_neighbors(self) -> torch.Tensor:
+        """[Hq, N, K] view, identical for every query head."""
+        return self.neighbors.unsqueeze(0).expand(self.num_query_heads, -1, -1)
+
+    @property
+    def num_neighbors(self) -> int:
+        return int(self.neighbors.shape[1])
+
+    @property
+    def stage_idx(self) -> int:
+        return self.metadata.stage_idx
+
+    @property
+    def stage_count(self) -> int:
+        return self.metadata.stage_count
+
+    @property
+    def local_window_blocks(self) -> int:
+        return self.metadata.local_window_blocks
+
+    @property
+    def partner_rule(self) -> str:
+        return self.metadata.partner_rule
+
+    @property
+    def partner_count(self) -> int:
+        return self.metadata.partner_count
+
+    @property
+    def sink_blocks(self) -> tuple[int, ...]:
+        return self.metadata.sink_blocks
+
+
+def build_block_butterfly_layout(*, seq_len: int, block_size: int, num_key_value_heads: int,
+                                 num_key_value_groups: int, layer_idx: int, local_window_blocks: int = 4,
+                                 sink_count: int = 1, partner_count: int = 1, partner_rule: str = "xor",
+                                 device=None) -> BlockButterflyLayout:
+    """Build (or fetch) the staged Butterfly block layout of one layer."""
+    if int(seq_len) <= 0:
+        raise ValueError("seq_len must be positive")
+    if int(block_size) <= 0:
+        raise ValueError("block_size must be positive")
+    if int(num_key_value_heads) <= 0:
+        raise ValueError("num_key_value_heads must be positive")
+    if int(num_key_value_groups) <= 0:
+        raise ValueError("num_key_value_groups must be positive")
+    if int(local_window_blocks) < 0:
+        raise ValueError("local_window_blocks must be >= 0")
+    if int(sink_count) < 0:
+        raise ValueError("sink_count must be >= 0")
+    if int(partner_count) < 0:
+        raise ValueError("partner_count must be >= 0")
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    n = (int(seq_len) + int(block_size) - 1) // int(block_size)
+    meta = butterfly_layout_metadata(num_blocks=n, layer_idx=layer_idx, partner_rule=partner_rule,
+                                     partner_count=partner_count, sink_count=sink_count,
+                                     local_window_blocks=local_window_blocks)
+    key = (n, meta.stage_idx, meta.partner_rule, meta.partner_bits, int(local_window_blocks), int(sink_count),
+           str(dev))
+    table = _TABLE_CACHE.get(key)
+    if table is None:
+        table = block_neighbor_table(num_blocks=n, layer_idx=layer_idx, partner_rule=partner_rule,
+                                     local_window_blocks=local_window_blocks, sink_count=sink_count,
+                                     partner_count=partner_count, device=dev)
+        _TABLE_CACHE[key] = table
+        while len(_TABLE_CACHE) > _TABLE_CACHE_MAX:
+            _TABLE_CACHE.popitem(last=False)
+    else:
+        _TABLE_CACHE.move_to_end(key)
+    return BlockButterflyLayout(
+        seq_len=int(seq_len), block_size=int(block_size), num_blocks=n,
+        num_query_heads=int(num_key_value_heads) * int(num_key_value_groups),
+        neighbors=table, metadata=meta,
+    )
+
+
+def clear_layout_cache() -> None:
+    _TABLE_CACHE.clear()

@@ -1,0 +1,191 @@
+/*
+ * butterfly_amd -- C ABI of the MI355X (gfx950) Butterfly compressed-attention library.
+ *
+ * Conventions
+ *   - Every tensor argument is a caller-owned DEVICE pointer, row-major and
+ *     contiguous in the stated shape ([B, H, T, d] means d fastest), with a
+ *     16-byte aligned base address (the kernels use 16-byte vector accesses).
+ *   - `dtype` is BFLY_DTYPE_F32 or BFLY_DTYPE_BF16 and applies to every
+ *     floating-point tensor of the call.
+ *   - Work is enqueued on `stream`; nothing synchronises and nothing allocates.
+ *   - Return 0 on success, a negative BFLY_ERR_* code otherwise; the message of
+ *     the last failure on the calling thread is returned by bfly_last_error().
+ *   - Partner rules: BFLY_RULE_* (the reference's ButterflyPartnerRule strings).
+ *
+ * Reference citations are `path:line` in Hmbown/Butterfly.
+ */
+#ifndef BUTTERFLY_AMD_H_
+#define BUTTERFLY_AMD_H_
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BFLY_ABI_VERSION 1
+
+#define BFLY_OK 0
+#define BFLY_ERR_INVALID (-1)     /* bad shape / argument: ValueError in the reference */
+#define BFLY_ERR_UNSUPPORTED (-2) /* valid but not implemented on this path */
+#define BFLY_ERR_HIP (-3)         /* HIP runtime failure */
+
+#define BFLY_DTYPE_F32 0
+#define BFLY_DTYPE_BF16 1
+
+#define BFLY_RULE_XOR 0
+#define BFLY_RULE_BIT_REVERSAL 1
+#define BFLY_RULE_BENES 2
+#define BFLY_RULE_CAUSAL_SHIFT 3
+#define BFLY_RULE_FIXED_STRIDE 4
+#define BFLY_RULE_RANDOM 5
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* bfly_last_error(void);
+
+/* BFLY_ABI_VERSION of the loaded library. */
+int bfly_abi_version(void);
+
+/*
+ * Host scalar topology metadata.
+ * Replaces butterfly_width / butterfly_stage_meta (bna/topology/butterfly.py:39-65).
+ * width = ceil(log2 N) (1 if N <= 1); stage_count = width, or max(1, 2*width-2)
+ * for benes; stage_idx = layer_idx mod stage_count.
+ */
+int bfly_stage_meta(int64_t num_blocks, int64_t layer_idx, int partner_rule,
+                    int32_t* stage_idx, int32_t* stage_count, int32_t* width);
+
+/*
+ * Host: partner bits of one stage, written to bits[0..partner_count).
+ * Replaces butterfly_partner_bits (bna/topology/butterfly.py:77-105).
+ */
+int bfly_partner_bits(int stage_idx, int stage_count, int width, int partner_count,
+                      int partner_rule, int32_t* bits);
+
+/*
+ * Device: the block-neighbour (partner) table of one layer.
+ * Replaces the row loop of build_block_butterfly_layout
+ * (bna/torch/attention_wayfinder_permute.py:627-662; bna/mlx/attention.py:235-262)
+ * built on butterfly_partner_block / build_butterfly_neighbor_role_row
+ * (bna/topology/butterfly.py:108-141, 219-284).
+ * neighbors: int32 [num_blocks, kcap]; row b = ordered unique
+ * [b, b-1..b-lwb, partners, sinks] (entries in [0, N)), padded with -1.
+ * degree: int32 [num_blocks], the row lengths (K = max over blocks).
+ * kcap must be >= 1 + local_window_blocks + partner_count + sink_count.
+ */
+int bfly_block_neighbors(int64_t num_blocks, int64_t layer_idx, int partner_rule,
+                         int local_window_blocks, int sink_count, int partner_count,
+                         int32_t* neighbors, int kcap, int32_t* degree, hipStream_t stream);
+
+/*
+ * Device: one-shot prefill routing tables (block-level cut-off
+ * local_start = max(0, b*BS - W + 1)).
+ * Replaces _compressed_butterfly_block_index_tensors
+ * (bna/torch/attention_wayfinder_permute.py:912-966; bna/mlx/attention.py:1202-1263).
+ * raw_idx int32 [N, W+BS-1]; raw_mask uint8 [N, BS, W+BS-1];
+ * summary_idx int32 [N, kcap]; summary_mask uint8 [N, BS, kcap].
+ */
+int bfly_prefill_tables(const int32_t* neighbors, int64_t num_blocks, int kcap, int block_size,
+                        int64_t seq_len, int window, int32_t* raw_idx, uint8_t* raw_mask,
+                        int32_t* summary_idx, uint8_t* summary_mask, hipStream_t stream);
+
+/*
+ * Device: active-row routing tables (token-level cut-off local_start = max(0, p - W + 1)).
+ * tail_len < 0: replaces _compressed_butterfly_active_index_tensors
+ *   (bna/torch/attention_wayfinder_permute.py:969-1019; bna/mlx/attention.py:1266-1324).
+ * tail_len >= 0: replaces _compressed_butterfly_active_indices_from_tail
+ *   (bna/mlx/attention.py:1601-1666): raw slots restricted to the tail
+ *   [tail_start, tail_start+tail_len) and re-based to it; summaries limited to
+ *   n < num_summary_blocks.
+ * query_positions int32 [tq]; raw_idx int32 [tq, W]; raw_mask uint8 [tq, W];
+ * summary_idx int32 [tq, kcap]; summary_mask uint8 [tq, kcap].
+ */
+int bfly_active_tables(const int32_t* neighbors, int64_t num_blocks, int kcap, int block_size,
+                       int64_t kv_len, int window, const int32_t* query_positions, int64_t tq,
+                       int64_t tail_start, int64_t tail_len, int64_t num_summary_blocks,
+                       int32_t* raw_idx, uint8_t* raw_mask, int32_t* summary_idx,
+                       uint8_t* summary_mask, hipStream_t stream);
+
+/*
+ * Device: mean-pool compressor. For each of `rows` (= B*H) sequences of
+ * seq_len tokens, out[row, n] = mean of the valid tokens of block n
+ * (fp32 accumulate, divide by max(count,1), round to dtype).
+ * Replaces _block_mean_summaries_torch (bna/torch/attention_wayfinder_permute.py:1022-1043)
+ * and _block_mean_summaries_impl (bna/mlx/attention.py:1373-1393).
+ * x: [rows, seq_len, d] -> out: [rows, num_blocks, d]. x2/out2 may be NULL;
+ * when given they are pooled in the same launch (keys and values together).
+ */
+int bfly_block_mean(const void* x, void* out, const void* x2, void* out2, int dtype, int64_t rows,
+                    int64_t seq_len, int head_dim, int block_size, int64_t num_blocks,
+                    hipStream_t stream);
+
+/*
+ * Device: one-shot compressed Butterfly prefill (q_len == k_len).
+ * Replaces butterfly_compressed_attention (bna/torch/attention_wayfinder_permute.py:1046-1122)
+ * and compressed_butterfly_attention (bna/mlx/attention.py:1401-1468):
+ * each query p of block b attends, in one softmax, to the raw keys
+ * [max(0, p-W+1), p] and to the mean summaries of the routed neighbours n of b
+ * with n < b and (n+1)*BS <= max(0, b*BS - W + 1).
+ * q: [B, Hq, T, d]; k, v: [B, Hkv, T, d]; k_summary, v_summary: [B, Hkv, N, d]
+ * (from bfly_block_mean); neighbors: int32 [N, kcap]; out: [B, Hq, T, d].
+ * Query head h reads kv head h / (Hq/Hkv).  scale multiplies q.k.
+ */
+int bfly_prefill(const void* q, const void* k, const void* v, const void* k_summary,
+                 const void* v_summary, int dtype, int64_t batch, int hq, int hkv, int64_t seq_len,
+                 int head_dim, const int32_t* neighbors, int64_t num_blocks, int kcap,
+                 int block_size, int window, float scale, void* out, hipStream_t stream);
+
+/*
+ * Device: active rows over a two-pool cache (token-level cut-off).
+ * Replaces compressed_butterfly_attention_from_cache (bna/mlx/attention.py:1816-1876,
+ * streams :1669-1813 merged by :519-548) and, with a linear cache
+ * (ring_capacity == 0, tail_start == 0, pools = block means of the full K/V,
+ * summary_count = N), butterfly_compressed_attention_active
+ * (bna/torch/attention_wayfinder_permute.py:1125-1197).
+ * Query r sits at position query_positions[r] (device int32 [tq]) or, when
+ * query_positions is NULL, at q_pos0 + r.  It attends to the tail keys in
+ * [max(tail_start, p-W+1), p] (p < kv_len) and to the routed summaries n of block
+ * min(p/BS, N-1) with n < that block, n < summary_count and (n+1)*BS <= max(0, p-W+1).
+ * q: [B, Hq, tq, d].  tail_k/tail_v: [B, Hkv, C, d] holding position p at
+ * slot p mod C (ring_capacity C > 0), or, when C == 0, the linear tail
+ * [B, Hkv, kv_len - tail_start, d] holding position p at row p - tail_start.
+ * pool_k/pool_v: [B, Hkv, pool_capacity, d] with rows [0, summary_count) valid.
+ * out: [B, Hq, tq, d].
+ */
+int bfly_attend_cache(const void* q, int dtype, int64_t batch, int hq, int hkv, int64_t tq,
+                      int head_dim, const int32_t* query_positions, int64_t q_pos0,
+                      const void* tail_k, const void* tail_v, int64_t ring_capacity,
+                      int64_t tail_start, int64_t kv_len, const void* pool_k, const void* pool_v,
+                      int64_t pool_capacity, int64_t summary_count, const int32_t* neighbors,
+                      int64_t num_blocks, int kcap, int block_size, int window, float scale,
+                      void* out, hipStream_t stream);
+
+/*
+ * Device: append `step` new tokens at positions [offset, offset+step) of the
+ * tail ring (slot = position mod ring_capacity).
+ * Replaces the tail append of CompressedKVCache.update_and_fetch
+ * (bna/mlx/compressed_cache.py:104-118).  k_new/v_new: [B, Hkv, step, d];
+ * ring_k/ring_v: [B, Hkv, ring_capacity, d].  Requires step <= ring_capacity.
+ */
+int bfly_cache_append(const void* k_new, const void* v_new, int dtype, int64_t batch, int hkv,
+                      int64_t step, int head_dim, void* ring_k, void* ring_v,
+                      int64_t ring_capacity, int64_t offset, hipStream_t stream);
+
+/*
+ * Device: summarise `n_blocks` complete blocks starting at position
+ * first_block_pos (a multiple of block_size) from the tail ring into pool slots
+ * [first_slot, first_slot + n_blocks): fp32 mean over block_size tokens, rounded to dtype.
+ * Replaces the summarise loop of CompressedKVCache.update_and_fetch
+ * (bna/mlx/compressed_cache.py:120-149).
+ */
+int bfly_cache_compress(const void* ring_k, const void* ring_v, int dtype, int64_t batch, int hkv,
+                        int head_dim, int64_t ring_capacity, int64_t first_block_pos,
+                        int64_t n_blocks, int block_size, void* pool_k, void* pool_v,
+                        int64_t pool_capacity, int64_t first_slot, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BUTTERFLY_AMD_H_ */

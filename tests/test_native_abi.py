@@ -1,0 +1,68 @@
+"""The C-ABI library loads and exports every entry point declared in include/*.h.
+
+Runs without a GPU: only host-side functions (stage metadata, partner bits,
+error reporting) are called; device entry points are checked for presence and
+argument validation only.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from butterfly_amd import _native
+from oracle import topology as tp
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(bfly_\w+)\s*\(", text, flags=re.M))
+    return names
+
+
+def test_header_declares_entry_points():
+    names = _declared_symbols()
+    assert {"bfly_prefill", "bfly_attend_cache", "bfly_block_mean", "bfly_block_neighbors"} <= names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.lib()
+    for name in sorted(_declared_symbols()):
+        assert hasattr(lib, name), name
+    assert set(_native.SIGNATURES) == _declared_symbols()
+    assert lib.bfly_abi_version() == 1
+
+
+@pytest.mark.parametrize("rule", list(tp.RULES))
+def test_host_stage_meta_matches_oracle(rule):
+    lib = _native.lib()
+    s, c, w = C.c_int32(), C.c_int32(), C.c_int32()
+    for n in [1, 2, 3, 7, 32, 33, 512, 1024, 1025, 2048, 100003]:
+        for layer in [0, 1, 4, 9, 13, 40]:
+            assert lib.bfly_stage_meta(n, layer, _native.RULES[rule], C.byref(s), C.byref(c), C.byref(w)) == 0
+            assert (s.value, c.value) == tp.stage_meta(n, layer, rule)
+            assert w.value == tp.width(n)
+            bits = (C.c_int32 * 3)()
+            assert lib.bfly_partner_bits(s.value, c.value, w.value, 3, _native.RULES[rule], bits) == 0
+            assert list(bits) == tp.partner_bits(s.value, c.value, w.value, 3, rule)
+
+
+def test_errors_are_reported():
+    lib = _native.lib()
+    s = C.c_int32()
+    rc = lib.bfly_stage_meta(8, 0, 99, C.byref(s), C.byref(s), C.byref(s))
+    assert rc == _native.ERR_INVALID
+    assert b"partner rule" in lib.bfly_last_error()
+    with pytest.raises(ValueError):
+        _native.check(rc, "bfly_stage_meta")
+    # device entry points validate arguments before touching the GPU
+    rc = lib.bfly_prefill(None, None, None, None, None, 1, 1, 8, 2, 64, 128, None, 1, 4, 128, 64, 1.0, None, None)
+    assert rc == _native.ERR_INVALID
+    rc = lib.bfly_block_neighbors(16, 0, 3, 1, 1, 1, None, 2, None, None)
+    assert rc == _native.ERR_INVALID and b"kcap" in lib.bfly_last_error()

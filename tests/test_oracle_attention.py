@@ -1,0 +1,147 @@
+"""Pins the CPU attention oracle (oracle/attention.py) against independent checks.
+
+* the reference tests' float64 brute force (oracle/brute.py, restating
+  tests/pytorch/test_compressed_butterfly_attention.py:31-85) on the
+  reference's own cases (seeds 23 and 29) and on GQA / ragged / larger cases;
+* block means against a float64 closed form;
+* the online-softmax merge against one softmax over the union, and associativity
+  (tests/mlx/test_online_softmax_merge.py:13-97 restated);
+* from-cache == active rows (tests/mlx/test_compressed_butterfly_from_cache.py:16-82
+  restated).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa, brute, topology as tp
+from oracle.cache import OracleCompressedKVCache
+
+
+def _layout(T, bs, layer, hkv=2, groups=1, rule="causal_shift"):
+    return tp.build_layout(seq_len=T, block_size=bs, num_key_value_heads=hkv, num_key_value_groups=groups,
+                           layer_idx=layer, local_window_blocks=1, sink_count=1, partner_count=1,
+                           partner_rule=rule)
+
+
+def test_reference_case_prefill_seed23():
+    rng = np.random.default_rng(23)
+    B, H, T, dh = 1, 2, 18, 8
+    lay = _layout(T, 4, 2, hkv=H)
+    q, k, v = (rng.standard_normal((B, H, T, dh), dtype=np.float32) for _ in range(3))
+    y = oa.prefill(*(torch.from_numpy(x) for x in (q, k, v)), layout=lay, W=4)
+    ref = brute.compressed_reference(q, k, v, lay.block_neighbors[0].numpy(), block_size=4, W=4)
+    assert np.allclose(y.numpy(), ref, atol=3e-4, rtol=3e-4)
+    assert np.abs(y.numpy() - ref).max() < 1e-5
+
+
+def test_reference_case_active_seed29():
+    rng = np.random.default_rng(29)
+    B, H, Tk, Tq, dh = 1, 2, 18, 3, 8
+    qp = np.asarray([9, 13, 17])
+    lay = _layout(Tk, 4, 3, hkv=H)
+    q = rng.standard_normal((B, H, Tq, dh), dtype=np.float32)
+    k = rng.standard_normal((B, H, Tk, dh), dtype=np.float32)
+    v = rng.standard_normal((B, H, Tk, dh), dtype=np.float32)
+    y = oa.active(*(torch.from_numpy(x) for x in (q, k, v)), layout=lay, query_positions=torch.from_numpy(qp), W=4)
+    ref = brute.compressed_reference(q, k, v, lay.block_neighbors[0].numpy(), block_size=4, W=4, query_positions=qp)
+    assert np.abs(y.numpy() - ref).max() < 1e-5
+
+
+@pytest.mark.parametrize("T,bs,W,layer,hkv,groups", [
+    (67, 8, 5, 1, 2, 4), (64, 16, 16, 3, 1, 2), (130, 32, 20, 2, 2, 1), (45, 4, 3, 4, 2, 2)])
+def test_prefill_matches_brute_force_gqa_ragged(T, bs, W, layer, hkv, groups):
+    rng = np.random.default_rng(T * 7 + layer)
+    hq, dh = hkv * groups, 16
+    lay = _layout(T, bs, layer, hkv=hkv, groups=groups)
+    q = rng.standard_normal((1, hq, T, dh), dtype=np.float32)
+    k = rng.standard_normal((1, hkv, T, dh), dtype=np.float32)
+    v = rng.standard_normal((1, hkv, T, dh), dtype=np.float32)
+    y = oa.prefill(*(torch.from_numpy(x) for x in (q, k, v)), layout=lay, W=W)
+    ref = brute.compressed_reference(q, k, v, lay.block_neighbors[0].numpy(), block_size=bs, W=W)
+    assert np.abs(y.numpy() - ref).max() < 1e-5
+
+
+def test_prefill_summary_terms_matter():
+    # Planted mistake: dropping the routed summaries must break agreement, so the
+    # brute force really exercises the compressed stream at this shape.
+    rng = np.random.default_rng(5)
+    T, bs, W = 96, 8, 4
+    lay = _layout(T, bs, 2)
+    q, k, v = (rng.standard_normal((1, 2, T, 8), dtype=np.float32) for _ in range(3))
+    ref = brute.compressed_reference(q, k, v, lay.block_neighbors[0].numpy(), block_size=bs, W=W)
+    no_sum = brute.compressed_reference(q, k, v, np.full_like(lay.block_neighbors[0].numpy(), -1),
+                                        block_size=bs, W=W)
+    assert np.abs(ref - no_sum).max() > 1e-2
+
+
+@pytest.mark.parametrize("T,bs", [(18, 4), (128, 128), (130, 64), (1, 128)])
+def test_block_mean_closed_form(T, bs):
+    rng = np.random.default_rng(T)
+    x = rng.standard_normal((2, 3, T, 8)).astype(np.float32)
+    n = (T + bs - 1) // bs
+    got = oa.block_mean(torch.from_numpy(x), seq_len=T, block_size=bs, num_blocks=n).numpy()
+    want = brute.block_summaries(x, bs)
+    assert np.abs(got - want).max() < 1e-6
+
+
+def test_merge_equals_union_softmax_and_is_associative():
+    rng = np.random.default_rng(0)
+    d = 16
+    q = torch.from_numpy(rng.standard_normal(d))
+    keys = torch.from_numpy(rng.standard_normal((30, d)))
+    vals = torch.from_numpy(rng.standard_normal((30, d)))
+    parts = [(0, 10), (10, 22), (22, 30)]
+
+    def stream(lo, hi):
+        s = (keys[lo:hi] @ q).view(1, -1) * 0.25
+        return oa._stream(s, torch.ones_like(s, dtype=torch.bool), vals[lo:hi])
+
+    a, b, c = (stream(*p) for p in parts)
+
+    def as_stream(o, ms):
+        # (o, l, m) of a merged pair, for a second-level merge
+        m = torch.maximum(ms[0][2], ms[1][2])
+        l = sum(torch.exp(x[2] - m) * x[1] for x in ms)
+        return o, l, m
+
+    ab = as_stream(oa.merge(a, b), (a, b))
+    left = oa.merge(ab, c)
+    bc = as_stream(oa.merge(b, c), (b, c))
+    right = oa.merge(a, bc)
+    dense = oa.dense_union_attention(q, keys, vals, scale=0.25)
+    assert torch.allclose(left.view(-1), dense, atol=1e-12)
+    assert torch.allclose(right.view(-1), dense, atol=1e-12)
+    empty = (torch.zeros(1, d, dtype=torch.float64), torch.zeros(1, 1, dtype=torch.float64),
+             torch.full((1, 1), oa.NEG, dtype=torch.float64))
+    assert torch.allclose(oa.merge(a, empty), a[0])
+
+
+def test_swa_stream_is_windowed_dense():
+    rng = np.random.default_rng(1)
+    t, d, W = 40, 8, 5
+    q, k, v = (torch.from_numpy(rng.standard_normal((1, 1, t, d))) for _ in range(3))
+    o, l, m = oa.swa_stream(q, k, v, W=W, scale=0.3)
+    for p in range(t):
+        lo = max(0, p - W + 1)
+        want = oa.dense_union_attention(q[0, 0, p], k[0, 0, lo:p + 1], v[0, 0, lo:p + 1], scale=0.3)
+        assert torch.allclose(o[0, 0, p].double(), want, atol=1e-6)
+
+
+def test_from_cache_equals_active_seed202():
+    rng = np.random.default_rng(202)
+    B, H, Tk, Tq, dh, bs, W = 1, 2, 24, 3, 8, 4, 4
+    q = torch.from_numpy(rng.standard_normal((B, H, Tq, dh), dtype=np.float32))
+    k = torch.from_numpy(rng.standard_normal((B, H, Tk, dh), dtype=np.float32))
+    v = torch.from_numpy(rng.standard_normal((B, H, Tk, dh), dtype=np.float32))
+    qp = torch.tensor([21, 22, 23])
+    lay = _layout(Tk, bs, 3, hkv=H)
+    ref = oa.active(q, k, v, layout=lay, query_positions=qp, W=W)
+    cache = OracleCompressedKVCache(block_size=bs, local_window_tokens=W)
+    for s in range(0, Tk, 3):
+        cache.update_and_fetch(k[:, :, s:s + 3], v[:, :, s:s + 3])
+    tk_, tv_, ks, vs, ts, off = cache.get_compressed_state()
+    got = oa.from_cache(q, tk_, tv_, ks, vs, layout=lay, query_positions=qp, W=W, tail_start=ts, kv_len=off)
+    assert torch.allclose(got, ref, atol=3e-4, rtol=3e-4)
+    assert (got - ref).abs().max() < 1e-5

@@ -235,6 +235,8 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device copy (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only (the hot path needs no collectives); "
@@ -248,6 +250,15 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no HIP GPU visible"}), flush=True)
         sys.exit(1)
+    if args.copy_calibration:
+        src = torch.ones(128 << 20, dtype=torch.bfloat16, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2,
+                          "launches": args.steps}), flush=True)
+        return
     pre = bench_prefill(args, torch, bf, tp)
     q, k, v, ref_lays = pre.pop("inputs")
     decode = None if args.no_decode else bench_decode(torch, bf)

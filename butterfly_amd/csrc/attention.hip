@@ -18,6 +18,8 @@
 //    fp32 softmax with wavefront shuffles between the 4 lane groups.
 //  * attn_generic_kernel<T>: fp32 or bf16, any shape; one wave per
 //    (batch, kv head, query); lanes over keys for scores and over d for output.
+#include <stdlib.h>
+
 #include "bfly_common.h"
 
 namespace bfly {
@@ -175,12 +177,21 @@ constexpr int kRing = 2 * kPage;       // ring slots (window <= 64 needs pages c
 constexpr int kSumSlots = 16;          // one 16-row MFMA tile of routed summaries
 constexpr int kSlots = kRing + kSumSlots;
 constexpr int kVPitch = kSlots + 4;    // bf16 per V^T row (296 B): spreads 16 rows over banks
+constexpr int kMaxSegChunks = 8;       // chunks per workgroup (host picks 1, 2, 4 or 8)
+constexpr int kMaxKcap = kSumSlots / 2;
+constexpr int kMaxSegBlocks = kMaxSegChunks * kPage / kPage + 1;   // block_size >= kPage
+constexpr int kQPipe = 2;              // query heads whose Q fragments are held in registers (one pair)
 
 template <int D>
 struct MfmaCfg {
   static constexpr int KP = D + 8;                 // bf16 per K row (pad 16 B)
   static constexpr int KSTEPS = D / 32;            // MFMA k-steps over head_dim
   static constexpr int DTILES = D / 16;            // output d tiles
+  static constexpr int PIECES = D / 8;             // 16-byte pieces per row
+  static constexpr int KLD = kPage * PIECES / 256;         // K pieces per thread per page
+  static constexpr int VLD = (kPage / 2) * PIECES / 256;   // V row pairs per thread per page
+  static constexpr int SITEMS = kSumSlots * PIECES;        // summary pieces per chunk
+  static constexpr int SLD = (SITEMS + 255) / 256;
   static constexpr int K_BYTES = kSlots * KP * 2;
   static constexpr int V_BYTES = D * kVPitch * 2;
   static constexpr int LDS = K_BYTES + V_BYTES;
@@ -194,12 +205,33 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
   return (bid % 8) * (n / 8) + bid / 8;
 }
 
+// Positions, block ids and counts fit in int32 (the host checks kv_len and the
+// query range); only tensor offsets use 64-bit arithmetic.
+struct MfmaArgs {
+  int qlo, qhi;          // query positions [qlo, qhi)
+  int key_lo, kv_len;    // raw keys are positions [key_lo, kv_len)
+  int ring;              // 0: linear rows (row = p - key_lo); else row = p mod ring (ring >= kPage)
+  int nblocks, nsum, kcap, bs, W;
+  int token_cutoff;
+};
+
+// Work unit = (batch, kv head, segment of seg_chunks 64-position chunks).
+// Software pipeline per chunk c:
+//   LDS <- staged page c (K rows, V transposed) and routed summary rows
+//   barrier
+//   issue global loads of page c+1 and its summaries into registers
+//   query heads in pairs: S^T = K Q^T for both heads from one K fragment read,
+//     softmax, O^T = V^T P^T for both heads from one V fragment read; after a
+//     head's scores its register Q slot is refilled with the next (chunk, head)
+//   barrier
+// so HBM traffic of chunk c+1 overlaps the MFMA/softmax work of chunk c.
 template <int D>
 __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1)
-attn_mfma_kernel(AttnArgs a, int seg_chunks, int64_t c_first, int64_t nchunks) {
+attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunks) {
   using C = MfmaCfg<D>;
   __shared__ __attribute__((aligned(16))) unsigned char smem[C::LDS];
   __shared__ int cand_n[kSumSlots], cand_b[kSumSlots];
+  __shared__ int s_nbr[kMaxSegBlocks * kMaxKcap];
   __bf16* Ks = reinterpret_cast<__bf16*>(smem);                 // [kSlots][KP]
   __bf16* Vt = reinterpret_cast<__bf16*>(smem + C::K_BYTES);    // [D][kVPitch]
 
@@ -207,194 +239,325 @@ attn_mfma_kernel(AttnArgs a, int seg_chunks, int64_t c_first, int64_t nchunks) {
   const int wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
   const int seg = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t bh = blockIdx.y;
-  const int64_t bi = bh / a.hkv;
-  const int kvh = (int)(bh % a.hkv);
+  const int bh = blockIdx.y;
+  const int bi = bh / a.hkv;
+  const int kvh = bh - bi * a.hkv;
   const int gsz = a.hq / a.hkv;
-  const int64_t cbeg = c_first + (int64_t)seg * seg_chunks;
-  int64_t cend = cbeg + seg_chunks;
-  if (cend > c_first + nchunks) cend = c_first + nchunks;
-  const int64_t qlo = a.q_pos0, qhi = a.q_pos0 + a.tq;
+  const int cbeg = c_first + seg * seg_chunks;
+  const int cend = min(cbeg + seg_chunks, c_first + nchunks);
 
-  const __bf16* kbase = reinterpret_cast<const __bf16*>(a.k) + (bi * a.hkv + kvh) * a.kv_rows * D;
-  const __bf16* vbase = reinterpret_cast<const __bf16*>(a.v) + (bi * a.hkv + kvh) * a.kv_rows * D;
-  const __bf16* ksb = reinterpret_cast<const __bf16*>(a.ks) + (bi * a.hkv + kvh) * a.pool_rows * D;
-  const __bf16* vsb = reinterpret_cast<const __bf16*>(a.vs) + (bi * a.hkv + kvh) * a.pool_rows * D;
-  const float sl2 = a.scale * 1.4426950408889634f;   // scores in log2 units
+  const int64_t kv_off = ((int64_t)bi * a.hkv + kvh) * a.kv_rows * D;
+  const int64_t pool_off = ((int64_t)bi * a.hkv + kvh) * a.pool_rows * D;
+  const __bf16* kbase = reinterpret_cast<const __bf16*>(a.k) + kv_off;
+  const __bf16* vbase = reinterpret_cast<const __bf16*>(a.v) + kv_off;
+  const __bf16* ksb = reinterpret_cast<const __bf16*>(a.ks) + pool_off;
+  const __bf16* vsb = reinterpret_cast<const __bf16*>(a.vs) + pool_off;
+  const float sl2 = a.scale * 1.4426950408889634f;   // host guarantees scale > 0
 
-  auto key_ok = [&](int64_t p) { return p >= 0 && p >= a.key_lo && p < a.kv_len; };
-  auto row_of = [&](int64_t p) { return a.ring ? posmod(p, a.ring) : p - a.key_lo; };
+  auto blk_of = [&](int p) { return min(max(p / m.bs, 0), m.nblocks - 1); };
+  auto chunk_blocks = [&](int c, int& bA, int& bB) {
+    bA = blk_of(max(c * kPage, m.qlo));
+    bB = blk_of(min((c + 1) * kPage, m.qhi) - 1);
+  };
 
-  // Stage one 64-position page into the ring: K row-major, V transposed.
-  auto load_page = [&](int64_t pg) {
-    const int sbase = (int)posmod(pg, 2) * kPage;
-    const int64_t p0 = pg * kPage;
-    constexpr int PIECES = D / 8;                  // 16-byte pieces per row
-    for (int i = tid; i < kPage * PIECES; i += 256) {
-      const int r = i / PIECES, pc = i % PIECES;
-      const int64_t p = p0 + r;
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (key_ok(p)) val = *reinterpret_cast<const uint4*>(kbase + row_of(p) * D + pc * 8);
-      *reinterpret_cast<uint4*>(Ks + (sbase + r) * C::KP + pc * 8) = val;
+  // ---- neighbour rows of every query block of the segment, once, into LDS
+  int b_lo, b_hi, tmp;
+  chunk_blocks(cbeg, b_lo, tmp);
+  chunk_blocks(cend - 1, tmp, b_hi);
+  {
+    const int cnt = (b_hi - b_lo + 1) * m.kcap;
+    for (int i = tid; i < cnt; i += 256) s_nbr[i] = a.nbr[(int64_t)b_lo * m.kcap + i];
+  }
+
+  // ---- register staging of one page (K rows and V row pairs) and of the routed summaries
+  uint4 kst[C::KLD], vst[2 * C::VLD];
+  auto fetch_page = [&](int pg) {
+    const int p0 = pg * kPage;
+    // row of position p0 (+ r): linear, or ring slot (ring >= kPage, so one wrap at most)
+    int r0 = 0;
+    if (m.ring) {
+      r0 = p0 % m.ring;
+      if (r0 < 0) r0 += m.ring;
+    } else {
+      r0 = p0 - m.key_lo;
     }
-    for (int i = tid; i < (kPage / 2) * PIECES; i += 256) {
+    auto rowp = [&](int r) {
+      int rr = r0 + r;
+      if (m.ring && rr >= m.ring) rr -= m.ring;
+      return rr;
+    };
+    auto ok = [&](int p) { return p >= m.key_lo && p >= 0 && p < m.kv_len; };
+    // Loads are unconditional (row 0 stands in for an invalid position) and the
+    // value is zeroed afterwards, so no branch splits the load batch.
+    auto ld = [&](const __bf16* base, int r, int pc) {
+      const bool v = ok(p0 + r);
+      const uint4 x = *reinterpret_cast<const uint4*>(base + (int64_t)(v ? rowp(r) : 0) * D + pc * 8);
+      return v ? x : make_uint4(0, 0, 0, 0);
+    };
+#pragma unroll
+    for (int it = 0; it < C::KLD; ++it) {
+      const int i = tid + it * 256;
+      kst[it] = ld(kbase, i / C::PIECES, i % C::PIECES);
+    }
+#pragma unroll
+    for (int it = 0; it < C::VLD; ++it) {
+      const int i = tid + it * 256;
       const int kp = i % (kPage / 2), pc = i / (kPage / 2);
-      const int64_t p = p0 + 2 * kp;
-      uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
-      if (key_ok(p)) v0 = *reinterpret_cast<const uint4*>(vbase + row_of(p) * D + pc * 8);
-      if (key_ok(p + 1)) v1 = *reinterpret_cast<const uint4*>(vbase + row_of(p + 1) * D + pc * 8);
-      const uint16_t* e0 = reinterpret_cast<const uint16_t*>(&v0);
-      const uint16_t* e1 = reinterpret_cast<const uint16_t*>(&v1);
+      vst[2 * it] = ld(vbase, 2 * kp, pc);
+      vst[2 * it + 1] = ld(vbase, 2 * kp + 1, pc);
+    }
+  };
+  auto store_page = [&](int pg) {
+    const int sbase = (pg & 1) * kPage;
+#pragma unroll
+    for (int it = 0; it < C::KLD; ++it) {
+      const int i = tid + it * 256;
+      const int r = i / C::PIECES, pc = i % C::PIECES;
+      *reinterpret_cast<uint4*>(Ks + (sbase + r) * C::KP + pc * 8) = kst[it];
+    }
+#pragma unroll
+    for (int it = 0; it < C::VLD; ++it) {
+      const int i = tid + it * 256;
+      const int kp = i % (kPage / 2), pc = i / (kPage / 2);
+      const uint16_t* e0 = reinterpret_cast<const uint16_t*>(&vst[2 * it]);
+      const uint16_t* e1 = reinterpret_cast<const uint16_t*>(&vst[2 * it + 1]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        uint32_t pair = (uint32_t)e0[j] | ((uint32_t)e1[j] << 16);
+        const uint32_t pair = (uint32_t)e0[j] | ((uint32_t)e1[j] << 16);
         *reinterpret_cast<uint32_t*>(Vt + (pc * 8 + j) * kVPitch + sbase + 2 * kp) = pair;
       }
     }
   };
 
-  for (int64_t c = cbeg; c < cend; ++c) {
-    // ---------------- stage keys/values and summaries
-    if (c == cbeg) load_page(c - 1);
-    load_page(c);
-    {
-      // Summary candidates of the blocks this chunk's valid queries fall in.
-      int64_t vp0 = c * kPage > qlo ? c * kPage : qlo;
-      int64_t vp1 = (c + 1) * kPage < qhi ? (c + 1) * kPage - 1 : qhi - 1;
-      const int64_t bA = clamp_block(vp0, a), bB = clamp_block(vp1, a);
-      constexpr int PIECES = D / 8;
-      for (int i = tid; i < kSumSlots * PIECES; i += 256) {
-        const int s = i / PIECES, pc = i % PIECES;
-        int cnt = 0, cn = -1, cb = -1;
-        for (int64_t bb = bA; bb <= bB && cn < 0; ++bb) {
-          for (int j = 0; j < a.kcap; ++j) {
-            int64_t n = a.nbr[bb * a.kcap + j];
-            if (n < 0 || n >= bb || n >= a.nsum) continue;
+  uint4 skst[C::SLD], svst[C::SLD];
+  int scn[C::SLD], scb[C::SLD];
+  // Summary candidates of chunk c: the s-th entry, over the chunk's query
+  // blocks in order, of each block's routed neighbours n < block (n < nsum).
+  auto fetch_sum = [&](int c) {
+    int bA, bB;
+    chunk_blocks(c, bA, bB);
+#pragma unroll
+    for (int it = 0; it < C::SLD; ++it) {
+      const int i = tid + it * 256;
+      const int s = i / C::PIECES, pc = i % C::PIECES;
+      int cn = -1, cb = -1;
+      if (i < C::SITEMS) {
+        int cnt = 0;
+        for (int bb = bA; bb <= bB && cn < 0; ++bb) {
+          for (int j = 0; j < m.kcap; ++j) {
+            const int n = s_nbr[(bb - b_lo) * m.kcap + j];
+            if (n < 0 || n >= bb || n >= m.nsum) continue;
             if (cnt == s) {
-              cn = (int)n;
-              cb = (int)bb;
+              cn = n;
+              cb = bb;
               break;
             }
             ++cnt;
           }
         }
-        uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-        if (cn >= 0) {
-          kv = *reinterpret_cast<const uint4*>(ksb + (int64_t)cn * D + pc * 8);
-          vv = *reinterpret_cast<const uint4*>(vsb + (int64_t)cn * D + pc * 8);
-        }
-        *reinterpret_cast<uint4*>(Ks + (kRing + s) * C::KP + pc * 8) = kv;
-        const __bf16* ve = reinterpret_cast<const __bf16*>(&vv);
+      }
+      scn[it] = cn;
+      scb[it] = cb;
+      const int64_t srow = (int64_t)(cn >= 0 ? cn : 0) * D + (i < C::SITEMS ? pc * 8 : 0);
+      const uint4 kx = *reinterpret_cast<const uint4*>(ksb + srow);
+      const uint4 vx = *reinterpret_cast<const uint4*>(vsb + srow);
+      skst[it] = cn >= 0 ? kx : make_uint4(0, 0, 0, 0);
+      svst[it] = cn >= 0 ? vx : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_sum = [&]() {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) Vt[(pc * 8 + j) * kVPitch + kRing + s] = ve[j];
-        if (pc == 0) {
-          cand_n[s] = cn;
-          cand_b[s] = cb;
-        }
+    for (int it = 0; it < C::SLD; ++it) {
+      const int i = tid + it * 256;
+      if (i >= C::SITEMS) continue;
+      const int s = i / C::PIECES, pc = i % C::PIECES;
+      *reinterpret_cast<uint4*>(Ks + (kRing + s) * C::KP + pc * 8) = skst[it];
+      const __bf16* ve = reinterpret_cast<const __bf16*>(&svst[it]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) Vt[(pc * 8 + j) * kVPitch + kRing + s] = ve[j];
+      if (pc == 0) {
+        cand_n[s] = scn[it];
+        cand_b[s] = scb[it];
       }
     }
-    __syncthreads();
+  };
 
-    // ---------------- compute: wave owns positions [pw, pw+16)
-    const int64_t pw = c * kPage + wave * 16;
-    const int64_t qp = pw + lq;                       // this lane's query position
-    const bool wave_active = (pw + 15 >= qlo) && (pw < qhi);
-    if (wave_active) {
-      const bool row_ok = qp >= qlo && qp < qhi;
-      const int64_t qblk = clamp_block(qp, a);
-      const int64_t qcut = summary_cutoff(qp, qblk, a);
-      int64_t wlo = qp - a.W + 1;
-      if (wlo < a.key_lo) wlo = a.key_lo;
-      if (wlo < 0) wlo = 0;
-      // Summary-slot eligibility of this lane's query for slots 4*lg + i.
-      bool sum_ok[4];
+  // ---- register-resident Q fragments: lane holds query (chunk row wave*16+lq),
+  // d in [lg*D/4, (lg+1)*D/4); k-step ks takes d = lg*D/4 + 8*ks + [0, 8)
+  // (the K fragments use the same map, so the k permutation cancels).
+  bf16x8 qbuf[kQPipe][C::KSTEPS];
+#pragma unroll
+  for (int u = 0; u < kQPipe; ++u)
+#pragma unroll
+    for (int ks = 0; ks < C::KSTEPS; ++ks) qbuf[u][ks] = bf16x8{};
+  const __bf16* qhead0 = reinterpret_cast<const __bf16*>(a.q) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz) * a.tq * D;
+  auto load_q = [&](int u, int c, int hh) {
+    const int qp = c * kPage + wave * 16 + lq;
+    const bool ok = qp >= m.qlo && qp < m.qhi;
+    // Rows outside the query range read row 0 instead: their scores are masked
+    // and their outputs are never stored.
+    const __bf16* qrow = qhead0 + ((int64_t)hh * a.tq + (ok ? qp - m.qlo : 0)) * D;
+#pragma unroll
+    for (int ks = 0; ks < C::KSTEPS; ++ks) qbuf[u][ks] = *reinterpret_cast<const bf16x8*>(qrow + lg * (D / 4) + 8 * ks);
+  };
+  // After head hh of chunk c used slot u = hh % kQPipe, refill it with the next
+  // (chunk, head) that uses the slot.
+  auto refill_q = [&](int u, int c, int hh) {
+    int nh = hh + kQPipe, nc = c;
+    if (nh >= gsz) {
+      nh = u;
+      nc = c + 1;
+    }
+    if (nc < cend) load_q(u, nc, nh);
+  };
+
+#pragma unroll
+  for (int u = 0; u < kQPipe; ++u)
+    if (u < gsz) load_q(u, cbeg, u);
+  fetch_page(cbeg - 1);
+  store_page(cbeg - 1);
+  fetch_page(cbeg);
+  __syncthreads();   // s_nbr visible
+  fetch_sum(cbeg);
+
+  __bf16* ohead0 = reinterpret_cast<__bf16*>(a.out) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz) * a.tq * D;
+
+  for (int c = cbeg; c < cend; ++c) {
+    store_page(c);
+    store_sum();
+    __syncthreads();
+    if (c + 1 < cend) {
+      fetch_page(c + 1);
+      fetch_sum(c + 1);
+    }
+
+    // ---------------- per-lane state shared by every head: wave owns positions [pw, pw+16)
+    const int pw = c * kPage + wave * 16;
+    const int qp = pw + lq;                          // this lane's query position
+    const bool wave_active = (pw + 15 >= m.qlo) && (pw < m.qhi);
+    const bool row_ok = qp >= m.qlo && qp < m.qhi;
+    const int qblk = blk_of(qp);
+    const int qcut = max(0, (m.token_cutoff ? qp : qblk * m.bs) - m.W + 1);
+    const int wlo = max(max(qp - m.W + 1, m.key_lo), 0);
+    // ok[t][i]: key 4*lg+i of tile t (window tiles 0..4 start at pw-64; tile 5 = summaries)
+    bool ok[6][4];
+#pragma unroll
+    for (int t = 0; t < 5; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int s = 4 * lg + i;
-        const int n = cand_n[s];
-        sum_ok[i] = row_ok && n >= 0 && cand_b[s] == qblk && (int64_t)(n + 1) * a.bs <= qcut;
+        const int kp = pw - kPage + 16 * t + 4 * lg + i;
+        ok[t][i] = row_ok && kp >= wlo && kp <= qp;
       }
-      const int64_t tile0 = pw - kPage;                 // position of window tile 0, key 0
-      for (int hh = 0; hh < gsz; ++hh) {
-        const int h = kvh * gsz + hh;
-        // Q^T fragments: lane holds query qp, d in [lg*D/4, (lg+1)*D/4); k-step ks
-        // takes d = lg*D/4 + 8*ks + [0, 8) (the K fragments use the same map).
-        bf16x8 qf[C::KSTEPS];
-        const __bf16* qrow = reinterpret_cast<const __bf16*>(a.q) +
-                             ((bi * a.hq + h) * a.tq + (row_ok ? qp - a.q_pos0 : 0)) * D;
 #pragma unroll
-        for (int ks = 0; ks < C::KSTEPS; ++ks) {
-          if (row_ok)
-            qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + lg * (D / 4) + 8 * ks);
-          else
-            qf[ks] = bf16x8{};
+    for (int i = 0; i < 4; ++i) {
+      const int s = 4 * lg + i;
+      const int n = cand_n[s];
+      ok[5][i] = row_ok && n >= 0 && cand_b[s] == qblk && (n + 1) * m.bs <= qcut;
+    }
+    int slot[6];
+#pragma unroll
+    for (int t = 0; t < 5; ++t) slot[t] = (pw - kPage + 16 * t) & (kRing - 1);
+    slot[5] = kRing;
+
+    // softmax of one head's 24 scores (already masked to -inf) -> bf16 P, 1/l
+    auto softmax = [&](f32x4 (&st)[6], bf16x8 (&pf)[3], float& inv) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 6; ++t) mx = fmaxf(mx, fmaxf(fmaxf(st[t][0], st[t][1]), fmaxf(st[t][2], st[t][3])));
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float nm = mx == -INFINITY ? 0.f : -mx * sl2;
+      float lsum = 0.f;
+#pragma unroll
+      for (int t = 0; t < 6; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(st[t][i], sl2, nm));
+          lsum += e;
+          pf[t / 2][(t % 2) * 4 + i] = (__bf16)e;
         }
-        // S^T for 5 window tiles + 1 summary tile.
-        f32x4 st[6];
-        float mx = -INFINITY;
+      lsum += __shfl_xor(lsum, 16);
+      lsum += __shfl_xor(lsum, 32);
+      inv = 1.f / fmaxf(lsum, 1e-30f);
+    };
+
+    for (int hb = 0; hb < gsz; hb += kQPipe) {
+#pragma unroll
+      for (int pp = 0; pp < kQPipe / 2; ++pp) {
+        const int h0 = hb + 2 * pp;
+        if (h0 >= gsz) break;
+        const bool two = h0 + 1 < gsz;
+        const int u0 = 2 * pp, u1 = 2 * pp + 1;
+        if (!wave_active) {
+          refill_q(u0, c, h0);
+          if (two) refill_q(u1, c, h0 + 1);
+          continue;
+        }
+        // S^T for both heads; one K fragment read feeds two MFMAs.
+        // (With an odd group the second head of the last pair is computed on a
+        // stale Q slot and discarded: no branch sits between the MFMAs.)
+        f32x4 s0[6], s1[6];
 #pragma unroll
         for (int t = 0; t < 6; ++t) {
-          const int slot0 = t < 5 ? (int)posmod(tile0 + 16 * t, kRing) : kRing;
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          bf16x8 kf[C::KSTEPS];
+#pragma unroll
+          for (int ks = 0; ks < C::KSTEPS; ++ks)
+            kf[ks] = *reinterpret_cast<const bf16x8*>(Ks + (slot[t] + lq) * C::KP + lg * (D / 4) + 8 * ks);
+          f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int ks = 0; ks < C::KSTEPS; ++ks) {
-            const bf16x8 kf = *reinterpret_cast<const bf16x8*>(
-                Ks + (slot0 + lq) * C::KP + lg * (D / 4) + 8 * ks);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], acc, 0, 0, 0);
+            a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qbuf[u0][ks], a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qbuf[u1][ks], a1, 0, 0, 0);
           }
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            bool ok;
-            if (t < 5) {
-              const int64_t kp = tile0 + 16 * t + 4 * lg + i;
-              ok = row_ok && kp >= wlo && kp <= qp;
-            } else {
-              ok = sum_ok[i];
+            s0[t][i] = ok[t][i] ? a0[i] : -INFINITY;
+            s1[t][i] = ok[t][i] ? a1[i] : -INFINITY;
+          }
+        }
+        refill_q(u0, c, h0);
+        if (two) refill_q(u1, c, h0 + 1);
+        bf16x8 p0[3], p1[3];
+        float inv0, inv1;
+        softmax(s0, p0, inv0);
+        softmax(s1, p1, inv1);
+        // O^T = V^T P^T.  Tile (mt, half), row r holds d = mt*32 + (r/4)*8 + half*4 + r%4,
+        // so the two halves give each lane 8 consecutive d: one 16-byte store per head.
+        __bf16* orow0 = ohead0 + ((int64_t)h0 * a.tq + (row_ok ? qp - m.qlo : 0)) * D;
+        __bf16* orow1 = orow0 + (int64_t)a.tq * D;
+#pragma unroll
+        for (int mt = 0; mt < C::DTILES / 2; ++mt) {
+          f32x4 o0[2], o1[2];
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const __bf16* vrow = Vt + (mt * 32 + (lq >> 2) * 8 + half * 4 + (lq & 3)) * kVPitch;
+            bf16x8 vf[3];
+#pragma unroll
+            for (int pr = 0; pr < 3; ++pr) {
+              const bf16x4 va = *reinterpret_cast<const bf16x4*>(vrow + slot[2 * pr] + 4 * lg);
+              const bf16x4 vb = *reinterpret_cast<const bf16x4*>(vrow + slot[2 * pr + 1] + 4 * lg);
+              vf[pr] = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
             }
-            const float s = ok ? acc[i] * sl2 : -INFINITY;
-            acc[i] = s;
-            mx = fmaxf(mx, s);
-          }
-          st[t] = acc;
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float msafe = mx == -INFINITY ? 0.f : mx;
-        float lsum = 0.f;
-        bf16x8 pf[3];
+            f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int t = 0; t < 6; ++t) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float e = __builtin_amdgcn_exp2f(st[t][i] - msafe);
-            lsum += e;
-            pf[t / 2][(t % 2) * 4 + i] = (__bf16)e;
-          }
-        }
-        lsum += __shfl_xor(lsum, 16);
-        lsum += __shfl_xor(lsum, 32);
-        const float inv = 1.f / fmaxf(lsum, 1e-30f);
-        // O^T = V^T P^T, one 16-row d tile at a time.
-        __bf16* orow = reinterpret_cast<__bf16*>(a.out) +
-                       ((bi * a.hq + h) * a.tq + (row_ok ? qp - a.q_pos0 : 0)) * D;
-#pragma unroll 2
-        for (int dt = 0; dt < C::DTILES; ++dt) {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-          const __bf16* vrow = Vt + (dt * 16 + lq) * kVPitch;
-#pragma unroll
-          for (int pr = 0; pr < 3; ++pr) {
-            const int sa = pr < 2 ? (int)posmod(tile0 + 32 * pr, kRing) : (int)posmod(tile0 + 64, kRing);
-            const int sb = pr < 2 ? (int)posmod(tile0 + 32 * pr + 16, kRing) : kRing;
-            const bf16x4 va = *reinterpret_cast<const bf16x4*>(vrow + sa + 4 * lg);
-            const bf16x4 vb = *reinterpret_cast<const bf16x4*>(vrow + sb + 4 * lg);
-            const bf16x8 vf = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[pr], acc, 0, 0, 0);
+            for (int pr = 0; pr < 3; ++pr) {
+              a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[pr], p0[pr], a0, 0, 0, 0);
+              a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[pr], p1[pr], a1, 0, 0, 0);
+            }
+            o0[half] = a0;
+            o1[half] = a1;
           }
           if (row_ok) {
-            bf16x4 o;
+            bf16x8 w0, w1;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] = (__bf16)(acc[i] * inv);
-            *reinterpret_cast<bf16x4*>(orow + dt * 16 + 4 * lg) = o;
+            for (int i = 0; i < 4; ++i) {
+              w0[i] = (__bf16)(o0[0][i] * inv0);
+              w0[4 + i] = (__bf16)(o0[1][i] * inv0);
+              w1[i] = (__bf16)(o1[0][i] * inv1);
+              w1[4 + i] = (__bf16)(o1[1][i] * inv1);
+            }
+            *reinterpret_cast<bf16x8*>(orow0 + mt * 32 + lg * 8) = w0;
+            if (two) *reinterpret_cast<bf16x8*>(orow1 + mt * 32 + lg * 8) = w1;
           }
         }
       }
@@ -408,8 +571,12 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
                      aligned16(a.vs),
                  "%s: tensor pointers must be 16-byte aligned", what);
   const bool contiguous = a.qpos == nullptr;
+  // The MFMA kernel keeps positions in int32 and assumes a positive scale (it
+  // folds the scale into exp2) and a ring of at least one page.
   const bool mfma_ok = dtype == BFLY_DTYPE_BF16 && contiguous && a.W <= kPage && a.bs >= kPage &&
-                       2 * a.kcap <= kSumSlots && (a.d == 64 || a.d == 128 || a.d == 256);
+                       2 * a.kcap <= kSumSlots && (a.d == 64 || a.d == 128 || a.d == 256) && a.scale > 0.f &&
+                       (a.ring == 0 || a.ring >= kPage) && a.kv_len + 2 * kPage < INT32_MAX &&
+                       a.nblocks < INT32_MAX && a.kv_rows < INT32_MAX && a.pool_rows < INT32_MAX;
   if (a.tq == 0) return BFLY_OK;
   if (mfma_ok) {
     const int64_t c_first = floordiv(a.q_pos0, kPage);
@@ -419,14 +586,33 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
     // keeping the halo page (re-read once per segment) a small fraction.
     const int64_t groups = a.batch * a.hkv;
     int seg = 1;
-    while (seg < 8 && (nchunks + 2 * seg - 1) / (2 * seg) * groups >= 512) seg *= 2;
+    while (seg < kMaxSegChunks && (nchunks + 2 * seg - 1) / (2 * seg) * groups >= 512) seg *= 2;
+    // Tuning override (chunks per workgroup): BFLY_PREFILL_SEG in {1, 2, 4, 8}.
+    static const int seg_env = [] {
+      const char* e = getenv("BFLY_PREFILL_SEG");
+      const int v = e ? atoi(e) : 0;
+      return (v == 1 || v == 2 || v == 4 || v == 8) ? v : 0;
+    }();
+    if (seg_env) seg = seg_env;
     int64_t nseg = (nchunks + seg - 1) / seg;
     BFLY_CHECK_ARG(nseg <= INT32_MAX && groups <= 65535, "%s: grid too large", what);
+    MfmaArgs m{};
+    m.qlo = (int)a.q_pos0;
+    m.qhi = (int)(a.q_pos0 + a.tq);
+    m.key_lo = (int)a.key_lo;
+    m.kv_len = (int)a.kv_len;
+    m.ring = (int)a.ring;
+    m.nblocks = (int)a.nblocks;
+    m.nsum = (int)(a.nsum < a.nblocks ? a.nsum : a.nblocks);
+    m.kcap = a.kcap;
+    m.bs = a.bs;
+    m.W = a.W;
+    m.token_cutoff = a.token_cutoff;
     dim3 grid((unsigned)nseg, (unsigned)groups);
     switch (a.d) {
-      case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, stream, a, seg, c_first, nchunks); break;
-      case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, stream, a, seg, c_first, nchunks); break;
-      default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(256), 0, stream, a, seg, c_first, nchunks); break;
+      case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks); break;
+      case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks); break;
+      default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks); break;
     }
   } else {
     BFLY_CHECK_ARG(a.d <= kGenericMaxD, "%s: head_dim=%d > %d", what, a.d, kGenericMaxD);

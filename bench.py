@@ -189,9 +189,8 @@ def bench_decode(torch, bf, batches=(1, 8, 32), steps=64, seed=0):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for s in range(steps):
-            cache.update(kn[s], vn[s])
-            o = bf.compressed_butterfly_attention_cached(qn[s], cache, layout=layout_for(cache.offset),
-                                                         local_window_tokens=W)
+            o = cache.update_and_attend(qn[s], kn[s], vn[s], layout=layout_for(cache.offset + 1),
+                                        local_window_tokens=W)
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / steps
         assert torch.isfinite(o.float()).all()

@@ -48,6 +48,8 @@ SIGNATURES = {
     "bfly_attend_cache": (_int, [_vp, _int, _i64, _int, _int, _i64, _int, _vp, _i64, _vp, _vp, _i64,
                                  _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _int, _int, _int, _f32,
                                  _vp, _vp]),
+    "bfly_decode": (_int, [_vp, _int, _i64, _int, _int, _int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp,
+                           _i64, _i64, _vp, _i64, _int, _int, _int, _f32, _vp, _vp]),
     "bfly_cache_append": (_int, [_vp, _vp, _int, _i64, _int, _i64, _int, _vp, _vp, _i64, _i64, _vp]),
     "bfly_cache_compress": (_int, [_vp, _vp, _int, _i64, _int, _int, _i64, _i64, _i64, _int, _vp, _vp,
                                    _i64, _i64, _vp]),

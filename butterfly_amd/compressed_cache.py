@@ -77,8 +77,13 @@ class CompressedKVCache:
         self._realign = False
 
     # ------------------------------------------------------------------ update
-    def update(self, keys: torch.Tensor, values: torch.Tensor) -> None:
-        """Append, summarise completed blocks, trim (compressed_cache.py:94-172)."""
+    def _advance(self, keys: torch.Tensor, values: torch.Tensor):
+        """Validate, allocate, and advance the counters for one appended chunk.
+
+        Returns ``(step, first_pos, first_slot, n_new, overflow)``: the blocks
+        ``[first_pos, first_pos + n_new*BS)`` are due to be summarised into pool
+        slots ``[first_slot, first_slot + n_new)`` (compressed_cache.py:94-149).
+        """
         if not keys.is_cuda or keys.shape != values.shape or keys.dtype != values.dtype:
             raise ValueError("keys/values must be matching GPU tensors [B, H, step, d]")
         step = int(keys.shape[2])
@@ -94,12 +99,6 @@ class CompressedKVCache:
                 f"CompressedKVCache.tail_capacity={self.tail_capacity} too small to fit "
                 f"tail_size={self.tail_size} + step={step}; raise max_chunk_size or "
                 f"local_window_tokens to make room.")
-        keys, values = _c(keys), _c(values)
-        dt = _dtype_code(keys)
-        st = _stream(keys)
-        with torch.cuda.device(keys.device):
-            _native.call("bfly_cache_append", keys.data_ptr(), values.data_ptr(), dt, b, h, step, d,
-                         self._ring_k.data_ptr(), self._ring_v.data_ptr(), self.tail_capacity, self.offset, st)
         self.tail_size += step
         self.offset += step
         first_pos, first_slot, n_new = self.summary_offset, self.summary_count, 0
@@ -114,19 +113,83 @@ class CompressedKVCache:
                 break
             n_new += 1
             self.summary_offset += bs
+        return step, first_pos, first_slot, n_new, overflow
+
+    def _compress(self, first_pos: int, first_slot: int, n_new: int, overflow: bool, st: int) -> None:
+        """Pool the due blocks (they predate the new tokens) and raise on overflow."""
+        b, h, _, d = self._ring_k.shape
         if n_new:
-            with torch.cuda.device(keys.device):
-                _native.call("bfly_cache_compress", self._ring_k.data_ptr(), self._ring_v.data_ptr(), dt, b, h, d,
-                             self.tail_capacity, first_pos, n_new, bs, self._pool_k.data_ptr(),
-                             self._pool_v.data_ptr(), self.summary_capacity, first_slot, st)
+            with torch.cuda.device(self._ring_k.device):
+                _native.call("bfly_cache_compress", self._ring_k.data_ptr(), self._ring_v.data_ptr(),
+                             _dtype_code(self._ring_k), b, h, d, self.tail_capacity, first_pos, n_new,
+                             self.block_size, self._pool_k.data_ptr(), self._pool_v.data_ptr(),
+                             self.summary_capacity, first_slot, st)
             self.summary_count += n_new
         if overflow:
             raise RuntimeError(
                 f"CompressedKVCache.summary_capacity={self.summary_capacity} exhausted "
                 f"at offset={self.offset}; raise max_kv_size at construction time.")
+
+    def _trim(self, step: int) -> None:
+        """Drop whole blocks from the tail (compressed_cache.py:151-164); a counter update here."""
+        bs, lw = self.block_size, self.local_window_tokens
         target = max(lw, step + lw - 1)
         while self.tail_size - bs >= target:
             self.tail_size -= bs
+
+    def update(self, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """Append, summarise completed blocks, trim (compressed_cache.py:94-172)."""
+        offset0 = self.offset
+        step, first_pos, first_slot, n_new, overflow = self._advance(keys, values)
+        b, h, d = int(keys.shape[0]), int(keys.shape[1]), int(keys.shape[3])
+        keys, values = _c(keys), _c(values)
+        st = _stream(keys)
+        with torch.cuda.device(keys.device):
+            _native.call("bfly_cache_append", keys.data_ptr(), values.data_ptr(), _dtype_code(keys), b, h, step, d,
+                         self._ring_k.data_ptr(), self._ring_v.data_ptr(), self.tail_capacity, offset0, st)
+        self._compress(first_pos, first_slot, n_new, overflow, st)
+        self._trim(step)
+
+    def update_and_attend(self, q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, *, layout,
+                          local_window_tokens: int, scale: Optional[float] = None) -> torch.Tensor:
+        """Append this step's keys/values and attend its queries (the last ``step`` positions).
+
+        Same result as ``update`` followed by
+        ``compressed_butterfly_attention_from_cache`` over ``get_compressed_state()``
+        (bna/integrations/qwen_mlx.py:1515-1581).  A single-token step runs
+        as one fused launch (append + attention; plus the block compressor on the
+        steps that complete a block); longer steps append, then attend.
+        """
+        from .attention import _attend, _require_cuda, _scale
+
+        _require_cuda(q)
+        step = int(keys.shape[2])
+        d = int(q.shape[3])
+        w = int(local_window_tokens)
+        fused = (step == 1 and int(q.shape[2]) == 1 and q.dtype == keys.dtype and w <= 64
+                 and layout.neighbors.shape[1] <= 16
+                 and (d in (64, 128) or (d == 256 and q.dtype == torch.bfloat16)))
+        if not fused:
+            self.update(keys, values)
+            return _attend(_c(q), self._ring_k, self._ring_v, self._pool_k, self._pool_v, layout=layout,
+                           q_pos0=self.offset - int(q.shape[2]), qpos_dev=None, ring_capacity=self.tail_capacity,
+                           tail_start=self.offset - self.tail_size, kv_len=self.offset,
+                           summary_count=self.summary_count, local_window_tokens=w, scale=scale)
+        _, first_pos, first_slot, n_new, overflow = self._advance(keys, values)
+        keys, values, q = _c(keys), _c(values), _c(q)
+        st = _stream(q)
+        self._compress(first_pos, first_slot, n_new, overflow, st)
+        self._trim(1)
+        b, hq = int(q.shape[0]), int(q.shape[1])
+        out = torch.empty_like(q)
+        nb = layout.neighbors
+        with torch.cuda.device(q.device):
+            _native.call("bfly_decode", q.data_ptr(), _dtype_code(q), b, hq, int(keys.shape[1]), d,
+                         keys.data_ptr(), values.data_ptr(), self._ring_k.data_ptr(), self._ring_v.data_ptr(),
+                         self.tail_capacity, self.offset - self.tail_size, self.offset, self._pool_k.data_ptr(),
+                         self._pool_v.data_ptr(), self.summary_capacity, self.summary_count, nb.data_ptr(),
+                         nb.shape[0], nb.shape[1], layout.block_size, w, _scale(scale, d), out.data_ptr(), st)
+        return out
 
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
         self.update(keys, values)

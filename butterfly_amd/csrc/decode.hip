@@ -1,0 +1,258 @@
+// Butterfly decode on gfx950: one new query per sequence over the two-pool
+// cache (ring tail of raw tokens + pool of mean-pooled block summaries).
+//
+// Reference semantics: compressed_butterfly_attention_from_cache
+// (bna/mlx/attention.py:1816-1876) for one active row at p = kv_len - 1:
+// the SWA stream over tail keys [max(tail_start, p-W+1), p] (:1669-1710) and
+// the routed-summary stream over the neighbours n of block p/BS with n < p/BS,
+// n < summary_count and (n+1)*BS <= max(0, p-W+1) (:1713-1813), merged by
+// online softmax (:519-548).  Both streams are scored under one max and one
+// sum here, which is that merge evaluated exactly; it equals the Torch
+// active-row path (bna/torch/attention_wayfinder_permute.py:1125-1197).
+//
+// The cache append of the new token (bna/mlx/compressed_cache.py:104-118) is
+// fused in: the kernel writes k_new/v_new to ring slot p mod C and scores the
+// new token from the k_new/v_new registers it staged, so nothing is read back
+// through memory in the same launch.
+//
+// Work unit = one workgroup per (batch, kv head), 256 threads.  The <= 64
+// window rows and <= 16 routed summary rows are staged once in LDS; wave w
+// takes query heads w, w+4, ... of the GQA group.  Scores: lanes over keys;
+// softmax reductions: wavefront shuffles; output: lanes over head_dim.
+#include "bfly_common.h"
+
+namespace bfly {
+
+constexpr int kDecMaxWin = 64;
+constexpr int kDecMaxSum = 16;
+constexpr int kDecMaxKeys = kDecMaxWin + kDecMaxSum;
+
+struct DecodeArgs {
+  const void* q;          // [B, Hq, 1, d]
+  void* out;              // [B, Hq, 1, d]
+  const void* k_new;      // [B, Hkv, 1, d] or null
+  const void* v_new;
+  void* ring_k;           // ring [B, Hkv, C, d] (C > 0) or linear tail [B, Hkv, kv_len - tail_start, d]
+  void* ring_v;
+  const void* pool_k;     // [B, Hkv, pool_rows, d]
+  const void* pool_v;
+  const int32_t* nbr;     // [nblocks, kcap]
+  int64_t ring;           // C, 0 = linear tail
+  int64_t kv_rows;        // rows per (b, kv head) of ring_k / ring_v
+  int64_t tail_start;
+  int64_t kv_len;         // query position is kv_len - 1
+  int64_t pool_rows;
+  int64_t nsum;
+  int64_t nblocks;
+  int hq, hkv, kcap, bs, W;
+  float scale;
+};
+
+__device__ __forceinline__ float dec_wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float dec_wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
+  constexpr int VEC = 16 / (int)sizeof(T);     // elements per 16-byte piece
+  constexpr int PIECES = D / VEC;
+  constexpr int KP = D + VEC;                  // padded K row: rows 16 B apart in bank space
+  constexpr int DPL = D / 64;                  // output elements per lane
+  __shared__ __attribute__((aligned(16))) T Ks[kDecMaxKeys * KP];
+  __shared__ __attribute__((aligned(16))) T Vs[kDecMaxKeys * D];
+  __shared__ __attribute__((aligned(16))) float qs[4][D];
+  __shared__ float ps[4][kDecMaxKeys];
+  __shared__ int sel[kDecMaxSum];
+  __shared__ int nsel;
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t bh = blockIdx.x;
+  const int64_t bi = bh / a.hkv;
+  const int kvh = (int)(bh - bi * a.hkv);
+  const int gsz = a.hq / a.hkv;
+  const int64_t p = a.kv_len - 1;
+  int64_t lo = p - a.W + 1;
+  if (lo < a.tail_start) lo = a.tail_start;
+  if (lo < 0) lo = 0;
+  const int nw = (int)(p - lo + 1);
+
+  const T* knew = a.k_new ? reinterpret_cast<const T*>(a.k_new) + bh * D : nullptr;
+  const T* vnew = a.v_new ? reinterpret_cast<const T*>(a.v_new) + bh * D : nullptr;
+  T* rk = reinterpret_cast<T*>(a.ring_k) + bh * a.kv_rows * D;
+  T* rv = reinterpret_cast<T*>(a.ring_v) + bh * a.kv_rows * D;
+  const T* pk = reinterpret_cast<const T*>(a.pool_k) + bh * a.pool_rows * D;
+  const T* pv = reinterpret_cast<const T*>(a.pool_v) + bh * a.pool_rows * D;
+  auto row_of = [&](int64_t pos) -> int64_t { return a.ring ? posmod(pos, a.ring) : pos - a.tail_start; };
+
+  // routed summaries of block p/BS (token-level cut-off)
+  if (tid == 0) {
+    int64_t blk = p / a.bs;
+    if (blk > a.nblocks - 1) blk = a.nblocks - 1;
+    int64_t cut = p - a.W + 1;
+    if (cut < 0) cut = 0;
+    int c = 0;
+    for (int j = 0; j < a.kcap && c < kDecMaxSum; ++j) {
+      const int64_t n = a.nbr[blk * a.kcap + j];
+      if (n < 0 || n >= blk || n >= a.nsum || (n + 1) * a.bs > cut) continue;
+      sel[c++] = (int)n;
+    }
+    nsel = c;
+  }
+  // window rows (the newest one from k_new/v_new when given; also appended to the ring)
+  for (int i = tid; i < nw * PIECES; i += 256) {
+    const int r = i / PIECES, pc = i % PIECES;
+    const int64_t pos = lo + r;
+    uint4 kx, vx;
+    if (knew != nullptr && pos == p) {
+      kx = *reinterpret_cast<const uint4*>(knew + pc * VEC);
+      vx = *reinterpret_cast<const uint4*>(vnew + pc * VEC);
+      *reinterpret_cast<uint4*>(rk + row_of(pos) * D + pc * VEC) = kx;
+      *reinterpret_cast<uint4*>(rv + row_of(pos) * D + pc * VEC) = vx;
+    } else {
+      kx = *reinterpret_cast<const uint4*>(rk + row_of(pos) * D + pc * VEC);
+      vx = *reinterpret_cast<const uint4*>(rv + row_of(pos) * D + pc * VEC);
+    }
+    *reinterpret_cast<uint4*>(Ks + r * KP + pc * VEC) = kx;
+    *reinterpret_cast<uint4*>(Vs + r * D + pc * VEC) = vx;
+  }
+  __syncthreads();
+  const int ns = nsel;
+  for (int i = tid; i < ns * PIECES; i += 256) {
+    const int r = i / PIECES, pc = i % PIECES;
+    const int64_t n = sel[r];
+    *reinterpret_cast<uint4*>(Ks + (nw + r) * KP + pc * VEC) = *reinterpret_cast<const uint4*>(pk + n * D + pc * VEC);
+    *reinterpret_cast<uint4*>(Vs + (nw + r) * D + pc * VEC) = *reinterpret_cast<const uint4*>(pv + n * D + pc * VEC);
+  }
+  const int nk = nw + ns;
+
+  for (int hb = 0; hb < gsz; hb += 4) {
+    const int hh = hb + wave;
+    const bool active = hh < gsz;
+    const int64_t h = (int64_t)kvh * gsz + hh;
+    if (active) {
+      const T* qrow = reinterpret_cast<const T*>(a.q) + (bi * a.hq + h) * D;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) qs[wave][lane * DPL + e] = to_f32(qrow[lane * DPL + e]) * a.scale;
+    }
+    __syncthreads();   // window/summary rows and q visible
+    if (active) {
+      // scores: lane owns keys lane and lane + 64
+      float s[2];
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int rnd = 0; rnd < 2; ++rnd) {
+        const int key = lane + 64 * rnd;
+        float acc = 0.f;
+        if (key < nk) {
+          const T* krow = Ks + key * KP;
+#pragma unroll 4
+          for (int pc = 0; pc < PIECES; ++pc) {
+            const uint4 raw = *reinterpret_cast<const uint4*>(krow + pc * VEC);
+            const T* kv = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc = fmaf(qs[wave][pc * VEC + e], to_f32(kv[e]), acc);
+          }
+          mloc = fmaxf(mloc, acc);
+        }
+        s[rnd] = acc;
+      }
+      const float m = dec_wave_max(mloc);
+      float lloc = 0.f;
+#pragma unroll
+      for (int rnd = 0; rnd < 2; ++rnd) {
+        const int key = lane + 64 * rnd;
+        const float e = key < nk ? expf(s[rnd] - m) : 0.f;
+        s[rnd] = e;
+        lloc += e;
+      }
+      const float inv = 1.f / fmaxf(dec_wave_sum(lloc), 1e-9f);
+#pragma unroll
+      for (int rnd = 0; rnd < 2; ++rnd) {
+        const int key = lane + 64 * rnd;
+        if (key < nk) ps[wave][key] = s[rnd] * inv;
+      }
+    }
+    __syncthreads();   // ps visible to the wave's lanes
+    if (active) {
+      float acc[DPL];
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+      for (int key = 0; key < nk; ++key) {
+        const float pk_ = ps[wave][key];
+        const T* vrow = Vs + key * D + lane * DPL;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[e] = fmaf(pk_, to_f32(vrow[e]), acc[e]);
+      }
+      T* orow = reinterpret_cast<T*>(a.out) + (bi * a.hq + h) * D;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) orow[lane * DPL + e] = from_f32<T>(acc[e]);
+    }
+    __syncthreads();   // qs/ps reused by the next head round
+  }
+}
+
+template <typename T>
+static void launch_decode(const DecodeArgs& a, int d, int64_t grid, hipStream_t stream) {
+  switch (d) {
+    case 64: hipLaunchKernelGGL((decode_kernel<T, 64>), dim3((unsigned)grid), dim3(256), 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((decode_kernel<T, 128>), dim3((unsigned)grid), dim3(256), 0, stream, a); break;
+    default:
+      // fp32 rows of 256 do not fit the LDS staging; the host rejects that case.
+      if constexpr (sizeof(T) == 2)
+        hipLaunchKernelGGL((decode_kernel<T, 256>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+      break;
+  }
+}
+
+}  // namespace bfly
+
+using namespace bfly;
+
+extern "C" int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,
+                           const void* k_new, const void* v_new, void* ring_k, void* ring_v,
+                           int64_t ring_capacity, int64_t tail_start, int64_t kv_len,
+                           const void* pool_k, const void* pool_v, int64_t pool_capacity,
+                           int64_t summary_count, const int32_t* neighbors, int64_t num_blocks, int kcap,
+                           int block_size, int window, float scale, void* out, hipStream_t stream) {
+  BFLY_CHECK_ARG(dtype == BFLY_DTYPE_F32 || dtype == BFLY_DTYPE_BF16, "unsupported dtype %d", dtype);
+  BFLY_CHECK_ARG(q && ring_k && ring_v && pool_k && pool_v && neighbors && out, "null pointer");
+  BFLY_CHECK_ARG((k_new == nullptr) == (v_new == nullptr), "k_new/v_new must both be given or both NULL");
+  BFLY_CHECK_ARG(aligned16(q) && aligned16(out) && aligned16(ring_k) && aligned16(ring_v) && aligned16(pool_k) &&
+                     aligned16(pool_v) && aligned16(k_new) && aligned16(v_new),
+                 "tensor pointers must be 16-byte aligned");
+  BFLY_CHECK_ARG(batch > 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "bad head counts hq=%d hkv=%d", hq, hkv);
+  BFLY_CHECK_ARG(batch * hkv <= INT32_MAX, "batch*hkv too large");
+  BFLY_CHECK_ARG(head_dim == 64 || head_dim == 128 || (head_dim == 256 && dtype == BFLY_DTYPE_BF16),
+                 "bfly_decode: head_dim=%d unsupported (64, 128; 256 for bf16)", head_dim);
+  BFLY_CHECK_ARG(window > 0 && window <= kDecMaxWin, "bfly_decode: window=%d must be in [1, %d]", window, kDecMaxWin);
+  BFLY_CHECK_ARG(kcap > 0 && kcap <= kDecMaxSum, "bfly_decode: kcap=%d must be in [1, %d]", kcap, kDecMaxSum);
+  BFLY_CHECK_ARG(block_size > 0 && num_blocks > 0, "bad block_size/num_blocks");
+  BFLY_CHECK_ARG(kv_len > 0 && tail_start >= 0 && tail_start < kv_len, "tail [%lld, %lld) must hold the query",
+                 (long long)tail_start, (long long)kv_len);
+  BFLY_CHECK_ARG(num_blocks * (int64_t)block_size >= kv_len, "num_blocks does not cover kv_len");
+  BFLY_CHECK_ARG(ring_capacity >= 0 && (ring_capacity == 0 || kv_len - tail_start <= ring_capacity),
+                 "tail [%lld, %lld) does not fit ring capacity %lld", (long long)tail_start, (long long)kv_len,
+                 (long long)ring_capacity);
+  BFLY_CHECK_ARG(summary_count >= 0 && summary_count <= pool_capacity, "summary_count > pool capacity");
+  DecodeArgs a{};
+  a.q = q; a.out = out; a.k_new = k_new; a.v_new = v_new;
+  a.ring_k = ring_k; a.ring_v = ring_v; a.pool_k = pool_k; a.pool_v = pool_v; a.nbr = neighbors;
+  a.ring = ring_capacity;
+  a.kv_rows = ring_capacity ? ring_capacity : kv_len - tail_start;
+  a.tail_start = tail_start; a.kv_len = kv_len;
+  a.pool_rows = pool_capacity; a.nsum = summary_count; a.nblocks = num_blocks;
+  a.hq = hq; a.hkv = hkv; a.kcap = kcap; a.bs = block_size; a.W = window; a.scale = scale;
+  if (dtype == BFLY_DTYPE_F32)
+    launch_decode<float>(a, head_dim, batch * hkv, stream);
+  else
+    launch_decode<__bf16>(a, head_dim, batch * hkv, stream);
+  BFLY_CHECK_LAUNCH("bfly_decode");
+  return BFLY_OK;
+}

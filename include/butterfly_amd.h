@@ -162,6 +162,29 @@ int bfly_attend_cache(const void* q, int dtype, int64_t batch, int hq, int hkv, 
                       void* out, hipStream_t stream);
 
 /*
+ * Device: one decode step -- a single new query per sequence at position
+ * p = kv_len - 1 over the two-pool cache, with the cache append fused in.
+ * Replaces, for one active row, compressed_butterfly_attention_from_cache
+ * (bna/mlx/attention.py:1816-1876) preceded by the tail append of
+ * CompressedKVCache.update_and_fetch (bna/mlx/compressed_cache.py:104-118).
+ * When k_new/v_new ([B, Hkv, 1, d]) are given they are the token at p: they are
+ * written to ring slot p mod ring_capacity and scored from the staged copy.
+ * Keys: tail positions [max(tail_start, p-W+1), p] and the routed summaries n of
+ * block min(p/BS, N-1) with n < that block, n < summary_count and
+ * (n+1)*BS <= max(0, p-W+1), one softmax (the exact two-stream merge).
+ * q/out: [B, Hq, 1, d].  ring_k/ring_v: [B, Hkv, C, d] ring (C = ring_capacity > 0),
+ * or, when C == 0, the linear tail [B, Hkv, kv_len - tail_start, d].
+ * pool_k/pool_v: [B, Hkv, pool_capacity, d].  head_dim 64 or 128 (256 for bf16);
+ * window <= 64; kcap <= 16.
+ */
+int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,
+                const void* k_new, const void* v_new, void* ring_k, void* ring_v,
+                int64_t ring_capacity, int64_t tail_start, int64_t kv_len, const void* pool_k,
+                const void* pool_v, int64_t pool_capacity, int64_t summary_count,
+                const int32_t* neighbors, int64_t num_blocks, int kcap, int block_size, int window,
+                float scale, void* out, hipStream_t stream);
+
+/*
  * Device: append `step` new tokens at positions [offset, offset+step) of the
  * tail ring (slot = position mod ring_capacity).
  * Replaces the tail append of CompressedKVCache.update_and_fetch

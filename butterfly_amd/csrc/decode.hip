@@ -68,7 +68,7 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) T Ks[kDecMaxKeys * KP];
   __shared__ __attribute__((aligned(16))) T Vs[kDecMaxKeys * D];
   __shared__ __attribute__((aligned(16))) float qs[4][D];
-  __shared__ float ps[4][kDecMaxKeys];
+  __shared__ __attribute__((aligned(16))) float ps[4][kDecMaxKeys];
   __shared__ int sel[kDecMaxSum];
   __shared__ int nsel;
 
@@ -143,7 +143,7 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
     }
     __syncthreads();   // window/summary rows and q visible
     if (active) {
-      // scores: lane owns keys lane and lane + 64
+      // scores: lane owns keys lane and lane + 64; 4 partial sums per dot product
       float s[2];
       float mloc = -INFINITY;
 #pragma unroll
@@ -152,13 +152,15 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
         float acc = 0.f;
         if (key < nk) {
           const T* krow = Ks + key * KP;
-#pragma unroll 4
+          float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
           for (int pc = 0; pc < PIECES; ++pc) {
             const uint4 raw = *reinterpret_cast<const uint4*>(krow + pc * VEC);
             const T* kv = reinterpret_cast<const T*>(&raw);
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) acc = fmaf(qs[wave][pc * VEC + e], to_f32(kv[e]), acc);
+            for (int e = 0; e < VEC; ++e) part[e & 3] = fmaf(qs[wave][pc * VEC + e], to_f32(kv[e]), part[e & 3]);
           }
+          acc = (part[0] + part[1]) + (part[2] + part[3]);
           mloc = fmaxf(mloc, acc);
         }
         s[rnd] = acc;
@@ -168,7 +170,7 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
 #pragma unroll
       for (int rnd = 0; rnd < 2; ++rnd) {
         const int key = lane + 64 * rnd;
-        const float e = key < nk ? expf(s[rnd] - m) : 0.f;
+        const float e = key < nk ? __expf(s[rnd] - m) : 0.f;
         s[rnd] = e;
         lloc += e;
       }
@@ -176,23 +178,39 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
 #pragma unroll
       for (int rnd = 0; rnd < 2; ++rnd) {
         const int key = lane + 64 * rnd;
-        if (key < nk) ps[wave][key] = s[rnd] * inv;
+        if (key < kDecMaxKeys) ps[wave][key] = key < nk ? s[rnd] * inv : 0.f;
       }
     }
     __syncthreads();   // ps visible to the wave's lanes
     if (active) {
-      float acc[DPL];
+      // output: lane owns d = lane*DPL + [0, DPL); keys in groups of 4 with
+      // independent accumulators (rows past nk carry p = 0 and are skipped)
+      float acc[DPL][4];
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
-      for (int key = 0; key < nk; ++key) {
+      for (int e = 0; e < DPL; ++e)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[e][j] = 0.f;
+      const int nk4 = nk & ~3;
+      for (int key = 0; key < nk4; key += 4) {
+        const float4 p4 = *reinterpret_cast<const float4*>(&ps[wave][key]);
+        const float pj[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const T* vrow = Vs + (key + j) * D + lane * DPL;
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) acc[e][j] = fmaf(pj[j], to_f32(vrow[e]), acc[e][j]);
+        }
+      }
+      for (int key = nk4; key < nk; ++key) {
         const float pk_ = ps[wave][key];
         const T* vrow = Vs + key * D + lane * DPL;
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[e] = fmaf(pk_, to_f32(vrow[e]), acc[e]);
+        for (int e = 0; e < DPL; ++e) acc[e][0] = fmaf(pk_, to_f32(vrow[e]), acc[e][0]);
       }
       T* orow = reinterpret_cast<T*>(a.out) + (bi * a.hq + h) * D;
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) orow[lane * DPL + e] = from_f32<T>(acc[e]);
+      for (int e = 0; e < DPL; ++e)
+        orow[lane * DPL + e] = from_f32<T>((acc[e][0] + acc[e][1]) + (acc[e][2] + acc[e][3]));
     }
     __syncthreads();   // qs/ps reused by the next head round
   }

@@ -162,6 +162,17 @@ def bench_decode(torch, bf, batches=(1, 8, 32), steps=64, seed=0):
     dev = torch.device("cuda:0")
     out = {}
     g = torch.Generator(device=dev).manual_seed(seed)
+    # warm-up: load the decode/compress kernels outside the timed loops
+    wc = bf.CompressedKVCache(block_size=bs, local_window_tokens=W, max_kv_size=4096)
+    wk = torch.randn(1, hkv, 300, d, generator=g, device=dev).bfloat16()
+    wc.update(wk[:, :, :256], wk[:, :, :256])
+    for s in range(256, 300):
+        lay = bf.build_block_butterfly_layout(seq_len=s + 1, block_size=bs, num_key_value_heads=hkv,
+                                              num_key_value_groups=hq // hkv, layer_idx=3, local_window_blocks=1,
+                                              sink_count=1, partner_count=1, partner_rule="causal_shift")
+        wc.update_and_attend(torch.randn(1, hq, 1, d, generator=g, device=dev).bfloat16(), wk[:, :, s:s + 1],
+                             wk[:, :, s:s + 1], layout=lay, local_window_tokens=W)
+    torch.cuda.synchronize()
     for B in batches:
         # State after a 384-chunked prefill of 131072 tokens (reference schedule):
         # tail = 256 tokens, 1023 summaries, summary_offset = 1023*128.
@@ -173,6 +184,7 @@ def bench_decode(torch, bf, batches=(1, 8, 32), steps=64, seed=0):
         sv = torch.randn(B, hkv, 1023, d, generator=g, device=dev).bfloat16()
         cache.state = (tk, tv, sk, sv)
         cache.meta_state = (str(bs), str(W), str(ctx), str(1023 * bs))
+        cache.ring_state()          # place the restored tail in ring order before timing
         kn = torch.randn(steps, B, hkv, 1, d, generator=g, device=dev).bfloat16()
         vn = torch.randn(steps, B, hkv, 1, d, generator=g, device=dev).bfloat16()
         qn = torch.randn(steps, B, hq, 1, d, generator=g, device=dev).bfloat16()
@@ -199,6 +211,47 @@ def bench_decode(torch, bf, batches=(1, 8, 32), steps=64, seed=0):
         out[str(B)] = {"ms_per_step": dt * 1e3, "tok_s": B / dt, "alg_bytes_per_step": bytes_step,
                        "wall_gbs": bytes_step / dt / 1e9}
     return out
+
+
+def bench_stream(torch, bf, seed=0, T=262144, chunk=384, layer=5):
+    """cfg4: streaming chunked prefill, Hq=16, Hkv=4, d=256, bf16, 384-token chunks.
+
+    Per chunk (the harness schedule): cache update (append + compress due
+    blocks), layout for the live kv_len, attention (first chunk one-shot, later
+    chunks from the device ring + pool).  Inputs are per-chunk contiguous
+    tensors resident in HBM (what each chunk's projections would produce).
+    """
+    hq, hkv, d, bs, W = 16, 4, 256, 128, 64
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    chunks = []
+    for s in range(0, T, chunk):
+        n = min(chunk, T - s)
+        chunks.append(tuple(torch.randn(1, h, n, d, generator=g, device=dev).bfloat16() for h in (hq, hkv, hkv)))
+    cfg = bf.QwenButterflyConfig()
+
+    def run():
+        cache = bf.CompressedKVCache(block_size=bs, local_window_tokens=W, max_kv_size=T, max_chunk_size=512)
+        core = bf.ButterflyAttentionCore(cfg, layer)
+        outs = bf.chunked_prefill(core, chunks, cache)
+        return cache, outs
+
+    cache, outs = run()                 # warm: kernels loaded, layouts for every kv_len built
+    del outs
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    t0 = time.perf_counter()
+    cache, outs = run()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    peak = torch.cuda.max_memory_allocated() - base
+    assert all(torch.isfinite(o[:, :, -1].float()).all() for o in outs[-3:])
+    dense = 2 * hkv * T * d * 2
+    return {"T": T, "chunks": len(chunks), "e2e_s": wall, "tok_s": T / wall, "ms_per_chunk": wall * 1e3 / len(chunks),
+            "peak_hbm_bytes_above_inputs": int(peak), "retained_kv_bytes": int(cache.nbytes),
+            "dense_kv_bytes": int(dense), "retained_over_dense": cache.nbytes / dense,
+            "final_tail": cache.tail_size, "final_summaries": cache.summary_count}
 
 
 def cpu_baseline(q, k, v, ref_lays, repeats=3, max_seconds=30.0):
@@ -234,6 +287,7 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-stream", action="store_true", help="skip the cfg4 streaming chunked-prefill leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -261,6 +315,7 @@ def main():
     pre = bench_prefill(args, torch, bf, tp)
     q, k, v, ref_lays = pre.pop("inputs")
     decode = None if args.no_decode else bench_decode(torch, bf)
+    stream = None if args.no_stream else bench_stream(torch, bf)
     cpu = None if args.no_cpu_baseline else cpu_baseline(q, k, v, ref_lays)
     line = {
         "metric": "prefill tok/s @64k (1 layer, bf16, 9-stage sweep)",
@@ -286,7 +341,8 @@ def main():
                      "mfma_frac": pre["achieved_tflops"] / MFMA_BF16_PEAK_TFLOPS},
         "cpu_baseline": cpu,
         "extra": {"gpu_ms_per_step": pre["gpu_ms_per_step"], "prefill_kernel_ms_min": pre["prefill_kernel_ms_min"],
-                  "compress_alg_bytes": pre["compress_bytes"], "decode_cfg3": decode},
+                  "compress_alg_bytes": pre["compress_bytes"], "decode_cfg3": decode,
+                  "stream_cfg4": stream},
     }
     print(json.dumps(line), flush=True)
 

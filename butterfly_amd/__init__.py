@@ -15,6 +15,15 @@ from .attention import (
     compressed_butterfly_block_index_tensors,
 )
 from .compressed_cache import CompressedKVCache
+from .integrations import (
+    AttentionProfile,
+    ButterflyAttentionCore,
+    QwenButterflyConfig,
+    chunked_prefill,
+    install_compressed_kv_caches,
+    split_chunks,
+    swap_qwen_attention_with_butterfly,
+)
 from .layout import BlockButterflyLayout, build_block_butterfly_layout, clear_layout_cache
 from .topology import (
     ButterflyLayoutMetadata,
@@ -27,6 +36,13 @@ from .topology import (
 )
 
 __all__ = [
+    "AttentionProfile",
+    "ButterflyAttentionCore",
+    "QwenButterflyConfig",
+    "chunked_prefill",
+    "install_compressed_kv_caches",
+    "split_chunks",
+    "swap_qwen_attention_with_butterfly",
     "BlockButterflyLayout",
     "ButterflyLayoutMetadata",
     "CompressedKVCache",

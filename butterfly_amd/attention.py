@@ -96,7 +96,7 @@ def compressed_butterfly_block_index_tensors(layout, *, T: int, local_window_tok
         raise ValueError("T must be positive")
     if int(local_window_tokens) <= 0:
         raise ValueError("local_window_tokens must be positive")
-    nb, bs = layout.neighbors, layout.block_size
+    nb, bs = layout.table.exact(), layout.block_size      # the reference's [N, K] width
     n, k = nb.shape
     slots = int(local_window_tokens) + bs - 1
     dev = nb.device
@@ -119,7 +119,7 @@ def compressed_butterfly_active_index_tensors(layout, *, kv_len: int, query_posi
     (attention_wayfinder_permute.py:969-1019); with ``tail_start``/``tail_len``
     given, _compressed_butterfly_active_indices_from_tail (bna/mlx/attention.py:1601-1666).
     """
-    nb, bs = layout.neighbors, layout.block_size
+    nb, bs = layout.table.exact(), layout.block_size      # the reference's [N, K] width
     n, k = nb.shape
     dev = nb.device
     qp = torch.as_tensor(query_positions).to(device=dev, dtype=torch.int32).view(-1).contiguous()

@@ -19,10 +19,27 @@ from dataclasses import dataclass
 
 import torch
 
-from .topology import ButterflyLayoutMetadata, block_neighbor_table, butterfly_layout_metadata
+from .topology import ButterflyLayoutMetadata, block_neighbor_table_padded, butterfly_layout_metadata
 
 _TABLE_CACHE: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
 _TABLE_CACHE_MAX = 256
+
+
+class _Table:
+    """A device neighbour table, its row degrees and (lazily) its exact width K."""
+
+    __slots__ = ("padded", "degree", "_exact")
+
+    def __init__(self, padded: torch.Tensor, degree: torch.Tensor) -> None:
+        self.padded = padded
+        self.degree = degree
+        self._exact = None
+
+    def exact(self) -> torch.Tensor:
+        if self._exact is None:
+            k = max(1, int(self.degree.max().item()))
+            self._exact = self.padded[:, :k].contiguous()
+        return self._exact
 
 
 @dataclass(frozen=True)
@@ -31,18 +48,25 @@ class BlockButterflyLayout:
     block_size: int
     num_blocks: int
     num_query_heads: int
-    neighbors: torch.Tensor          # device int32 [N, K], -1 padded
+    table: _Table
     metadata: ButterflyLayoutMetadata
     topology_name: str = "butterfly"
 
     @property
+    def neighbors(self) -> torch.Tensor:
+        """Device int32 [N, kcap] table the kernels read (kcap = 1 + lwb + partners + sinks,
+        -1 padded); no host synchronisation."""
+        return self.table.padded
+
+    @property
     def block_neighbors(self) -> torch.Tensor:
-        """[Hq, N, K] view, identical for every query head."""
-        return self.neighbors.unsqueeze(0).expand(self.num_query_heads, -1, -1)
+        """The reference's [Hq, N, K] tensor (K = max row length), identical for every
+        query head; the first access reads K back from the device."""
+        return self.table.exact().unsqueeze(0).expand(self.num_query_heads, -1, -1)
 
     @property
     def num_neighbors(self) -> int:
-        return int(self.neighbors.shape[1])
+        return int(self.table.exact().shape[1])
 
     @property
     def stage_idx(self) -> int:
@@ -94,12 +118,12 @@ def build_block_butterfly_layout(*, seq_len: int, block_size: int, num_key_value
                                      partner_count=partner_count, sink_count=sink_count,
                                      local_window_blocks=local_window_blocks)
     key = (n, meta.stage_idx, meta.partner_rule, meta.partner_bits, int(local_window_blocks), int(sink_count),
-           str(dev))
+           int(partner_count), str(dev))
     table = _TABLE_CACHE.get(key)
     if table is None:
-        table = block_neighbor_table(num_blocks=n, layer_idx=layer_idx, partner_rule=partner_rule,
-                                     local_window_blocks=local_window_blocks, sink_count=sink_count,
-                                     partner_count=partner_count, device=dev)
+        table = _Table(*block_neighbor_table_padded(num_blocks=n, layer_idx=layer_idx, partner_rule=partner_rule,
+                                                    local_window_blocks=local_window_blocks, sink_count=sink_count,
+                                                    partner_count=partner_count, device=dev))
         _TABLE_CACHE[key] = table
         while len(_TABLE_CACHE) > _TABLE_CACHE_MAX:
             _TABLE_CACHE.popitem(last=False)
@@ -108,7 +132,7 @@ def build_block_butterfly_layout(*, seq_len: int, block_size: int, num_key_value
     return BlockButterflyLayout(
         seq_len=int(seq_len), block_size=int(block_size), num_blocks=n,
         num_query_heads=int(num_key_value_heads) * int(num_key_value_groups),
-        neighbors=table, metadata=meta,
+        table=table, metadata=meta,
     )
 
 

@@ -91,13 +91,15 @@ def butterfly_layout_metadata(*, num_blocks: int, layer_idx: int, partner_rule: 
     )
 
 
-def block_neighbor_table(*, num_blocks: int, layer_idx: int, partner_rule: str, local_window_blocks: int,
-                         sink_count: int, partner_count: int, device=None) -> torch.Tensor:
-    """Device int32 [N, K] neighbour table, -1 padded, K = max row length.
+def block_neighbor_table_padded(*, num_blocks: int, layer_idx: int, partner_rule: str, local_window_blocks: int,
+                                sink_count: int, partner_count: int, device=None):
+    """Device (table int32 [N, kcap], degree int32 [N]) with kcap = 1 + lwb + partners + sinks.
 
-    Row b is the ordered unique list [b, b-1..b-lwb, partners, sinks]
+    Row b is the ordered unique list [b, b-1..b-lwb, partners, sinks], -1 padded
     (reference: bna/torch/attention_wayfinder_permute.py:627-662,
-    bna/topology/butterfly.py:219-284).  One GPU launch; K is read back once.
+    bna/topology/butterfly.py:219-284).  One GPU launch, no host synchronisation:
+    the kernels skip -1 entries, so the padded width is equivalent to the
+    reference's K = max row length.
     """
     if int(num_blocks) <= 0:
         raise ValueError("num_blocks must be positive")
@@ -115,5 +117,15 @@ def block_neighbor_table(*, num_blocks: int, layer_idx: int, partner_rule: str, 
         _native.call("bfly_block_neighbors", int(num_blocks), int(layer_idx), _rule_code(partner_rule),
                      int(local_window_blocks), int(sink_count), int(partner_count), table.data_ptr(), kcap,
                      degree.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+    return table, degree
+
+
+def block_neighbor_table(*, num_blocks: int, layer_idx: int, partner_rule: str, local_window_blocks: int,
+                         sink_count: int, partner_count: int, device=None) -> torch.Tensor:
+    """Device int32 [N, K] neighbour table, -1 padded, K = max row length (the
+    reference's ``block_neighbors[0]`` shape); reads K back from the device."""
+    table, degree = block_neighbor_table_padded(num_blocks=num_blocks, layer_idx=layer_idx, partner_rule=partner_rule,
+                                                local_window_blocks=local_window_blocks, sink_count=sink_count,
+                                                partner_count=partner_count, device=device)
     k = max(1, int(degree.max().item()))
     return table[:, :k].contiguous()

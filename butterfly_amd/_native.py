@@ -29,6 +29,16 @@ RULES = {
 }
 
 _i32, _i64, _f32, _vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
+
+MAX_PARTNERS = 16
+
+
+class Topology(C.Structure):
+    """bfly_topology_t (include/butterfly_amd.h)."""
+
+    _fields_ = [("rule", C.c_int32), ("width", C.c_int32), ("stage_idx", C.c_int32), ("stage_count", C.c_int32),
+                ("local_window_blocks", C.c_int32), ("sink_count", C.c_int32), ("partner_count", C.c_int32),
+                ("partner_bits", C.c_int32 * MAX_PARTNERS)]
 _int = C.c_int
 _pi32 = C.POINTER(C.c_int32)
 
@@ -48,8 +58,9 @@ SIGNATURES = {
     "bfly_attend_cache": (_int, [_vp, _int, _i64, _int, _int, _i64, _int, _vp, _i64, _vp, _vp, _i64,
                                  _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _int, _int, _int, _f32,
                                  _vp, _vp]),
+    "bfly_topology_init": (_int, [_i64, _i64, _int, _int, _int, _int, C.POINTER(Topology)]),
     "bfly_decode": (_int, [_vp, _int, _i64, _int, _int, _int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp,
-                           _i64, _i64, _vp, _i64, _int, _int, _int, _f32, _vp, _vp]),
+                           _i64, _i64, C.POINTER(Topology), _i64, _int, _int, _f32, _vp, _vp]),
     "bfly_cache_append": (_int, [_vp, _vp, _int, _i64, _int, _i64, _int, _vp, _vp, _i64, _i64, _vp]),
     "bfly_cache_compress": (_int, [_vp, _vp, _int, _i64, _int, _int, _i64, _i64, _i64, _int, _vp, _vp,
                                    _i64, _i64, _vp]),

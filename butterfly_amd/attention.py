@@ -207,14 +207,14 @@ def _attend(q, tail_k, tail_v, pool_k, pool_v, *, layout, q_pos0, qpos_dev, ring
     out = torch.empty_like(q)
     nb = layout.neighbors
     if (tq == 1 and qpos_dev is None and int(q_pos0) == int(kv_len) - 1 and int(tail_start) < int(kv_len)
-            and int(local_window_tokens) <= 64 and nb.shape[1] <= 16
+            and int(local_window_tokens) <= 64 and nb.shape[1] <= 16 and pool_k.shape[2] > 0
             and (d in (64, 128) or (d == 256 and q.dtype == torch.bfloat16))):
         # a single row at the newest position: the decode kernel
         with torch.cuda.device(q.device):
             _native.call("bfly_decode", q.data_ptr(), _dtype_code(q), b, hq, hk, d, None, None,
                          tail_k.data_ptr(), tail_v.data_ptr(), int(ring_capacity), int(tail_start), int(kv_len),
                          pool_k.data_ptr(), pool_v.data_ptr(), pool_k.shape[2], int(summary_count),
-                         nb.data_ptr(), nb.shape[0], nb.shape[1], layout.block_size, int(local_window_tokens),
+                         layout.table.topology, nb.shape[0], layout.block_size, int(local_window_tokens),
                          _scale(scale, d), out.data_ptr(), _stream(q))
         return out
     with torch.cuda.device(q.device):

@@ -187,8 +187,8 @@ class CompressedKVCache:
             _native.call("bfly_decode", q.data_ptr(), _dtype_code(q), b, hq, int(keys.shape[1]), d,
                          keys.data_ptr(), values.data_ptr(), self._ring_k.data_ptr(), self._ring_v.data_ptr(),
                          self.tail_capacity, self.offset - self.tail_size, self.offset, self._pool_k.data_ptr(),
-                         self._pool_v.data_ptr(), self.summary_capacity, self.summary_count, nb.data_ptr(),
-                         nb.shape[0], nb.shape[1], layout.block_size, w, _scale(scale, d), out.data_ptr(), st)
+                         self._pool_v.data_ptr(), self.summary_capacity, self.summary_count, layout.table.topology,
+                         nb.shape[0], layout.block_size, w, _scale(scale, d), out.data_ptr(), st)
         return out
 
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):

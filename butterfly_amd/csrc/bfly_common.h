@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/butterfly_amd.h"
 
 namespace bfly {
@@ -44,6 +46,16 @@ __device__ __forceinline__ __bf16 from_f32<__bf16>(float x) { return (__bf16)x; 
 
 // Vectorised paths issue 16-byte loads/stores: tensor base pointers must be 16-byte aligned.
 __host__ __forceinline__ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Compile-time loop: f(std::integral_constant<int, I>{}) for I = 0..N-1, so
+// register arrays indexed by I never become private (scratch) memory.
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (N > 0) {
+    static_for<N - 1>(f);
+    f(std::integral_constant<int, N - 1>{});
+  }
+}
 
 // Floor division / modulo for possibly negative positions.
 __host__ __device__ __forceinline__ int64_t floordiv(int64_t a, int64_t b) {

@@ -15,11 +15,14 @@
 // new token from the k_new/v_new registers it staged, so nothing is read back
 // through memory in the same launch.
 //
-// Work unit = one workgroup per (batch, kv head), 256 threads.  The <= 64
-// window rows and <= 16 routed summary rows are staged once in LDS; wave w
-// takes query heads w, w+4, ... of the GQA group.  Scores: lanes over keys;
-// softmax reductions: wavefront shuffles; output: lanes over head_dim.
-#include "bfly_common.h"
+// Work unit = one workgroup per (batch, kv head), 256 threads.  Every thread
+// issues its q and window-row loads at once while thread 0 computes the routed
+// row of the query block from the topology (no table read); the <= 16 summary
+// rows follow after one barrier.  The <= 64 window rows and the summaries sit
+// in LDS; wave w takes query heads w, w+4, ... of the GQA group.
+// Scores: lanes over keys; softmax reductions: wavefront shuffles; output:
+// lanes over head_dim.
+#include "bfly_topology.h"
 
 namespace bfly {
 
@@ -36,7 +39,7 @@ struct DecodeArgs {
   void* ring_v;
   const void* pool_k;     // [B, Hkv, pool_rows, d]
   const void* pool_v;
-  const int32_t* nbr;     // [nblocks, kcap]
+  bfly_topology_t topo;   // routed row of the query block, computed in-kernel
   int64_t ring;           // C, 0 = linear tail
   int64_t kv_rows;        // rows per (b, kv head) of ring_k / ring_v
   int64_t tail_start;
@@ -44,7 +47,7 @@ struct DecodeArgs {
   int64_t pool_rows;
   int64_t nsum;
   int64_t nblocks;
-  int hq, hkv, kcap, bs, W;
+  int hq, hkv, bs, W;
   float scale;
 };
 
@@ -60,15 +63,16 @@ __device__ __forceinline__ float dec_wave_sum(float v) {
 }
 
 template <typename T, int D>
-__global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a) {
   constexpr int VEC = 16 / (int)sizeof(T);     // elements per 16-byte piece
   constexpr int PIECES = D / VEC;
   constexpr int KP = D + VEC;                  // padded K row: rows 16 B apart in bank space
-  constexpr int DPL = D / 64;                  // output elements per lane
+  constexpr int DPL = D / 64;                  // q/output elements per lane
   __shared__ __attribute__((aligned(16))) T Ks[kDecMaxKeys * KP];
   __shared__ __attribute__((aligned(16))) T Vs[kDecMaxKeys * D];
   __shared__ __attribute__((aligned(16))) float qs[4][D];
   __shared__ __attribute__((aligned(16))) float ps[4][kDecMaxKeys];
+  __shared__ int32_t rowbuf[kDecMaxSum];
   __shared__ int sel[kDecMaxSum];
   __shared__ int nsel;
 
@@ -91,21 +95,30 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
   const T* pv = reinterpret_cast<const T*>(a.pool_v) + bh * a.pool_rows * D;
   auto row_of = [&](int64_t pos) -> int64_t { return a.ring ? posmod(pos, a.ring) : pos - a.tail_start; };
 
-  // routed summaries of block p/BS (token-level cut-off)
+  // ---- this wave's first q row into registers (its load overlaps the staging below)
+  float qv[DPL];
+  {
+    const int hh = wave < gsz ? wave : 0;
+    const T* qrow = reinterpret_cast<const T*>(a.q) + (bi * a.hq + (int64_t)kvh * gsz + hh) * D + lane * DPL;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) qv[e] = to_f32(qrow[e]);
+  }
+  // ---- routed summaries of block p/BS (token-level cut-off), from the topology
   if (tid == 0) {
     int64_t blk = p / a.bs;
     if (blk > a.nblocks - 1) blk = a.nblocks - 1;
     int64_t cut = p - a.W + 1;
     if (cut < 0) cut = 0;
+    const int len = neighbor_row(blk, a.nblocks, a.topo, rowbuf, kDecMaxSum);
     int c = 0;
-    for (int j = 0; j < a.kcap && c < kDecMaxSum; ++j) {
-      const int64_t n = a.nbr[blk * a.kcap + j];
-      if (n < 0 || n >= blk || n >= a.nsum || (n + 1) * a.bs > cut) continue;
+    for (int j = 0; j < len; ++j) {
+      const int64_t n = rowbuf[j];
+      if (n >= blk || n >= a.nsum || (n + 1) * a.bs > cut) continue;
       sel[c++] = (int)n;
     }
     nsel = c;
   }
-  // window rows (the newest one from k_new/v_new when given; also appended to the ring)
+  // ---- window rows into LDS (the newest from k_new/v_new when given, also appended to the ring)
   for (int i = tid; i < nw * PIECES; i += 256) {
     const int r = i / PIECES, pc = i % PIECES;
     const int64_t pos = lo + r;
@@ -137,9 +150,13 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
     const bool active = hh < gsz;
     const int64_t h = (int64_t)kvh * gsz + hh;
     if (active) {
-      const T* qrow = reinterpret_cast<const T*>(a.q) + (bi * a.hq + h) * D;
+      if (hb > 0) {
+        const T* qrow = reinterpret_cast<const T*>(a.q) + (bi * a.hq + h) * D + lane * DPL;
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) qs[wave][lane * DPL + e] = to_f32(qrow[lane * DPL + e]) * a.scale;
+        for (int e = 0; e < DPL; ++e) qv[e] = to_f32(qrow[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) qs[wave][lane * DPL + e] = qv[e] * a.scale;
     }
     __syncthreads();   // window/summary rows and q visible
     if (active) {
@@ -237,10 +254,10 @@ extern "C" int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int 
                            const void* k_new, const void* v_new, void* ring_k, void* ring_v,
                            int64_t ring_capacity, int64_t tail_start, int64_t kv_len,
                            const void* pool_k, const void* pool_v, int64_t pool_capacity,
-                           int64_t summary_count, const int32_t* neighbors, int64_t num_blocks, int kcap,
+                           int64_t summary_count, const bfly_topology_t* topology, int64_t num_blocks,
                            int block_size, int window, float scale, void* out, hipStream_t stream) {
   BFLY_CHECK_ARG(dtype == BFLY_DTYPE_F32 || dtype == BFLY_DTYPE_BF16, "unsupported dtype %d", dtype);
-  BFLY_CHECK_ARG(q && ring_k && ring_v && pool_k && pool_v && neighbors && out, "null pointer");
+  BFLY_CHECK_ARG(q && ring_k && ring_v && pool_k && pool_v && topology && out, "null pointer");
   BFLY_CHECK_ARG((k_new == nullptr) == (v_new == nullptr), "k_new/v_new must both be given or both NULL");
   BFLY_CHECK_ARG(aligned16(q) && aligned16(out) && aligned16(ring_k) && aligned16(ring_v) && aligned16(pool_k) &&
                      aligned16(pool_v) && aligned16(k_new) && aligned16(v_new),
@@ -250,7 +267,9 @@ extern "C" int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int 
   BFLY_CHECK_ARG(head_dim == 64 || head_dim == 128 || (head_dim == 256 && dtype == BFLY_DTYPE_BF16),
                  "bfly_decode: head_dim=%d unsupported (64, 128; 256 for bf16)", head_dim);
   BFLY_CHECK_ARG(window > 0 && window <= kDecMaxWin, "bfly_decode: window=%d must be in [1, %d]", window, kDecMaxWin);
-  BFLY_CHECK_ARG(kcap > 0 && kcap <= kDecMaxSum, "bfly_decode: kcap=%d must be in [1, %d]", kcap, kDecMaxSum);
+  BFLY_CHECK_ARG(1 + topology->local_window_blocks + topology->partner_count + topology->sink_count <= kDecMaxSum &&
+                     topology->partner_count >= 0 && topology->partner_count <= BFLY_MAX_PARTNERS,
+                 "bfly_decode: the routed row must fit %d slots", kDecMaxSum);
   BFLY_CHECK_ARG(block_size > 0 && num_blocks > 0, "bad block_size/num_blocks");
   BFLY_CHECK_ARG(kv_len > 0 && tail_start >= 0 && tail_start < kv_len, "tail [%lld, %lld) must hold the query",
                  (long long)tail_start, (long long)kv_len);
@@ -258,15 +277,16 @@ extern "C" int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int 
   BFLY_CHECK_ARG(ring_capacity >= 0 && (ring_capacity == 0 || kv_len - tail_start <= ring_capacity),
                  "tail [%lld, %lld) does not fit ring capacity %lld", (long long)tail_start, (long long)kv_len,
                  (long long)ring_capacity);
-  BFLY_CHECK_ARG(summary_count >= 0 && summary_count <= pool_capacity, "summary_count > pool capacity");
+  BFLY_CHECK_ARG(summary_count >= 0 && summary_count <= pool_capacity && pool_capacity > 0,
+                 "summary_count must be in [0, pool_capacity]");
   DecodeArgs a{};
   a.q = q; a.out = out; a.k_new = k_new; a.v_new = v_new;
-  a.ring_k = ring_k; a.ring_v = ring_v; a.pool_k = pool_k; a.pool_v = pool_v; a.nbr = neighbors;
+  a.ring_k = ring_k; a.ring_v = ring_v; a.pool_k = pool_k; a.pool_v = pool_v; a.topo = *topology;
   a.ring = ring_capacity;
   a.kv_rows = ring_capacity ? ring_capacity : kv_len - tail_start;
   a.tail_start = tail_start; a.kv_len = kv_len;
   a.pool_rows = pool_capacity; a.nsum = summary_count; a.nblocks = num_blocks;
-  a.hq = hq; a.hkv = hkv; a.kcap = kcap; a.bs = block_size; a.W = window; a.scale = scale;
+  a.hq = hq; a.hkv = hkv; a.bs = block_size; a.W = window; a.scale = scale;
   if (dtype == BFLY_DTYPE_F32)
     launch_decode<float>(a, head_dim, batch * hkv, stream);
   else

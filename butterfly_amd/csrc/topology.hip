@@ -9,7 +9,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include "bfly_common.h"
+#include "bfly_topology.h"
 
 namespace bfly {
 
@@ -30,61 +30,13 @@ static int host_width(int64_t n) {
 
 static bool valid_rule(int rule) { return rule >= BFLY_RULE_XOR && rule <= BFLY_RULE_RANDOM; }
 
-constexpr int kMaxPartners = 16;
-struct PartnerBits {
-  int32_t bit[kMaxPartners];
-};
-
-__device__ __forceinline__ int64_t bit_reverse(int64_t value, int nbits) {
-  int64_t out = 0;
-  for (int i = 0; i < nbits; ++i) out = (out << 1) | ((value >> i) & 1);
-  return out;
-}
-
-// Partner of `block` for one bit; -1 where the reference returns None.
-__device__ __forceinline__ int64_t partner_block(int64_t block, int bit, int64_t nblocks, int rule,
-                                                 int width) {
-  if (bit < 0 || bit >= (width > 1 ? width : 1)) return -1;
-  int64_t p;
-  switch (rule) {
-    case BFLY_RULE_CAUSAL_SHIFT: p = block - ((int64_t)1 << bit); break;
-    case BFLY_RULE_XOR:
-    case BFLY_RULE_BENES: p = block ^ ((int64_t)1 << bit); break;
-    case BFLY_RULE_FIXED_STRIDE: p = block - 1; break;
-    case BFLY_RULE_RANDOM: {
-      if (block <= 0) return -1;
-      uint32_t seed = (uint32_t)block * 2654435761u + (uint32_t)bit * 374761393u;
-      p = (int64_t)(seed % (uint64_t)block);
-      break;
-    }
-    default: p = bit_reverse(bit_reverse(block, width) ^ ((int64_t)1 << bit), width); break;
-  }
-  if (p < 0 || p >= nblocks || p > block) return -1;
-  return p;
-}
-
 // One thread per block: row = ordered unique [b, b-1..b-lwb, partners, sinks].
-__global__ void neighbors_kernel(int64_t nblocks, int rule, int width, int lwb, int sinks,
-                                 int npartners, PartnerBits bits, int32_t* __restrict__ out,
-                                 int kcap, int32_t* __restrict__ degree) {
+__global__ void neighbors_kernel(int64_t nblocks, bfly_topology_t topo, int32_t* __restrict__ out, int kcap,
+                                 int32_t* __restrict__ degree) {
   int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= nblocks) return;
   int32_t* row = out + b * kcap;
-  int len = 0;
-  auto push = [&](int64_t v) {
-    if (v < 0 || v >= nblocks) return;
-    for (int i = 0; i < len; ++i)
-      if (row[i] == (int32_t)v) return;
-    if (len < kcap) row[len++] = (int32_t)v;
-  };
-  push(b);
-  for (int off = 1; off <= lwb; ++off) {
-    if (b - off < 0) break;
-    push(b - off);
-  }
-  for (int j = 0; j < npartners; ++j) push(partner_block(b, bits.bit[j], nblocks, rule, width));
-  int64_t ns = sinks < nblocks ? sinks : nblocks;
-  for (int64_t s = 0; s < ns; ++s) push(s);
+  const int len = neighbor_row(b, nblocks, topo, row, kcap);
   for (int i = len; i < kcap; ++i) row[i] = -1;
   degree[b] = len;
 }
@@ -224,29 +176,38 @@ extern "C" int bfly_partner_bits(int stage_idx, int stage_count, int width, int 
   return BFLY_OK;
 }
 
+extern "C" int bfly_topology_init(int64_t num_blocks, int64_t layer_idx, int partner_rule, int local_window_blocks,
+                                  int sink_count, int partner_count, bfly_topology_t* out) {
+  BFLY_CHECK_ARG(num_blocks > 0 && num_blocks <= INT32_MAX, "num_blocks out of range: %lld", (long long)num_blocks);
+  BFLY_CHECK_ARG(local_window_blocks >= 0 && sink_count >= 0 && partner_count >= 0, "negative topology parameter");
+  BFLY_CHECK_ARG(partner_count <= BFLY_MAX_PARTNERS, "partner_count > %d", BFLY_MAX_PARTNERS);
+  BFLY_CHECK_ARG(out != nullptr, "null output pointer");
+  bfly_topology_t t{};
+  int rc = bfly_stage_meta(num_blocks, layer_idx, partner_rule, &t.stage_idx, &t.stage_count, &t.width);
+  if (rc) return rc;
+  rc = bfly_partner_bits(t.stage_idx, t.stage_count, t.width, partner_count, partner_rule, t.partner_bits);
+  if (rc) return rc;
+  t.rule = partner_rule;
+  t.local_window_blocks = local_window_blocks;
+  t.sink_count = sink_count;
+  t.partner_count = partner_count;
+  *out = t;
+  return BFLY_OK;
+}
+
 extern "C" int bfly_block_neighbors(int64_t num_blocks, int64_t layer_idx, int partner_rule,
                                     int local_window_blocks, int sink_count, int partner_count,
                                     int32_t* neighbors, int kcap, int32_t* degree,
                                     hipStream_t stream) {
-  BFLY_CHECK_ARG(num_blocks > 0 && num_blocks <= INT32_MAX, "num_blocks out of range: %lld",
-                 (long long)num_blocks);
-  BFLY_CHECK_ARG(local_window_blocks >= 0 && sink_count >= 0 && partner_count >= 0,
-                 "negative topology parameter");
-  BFLY_CHECK_ARG(partner_count <= kMaxPartners, "partner_count > %d", kMaxPartners);
   BFLY_CHECK_ARG(kcap >= 1 + local_window_blocks + partner_count + sink_count && kcap <= 64,
                  "kcap=%d must be in [1+lwb+partners+sinks, 64]", kcap);
   BFLY_CHECK_ARG(neighbors && degree, "null output pointer");
-  int32_t s, count, w;
-  int rc = bfly_stage_meta(num_blocks, layer_idx, partner_rule, &s, &count, &w);
-  if (rc) return rc;
-  PartnerBits pb{};
-  rc = bfly_partner_bits(s, count, w, partner_count, partner_rule, pb.bit);
+  bfly_topology_t t;
+  int rc = bfly_topology_init(num_blocks, layer_idx, partner_rule, local_window_blocks, sink_count, partner_count, &t);
   if (rc) return rc;
   const int threads = 256;
   const int grid = (int)((num_blocks + threads - 1) / threads);
-  hipLaunchKernelGGL(neighbors_kernel, dim3(grid), dim3(threads), 0, stream, num_blocks,
-                     partner_rule, (int)w, local_window_blocks, sink_count, partner_count, pb,
-                     neighbors, kcap, degree);
+  hipLaunchKernelGGL(neighbors_kernel, dim3(grid), dim3(threads), 0, stream, num_blocks, t, neighbors, kcap, degree);
   BFLY_CHECK_LAUNCH("bfly_block_neighbors");
   return BFLY_OK;
 }

@@ -14,11 +14,13 @@ count does.
 """
 from __future__ import annotations
 
+import ctypes as C
 from collections import OrderedDict
 from dataclasses import dataclass
 
 import torch
 
+from . import _native
 from .topology import ButterflyLayoutMetadata, block_neighbor_table_padded, butterfly_layout_metadata
 
 _TABLE_CACHE: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
@@ -26,14 +28,16 @@ _TABLE_CACHE_MAX = 256
 
 
 class _Table:
-    """A device neighbour table, its row degrees and (lazily) its exact width K."""
+    """A device neighbour table, its row degrees, (lazily) its exact width K, and
+    the host topology struct the decode kernel computes rows from."""
 
-    __slots__ = ("padded", "degree", "_exact")
+    __slots__ = ("padded", "degree", "_exact", "topology")
 
-    def __init__(self, padded: torch.Tensor, degree: torch.Tensor) -> None:
+    def __init__(self, padded: torch.Tensor, degree: torch.Tensor, topology) -> None:
         self.padded = padded
         self.degree = degree
         self._exact = None
+        self.topology = topology
 
     def exact(self) -> torch.Tensor:
         if self._exact is None:
@@ -93,11 +97,34 @@ class BlockButterflyLayout:
         return self.metadata.sink_blocks
 
 
+_LAYOUT_CACHE: "OrderedDict[tuple, BlockButterflyLayout]" = OrderedDict()
+_LAYOUT_CACHE_MAX = 8192
+
+
 def build_block_butterfly_layout(*, seq_len: int, block_size: int, num_key_value_heads: int,
                                  num_key_value_groups: int, layer_idx: int, local_window_blocks: int = 4,
                                  sink_count: int = 1, partner_count: int = 1, partner_rule: str = "xor",
                                  device=None) -> BlockButterflyLayout:
     """Build (or fetch) the staged Butterfly block layout of one layer."""
+    dev = device if device is not None else torch.cuda.current_device()
+    args = (seq_len, block_size, num_key_value_heads, num_key_value_groups, layer_idx, local_window_blocks,
+            sink_count, partner_count, partner_rule, str(dev))
+    hit = _LAYOUT_CACHE.get(args)
+    if hit is not None:
+        return hit
+    lay = _build_layout(seq_len=seq_len, block_size=block_size, num_key_value_heads=num_key_value_heads,
+                        num_key_value_groups=num_key_value_groups, layer_idx=layer_idx,
+                        local_window_blocks=local_window_blocks, sink_count=sink_count, partner_count=partner_count,
+                        partner_rule=partner_rule, device=device)
+    _LAYOUT_CACHE[args] = lay
+    while len(_LAYOUT_CACHE) > _LAYOUT_CACHE_MAX:
+        _LAYOUT_CACHE.popitem(last=False)
+    return lay
+
+
+def _build_layout(*, seq_len: int, block_size: int, num_key_value_heads: int, num_key_value_groups: int,
+                  layer_idx: int, local_window_blocks: int, sink_count: int, partner_count: int, partner_rule: str,
+                  device) -> BlockButterflyLayout:
     if int(seq_len) <= 0:
         raise ValueError("seq_len must be positive")
     if int(block_size) <= 0:
@@ -121,9 +148,12 @@ def build_block_butterfly_layout(*, seq_len: int, block_size: int, num_key_value
            int(partner_count), str(dev))
     table = _TABLE_CACHE.get(key)
     if table is None:
+        topo = _native.Topology()
+        _native.call("bfly_topology_init", n, int(layer_idx), _native.RULES[meta.partner_rule],
+                     int(local_window_blocks), int(sink_count), int(partner_count), C.byref(topo))
         table = _Table(*block_neighbor_table_padded(num_blocks=n, layer_idx=layer_idx, partner_rule=partner_rule,
                                                     local_window_blocks=local_window_blocks, sink_count=sink_count,
-                                                    partner_count=partner_count, device=dev))
+                                                    partner_count=partner_count, device=dev), topo)
         _TABLE_CACHE[key] = table
         while len(_TABLE_CACHE) > _TABLE_CACHE_MAX:
             _TABLE_CACHE.popitem(last=False)
@@ -138,3 +168,4 @@ def build_block_butterfly_layout(*, seq_len: int, block_size: int, num_key_value
 
 def clear_layout_cache() -> None:
     _TABLE_CACHE.clear()
+    _LAYOUT_CACHE.clear()

@@ -41,6 +41,23 @@ extern "C" {
 #define BFLY_RULE_FIXED_STRIDE 4
 #define BFLY_RULE_RANDOM 5
 
+#define BFLY_MAX_PARTNERS 16
+
+/*
+ * The staged topology of one layer at one block count: what a neighbour row
+ * is computed from (filled by bfly_topology_init).
+ */
+typedef struct bfly_topology {
+  int32_t rule;                 /* BFLY_RULE_* */
+  int32_t width;                /* ceil(log2 N), 1 if N <= 1 */
+  int32_t stage_idx;
+  int32_t stage_count;
+  int32_t local_window_blocks;
+  int32_t sink_count;
+  int32_t partner_count;        /* <= BFLY_MAX_PARTNERS */
+  int32_t partner_bits[BFLY_MAX_PARTNERS];
+} bfly_topology_t;
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* bfly_last_error(void);
 
@@ -62,6 +79,13 @@ int bfly_stage_meta(int64_t num_blocks, int64_t layer_idx, int partner_rule,
  */
 int bfly_partner_bits(int stage_idx, int stage_count, int width, int partner_count,
                       int partner_rule, int32_t* bits);
+
+/*
+ * Host: the topology of layer `layer_idx` at `num_blocks` blocks.
+ * Replaces butterfly_layout_metadata (bna/topology/butterfly.py:144-180).
+ */
+int bfly_topology_init(int64_t num_blocks, int64_t layer_idx, int partner_rule, int local_window_blocks,
+                       int sink_count, int partner_count, bfly_topology_t* out);
 
 /*
  * Device: the block-neighbour (partner) table of one layer.
@@ -175,13 +199,15 @@ int bfly_attend_cache(const void* q, int dtype, int64_t batch, int hq, int hkv, 
  * q/out: [B, Hq, 1, d].  ring_k/ring_v: [B, Hkv, C, d] ring (C = ring_capacity > 0),
  * or, when C == 0, the linear tail [B, Hkv, kv_len - tail_start, d].
  * pool_k/pool_v: [B, Hkv, pool_capacity, d].  head_dim 64 or 128 (256 for bf16);
- * window <= 64; kcap <= 16.
+ * window <= 64.  The routed row of block min(p/BS, N-1) is computed in the
+ * kernel from `topology` (host struct, from bfly_topology_init at num_blocks),
+ * so a step needs no device table and no dependent table read.
  */
 int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,
                 const void* k_new, const void* v_new, void* ring_k, void* ring_v,
                 int64_t ring_capacity, int64_t tail_start, int64_t kv_len, const void* pool_k,
                 const void* pool_v, int64_t pool_capacity, int64_t summary_count,
-                const int32_t* neighbors, int64_t num_blocks, int kcap, int block_size, int window,
+                const bfly_topology_t* topology, int64_t num_blocks, int block_size, int window,
                 float scale, void* out, hipStream_t stream);
 
 /*

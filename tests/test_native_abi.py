@@ -66,3 +66,18 @@ def test_errors_are_reported():
     assert rc == _native.ERR_INVALID
     rc = lib.bfly_block_neighbors(16, 0, 3, 1, 1, 1, None, 2, None, None)
     assert rc == _native.ERR_INVALID and b"kcap" in lib.bfly_last_error()
+
+
+@pytest.mark.parametrize("rule", list(tp.RULES))
+def test_topology_init_matches_oracle(rule):
+    lib = _native.lib()
+    for n in [1, 2, 33, 512, 1025, 2048]:
+        for layer in [0, 3, 11, 29]:
+            t = _native.Topology()
+            assert lib.bfly_topology_init(n, layer, _native.RULES[rule], 1, 1, 2, C.byref(t)) == 0
+            s, count = tp.stage_meta(n, layer, rule)
+            assert (t.stage_idx, t.stage_count, t.width) == (s, count, tp.width(n))
+            assert list(t.partner_bits[:2]) == tp.partner_bits(s, count, tp.width(n), 2, rule)
+            assert (t.rule, t.local_window_blocks, t.sink_count, t.partner_count) == (_native.RULES[rule], 1, 1, 2)
+    t = _native.Topology()
+    assert lib.bfly_topology_init(8, 0, 3, 1, 1, 17, C.byref(t)) == _native.ERR_INVALID

@@ -556,8 +556,10 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
               w1[i] = (__bf16)(o1[0][i] * inv1);
               w1[4 + i] = (__bf16)(o1[1][i] * inv1);
             }
-            *reinterpret_cast<bf16x8*>(orow0 + mt * 32 + lg * 8) = w0;
-            if (two) *reinterpret_cast<bf16x8*>(orow1 + mt * 32 + lg * 8) = w1;
+            // O is written once and never re-read here: non-temporal stores keep it
+            // from evicting the K/V pages and Q rows still in flight from L2.
+            __builtin_nontemporal_store(w0, reinterpret_cast<bf16x8*>(orow0 + mt * 32 + lg * 8));
+            if (two) __builtin_nontemporal_store(w1, reinterpret_cast<bf16x8*>(orow1 + mt * 32 + lg * 8));
           }
         }
       }

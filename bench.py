@@ -282,6 +282,89 @@ def bench_stream(torch, bf, seed=0, T=262144, chunk=384, layer=5):
             "final_tail": cache.tail_size, "final_summaries": cache.summary_count}
 
 
+def bench_decoder(torch, bf, seed=0, prompt_len=32768, new_tokens=32, agree_prompt=8192, agree_tokens=32,
+                  cpu_agreement=True):
+    """cfg5: random-init 24-layer decoder (4-bit affine weights, group 64), every attention
+    layer swapped to Butterfly; 32768-token prompt then 32 greedy tokens.
+
+    Greedy agreement with the CPU reference Torch path (the same decoder on the host
+    with the oracle attention) is checked on a bounded sample: the first
+    ``agree_prompt`` prompt tokens and ``agree_tokens`` greedy steps (the CPU cannot
+    run 24 layers over 32768 tokens within the bench's time budget).
+    """
+    import copy
+
+    from butterfly_amd.decoder import Decoder, DecoderConfig
+    from oracle.decoder_ref import swap_to_oracle
+
+    dev = torch.device("cuda:0")
+    cfg = DecoderConfig()
+    model = Decoder(cfg, seed=seed, device=dev)
+    cpu_model = copy.deepcopy(model).to("cpu") if cpu_agreement else None
+    bcfg = bf.QwenButterflyConfig()
+    bf.swap_qwen_attention_with_butterfly(model, cfg=bcfg)
+    prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=torch.Generator().manual_seed(seed + 1))
+    pd = prompt.to(dev)
+
+    def fresh(max_kv):
+        # the one-shot prompt is one update: the tail must hold it (capacity W + 2*max_chunk + 2*BS)
+        caches = [None] * cfg.num_layers
+        bf.install_compressed_kv_caches(model, caches, block_size=128, local_window_tokens=64, max_kv_size=max_kv,
+                                        max_chunk_size=max(512, max_kv))
+        return caches
+
+    model.greedy(pd[:, :512], 4, fresh(1024))           # warm-up: kernels, layouts
+    torch.cuda.synchronize()
+    caches = fresh(prompt_len + new_tokens)
+    t0 = time.perf_counter()
+    logits = model.forward(pd, caches, 0)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    toks = [logits.argmax(-1, keepdim=True)]
+    t0 = time.perf_counter()
+    pos = prompt_len
+    for _ in range(new_tokens - 1):
+        logits = model.forward(toks[-1], caches, pos)
+        toks.append(logits.argmax(-1, keepdim=True))
+        pos += 1
+    torch.cuda.synchronize()
+    decode_s = time.perf_counter() - t0
+    res = {"prompt": prompt_len, "new_tokens": new_tokens, "prefill_s": prefill_s, "prefill_tok_s": prompt_len / prefill_s,
+           "decode_ms_per_token": decode_s * 1e3 / (new_tokens - 1), "decode_tok_s": (new_tokens - 1) / decode_s,
+           "retained_kv_bytes": int(sum(c.nbytes for c in caches)),
+           "peak_hbm_bytes": int(torch.cuda.max_memory_allocated())}
+    if cpu_agreement:
+        swap_to_oracle(cpu_model, bcfg)
+        threads = os.cpu_count() or 1
+        torch.set_num_threads(threads)
+        gp = model.greedy(pd[:, :agree_prompt], agree_tokens, fresh(agree_prompt + agree_tokens)).cpu()
+        # teacher-forced: both paths fed the reference's greedy tokens, logits compared per step
+        gcache, ccache = fresh(agree_prompt + agree_tokens), [[] for _ in range(cfg.num_layers)]
+        t0 = time.perf_counter()
+        lc = cpu_model.forward(prompt[:, :agree_prompt], ccache, 0)
+        lg = model.forward(pd[:, :agree_prompt], gcache, 0).cpu()
+        cp, top1, diffs, pos = [], [], [], agree_prompt
+        for i in range(agree_tokens):
+            tok = lc.argmax(-1, keepdim=True)
+            cp.append(int(tok))
+            top1.append(int(lg.argmax()) == int(tok))
+            diffs.append(float((lg - lc).abs().max()))
+            if i + 1 < agree_tokens:
+                lc = cpu_model.forward(tok, ccache, pos)
+                lg = model.forward(tok.to(dev), gcache, pos).cpu()
+                pos += 1
+        cpu_s = time.perf_counter() - t0
+        same = [int(a) == b for a, b in zip(gp[0].tolist(), cp)]
+        prefix = next((i for i, m in enumerate(same) if not m), len(same))
+        res["agreement"] = {"prompt": agree_prompt, "tokens": agree_tokens,
+                            "free_running_match_rate": sum(same) / len(same), "identical_prefix": prefix,
+                            "teacher_forced_top1_agreement": sum(top1) / len(top1),
+                            "logit_max_abs_diff": max(diffs), "logit_std": float(lc.std()),
+                            "gpu": gp[0].tolist(), "cpu": cp, "cpu_s": cpu_s,
+                            "cpu_threads": torch.get_num_threads()}
+    return res
+
+
 def cpu_baseline(q, k, v, ref_lays, repeats=3, max_seconds=30.0):
     """The CPU oracle (PyTorch restatement of the reference Torch path) on the host cores."""
     import torch
@@ -316,6 +399,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-stream", action="store_true", help="skip the cfg4 streaming chunked-prefill leg")
+    ap.add_argument("--no-model", action="store_true", help="skip the cfg5 swapped-decoder leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -344,6 +428,7 @@ def main():
     q, k, v, ref_lays = pre.pop("inputs")
     decode = None if args.no_decode else bench_decode(torch, bf)
     stream = None if args.no_stream else bench_stream(torch, bf)
+    model = None if args.no_model else bench_decoder(torch, bf, cpu_agreement=not args.no_cpu_baseline)
     cpu = None if args.no_cpu_baseline else cpu_baseline(q, k, v, ref_lays)
     line = {
         "metric": "prefill tok/s @64k (1 layer, bf16, 9-stage sweep)",
@@ -373,7 +458,7 @@ def main():
                   "prefill_event_ms_in_step_avg": pre["prefill_event_ms_in_step_avg"],
                   "prefill_event_ms_in_step_min": pre["prefill_event_ms_in_step_min"],
                   "compress_alg_bytes": pre["compress_bytes"], "decode_cfg3": decode,
-                  "stream_cfg4": stream},
+                  "stream_cfg4": stream, "model_cfg5": model},
     }
     print(json.dumps(line), flush=True)
 

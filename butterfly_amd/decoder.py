@@ -1,0 +1,268 @@
+"""A random-init Qwen3-style decoder in PyTorch, the model the layer swap plugs into.
+
+The reference swaps attention inside third-party decoders (mlx_lm / HF
+transformers Qwen models, bna/integrations/qwen_mlx.py:1822-1846,
+qwen_torch.py:1652-1700); none can be downloaded here, so this module
+provides the same structure with random weights: ``model.layers[i].self_attn``
+with q/k/v/o projections, per-head q/k RMSNorm and RoPE (qwen_mlx.py:260-357),
+SwiGLU MLP, RMSNorm, tied embeddings.  Linear weights are stored 4-bit affine
+(group 64 along the input dimension, bf16 scale and bias per group:
+w = q * scale + bias, q in [0, 15]) and dequantized once to bf16; the
+non-attention GEMMs run through PyTorch-ROCm.
+
+``swap_qwen_attention_with_butterfly(model, cfg=...)`` replaces every
+attention by :class:`ButterflyAttention`, which keeps the projections, norms
+and RoPE and routes the attention core through the HIP kernels
+(:class:`butterfly_amd.ButterflyAttentionCore`).  The stock attention that it
+replaces is plain causal GQA softmax attention (PyTorch SDPA).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Callable, List, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .integrations import ButterflyAttentionCore, QwenButterflyConfig
+
+
+@dataclass
+class DecoderConfig:
+    vocab_size: int = 151936
+    hidden_size: int = 2048
+    num_layers: int = 24
+    num_heads: int = 16
+    num_kv_heads: int = 4
+    head_dim: int = 128
+    intermediate_size: int = 6144
+    rope_theta: float = 1e6
+    rms_eps: float = 1e-6
+    quant_group: int = 64
+    quant_bits: int = 4
+
+
+# ----------------------------------------------------------------------------- 4-bit affine weights
+def quantize_affine(w: torch.Tensor, group: int = 64, bits: int = 4):
+    """Per-group affine quantisation along the input dimension.
+
+    Returns ``(packed uint8 [out, in/2], scale bf16 [out, in/group], bias bf16 [out, in/group])``
+    with ``w ~= q * scale + bias``; two 4-bit codes per byte, low nibble first.
+    """
+    out_f, in_f = w.shape
+    if in_f % group != 0 or bits != 4:
+        raise ValueError("in_features must be a multiple of the group; only 4-bit codes are supported")
+    g = w.float().view(out_f, in_f // group, group)
+    lo = g.amin(-1, keepdim=True)
+    hi = g.amax(-1, keepdim=True)
+    scale = ((hi - lo) / 15.0).clamp_min(1e-8)
+    scale_b, bias_b = scale.to(torch.bfloat16), lo.to(torch.bfloat16)
+    q = torch.round((g - bias_b.float()) / scale_b.float()).clamp_(0, 15).to(torch.uint8).view(out_f, in_f)
+    packed = q[:, 0::2] | (q[:, 1::2] << 4)
+    return packed.contiguous(), scale_b.view(out_f, -1).contiguous(), bias_b.view(out_f, -1).contiguous()
+
+
+def dequantize_affine(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, group: int = 64) -> torch.Tensor:
+    out_f = packed.shape[0]
+    q = torch.stack([packed & 0xF, packed >> 4], dim=-1).view(out_f, -1).float()
+    w = q.view(out_f, -1, group) * scale.float().unsqueeze(-1) + bias.float().unsqueeze(-1)
+    return w.view(out_f, -1).to(torch.bfloat16)
+
+
+class QuantLinear(nn.Module):
+    """Linear layer with 4-bit affine weights, dequantized once to bf16 for the GEMM."""
+
+    def __init__(self, in_features: int, out_features: int, *, generator: torch.Generator, device, group: int = 64):
+        super().__init__()
+        w = torch.randn(out_features, in_features, generator=generator, device=device) / math.sqrt(in_features)
+        packed, scale, bias = quantize_affine(w, group)
+        self.register_buffer("packed", packed)
+        self.register_buffer("scale", scale)
+        self.register_buffer("bias", bias)
+        self.group = group
+        self.register_buffer("weight", dequantize_affine(packed, scale, bias, group))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return F.linear(x, self.weight)
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float, device):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim, device=device, dtype=torch.bfloat16), requires_grad=False)
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (y * self.weight.float()).to(x.dtype)
+
+
+def rope_cos_sin(positions: torch.Tensor, head_dim: int, theta: float):
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=positions.device, dtype=torch.float32) / head_dim))
+    ang = positions.float()[:, None] * inv[None, :]
+    emb = torch.cat([ang, ang], dim=-1)
+    return emb.cos(), emb.sin()
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x [B, H, T, d]; rotate-half RoPE in fp32."""
+    d = x.shape[-1]
+    xf = x.float()
+    rot = torch.cat([-xf[..., d // 2:], xf[..., : d // 2]], dim=-1)
+    return (xf * cos + rot * sin).to(x.dtype)
+
+
+# ----------------------------------------------------------------------------- attention
+class Attention(nn.Module):
+    """Stock attention: projections, q/k RMSNorm, RoPE and causal GQA softmax attention."""
+
+    def __init__(self, cfg: DecoderConfig, *, generator: torch.Generator, device):
+        super().__init__()
+        h, d = cfg.hidden_size, cfg.head_dim
+        self.cfg = cfg
+        self.q_proj = QuantLinear(h, cfg.num_heads * d, generator=generator, device=device, group=cfg.quant_group)
+        self.k_proj = QuantLinear(h, cfg.num_kv_heads * d, generator=generator, device=device, group=cfg.quant_group)
+        self.v_proj = QuantLinear(h, cfg.num_kv_heads * d, generator=generator, device=device, group=cfg.quant_group)
+        self.o_proj = QuantLinear(cfg.num_heads * d, h, generator=generator, device=device, group=cfg.quant_group)
+        self.q_norm = RMSNorm(d, cfg.rms_eps, device)
+        self.k_norm = RMSNorm(d, cfg.rms_eps, device)
+
+    def project(self, x: torch.Tensor, positions: torch.Tensor, rope=None):
+        """x [B, T, hidden] -> q [B, Hq, T, d], k/v [B, Hkv, T, d] (normed, RoPE applied).
+
+        ``rope`` is an optional precomputed ``(cos, sin)`` for ``positions``."""
+        b, t, _ = x.shape
+        c = self.cfg
+        q = self.q_proj(x).view(b, t, c.num_heads, c.head_dim).transpose(1, 2)
+        k = self.k_proj(x).view(b, t, c.num_kv_heads, c.head_dim).transpose(1, 2)
+        v = self.v_proj(x).view(b, t, c.num_kv_heads, c.head_dim).transpose(1, 2)
+        q, k = self.q_norm(q), self.k_norm(k)
+        cos, sin = rope if rope is not None else rope_cos_sin(positions, c.head_dim, c.rope_theta)
+        return apply_rope(q, cos, sin).contiguous(), apply_rope(k, cos, sin).contiguous(), v.contiguous()
+
+    def output(self, o: torch.Tensor) -> torch.Tensor:
+        b, _, t, _ = o.shape
+        return self.o_proj(o.transpose(1, 2).reshape(b, t, -1))
+
+    def forward(self, x: torch.Tensor, positions: torch.Tensor, cache=None, rope=None) -> torch.Tensor:
+        q, k, v = self.project(x, positions, rope)
+        if cache is not None:           # a list cache [k, v] of the full history
+            if cache:
+                k = torch.cat([cache[0], k], 2)
+                v = torch.cat([cache[1], v], 2)
+            cache[:] = [k, v]
+        groups = q.shape[1] // k.shape[1]
+        kk = k.repeat_interleave(groups, 1)
+        vv = v.repeat_interleave(groups, 1)
+        tq, tk = q.shape[2], kk.shape[2]
+        mask = torch.ones(tq, tk, dtype=torch.bool, device=q.device).tril(tk - tq)
+        o = F.scaled_dot_product_attention(q, kk, vv, attn_mask=mask)
+        return self.output(o)
+
+    def butterfly_module(self, cfg: QwenButterflyConfig, layer_idx: int) -> "ButterflyAttention":
+        return ButterflyAttention(self, cfg, layer_idx)
+
+
+class ButterflyAttention(nn.Module):
+    """The swapped attention: the base module's projections, norms and RoPE, with the
+    attention core run by the Butterfly kernels over a ``CompressedKVCache``.
+
+    Counterpart of ``QwenButterflyAttention`` (bna/integrations/qwen_mlx.py:1295-1792)
+    and ``QwenCUDAButterflyAttention.forward`` (qwen_torch.py:1221-1622).
+    """
+
+    def __init__(self, base: Attention, cfg: QwenButterflyConfig, layer_idx: int):
+        super().__init__()
+        self.base = base
+        self.layer_idx = int(layer_idx)
+        self.core = ButterflyAttentionCore(cfg, layer_idx)
+
+    @property
+    def last_profile(self):
+        return self.core.last_profile
+
+    def forward(self, x: torch.Tensor, positions: torch.Tensor, cache=None, rope=None) -> torch.Tensor:
+        q, k, v = self.base.project(x, positions, rope)
+        return self.base.output(self.core(q, k, v, cache))
+
+
+class MLP(nn.Module):
+    def __init__(self, cfg: DecoderConfig, *, generator: torch.Generator, device):
+        super().__init__()
+        h, f = cfg.hidden_size, cfg.intermediate_size
+        self.gate_proj = QuantLinear(h, f, generator=generator, device=device, group=cfg.quant_group)
+        self.up_proj = QuantLinear(h, f, generator=generator, device=device, group=cfg.quant_group)
+        self.down_proj = QuantLinear(f, h, generator=generator, device=device, group=cfg.quant_group)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, cfg: DecoderConfig, *, generator: torch.Generator, device):
+        super().__init__()
+        self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_eps, device)
+        self.self_attn = Attention(cfg, generator=generator, device=device)
+        self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_eps, device)
+        self.mlp = MLP(cfg, generator=generator, device=device)
+
+    def forward(self, x: torch.Tensor, positions: torch.Tensor, cache=None, rope=None) -> torch.Tensor:
+        x = x + self.self_attn(self.input_layernorm(x), positions, cache, rope)
+        return x + self.mlp(self.post_attention_layernorm(x))
+
+
+class Decoder(nn.Module):
+    """Random-init decoder; ``forward(tokens, caches, start)`` returns last-position logits."""
+
+    def __init__(self, cfg: DecoderConfig, *, seed: int = 0, device=None):
+        super().__init__()
+        device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        g = torch.Generator(device=device).manual_seed(seed)
+        self.cfg = cfg
+        self.embed_tokens = nn.Parameter(
+            (torch.randn(cfg.vocab_size, cfg.hidden_size, generator=g, device=device) * 0.02).to(torch.bfloat16),
+            requires_grad=False)
+        self.layers = nn.ModuleList(DecoderLayer(cfg, generator=g, device=device) for _ in range(cfg.num_layers))
+        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_eps, device)
+
+    def _rope(self, start: int, t: int, device):
+        """cos/sin rows for positions [start, start+t) from a table grown on demand."""
+        need = start + t
+        tab = getattr(self, "_rope_tab", None)
+        if tab is None or tab[0].shape[0] < need or tab[0].device != device:
+            n = max(need, 2 * (tab[0].shape[0] if tab is not None else 0), 4096)
+            tab = rope_cos_sin(torch.arange(n, device=device), self.cfg.head_dim, self.cfg.rope_theta)
+            self._rope_tab = tab
+        return tab[0][start:need], tab[1][start:need]
+
+    @torch.no_grad()
+    def forward(self, tokens: torch.Tensor, caches: List, start: int) -> torch.Tensor:
+        """tokens [B, T] at positions [start, start+T); returns logits [B, vocab] of the last position."""
+        x = F.embedding(tokens, self.embed_tokens)
+        positions = torch.arange(start, start + tokens.shape[1], device=tokens.device)
+        rope = self._rope(start, tokens.shape[1], tokens.device)
+        for layer, cache in zip(self.layers, caches):
+            x = layer(x, positions, cache, rope)
+        h = self.norm(x[:, -1])
+        return F.linear(h, self.embed_tokens).float()
+
+    @torch.no_grad()
+    def greedy(self, prompt: torch.Tensor, new_tokens: int, caches: List,
+               on_token: Optional[Callable[[int], None]] = None) -> torch.Tensor:
+        """Prefill ``prompt`` [B, T] in one call, then ``new_tokens`` greedy steps; returns [B, new_tokens]."""
+        logits = self.forward(prompt, caches, 0)
+        out = []
+        pos = prompt.shape[1]
+        for i in range(new_tokens):
+            nxt = logits.argmax(-1, keepdim=True)
+            out.append(nxt)
+            if on_token is not None:
+                on_token(i)
+            if i + 1 == new_tokens:
+                break
+            logits = self.forward(nxt, caches, pos)
+            pos += 1
+        return torch.cat(out, 1)

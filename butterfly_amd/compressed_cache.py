@@ -51,6 +51,8 @@ class CompressedKVCache:
         self._pool_k: Optional[torch.Tensor] = None
         self._pool_v: Optional[torch.Tensor] = None
         self._realign = False   # tail stored at slots [0, tail_size) by the state setter
+        self._dev: Optional[torch.Tensor] = None   # device counters (use_device_counters)
+        self._dev_dirty = False
         self.tail_capacity = 0
         self.summary_capacity = 0
         self.tail_size = 0
@@ -75,6 +77,84 @@ class CompressedKVCache:
                 self._ring_k = torch.roll(self._ring_k, shifts=shift, dims=2).contiguous()
                 self._ring_v = torch.roll(self._ring_v, shifts=shift, dims=2).contiguous()
         self._realign = False
+
+    # ------------------------------------------------------------------ device counters
+    def use_device_counters(self, enable: bool = True) -> None:
+        """Keep the counters in device memory so ``decode_step`` runs with fixed
+        arguments (no host bookkeeping, capturable in a HIP graph).
+
+        Every other method first reads the counters back (a device synchronisation)
+        and writes them again after changing them.
+        """
+        if not enable:
+            self.sync()
+            self._dev = None
+            return
+        if self._ring_k is None:
+            raise ValueError("allocate the cache with a first update before enabling device counters")
+        self._apply_realign()
+        self._dev = torch.zeros(6, dtype=torch.int64, device=self._ring_k.device)
+        self._dev_dirty = False
+        self._push()
+
+    @property
+    def device_counters(self) -> Optional[torch.Tensor]:
+        """The device int64[6] {offset, tail_size, summary_count, summary_offset, error, done}, or None."""
+        return self._dev
+
+    def sync(self) -> None:
+        """Read device counters back; raise the capacity error a device step recorded."""
+        if self._dev is None or not self._dev_dirty:
+            return
+        off, ts, sc, so, err, _ = (int(x) for x in self._dev.tolist())
+        self._dev_dirty = False
+        if err:
+            self._push()
+            raise RuntimeError(
+                f"CompressedKVCache capacity exceeded in a device decode step at offset={off} "
+                f"(tail_capacity={self.tail_capacity}, summary_capacity={self.summary_capacity}); "
+                f"raise max_chunk_size / max_kv_size at construction time.")
+        self.offset, self.tail_size, self.summary_count, self.summary_offset = off, ts, sc, so
+
+    def _push(self) -> None:
+        if self._dev is not None:
+            self._dev.copy_(torch.tensor([self.offset, self.tail_size, self.summary_count, self.summary_offset, 0, 0],
+                                         dtype=torch.int64))
+            self._dev_dirty = False
+
+    def decode_step(self, q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, *, layer_idx: int,
+                    local_window_tokens: int, partner_rule: str = "causal_shift", local_window_blocks: int = 1,
+                    sink_count: int = 1, partner_count: int = 1, scale: Optional[float] = None,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """One token per sequence with device counters: ``update_and_attend`` of one step,
+        with the layer's layout at the live kv_len computed on the device.
+
+        q [B, Hq, 1, d]; keys/values [B, Hkv, 1, d].  One kernel launch, fixed
+        arguments; the host counters are stale until ``sync()``.
+        """
+        from .attention import _scale
+
+        if self._dev is None:
+            raise ValueError("call use_device_counters() first")
+        b, hq, tq, d = q.shape
+        if tq != 1 or keys.shape[2] != 1 or keys.shape != values.shape:
+            raise ValueError("decode_step takes one new token per sequence")
+        if tuple(keys.shape[:2]) != tuple(self._ring_k.shape[:2]) or keys.shape[3] != self._ring_k.shape[3] or \
+                keys.dtype != self._ring_k.dtype or q.dtype != keys.dtype:
+            raise ValueError("q/keys do not match the cache's batch/head/dim/dtype")
+        rule = _native.RULES.get(str(partner_rule))
+        if rule is None:
+            raise ValueError(f"Unsupported Butterfly partner rule: {partner_rule!r}")
+        q, keys, values = _c(q), _c(keys), _c(values)
+        if out is None:
+            out = torch.empty_like(q)
+        _native.call("bfly_decode_step", q.data_ptr(), _dtype_code(q), b, hq, int(keys.shape[1]), d, keys.data_ptr(),
+                     values.data_ptr(), self._ring_k.data_ptr(), self._ring_v.data_ptr(), self.tail_capacity,
+                     self._pool_k.data_ptr(), self._pool_v.data_ptr(), self.summary_capacity, self._dev.data_ptr(),
+                     int(layer_idx), rule, int(local_window_blocks), int(sink_count), int(partner_count),
+                     self.block_size, int(local_window_tokens), _scale(scale, d), out.data_ptr(), _stream(q))
+        self._dev_dirty = True
+        return out
 
     # ------------------------------------------------------------------ update
     def _advance(self, keys: torch.Tensor, values: torch.Tensor):
@@ -139,6 +219,7 @@ class CompressedKVCache:
 
     def update(self, keys: torch.Tensor, values: torch.Tensor) -> None:
         """Append, summarise completed blocks, trim (compressed_cache.py:94-172)."""
+        self.sync()
         offset0 = self.offset
         step, first_pos, first_slot, n_new, overflow = self._advance(keys, values)
         b, h, d = int(keys.shape[0]), int(keys.shape[1]), int(keys.shape[3])
@@ -149,6 +230,7 @@ class CompressedKVCache:
                          self._ring_k.data_ptr(), self._ring_v.data_ptr(), self.tail_capacity, offset0, st)
         self._compress(first_pos, first_slot, n_new, overflow, st)
         self._trim(step)
+        self._push()
 
     def update_and_attend(self, q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, *, layout,
                           local_window_tokens: int, scale: Optional[float] = None) -> torch.Tensor:
@@ -163,6 +245,7 @@ class CompressedKVCache:
         from .attention import _attend, _require_cuda, _scale
 
         _require_cuda(q)
+        self.sync()
         step = int(keys.shape[2])
         d = int(q.shape[3])
         w = int(local_window_tokens)
@@ -180,6 +263,7 @@ class CompressedKVCache:
         st = _stream(q)
         self._compress(first_pos, first_slot, n_new, overflow, st)
         self._trim(1)
+        self._push()
         b, hq = int(q.shape[0]), int(q.shape[1])
         out = torch.empty_like(q)
         nb = layout.neighbors
@@ -199,6 +283,7 @@ class CompressedKVCache:
     def _tail_view(self, ring: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
         if ring is None:
             return None
+        self.sync()
         if self._realign:
             return ring[:, :, : self.tail_size]
         start = self.offset - self.tail_size
@@ -215,13 +300,16 @@ class CompressedKVCache:
 
     @property
     def k_summary(self) -> Optional[torch.Tensor]:
+        self.sync()
         return None if self._pool_k is None else self._pool_k[:, :, : self.summary_count]
 
     @property
     def v_summary(self) -> Optional[torch.Tensor]:
+        self.sync()
         return None if self._pool_v is None else self._pool_v[:, :, : self.summary_count]
 
     def get_compressed_state(self):
+        self.sync()
         if self._ring_k is None:
             raise ValueError("CompressedKVCache is empty")
         return (self.keys, self.values, self.k_summary, self.v_summary,
@@ -231,12 +319,14 @@ class CompressedKVCache:
         """Device buffers and counters for the attention kernel (no copies)."""
         if self._ring_k is None:
             raise ValueError("CompressedKVCache is empty")
+        self.sync()
         self._apply_realign()
         return RingState(self._ring_k, self._ring_v, self.tail_capacity, self.offset - self.tail_size,
                          self.offset, self._pool_k, self._pool_v, self.summary_count)
 
     # ------------------------------------------------------------------ mlx_lm cache protocol
     def size(self) -> int:
+        self.sync()
         return int(self.offset)
 
     def is_trimmable(self) -> bool:
@@ -260,6 +350,7 @@ class CompressedKVCache:
         return None
 
     def empty(self) -> bool:
+        self.sync()
         return self._ring_k is None or self.tail_size == 0
 
     @property
@@ -267,12 +358,14 @@ class CompressedKVCache:
         """Bytes of the valid slices only (compressed_cache.py:231-244)."""
         if self._ring_k is None:
             return 0
+        self.sync()
         b, h, _, d = self._ring_k.shape
         e = self._ring_k.element_size()
         return 2 * b * h * d * e * (self.tail_size + self.summary_count)
 
     @property
     def state(self) -> tuple[Any, Any, Any, Any]:
+        self.sync()
         return self.keys, self.values, self.k_summary, self.v_summary
 
     @state.setter
@@ -301,11 +394,15 @@ class CompressedKVCache:
             self._pool_k[:, :, :s] = k_summary
             self._pool_v[:, :, :s] = v_summary
             self.summary_count = int(s)
+        self._push()
 
     @property
     def meta_state(self) -> tuple[str, str, str, str]:
+        self.sync()
         return tuple(map(str, (self.block_size, self.local_window_tokens, self.offset, self.summary_offset)))
 
     @meta_state.setter
     def meta_state(self, v) -> None:
+        self.sync()
         self.block_size, self.local_window_tokens, self.offset, self.summary_offset = map(int, v)
+        self._push()

@@ -22,6 +22,16 @@
 // in LDS; wave w takes query heads w, w+4, ... of the GQA group.
 // Scores: lanes over keys; softmax reductions: wavefront shuffles; output:
 // lanes over head_dim.
+//
+// Step mode (bfly_decode_step): the cache counters (offset, tail_size,
+// summary_count, summary_offset) live in a device array.  Every workgroup
+// derives the post-update counters from them with the reference's rules
+// (append one token, summarise every block with end + W <= offset, trim whole
+// blocks while tail_size - BS >= W; compressed_cache.py:94-172), pools a newly
+// due block itself (same summation order as bfly_cache_compress), computes the
+// layer's topology at the live block count, and attends; the last workgroup to
+// finish writes the new counters.  A step then has fixed arguments and can be
+// captured in a HIP graph.
 #include "bfly_topology.h"
 
 namespace bfly {
@@ -29,6 +39,47 @@ namespace bfly {
 constexpr int kDecMaxWin = 64;
 constexpr int kDecMaxSum = 16;
 constexpr int kDecMaxKeys = kDecMaxWin + kDecMaxSum;
+constexpr int kDecMaxNew = 2;   // blocks pooled in one step (one per 128 steps in steady state)
+
+// Device cache counters of step mode: {offset, tail_size, summary_count,
+// summary_offset, error, done}.
+enum { kStOffset = 0, kStTail = 1, kStCount = 2, kStSumOff = 3, kStError = 4, kStDone = 5 };
+
+struct StepArgs {
+  int64_t* state;
+  int64_t layer_idx;
+  int rule, lwb, sinks, partners;
+};
+
+// bfly_topology_init on the device: width = ceil(log2 N) (1 if N <= 1),
+// stage = layer mod stage_count, partner bits per the rule
+// (bna/topology/butterfly.py:39-105).
+__device__ __forceinline__ bfly_topology_t topology_at(int64_t n, const StepArgs& s) {
+  bfly_topology_t t{};
+  const int w = n <= 1 ? 1 : 64 - __clzll((unsigned long long)(n - 1));
+  const int count = s.rule == BFLY_RULE_BENES ? (2 * w - 2 > 1 ? 2 * w - 2 : 1) : w;
+  int64_t st = s.layer_idx % count;
+  if (st < 0) st += count;
+  t.rule = s.rule;
+  t.width = w;
+  t.stage_idx = (int)st;
+  t.stage_count = count;
+  t.local_window_blocks = s.lwb;
+  t.sink_count = s.sinks;
+  t.partner_count = s.partners;
+#pragma unroll
+  for (int j = 0; j < BFLY_MAX_PARTNERS; ++j) {
+    if (j >= s.partners) continue;
+    if (s.rule == BFLY_RULE_BENES) {
+      const int base = count <= 1 ? 0 : (int)st % count;
+      const int phase = (base + j) % count;
+      t.partner_bits[j] = w <= 1 ? 0 : (phase < w ? phase : 2 * w - 2 - phase);
+    } else {
+      t.partner_bits[j] = (int)((st + j) % w);
+    }
+  }
+  return t;
+}
 
 struct DecodeArgs {
   const void* q;          // [B, Hq, 1, d]
@@ -62,12 +113,14 @@ __device__ __forceinline__ float dec_wave_sum(float v) {
   return v;
 }
 
-template <typename T, int D>
-__global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a) {
+template <typename T, int D, bool kStep>
+__global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs sa) {
   constexpr int VEC = 16 / (int)sizeof(T);     // elements per 16-byte piece
   constexpr int PIECES = D / VEC;
   constexpr int KP = D + VEC;                  // padded K row: rows 16 B apart in bank space
   constexpr int DPL = D / 64;                  // q/output elements per lane
+  constexpr int LPR = D / VEC;                 // compressor: lanes per row
+  constexpr int RS = 256 / LPR;                // compressor: row slots
   __shared__ __attribute__((aligned(16))) T Ks[kDecMaxKeys * KP];
   __shared__ __attribute__((aligned(16))) T Vs[kDecMaxKeys * D];
   __shared__ __attribute__((aligned(16))) float qs[4][D];
@@ -81,9 +134,46 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a) {
   const int64_t bi = bh / a.hkv;
   const int kvh = (int)(bh - bi * a.hkv);
   const int gsz = a.hq / a.hkv;
-  const int64_t p = a.kv_len - 1;
+
+  // ---- this step's counters: from the arguments, or (step mode) derived on the device
+  int64_t kv_len = a.kv_len, tail_start = a.tail_start, nsum = a.nsum, nblocks = a.nblocks;
+  bfly_topology_t topo = a.topo;
+  int64_t sc0 = 0, so0 = 0, ts1 = 0, sc1 = 0, so1 = 0;
+  int n_new = 0;
+  if constexpr (kStep) {
+    const int64_t off0 = sa.state[kStOffset], ts0 = sa.state[kStTail];
+    sc0 = sa.state[kStCount];
+    so0 = sa.state[kStSumOff];
+    const int64_t off1 = off0 + 1;
+    ts1 = ts0 + 1;
+    bool err = ts1 > a.ring;                              // tail capacity (compressed_cache.py:105-110)
+    sc1 = sc0;
+    so1 = so0;
+    while (!err && so1 + a.bs <= off1 - a.W) {            // summarise (:120-149)
+      const int64_t bstart = so1 - (off1 - ts1);
+      if (bstart < 0 || bstart + a.bs > ts1) break;
+      if (sc1 >= a.pool_rows || n_new == kDecMaxNew) {    // pool capacity (:128-132)
+        err = true;
+        break;
+      }
+      ++n_new;
+      ++sc1;
+      so1 += a.bs;
+    }
+    while (ts1 - a.bs >= a.W) ts1 -= a.bs;                // trim: target max(W, step + W - 1) = W
+    if (err) {
+      if (tid == 0) sa.state[kStError] = 1;               // the host raises at its next synchronisation
+      return;                                             // uniform: every workgroup sees the same counters
+    }
+    kv_len = off1;
+    tail_start = off1 - ts1;
+    nsum = sc1;
+    nblocks = (off1 + a.bs - 1) / a.bs;
+    topo = topology_at(nblocks, sa);
+  }
+  const int64_t p = kv_len - 1;
   int64_t lo = p - a.W + 1;
-  if (lo < a.tail_start) lo = a.tail_start;
+  if (lo < tail_start) lo = tail_start;
   if (lo < 0) lo = 0;
   const int nw = (int)(p - lo + 1);
 
@@ -91,9 +181,9 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a) {
   const T* vnew = a.v_new ? reinterpret_cast<const T*>(a.v_new) + bh * D : nullptr;
   T* rk = reinterpret_cast<T*>(a.ring_k) + bh * a.kv_rows * D;
   T* rv = reinterpret_cast<T*>(a.ring_v) + bh * a.kv_rows * D;
-  const T* pk = reinterpret_cast<const T*>(a.pool_k) + bh * a.pool_rows * D;
-  const T* pv = reinterpret_cast<const T*>(a.pool_v) + bh * a.pool_rows * D;
-  auto row_of = [&](int64_t pos) -> int64_t { return a.ring ? posmod(pos, a.ring) : pos - a.tail_start; };
+  T* pk = reinterpret_cast<T*>(const_cast<void*>(a.pool_k)) + bh * a.pool_rows * D;
+  T* pv = reinterpret_cast<T*>(const_cast<void*>(a.pool_v)) + bh * a.pool_rows * D;
+  auto row_of = [&](int64_t pos) -> int64_t { return a.ring ? posmod(pos, a.ring) : pos - tail_start; };
 
   // ---- this wave's first q row into registers (its load overlaps the staging below)
   float qv[DPL];
@@ -106,17 +196,53 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a) {
   // ---- routed summaries of block p/BS (token-level cut-off), from the topology
   if (tid == 0) {
     int64_t blk = p / a.bs;
-    if (blk > a.nblocks - 1) blk = a.nblocks - 1;
+    if (blk > nblocks - 1) blk = nblocks - 1;
     int64_t cut = p - a.W + 1;
     if (cut < 0) cut = 0;
-    const int len = neighbor_row(blk, a.nblocks, a.topo, rowbuf, kDecMaxSum);
+    const int len = neighbor_row(blk, nblocks, topo, rowbuf, kDecMaxSum);
     int c = 0;
     for (int j = 0; j < len; ++j) {
       const int64_t n = rowbuf[j];
-      if (n >= blk || n >= a.nsum || (n + 1) * a.bs > cut) continue;
+      if (n >= blk || n >= nsum || (n + 1) * a.bs > cut) continue;
       sel[c++] = (int)n;
     }
     nsel = c;
+  }
+  // ---- step mode: pool the newly due blocks of this (batch, kv head) (the
+  // summation order of block_mean_kernel: slot s sums tokens s, s+RS, ...; the
+  // slots are added in order; divided by BS; rounded once)
+  __shared__ __attribute__((aligned(16))) T newrow[kStep ? kDecMaxNew * 2 : 1][kStep ? D : 1];
+  if constexpr (kStep) {
+    __shared__ float part[RS * D];
+    for (int j = 0; j < n_new; ++j) {
+      const int64_t pos0 = so0 + (int64_t)j * a.bs;
+#pragma unroll
+      for (int kv = 0; kv < 2; ++kv) {
+        const T* src = kv ? rv : rk;
+        T* dst = (kv ? pv : pk) + (sc0 + j) * D;
+        const int c = tid % LPR, sl = tid / LPR;
+        float acc[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+        for (int tok = sl; tok < a.bs; tok += RS) {
+          const uint4 raw = *reinterpret_cast<const uint4*>(src + posmod(pos0 + tok, a.ring) * D + c * VEC);
+          const T* x = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[e] += to_f32(x[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) part[sl * D + c * VEC + e] = acc[e];
+        __syncthreads();
+        for (int col = tid; col < D; col += 256) {
+          float tot = 0.f;
+          for (int k = 0; k < RS; ++k) tot += part[k * D + col];
+          const T val = from_f32<T>(tot / (float)a.bs);
+          dst[col] = val;
+          newrow[2 * j + kv][col] = val;
+        }
+        __syncthreads();
+      }
+    }
   }
   // ---- window rows into LDS (the newest from k_new/v_new when given, also appended to the ring)
   for (int i = tid; i < nw * PIECES; i += 256) {
@@ -140,8 +266,16 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a) {
   for (int i = tid; i < ns * PIECES; i += 256) {
     const int r = i / PIECES, pc = i % PIECES;
     const int64_t n = sel[r];
-    *reinterpret_cast<uint4*>(Ks + (nw + r) * KP + pc * VEC) = *reinterpret_cast<const uint4*>(pk + n * D + pc * VEC);
-    *reinterpret_cast<uint4*>(Vs + (nw + r) * D + pc * VEC) = *reinterpret_cast<const uint4*>(pv + n * D + pc * VEC);
+    uint4 kx, vx;
+    if (kStep && n >= sc0) {           // pooled in this step: take the LDS copy
+      kx = *reinterpret_cast<const uint4*>(&newrow[2 * (n - sc0)][pc * VEC]);
+      vx = *reinterpret_cast<const uint4*>(&newrow[2 * (n - sc0) + 1][pc * VEC]);
+    } else {
+      kx = *reinterpret_cast<const uint4*>(pk + n * D + pc * VEC);
+      vx = *reinterpret_cast<const uint4*>(pv + n * D + pc * VEC);
+    }
+    *reinterpret_cast<uint4*>(Ks + (nw + r) * KP + pc * VEC) = kx;
+    *reinterpret_cast<uint4*>(Vs + (nw + r) * D + pc * VEC) = vx;
   }
   const int nk = nw + ns;
 
@@ -231,17 +365,37 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a) {
     }
     __syncthreads();   // qs/ps reused by the next head round
   }
+  if constexpr (kStep) {
+    // the last workgroup to finish publishes the counters (all others have read them)
+    if (tid == 0) {
+      __threadfence();
+      const unsigned long long prev =
+          atomicAdd(reinterpret_cast<unsigned long long*>(sa.state + kStDone), 1ull);
+      if (prev == (unsigned long long)gridDim.x - 1) {
+        sa.state[kStOffset] = kv_len;
+        sa.state[kStTail] = ts1;
+        sa.state[kStCount] = sc1;
+        sa.state[kStSumOff] = so1;
+        sa.state[kStDone] = 0;
+        __threadfence();
+      }
+    }
+  }
 }
 
-template <typename T>
-static void launch_decode(const DecodeArgs& a, int d, int64_t grid, hipStream_t stream) {
+template <typename T, bool kStep>
+static void launch_decode(const DecodeArgs& a, const StepArgs& sa, int d, int64_t grid, hipStream_t stream) {
   switch (d) {
-    case 64: hipLaunchKernelGGL((decode_kernel<T, 64>), dim3((unsigned)grid), dim3(256), 0, stream, a); break;
-    case 128: hipLaunchKernelGGL((decode_kernel<T, 128>), dim3((unsigned)grid), dim3(256), 0, stream, a); break;
+    case 64:
+      hipLaunchKernelGGL((decode_kernel<T, 64, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, a, sa);
+      break;
+    case 128:
+      hipLaunchKernelGGL((decode_kernel<T, 128, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, a, sa);
+      break;
     default:
       // fp32 rows of 256 do not fit the LDS staging; the host rejects that case.
       if constexpr (sizeof(T) == 2)
-        hipLaunchKernelGGL((decode_kernel<T, 256>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<T, 256, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, a, sa);
       break;
   }
 }
@@ -287,10 +441,51 @@ extern "C" int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int 
   a.tail_start = tail_start; a.kv_len = kv_len;
   a.pool_rows = pool_capacity; a.nsum = summary_count; a.nblocks = num_blocks;
   a.hq = hq; a.hkv = hkv; a.bs = block_size; a.W = window; a.scale = scale;
+  const StepArgs none{};
   if (dtype == BFLY_DTYPE_F32)
-    launch_decode<float>(a, head_dim, batch * hkv, stream);
+    launch_decode<float, false>(a, none, head_dim, batch * hkv, stream);
   else
-    launch_decode<__bf16>(a, head_dim, batch * hkv, stream);
+    launch_decode<__bf16, false>(a, none, head_dim, batch * hkv, stream);
   BFLY_CHECK_LAUNCH("bfly_decode");
+  return BFLY_OK;
+}
+
+extern "C" int bfly_decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,
+                                const void* k_new, const void* v_new, void* ring_k, void* ring_v,
+                                int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity,
+                                int64_t* state, int64_t layer_idx, int partner_rule, int local_window_blocks,
+                                int sink_count, int partner_count, int block_size, int window, float scale,
+                                void* out, hipStream_t stream) {
+  BFLY_CHECK_ARG(dtype == BFLY_DTYPE_F32 || dtype == BFLY_DTYPE_BF16, "unsupported dtype %d", dtype);
+  BFLY_CHECK_ARG(q && k_new && v_new && ring_k && ring_v && pool_k && pool_v && state && out, "null pointer");
+  BFLY_CHECK_ARG(aligned16(q) && aligned16(out) && aligned16(ring_k) && aligned16(ring_v) && aligned16(pool_k) &&
+                     aligned16(pool_v) && aligned16(k_new) && aligned16(v_new) &&
+                     (reinterpret_cast<uintptr_t>(state) & 7) == 0,
+                 "tensor pointers must be 16-byte aligned (state 8-byte)");
+  BFLY_CHECK_ARG(batch > 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "bad head counts hq=%d hkv=%d", hq, hkv);
+  BFLY_CHECK_ARG(batch * hkv <= INT32_MAX, "batch*hkv too large");
+  BFLY_CHECK_ARG(head_dim == 64 || head_dim == 128 || (head_dim == 256 && dtype == BFLY_DTYPE_BF16),
+                 "bfly_decode_step: head_dim=%d unsupported (64, 128; 256 for bf16)", head_dim);
+  BFLY_CHECK_ARG(window > 0 && window <= kDecMaxWin, "bfly_decode_step: window=%d must be in [1, %d]", window,
+                 kDecMaxWin);
+  BFLY_CHECK_ARG(partner_rule >= BFLY_RULE_XOR && partner_rule <= BFLY_RULE_RANDOM, "unsupported partner rule %d",
+                 partner_rule);
+  BFLY_CHECK_ARG(local_window_blocks >= 0 && sink_count >= 0 && partner_count >= 0 &&
+                     partner_count <= BFLY_MAX_PARTNERS &&
+                     1 + local_window_blocks + partner_count + sink_count <= kDecMaxSum,
+                 "bfly_decode_step: the routed row must fit %d slots", kDecMaxSum);
+  BFLY_CHECK_ARG(block_size > 0 && ring_capacity >= window + block_size && pool_capacity > 0,
+                 "bfly_decode_step: ring must hold W + BS rows and the pool at least one");
+  DecodeArgs a{};
+  a.q = q; a.out = out; a.k_new = k_new; a.v_new = v_new;
+  a.ring_k = ring_k; a.ring_v = ring_v; a.pool_k = pool_k; a.pool_v = pool_v;
+  a.ring = ring_capacity; a.kv_rows = ring_capacity; a.pool_rows = pool_capacity;
+  a.hq = hq; a.hkv = hkv; a.bs = block_size; a.W = window; a.scale = scale;
+  StepArgs sa{state, layer_idx, partner_rule, local_window_blocks, sink_count, partner_count};
+  if (dtype == BFLY_DTYPE_F32)
+    launch_decode<float, true>(a, sa, head_dim, batch * hkv, stream);
+  else
+    launch_decode<__bf16, true>(a, sa, head_dim, batch * hkv, stream);
+  BFLY_CHECK_LAUNCH("bfly_decode_step");
   return BFLY_OK;
 }

@@ -19,6 +19,7 @@ replaces is plain causal GQA softmax attention (PyTorch SDPA).
 from __future__ import annotations
 
 import math
+import time
 from dataclasses import dataclass
 from typing import Callable, List, Optional
 
@@ -248,6 +249,71 @@ class Decoder(nn.Module):
             x = layer(x, positions, cache, rope)
         h = self.norm(x[:, -1])
         return F.linear(h, self.embed_tokens).float()
+
+    @torch.no_grad()
+    def greedy_graph(self, prompt: torch.Tensor, new_tokens: int, caches: List) -> torch.Tensor:
+        """``greedy`` with the decode steps replayed from one captured HIP graph.
+
+        ``caches`` must be ``CompressedKVCache`` objects; the prompt is prefilled
+        eagerly, then the caches switch to device counters; the first decode step
+        runs eagerly and the next one (every layer, argmax, position advance) is
+        captured and replayed ``new_tokens - 2`` times with no host
+        synchronisation in between.
+        """
+        logits = self.forward(prompt, caches, 0)
+        return self.greedy_graph_from_logits(logits, prompt.shape[1], new_tokens, caches)
+
+    @torch.no_grad()
+    def greedy_graph_from_logits(self, logits: torch.Tensor, t: int, new_tokens: int, caches: List,
+                                 timed: bool = False) -> torch.Tensor:
+        """The decode part of ``greedy_graph`` after a prefill of ``t`` tokens that produced ``logits``.
+
+        With ``timed`` the replays are bracketed by device synchronisations and
+        their wall time is kept in ``self.last_graph_decode_s``."""
+        dev = logits.device
+        b = logits.shape[0]
+        for c in caches:
+            c.use_device_counters()
+        self._rope(0, t + new_tokens + 1, dev)               # table sized before capture
+        tok = logits.argmax(-1, keepdim=True)
+        out = torch.empty(b, new_tokens, dtype=torch.long, device=dev)
+        out[:, :1] = tok
+        pos = torch.full((1,), t, dtype=torch.long, device=dev)
+        step = torch.ones(1, dtype=torch.long, device=dev)
+        cos_tab, sin_tab = self._rope_tab
+
+        def one_step():
+            x = F.embedding(tok, self.embed_tokens)
+            rope = (cos_tab.index_select(0, pos), sin_tab.index_select(0, pos))
+            for layer, cache in zip(self.layers, caches):
+                x = layer(x, pos, cache, rope)
+            nxt = F.linear(self.norm(x[:, -1]), self.embed_tokens).argmax(-1, keepdim=True)
+            tok.copy_(nxt)
+            out.index_copy_(1, step, nxt)
+            pos.add_(1)
+            step.add_(1)
+
+        if new_tokens > 1:
+            one_step()           # eager first step: every op meets its decode shapes before capture
+        if new_tokens > 2:
+            graph = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream(device=dev)
+            side.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(graph, stream=side):
+                    one_step()   # recorded, not run
+            torch.cuda.current_stream(dev).wait_stream(side)
+            if timed:
+                torch.cuda.synchronize(dev)
+            t0 = time.perf_counter()
+            for _ in range(new_tokens - 2):
+                graph.replay()
+            if timed:
+                torch.cuda.synchronize(dev)
+            self.last_graph_decode_s = time.perf_counter() - t0
+        for c in caches:
+            c.use_device_counters(False)
+        return out
 
     @torch.no_grad()
     def greedy(self, prompt: torch.Tensor, new_tokens: int, caches: List,

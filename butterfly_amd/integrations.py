@@ -135,6 +135,20 @@ class ButterflyAttentionCore:
             raise ValueError(f"query heads {hq} must be a multiple of kv heads {hkv}")
         groups = hq // hkv
         w = int(self.cfg.compressed_local_window_tokens)
+        c = self.cfg
+        if (cache is not None and cache.device_counters is not None and q_len == 1
+                and c.butterfly_decode_backend != "dense"):
+            # device counters: one fixed-argument launch, no host bookkeeping (graph-capturable)
+            out = cache.decode_step(q, k, v, layer_idx=self.layer_idx, local_window_tokens=w,
+                                    partner_rule=c.block_partner_rule, local_window_blocks=c.block_local_window_blocks,
+                                    sink_count=c.block_sink_blocks, partner_count=c.block_partner_count,
+                                    scale=self.scale)
+            self.last_profile = AttentionProfile(total_ms=_now_ms() - t0, path="block_sparse_compressed_active",
+                                                 notes={"q_len": 1, "device_counters": True,
+                                                        "block_sparse_active_mode": True})
+            return out
+        if cache is not None:
+            cache.sync()
         k_len = q_len + (cache.offset if cache is not None else 0)
         notes: Dict[str, Any] = {"seq_len": int(k_len), "q_len": int(q_len)}
         if cache is not None and q_len < k_len and q_len <= 2 and self.cfg.butterfly_decode_backend == "dense":

@@ -211,6 +211,27 @@ int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int hkv, int he
                 float scale, void* out, hipStream_t stream);
 
 /*
+ * Device: one decode step with the cache counters held on the device, so a
+ * step has fixed arguments and can be captured in a HIP graph.  Same result as
+ * CompressedKVCache.update_and_fetch of one token (bna/mlx/compressed_cache.py:94-172:
+ * append, summarise every block with end + W <= offset, trim whole blocks while
+ * tail_size - BS >= W) followed by compressed_butterfly_attention_from_cache for
+ * that token (bna/mlx/attention.py:1816-1876), with the layout of the live
+ * kv_len (stage = layer_idx mod stage_count at ceil(kv_len / BS) blocks).
+ * state: device int64[6] = {offset, tail_size, summary_count, summary_offset,
+ * error, done}; `done` must be 0 between steps (the kernel leaves it so).  On a
+ * capacity overflow the step changes nothing and sets state[4] = 1 (the
+ * reference's RuntimeError; read it back to raise).
+ * Other arguments as bfly_decode; ring_k/ring_v is the ring (capacity > 0).
+ */
+int bfly_decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,
+                     const void* k_new, const void* v_new, void* ring_k, void* ring_v,
+                     int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity,
+                     int64_t* state, int64_t layer_idx, int partner_rule, int local_window_blocks,
+                     int sink_count, int partner_count, int block_size, int window, float scale,
+                     void* out, hipStream_t stream);
+
+/*
  * Device: append `step` new tokens at positions [offset, offset+step) of the
  * tail ring (slot = position mod ring_capacity).
  * Replaces the tail append of CompressedKVCache.update_and_fetch

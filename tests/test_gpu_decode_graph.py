@@ -1,0 +1,124 @@
+"""GPU: decode with device-side cache counters (bfly_decode_step) and HIP-graph replay.
+
+The device-counter step must reproduce the host-bookkeeping path bit for bit
+(same kernels' arithmetic, same pooled summaries), and every replay of a
+captured step must equal the eager step on a twin cache; replays are
+interleaved with eager work and synchronisations.
+"""
+from __future__ import annotations
+
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+import butterfly_amd as bf
+from butterfly_amd.decoder import Decoder, DecoderConfig
+from oracle import attention as oa, topology as tp
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(seed, shape, dtype):
+    rng = np.random.default_rng(seed)
+    return torch.from_numpy(rng.standard_normal(shape, dtype=np.float32)).to(dtype)
+
+
+def _layout(t, hkv, groups, layer):
+    return bf.build_block_butterfly_layout(seq_len=t, block_size=128, num_key_value_heads=hkv,
+                                           num_key_value_groups=groups, layer_idx=layer, local_window_blocks=1,
+                                           sink_count=1, partner_count=1, partner_rule="causal_shift")
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float32, 64), (torch.bfloat16, 256)])
+def test_device_counter_steps_equal_host_steps(dtype, d):
+    b, hq, hkv, layer, prompt, steps = 2, 8, 2, 5, 333, 300
+    total = prompt + steps
+    q = _rand(61, (b, hq, total, d), dtype).cuda()
+    k = _rand(62, (b, hkv, total, d), dtype).cuda()
+    v = _rand(63, (b, hkv, total, d), dtype).cuda()
+    host = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=total)
+    dev = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=total)
+    host.update(k[:, :, :prompt], v[:, :, :prompt])
+    dev.update(k[:, :, :prompt], v[:, :, :prompt])
+    dev.use_device_counters()
+    for p in range(prompt, total):
+        a = host.update_and_attend(q[:, :, p:p + 1], k[:, :, p:p + 1], v[:, :, p:p + 1],
+                                   layout=_layout(p + 1, hkv, hq // hkv, layer), local_window_tokens=64)
+        c = dev.decode_step(q[:, :, p:p + 1], k[:, :, p:p + 1], v[:, :, p:p + 1], layer_idx=layer,
+                            local_window_tokens=64)
+        assert torch.equal(a, c), p
+    dev.sync()
+    assert (dev.offset, dev.tail_size, dev.summary_count, dev.summary_offset) == \
+           (host.offset, host.tail_size, host.summary_count, host.summary_offset)
+    assert torch.equal(dev.k_summary, host.k_summary) and torch.equal(dev.values, host.values)
+
+
+def test_device_counter_overflow_raises_at_sync():
+    cache = bf.CompressedKVCache(block_size=4, local_window_tokens=4, max_kv_size=12)   # 7 summary slots
+    kv = torch.randn(1, 1, 8, 64, device="cuda").bfloat16()
+    cache.update(kv, kv)
+    cache.use_device_counters()
+    q = torch.randn(1, 1, 1, 64, device="cuda").bfloat16()
+    with pytest.raises(RuntimeError):
+        for _ in range(40):
+            cache.decode_step(q, kv[:, :, :1], kv[:, :, :1], layer_idx=0, local_window_tokens=4)
+            cache.sync()
+
+
+def test_graph_replays_match_eager_steps():
+    b, hq, hkv, d, layer, prompt, steps = 4, 8, 2, 128, 3, 1000, 150
+    total = prompt + steps
+    q = _rand(71, (b, hq, total, d), torch.bfloat16).cuda()
+    k = _rand(72, (b, hkv, total, d), torch.bfloat16).cuda()
+    v = _rand(73, (b, hkv, total, d), torch.bfloat16).cuda()
+    eager = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=total)
+    graphed = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=total)
+    for c in (eager, graphed):
+        c.update(k[:, :, :prompt], v[:, :, :prompt])
+        c.use_device_counters()
+    # static inputs of the captured step; the step index lives on the device
+    qs, ks, vs = q[:, :, prompt:prompt + 1].clone(), k[:, :, prompt:prompt + 1].clone(), v[:, :, prompt:prompt + 1].clone()
+    out = torch.empty_like(qs)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            graphed.decode_step(qs, ks, vs, layer_idx=layer, local_window_tokens=64, out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    for p in range(prompt, total):
+        qs.copy_(q[:, :, p:p + 1]); ks.copy_(k[:, :, p:p + 1]); vs.copy_(v[:, :, p:p + 1])
+        graph.replay()
+        want = eager.decode_step(q[:, :, p:p + 1], k[:, :, p:p + 1], v[:, :, p:p + 1], layer_idx=layer,
+                                 local_window_tokens=64)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), p
+    graphed.sync(); eager.sync()
+    assert graphed.offset == eager.offset == total and graphed.summary_count == eager.summary_count
+    # and the result is the reference's active row at the last position
+    lay = tp.build_layout(seq_len=total, block_size=128, num_key_value_heads=hkv, num_key_value_groups=hq // hkv,
+                          layer_idx=layer, local_window_blocks=1, sink_count=1, partner_count=1,
+                          partner_rule="causal_shift")
+    ref = oa.active(q[:, :, total - 1:].cpu(), k.cpu(), v.cpu(), layout=lay,
+                    query_positions=torch.tensor([total - 1]), W=64)
+    err = (out.float().cpu() - ref.float()).abs().max().item()
+    assert err <= 2e-2, err
+
+
+def test_decoder_graph_greedy_equals_eager_greedy():
+    cfg = DecoderConfig(vocab_size=2048, hidden_size=512, num_layers=3, num_heads=8, num_kv_heads=2, head_dim=64,
+                        intermediate_size=1024)
+    model = Decoder(cfg, seed=11)
+    bf.swap_qwen_attention_with_butterfly(model, cfg=bf.QwenButterflyConfig())
+    prompt = torch.randint(0, cfg.vocab_size, (2, 300), generator=torch.Generator().manual_seed(5)).cuda()
+
+    def caches():
+        c = [None] * cfg.num_layers
+        bf.install_compressed_kv_caches(model, c, block_size=128, local_window_tokens=64, max_kv_size=600)
+        return c
+
+    eager = model.greedy(prompt, 40, caches())
+    graphed = model.greedy_graph(prompt, 40, caches())
+    assert torch.equal(eager, graphed), (eager, graphed)

@@ -24,7 +24,8 @@ FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-shared",
-    # Keep hipcc from forming packed fp32 ops (build notes).
+    # Keep hipcc from forming packed fp32 ops: some of their forms have given
+    # silently wrong results on the target boxes.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
 ]

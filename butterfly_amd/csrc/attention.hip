@@ -197,6 +197,16 @@ struct MfmaCfg {
   static constexpr int LDS = K_BYTES + V_BYTES;
 };
 
+// Swap 16 bytes with lane ^ 8 (within each 16-lane row).
+__device__ __forceinline__ bf16x8 xchg8(bf16x8 v) {
+  uint4 u = __builtin_bit_cast(uint4, v);
+  u.x = __shfl_xor(u.x, 8);
+  u.y = __shfl_xor(u.y, 8);
+  u.z = __shfl_xor(u.z, 8);
+  u.w = __shfl_xor(u.w, 8);
+  return __builtin_bit_cast(bf16x8, u);
+}
+
 __device__ __forceinline__ int xcd_remap(int bid, int n) {
   // Consecutive workgroup ids are dispatched round-robin over the 8 XCDs;
   // give each XCD a contiguous run of segments so neighbouring segments (which
@@ -522,45 +532,64 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
         softmax(s0, p0, inv0);
         softmax(s1, p1, inv1);
         // O^T = V^T P^T.  Tile (mt, half), row r holds d = mt*32 + (r/4)*8 + half*4 + r%4,
-        // so the two halves give each lane 8 consecutive d: one 16-byte store per head.
-        __bf16* orow0 = ohead0 + ((int64_t)h0 * a.tq + (row_ok ? qp - m.qlo : 0)) * D;
-        __bf16* orow1 = orow0 + (int64_t)a.tq * D;
+        // so the two halves give each lane 8 consecutive d (16 bytes) of its position.
+        // Tiles mt and mt+1 together hold d [mt*32, mt*32+64) = one 128-byte line per
+        // position.  Lanes lq and lq^8 swap one 16-byte piece so that each store
+        // instruction writes 8 whole lines (positions 0..7, then 8..15): whole-line
+        // non-temporal stores stream to HBM at full rate, half lines do not.
+        const bool lo8 = lq < 8;
+        const int pA = pw + (lq & 7), pB = pA + 8;        // positions of the two store passes
+        const bool okA = pA >= m.qlo && pA < m.qhi, okB = pB >= m.qlo && pB < m.qhi;
+        __bf16* oA0 = ohead0 + ((int64_t)h0 * a.tq + (okA ? pA - m.qlo : 0)) * D;
+        __bf16* oB0 = ohead0 + ((int64_t)h0 * a.tq + (okB ? pB - m.qlo : 0)) * D;
+        const int64_t hstride = (int64_t)a.tq * D;
 #pragma unroll
-        for (int mt = 0; mt < C::DTILES / 2; ++mt) {
-          f32x4 o0[2], o1[2];
+        for (int mp = 0; mp < C::DTILES / 4; ++mp) {
+          bf16x8 w0[2], w1[2];
 #pragma unroll
-          for (int half = 0; half < 2; ++half) {
-            const __bf16* vrow = Vt + (mt * 32 + (lq >> 2) * 8 + half * 4 + (lq & 3)) * kVPitch;
-            bf16x8 vf[3];
+          for (int sub = 0; sub < 2; ++sub) {
+            const int mt = 2 * mp + sub;
+            f32x4 o0[2], o1[2];
 #pragma unroll
-            for (int pr = 0; pr < 3; ++pr) {
-              const bf16x4 va = *reinterpret_cast<const bf16x4*>(vrow + slot[2 * pr] + 4 * lg);
-              const bf16x4 vb = *reinterpret_cast<const bf16x4*>(vrow + slot[2 * pr + 1] + 4 * lg);
-              vf[pr] = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
+            for (int half = 0; half < 2; ++half) {
+              const __bf16* vrow = Vt + (mt * 32 + (lq >> 2) * 8 + half * 4 + (lq & 3)) * kVPitch;
+              bf16x8 vf[3];
+#pragma unroll
+              for (int pr = 0; pr < 3; ++pr) {
+                const bf16x4 va = *reinterpret_cast<const bf16x4*>(vrow + slot[2 * pr] + 4 * lg);
+                const bf16x4 vb = *reinterpret_cast<const bf16x4*>(vrow + slot[2 * pr + 1] + 4 * lg);
+                vf[pr] = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
+              }
+              f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int pr = 0; pr < 3; ++pr) {
+                a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[pr], p0[pr], a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[pr], p1[pr], a1, 0, 0, 0);
+              }
+              o0[half] = a0;
+              o1[half] = a1;
             }
-            f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int pr = 0; pr < 3; ++pr) {
-              a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[pr], p0[pr], a0, 0, 0, 0);
-              a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[pr], p1[pr], a1, 0, 0, 0);
-            }
-            o0[half] = a0;
-            o1[half] = a1;
-          }
-          if (row_ok) {
-            bf16x8 w0, w1;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              w0[i] = (__bf16)(o0[0][i] * inv0);
-              w0[4 + i] = (__bf16)(o0[1][i] * inv0);
-              w1[i] = (__bf16)(o1[0][i] * inv1);
-              w1[4 + i] = (__bf16)(o1[1][i] * inv1);
+              w0[sub][i] = (__bf16)(o0[0][i] * inv0);
+              w0[sub][4 + i] = (__bf16)(o0[1][i] * inv0);
+              w1[sub][i] = (__bf16)(o1[0][i] * inv1);
+              w1[sub][4 + i] = (__bf16)(o1[1][i] * inv1);
             }
-            // O is written once and never re-read here: non-temporal stores keep it
-            // from evicting the K/V pages and Q rows still in flight from L2.
-            __builtin_nontemporal_store(w0, reinterpret_cast<bf16x8*>(orow0 + mt * 32 + lg * 8));
-            if (two) __builtin_nontemporal_store(w1, reinterpret_cast<bf16x8*>(orow1 + mt * 32 + lg * 8));
           }
+          // lanes lq < 8 keep tile mt (sub 0) and receive the partner's tile mt;
+          // lanes lq >= 8 keep tile mt+1 (sub 1) and receive the partner's tile mt+1
+          const bf16x8 x0 = xchg8(lo8 ? w0[1] : w0[0]);
+          const bf16x8 x1 = xchg8(lo8 ? w1[1] : w1[0]);
+          const int dA = (2 * mp + (lo8 ? 0 : 1)) * 32 + lg * 8;   // d of this lane's piece
+          const bf16x8 a0 = lo8 ? w0[0] : x0, b0 = lo8 ? x0 : w0[1];
+          const bf16x8 a1 = lo8 ? w1[0] : x1, b1 = lo8 ? x1 : w1[1];
+          // O is written once and never re-read here: non-temporal stores keep it
+          // from evicting the K/V pages and Q rows still in flight from L2.
+          if (okA) __builtin_nontemporal_store(a0, reinterpret_cast<bf16x8*>(oA0 + dA));
+          if (okB) __builtin_nontemporal_store(b0, reinterpret_cast<bf16x8*>(oB0 + dA));
+          if (two && okA) __builtin_nontemporal_store(a1, reinterpret_cast<bf16x8*>(oA0 + hstride + dA));
+          if (two && okB) __builtin_nontemporal_store(b1, reinterpret_cast<bf16x8*>(oB0 + hstride + dA));
         }
       }
     }

@@ -25,6 +25,7 @@ from .integrations import (
     swap_qwen_attention_with_butterfly,
 )
 from .layout import BlockButterflyLayout, build_block_butterfly_layout, clear_layout_cache
+from .streams import compressed_stream_attention, online_softmax_merge, swa_stream_attention
 from .topology import (
     ButterflyLayoutMetadata,
     block_neighbor_table,
@@ -36,6 +37,9 @@ from .topology import (
 )
 
 __all__ = [
+    "compressed_stream_attention",
+    "online_softmax_merge",
+    "swa_stream_attention",
     "AttentionProfile",
     "ButterflyAttentionCore",
     "QwenButterflyConfig",

@@ -55,6 +55,10 @@ SIGNATURES = {
     "bfly_block_mean": (_int, [_vp, _vp, _vp, _vp, _int, _i64, _i64, _int, _int, _i64, _vp]),
     "bfly_prefill": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _i64, _int, _int, _i64, _int, _vp, _i64,
                             _int, _int, _int, _f32, _vp, _vp]),
+    "bfly_swa_stream": (_int, [_vp, _vp, _vp, _int, _i64, _int, _int, _i64, _int, _int, _f32, _vp, _vp, _vp, _vp]),
+    "bfly_compressed_stream": (_int, [_vp, _vp, _vp, _int, _i64, _int, _int, _i64, _int, _i64, _int, _vp, _i64,
+                                      _int, _f32, _vp, _vp, _vp, _vp]),
+    "bfly_softmax_merge": (_int, [_vp, _int, _vp, _vp, _vp, _int, _vp, _vp, _i64, _int, _vp, _vp]),
     "bfly_attend_cache": (_int, [_vp, _int, _i64, _int, _int, _i64, _int, _vp, _i64, _vp, _vp, _i64,
                                  _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _int, _int, _int, _f32,
                                  _vp, _vp]),

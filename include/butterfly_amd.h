@@ -161,6 +161,44 @@ int bfly_prefill(const void* q, const void* k, const void* v, const void* k_summ
                  int block_size, int window, float scale, void* out, hipStream_t stream);
 
 /*
+ * Device: sliding-window attention stream with online-softmax state.
+ * Replaces _swa_stream_attention (bna/mlx/attention.py:304-369): query t attends to
+ * raw keys [max(0, t - window + 1), t] (window < 1 counts as 1).
+ * q: [B, Hq, T, d]; k, v: [B, Hkv, T, d] (head h reads kv head h / (Hq/Hkv));
+ * o: [B, Hq, T, d] in dtype; l, m: fp32 [B, Hq, T] = sum of exp(score - m) and the row max.
+ * head_dim <= 512.
+ */
+int bfly_swa_stream(const void* q, const void* k, const void* v, int dtype, int64_t batch, int hq, int hkv,
+                    int64_t seq_len, int head_dim, int window, float scale, void* o, float* l, float* m,
+                    hipStream_t stream);
+
+/*
+ * Device: compressed-block attention stream with online-softmax state.
+ * Replaces _compressed_stream_attention (bna/mlx/attention.py:372-516).
+ * routed == NULL (HCA mode, :411-439): query t of block b = t / block_size attends to
+ * every summary n < b (n < num_summaries).  Otherwise (routed mode, :441-516) it attends
+ * to routed[h, b, j] for j < kcap where 0 <= routed[h, b, j] < b (and < num_summaries);
+ * routed: int32 [Hq, routed_blocks, kcap] with routed_blocks >= ceil(T / block_size).
+ * Rows with no key give o = 0, l = 0, m = -1e30.  Shapes as bfly_swa_stream with
+ * k_summary, v_summary: [B, Hkv, num_summaries, d].
+ */
+int bfly_compressed_stream(const void* q, const void* k_summary, const void* v_summary, int dtype,
+                           int64_t batch, int hq, int hkv, int64_t seq_len, int head_dim, int64_t num_summaries,
+                           int block_size, const int32_t* routed, int64_t routed_blocks, int kcap, float scale,
+                           void* o, float* l, float* m, hipStream_t stream);
+
+/*
+ * Device: merge of two (o, l, m) streams into one softmax over the union of their keys.
+ * Replaces _online_softmax_merge (bna/mlx/attention.py:519-548):
+ * out = (e^(ma-mt) la oa + e^(mb-mt) lb ob) / max(e^(ma-mt) la + e^(mb-mt) lb, 1e-9),
+ * mt = max(ma, mb).  oa, ob: [rows, d] in dtype_a / dtype_b; la, ma, lb, mb: fp32 [rows];
+ * out: fp32 [rows, d].
+ */
+int bfly_softmax_merge(const void* oa, int dtype_a, const float* la, const float* ma, const void* ob,
+                       int dtype_b, const float* lb, const float* mb, int64_t rows, int head_dim, float* out,
+                       hipStream_t stream);
+
+/*
  * Device: active rows over a two-pool cache (token-level cut-off).
  * Replaces compressed_butterfly_attention_from_cache (bna/mlx/attention.py:1816-1876,
  * streams :1669-1813 merged by :519-548) and, with a linear cache

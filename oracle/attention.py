@@ -228,12 +228,49 @@ def merge(a, b):
 
 
 def swa_stream(q, k, v, *, W: int, scale: float):
-    """Sliding-window stream over raw keys.  bna/mlx/attention.py:304-369 (fp32, unchunked)."""
+    """Sliding-window stream over raw keys.  bna/mlx/attention.py:304-369 (fp32, unchunked).
+
+    Returns (o in q's dtype, l fp32 [B,H,T,1], m fp32 [B,H,T,1]); q, k, v share heads.
+    """
     t = q.shape[2]
     pos = torch.arange(t)
     mask = (pos[None, :] <= pos[:, None]) & (pos[None, :] > pos[:, None] - max(1, W))
     s = (q.float() @ k.float().transpose(-1, -2)) * scale
-    return _stream(s, mask.view(1, 1, t, t), v.float())
+    o, l, m = _stream(s, mask.view(1, 1, t, t), v.float())
+    return o.to(q.dtype), l, m
+
+
+def compressed_stream(q, k_summary, v_summary, *, block_size: int, scale: float, routed_indices=None):
+    """Compressed-block stream.  bna/mlx/attention.py:372-516.
+
+    HCA mode (``routed_indices is None``, :411-439): the query at position t of
+    block b = t // block_size attends to every summary n < b.  Routed mode
+    (:441-516): it attends to ``routed_indices[h, b, j]`` for the entries with
+    0 <= idx < b (idx >= num_summaries is treated as invalid; the reference
+    gathers such an index out of range).  Rows with nothing to attend give
+    (0, 0, -1e30).  Returns (o in q's dtype, l fp32, m fp32); q and the summaries
+    share heads.
+    """
+    b, h, t, d = q.shape
+    nb = k_summary.shape[2]
+    qblk = torch.arange(t) // int(block_size)
+    if routed_indices is None:
+        s = (q.float() @ k_summary.float().transpose(-1, -2)) * scale          # [B, H, T, nb]
+        valid = torch.arange(nb)[None, :] < qblk[:, None]                     # [T, nb]
+        o, l, m = _stream(s, valid.view(1, 1, t, nb), v_summary.float())
+        return o.to(q.dtype), l, m
+    ri = torch.as_tensor(routed_indices).long()                               # [H, NQB, K]
+    if ri.shape[0] != h or ri.shape[1] < int(qblk[-1]) + 1 if t else False:
+        raise ValueError("routed_indices must be [H, >= num query blocks, K]")
+    idx = ri[:, qblk, :]                                                       # [H, T, K]
+    valid = (idx >= 0) & (idx < qblk.view(1, t, 1)) & (idx < nb)
+    safe = torch.where(valid, idx, torch.zeros_like(idx))
+    heads = torch.arange(h).view(h, 1, 1)
+    kg = k_summary.float()[:, heads, safe]                                     # [B, H, T, K, d]
+    vg = v_summary.float()[:, heads, safe]
+    s = (q.float().unsqueeze(-2) * kg).sum(-1) * scale                         # [B, H, T, K]
+    o, l, m = _stream(s, valid.unsqueeze(0), vg)
+    return o.to(q.dtype), l, m
 
 
 def from_cache(q, tail_k, tail_v, k_summary, v_summary, *, layout, query_positions, W: int,

@@ -11,6 +11,8 @@
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -145,3 +147,99 @@ def test_from_cache_equals_active_seed202():
     got = oa.from_cache(q, tk_, tv_, ks, vs, layout=lay, query_positions=qp, W=W, tail_start=ts, kv_len=off)
     assert torch.allclose(got, ref, atol=3e-4, rtol=3e-4)
     assert (got - ref).abs().max() < 1e-5
+
+
+# ---- compressed stream (bna/mlx/attention.py:372-516), pinned by the reference's
+# tests/mlx/test_compressed_butterfly_hca_stream.py brute forces, restated in numpy
+def _softmax_rows(q, kk, vv, scale):
+    s = (q @ kk.T) * scale
+    w = np.exp(s - s.max())
+    return (w / w.sum()) @ vv
+
+
+def test_hca_stream_dense_over_prior_blocks_seed13():
+    rng = np.random.default_rng(13)
+    B, H, T, dh, bs = 1, 2, 32, 8, 8
+    nb = T // bs
+    q = rng.standard_normal((B, H, T, dh)).astype(np.float32)
+    ks = rng.standard_normal((B, H, nb, dh)).astype(np.float32)
+    vs = rng.standard_normal((B, H, nb, dh)).astype(np.float32)
+    scale = 1.0 / math.sqrt(dh)
+    o, l, m = oa.compressed_stream(torch.from_numpy(q), torch.from_numpy(ks), torch.from_numpy(vs),
+                                   block_size=bs, scale=scale)
+    for t in range(T):
+        qb = t // bs
+        for h in range(H):
+            if qb == 0:
+                assert l[0, h, t, 0] == 0.0 and m[0, h, t, 0] < -1e20 and (o[0, h, t] == 0).all()
+                continue
+            want = _softmax_rows(q[0, h, t], ks[0, h, :qb], vs[0, h, :qb], scale)
+            assert np.allclose(o[0, h, t].numpy(), want, atol=3e-6)
+            s = (ks[0, h, :qb] @ q[0, h, t]) * scale
+            assert abs(m[0, h, t, 0].item() - s.max()) < 1e-5
+            assert abs(l[0, h, t, 0].item() - np.exp(s - s.max()).sum()) < 1e-5
+
+
+def test_routed_stream_via_indices_seed17():
+    rng = np.random.default_rng(17)
+    B, H, T, dh, bs = 1, 2, 16, 8, 4
+    nb = T // bs
+    q = rng.standard_normal((B, H, T, dh)).astype(np.float32)
+    ks = rng.standard_normal((B, H, nb, dh)).astype(np.float32)
+    vs = rng.standard_normal((B, H, nb, dh)).astype(np.float32)
+    routed = np.full((H, nb, 1), -1, dtype=np.int32)
+    for b in range(1, nb):
+        routed[:, b, 0] = b - 1
+    scale = 1.0 / math.sqrt(dh)
+    o, l, m = oa.compressed_stream(torch.from_numpy(q), torch.from_numpy(ks), torch.from_numpy(vs),
+                                   block_size=bs, scale=scale, routed_indices=torch.from_numpy(routed))
+    for t in range(T):
+        b = t // bs
+        for h in range(H):
+            if b == 0:
+                assert l[0, h, t, 0] == 0.0 and m[0, h, t, 0] < -1e20
+                continue
+            assert np.allclose(o[0, h, t].numpy(), vs[0, h, b - 1], atol=1e-6)   # one key: its value
+            assert abs(l[0, h, t, 0].item() - 1.0) < 1e-6
+
+
+def test_routed_stream_drops_non_causal_and_invalid_entries():
+    rng = np.random.default_rng(5)
+    B, H, T, dh, bs = 1, 1, 12, 4, 4
+    nb = 3
+    q = torch.from_numpy(rng.standard_normal((B, H, T, dh)).astype(np.float32))
+    ks = torch.from_numpy(rng.standard_normal((B, H, nb, dh)).astype(np.float32))
+    vs = torch.from_numpy(rng.standard_normal((B, H, nb, dh)).astype(np.float32))
+    routed = torch.tensor([[[0, 1, 2, -1], [1, 0, 0, 2], [2, 1, 0, 7]]], dtype=torch.int32)   # [H, 3, 4]
+    o, l, m = oa.compressed_stream(q, ks, vs, block_size=bs, scale=0.5, routed_indices=routed)
+    hca, lh, mh = oa.compressed_stream(q, ks, vs, block_size=bs, scale=0.5)
+    # block 1 routes {1 (self, dropped), 0, 0 (duplicate, both count), 2 (future, dropped)}
+    t = 5
+    s0 = (ks[0, 0, 0] @ q[0, 0, t]).item() * 0.5
+    assert abs(m[0, 0, t, 0].item() - s0) < 1e-6 and abs(l[0, 0, t, 0].item() - 2.0) < 1e-6
+    # block 2 routes {2 (self), 1, 0, 7 (out of range)}: the same keys as HCA
+    assert torch.allclose(o[0, 0, 8:], hca[0, 0, 8:], atol=1e-6)
+    assert torch.allclose(l[0, 0, 8:], lh[0, 0, 8:], atol=1e-6)
+
+
+def test_swa_and_routed_streams_merge_to_one_shot_prefill():
+    """The reference's one-shot entry is merge(swa, compressed(routed)) with the
+    block-level routing (bna/mlx/attention.py:1455-1467): check the oracle's two
+    halves against its SDPA one-shot restatement."""
+    rng = np.random.default_rng(29)
+    B, H, T, dh, bs, W = 1, 2, 70, 8, 8, 6
+    q, k, v = (torch.from_numpy(rng.standard_normal((B, H, T, dh), dtype=np.float32)) for _ in range(3))
+    lay = _layout(T, bs, 3, hkv=H)
+    n = lay.num_blocks
+    ks = oa.block_mean(k, seq_len=T, block_size=bs, num_blocks=n)
+    vs = oa.block_mean(v, seq_len=T, block_size=bs, num_blocks=n)
+    _, _, sidx, smask = oa.prefill_tables(lay, T=T, W=W)
+    # the Torch table pads with index 0 and a False mask; the stream takes -1 for "no entry"
+    routed = torch.where(smask.any(1), sidx, torch.full_like(sidx, -1)).to(torch.int32)
+    routed = routed.unsqueeze(0).expand(H, -1, -1)
+    scale = dh ** -0.5
+    a = oa.swa_stream(q, k, v, W=W, scale=scale)
+    c = oa.compressed_stream(q, ks, vs, block_size=bs, scale=scale, routed_indices=routed)
+    got = oa.merge(a, c)
+    want = oa.prefill(q, k, v, layout=lay, W=W)
+    assert torch.allclose(got, want, atol=2e-6)

@@ -15,13 +15,14 @@
 // new token from the k_new/v_new registers it staged, so nothing is read back
 // through memory in the same launch.
 //
-// Work unit = one workgroup per (batch, kv head), 256 threads.  Every thread
-// issues its q and window-row loads at once while thread 0 computes the routed
-// row of the query block from the topology (no table read); the <= 16 summary
-// rows follow after one barrier.  The <= 64 window rows and the summaries sit
-// in LDS; wave w takes query heads w, w+4, ... of the GQA group.
-// Scores: lanes over keys; softmax reductions: wavefront shuffles; output:
-// lanes over head_dim.
+// Work unit = one workgroup per (batch, kv head), 256 threads.  Each wave
+// computes the routed row of the query block from the topology (no table read:
+// one candidate per lane, first-occurrence dedup by shuffles, slots by ballot),
+// so every thread issues its q, window-row and summary-row loads in one batch;
+// one barrier later the <= 64 window rows and <= 16 summaries sit in LDS.
+// Wave w takes query heads w, w+4, ... of the GQA group with its own q and p
+// buffers (no further workgroup barriers).  Scores: lanes over keys; softmax
+// reductions: wavefront shuffles; output: lanes over head_dim.
 //
 // Step mode (bfly_decode_step): the cache counters (offset, tail_size,
 // summary_count, summary_offset) live in a device array.  Every workgroup
@@ -125,9 +126,7 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
   __shared__ __attribute__((aligned(16))) T Vs[kDecMaxKeys * D];
   __shared__ __attribute__((aligned(16))) float qs[4][D];
   __shared__ __attribute__((aligned(16))) float ps[4][kDecMaxKeys];
-  __shared__ int32_t rowbuf[kDecMaxSum];
-  __shared__ int sel[kDecMaxSum];
-  __shared__ int nsel;
+  __shared__ int selw[4][kDecMaxSum];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t bh = blockIdx.x;
@@ -183,7 +182,6 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
   T* rv = reinterpret_cast<T*>(a.ring_v) + bh * a.kv_rows * D;
   T* pk = reinterpret_cast<T*>(const_cast<void*>(a.pool_k)) + bh * a.pool_rows * D;
   T* pv = reinterpret_cast<T*>(const_cast<void*>(a.pool_v)) + bh * a.pool_rows * D;
-  auto row_of = [&](int64_t pos) -> int64_t { return a.ring ? posmod(pos, a.ring) : pos - tail_start; };
 
   // ---- this wave's first q row into registers (its load overlaps the staging below)
   float qv[DPL];
@@ -192,21 +190,6 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
     const T* qrow = reinterpret_cast<const T*>(a.q) + (bi * a.hq + (int64_t)kvh * gsz + hh) * D + lane * DPL;
 #pragma unroll
     for (int e = 0; e < DPL; ++e) qv[e] = to_f32(qrow[e]);
-  }
-  // ---- routed summaries of block p/BS (token-level cut-off), from the topology
-  if (tid == 0) {
-    int64_t blk = p / a.bs;
-    if (blk > nblocks - 1) blk = nblocks - 1;
-    int64_t cut = p - a.W + 1;
-    if (cut < 0) cut = 0;
-    const int len = neighbor_row(blk, nblocks, topo, rowbuf, kDecMaxSum);
-    int c = 0;
-    for (int j = 0; j < len; ++j) {
-      const int64_t n = rowbuf[j];
-      if (n >= blk || n >= nsum || (n + 1) * a.bs > cut) continue;
-      sel[c++] = (int)n;
-    }
-    nsel = c;
   }
   // ---- step mode: pool the newly due blocks of this (batch, kv head) (the
   // summation order of block_mean_kernel: slot s sums tokens s, s+RS, ...; the
@@ -244,131 +227,191 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
       }
     }
   }
-  // ---- window rows into LDS (the newest from k_new/v_new when given, also appended to the ring)
-  for (int i = tid; i < nw * PIECES; i += 256) {
-    const int r = i / PIECES, pc = i % PIECES;
-    const int64_t pos = lo + r;
-    uint4 kx, vx;
-    if (knew != nullptr && pos == p) {
-      kx = *reinterpret_cast<const uint4*>(knew + pc * VEC);
-      vx = *reinterpret_cast<const uint4*>(vnew + pc * VEC);
-      *reinterpret_cast<uint4*>(rk + row_of(pos) * D + pc * VEC) = kx;
-      *reinterpret_cast<uint4*>(rv + row_of(pos) * D + pc * VEC) = vx;
-    } else {
-      kx = *reinterpret_cast<const uint4*>(rk + row_of(pos) * D + pc * VEC);
-      vx = *reinterpret_cast<const uint4*>(rv + row_of(pos) * D + pc * VEC);
+  // ---- routed summaries of block p/BS (token-level cut-off), computed by every
+  // wave on its own: lane j < kc holds entry j of the ordered row
+  // [b, b-1..b-lwb, partners, sinks] (-1 where the reference pushes nothing),
+  // keeps it at its first occurrence, and the ballot of the entries that pass
+  // the filter gives their slots in row order.  No thread waits on another.
+  int ns;
+  {
+    int64_t blk = p / a.bs;
+    if (blk > nblocks - 1) blk = nblocks - 1;
+    int64_t cut = p - a.W + 1;
+    if (cut < 0) cut = 0;
+    const int lwb = topo.local_window_blocks, npart = topo.partner_count;
+    const int64_t nsink = topo.sink_count < nblocks ? topo.sink_count : nblocks;
+    const int kc = 1 + lwb + npart + topo.sink_count;
+    int64_t cand = -1;
+    if (lane < kc) {
+      if (lane == 0) {
+        cand = blk;
+      } else if (lane <= lwb) {
+        cand = blk - lane >= 0 ? blk - lane : -1;
+      } else if (lane <= lwb + npart) {
+        const int j = lane - 1 - lwb;
+        int bit = 0;
+#pragma unroll
+        for (int jj = 0; jj < BFLY_MAX_PARTNERS; ++jj)
+          if (jj == j) bit = topo.partner_bits[jj];
+        cand = partner_block(blk, bit, nblocks, topo.rule, topo.width);
+      } else {
+        const int64_t sk = lane - 1 - lwb - npart;
+        cand = sk < nsink ? sk : -1;
+      }
+      if (cand >= nblocks) cand = -1;
     }
-    *reinterpret_cast<uint4*>(Ks + r * KP + pc * VEC) = kx;
-    *reinterpret_cast<uint4*>(Vs + r * D + pc * VEC) = vx;
-  }
-  __syncthreads();
-  const int ns = nsel;
-  for (int i = tid; i < ns * PIECES; i += 256) {
-    const int r = i / PIECES, pc = i % PIECES;
-    const int64_t n = sel[r];
-    uint4 kx, vx;
-    if (kStep && n >= sc0) {           // pooled in this step: take the LDS copy
-      kx = *reinterpret_cast<const uint4*>(&newrow[2 * (n - sc0)][pc * VEC]);
-      vx = *reinterpret_cast<const uint4*>(&newrow[2 * (n - sc0) + 1][pc * VEC]);
-    } else {
-      kx = *reinterpret_cast<const uint4*>(pk + n * D + pc * VEC);
-      vx = *reinterpret_cast<const uint4*>(pv + n * D + pc * VEC);
+    const int c32 = (int)cand;
+    bool keep = cand >= 0;
+    for (int i = 0; i < kDecMaxSum; ++i) {
+      const int ci = __shfl(c32, i);
+      if (i < lane && ci == c32) keep = false;
     }
-    *reinterpret_cast<uint4*>(Ks + (nw + r) * KP + pc * VEC) = kx;
-    *reinterpret_cast<uint4*>(Vs + (nw + r) * D + pc * VEC) = vx;
+    const bool take = keep && cand < blk && cand < nsum && (cand + 1) * a.bs <= cut;
+    const unsigned long long mask = __ballot(take);
+    ns = __popcll(mask);
+    if (take) selw[wave][__popcll(mask & ((1ull << lane) - 1ull))] = c32;
+    __builtin_amdgcn_wave_barrier();
   }
   const int nk = nw + ns;
 
-  for (int hb = 0; hb < gsz; hb += 4) {
-    const int hh = hb + wave;
-    const bool active = hh < gsz;
-    const int64_t h = (int64_t)kvh * gsz + hh;
-    if (active) {
-      if (hb > 0) {
-        const T* qrow = reinterpret_cast<const T*>(a.q) + (bi * a.hq + h) * D + lane * DPL;
+  // ---- window rows (the newest from k_new/v_new when given, also appended to the
+  // ring) and routed summaries: all loads of a thread issued together, then LDS
+  constexpr int kStage = (kDecMaxKeys * PIECES + 255) / 256;
+  {
+    uint4 kx[kStage], vx[kStage];
+    const int64_t slot_lo = a.ring ? posmod(lo, a.ring) : lo - tail_start;
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) qv[e] = to_f32(qrow[e]);
-      }
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) qs[wave][lane * DPL + e] = qv[e] * a.scale;
-    }
-    __syncthreads();   // window/summary rows and q visible
-    if (active) {
-      // scores: lane owns keys lane and lane + 64; 4 partial sums per dot product
-      float s[2];
-      float mloc = -INFINITY;
-#pragma unroll
-      for (int rnd = 0; rnd < 2; ++rnd) {
-        const int key = lane + 64 * rnd;
-        float acc = 0.f;
-        if (key < nk) {
-          const T* krow = Ks + key * KP;
-          float part[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int pc = 0; pc < PIECES; ++pc) {
-            const uint4 raw = *reinterpret_cast<const uint4*>(krow + pc * VEC);
-            const T* kv = reinterpret_cast<const T*>(&raw);
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) part[e & 3] = fmaf(qs[wave][pc * VEC + e], to_f32(kv[e]), part[e & 3]);
+    for (int it = 0; it < kStage; ++it) {
+      const int i = tid + it * 256;
+      kx[it] = vx[it] = make_uint4(0, 0, 0, 0);
+      if (i < nk * PIECES) {
+        const int r = i / PIECES, pc = i % PIECES;
+        if (r < nw) {
+          const int64_t pos = lo + r;
+          int64_t row = slot_lo + r;
+          if (a.ring && row >= a.ring) row -= a.ring;
+          if (knew != nullptr && pos == p) {
+            kx[it] = *reinterpret_cast<const uint4*>(knew + pc * VEC);
+            vx[it] = *reinterpret_cast<const uint4*>(vnew + pc * VEC);
+            *reinterpret_cast<uint4*>(rk + row * D + pc * VEC) = kx[it];
+            *reinterpret_cast<uint4*>(rv + row * D + pc * VEC) = vx[it];
+          } else {
+            kx[it] = *reinterpret_cast<const uint4*>(rk + row * D + pc * VEC);
+            vx[it] = *reinterpret_cast<const uint4*>(rv + row * D + pc * VEC);
           }
-          acc = (part[0] + part[1]) + (part[2] + part[3]);
-          mloc = fmaxf(mloc, acc);
-        }
-        s[rnd] = acc;
-      }
-      const float m = dec_wave_max(mloc);
-      float lloc = 0.f;
-#pragma unroll
-      for (int rnd = 0; rnd < 2; ++rnd) {
-        const int key = lane + 64 * rnd;
-        const float e = key < nk ? __expf(s[rnd] - m) : 0.f;
-        s[rnd] = e;
-        lloc += e;
-      }
-      const float inv = 1.f / fmaxf(dec_wave_sum(lloc), 1e-9f);
-#pragma unroll
-      for (int rnd = 0; rnd < 2; ++rnd) {
-        const int key = lane + 64 * rnd;
-        if (key < kDecMaxKeys) ps[wave][key] = key < nk ? s[rnd] * inv : 0.f;
-      }
-    }
-    __syncthreads();   // ps visible to the wave's lanes
-    if (active) {
-      // output: lane owns d = lane*DPL + [0, DPL); keys in groups of 4 with
-      // independent accumulators (rows past nk carry p = 0 and are skipped)
-      float acc[DPL][4];
-#pragma unroll
-      for (int e = 0; e < DPL; ++e)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[e][j] = 0.f;
-      const int nk4 = nk & ~3;
-      for (int key = 0; key < nk4; key += 4) {
-        const float4 p4 = *reinterpret_cast<const float4*>(&ps[wave][key]);
-        const float pj[4] = {p4.x, p4.y, p4.z, p4.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const T* vrow = Vs + (key + j) * D + lane * DPL;
-#pragma unroll
-          for (int e = 0; e < DPL; ++e) acc[e][j] = fmaf(pj[j], to_f32(vrow[e]), acc[e][j]);
+        } else {
+          const int64_t n = selw[wave][r - nw];
+          if (kStep && n >= sc0) {           // pooled in this step: take the LDS copy
+            kx[it] = *reinterpret_cast<const uint4*>(&newrow[2 * (n - sc0)][pc * VEC]);
+            vx[it] = *reinterpret_cast<const uint4*>(&newrow[2 * (n - sc0) + 1][pc * VEC]);
+          } else {
+            kx[it] = *reinterpret_cast<const uint4*>(pk + n * D + pc * VEC);
+            vx[it] = *reinterpret_cast<const uint4*>(pv + n * D + pc * VEC);
+          }
         }
       }
-      for (int key = nk4; key < nk; ++key) {
-        const float pk_ = ps[wave][key];
-        const T* vrow = Vs + key * D + lane * DPL;
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[e][0] = fmaf(pk_, to_f32(vrow[e]), acc[e][0]);
-      }
-      T* orow = reinterpret_cast<T*>(a.out) + (bi * a.hq + h) * D;
-#pragma unroll
-      for (int e = 0; e < DPL; ++e)
-        orow[lane * DPL + e] = from_f32<T>((acc[e][0] + acc[e][1]) + (acc[e][2] + acc[e][3]));
     }
-    __syncthreads();   // qs/ps reused by the next head round
+#pragma unroll
+    for (int it = 0; it < kStage; ++it) {
+      const int i = tid + it * 256;
+      if (i < nk * PIECES) {
+        const int r = i / PIECES, pc = i % PIECES;
+        *reinterpret_cast<uint4*>(Ks + r * KP + pc * VEC) = kx[it];
+        *reinterpret_cast<uint4*>(Vs + r * D + pc * VEC) = vx[it];
+      }
+    }
+  }
+  // this wave's first head: q (already in registers) into its LDS slot
+  if (wave < gsz) {
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) qs[wave][lane * DPL + e] = qv[e] * a.scale;
+  }
+  __syncthreads();   // window and summary rows visible to every wave
+
+  // ---- heads: wave w takes heads w, w+4, ...; qs[wave] and ps[wave] are the
+  // wave's own, so the rounds need no workgroup barrier
+  for (int hh = wave; hh < gsz; hh += 4) {
+    const int64_t h = (int64_t)kvh * gsz + hh;
+    if (hh != wave) {
+      const T* qrow = reinterpret_cast<const T*>(a.q) + (bi * a.hq + h) * D + lane * DPL;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) qs[wave][lane * DPL + e] = to_f32(qrow[e]) * a.scale;
+    }
+    __builtin_amdgcn_wave_barrier();
+    // scores: lane owns keys lane and lane + 64; 4 partial sums per dot product
+    float s[2];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int rnd = 0; rnd < 2; ++rnd) {
+      const int key = lane + 64 * rnd;
+      float acc = 0.f;
+      if (key < nk) {
+        const T* krow = Ks + key * KP;
+        float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int pc = 0; pc < PIECES; ++pc) {
+          const uint4 raw = *reinterpret_cast<const uint4*>(krow + pc * VEC);
+          const T* kv = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) part[e & 3] = fmaf(qs[wave][pc * VEC + e], to_f32(kv[e]), part[e & 3]);
+        }
+        acc = (part[0] + part[1]) + (part[2] + part[3]);
+        mloc = fmaxf(mloc, acc);
+      }
+      s[rnd] = acc;
+    }
+    const float m = dec_wave_max(mloc);
+    float lloc = 0.f;
+#pragma unroll
+    for (int rnd = 0; rnd < 2; ++rnd) {
+      const int key = lane + 64 * rnd;
+      const float e = key < nk ? __expf(s[rnd] - m) : 0.f;
+      s[rnd] = e;
+      lloc += e;
+    }
+    const float inv = 1.f / fmaxf(dec_wave_sum(lloc), 1e-9f);
+#pragma unroll
+    for (int rnd = 0; rnd < 2; ++rnd) {
+      const int key = lane + 64 * rnd;
+      if (key < kDecMaxKeys) ps[wave][key] = key < nk ? s[rnd] * inv : 0.f;
+    }
+    __builtin_amdgcn_wave_barrier();
+    // output: lane owns d = lane*DPL + [0, DPL); keys in groups of 4 with
+    // independent accumulators (rows past nk carry p = 0 and are skipped)
+    float acc[DPL][4];
+#pragma unroll
+    for (int e = 0; e < DPL; ++e)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[e][j] = 0.f;
+    const int nk4 = nk & ~3;
+    for (int key = 0; key < nk4; key += 4) {
+      const float4 p4 = *reinterpret_cast<const float4*>(&ps[wave][key]);
+      const float pj[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const T* vrow = Vs + (key + j) * D + lane * DPL;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[e][j] = fmaf(pj[j], to_f32(vrow[e]), acc[e][j]);
+      }
+    }
+    for (int key = nk4; key < nk; ++key) {
+      const float pk_ = ps[wave][key];
+      const T* vrow = Vs + key * D + lane * DPL;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) acc[e][0] = fmaf(pk_, to_f32(vrow[e]), acc[e][0]);
+    }
+    T* orow = reinterpret_cast<T*>(a.out) + (bi * a.hq + h) * D;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e)
+      orow[lane * DPL + e] = from_f32<T>((acc[e][0] + acc[e][1]) + (acc[e][2] + acc[e][3]));
+    __builtin_amdgcn_wave_barrier();   // qs/ps reused by this wave's next head
   }
   if constexpr (kStep) {
-    // the last workgroup to finish publishes the counters (all others have read them)
+    // The last workgroup to finish publishes the counters.  Every workgroup read
+    // the old counters at its start and used them before its increment, and no
+    // workgroup reads another's pool, ring or output within the step, so no
+    // fence is needed: the next launch sees everything at the kernel boundary.
     if (tid == 0) {
-      __threadfence();
       const unsigned long long prev =
           atomicAdd(reinterpret_cast<unsigned long long*>(sa.state + kStDone), 1ull);
       if (prev == (unsigned long long)gridDim.x - 1) {
@@ -377,7 +420,6 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
         sa.state[kStCount] = sc1;
         sa.state[kStSumOff] = so1;
         sa.state[kStDone] = 0;
-        __threadfence();
       }
     }
   }

@@ -52,6 +52,12 @@ struct StepArgs {
   int rule, lwb, sinks, partners;
 };
 
+// layer mod count (non-negative), one 32-bit division for any real layer index
+__device__ __forceinline__ int64_t dec_mod_layer(int64_t x, int count) {
+  if (x >= 0 && x <= INT32_MAX) return (int64_t)((uint32_t)x % (uint32_t)count);
+  return posmod(x, count);
+}
+
 // bfly_topology_init on the device: width = ceil(log2 N) (1 if N <= 1),
 // stage = layer mod stage_count, partner bits per the rule
 // (bna/topology/butterfly.py:39-105).
@@ -59,8 +65,7 @@ __device__ __forceinline__ bfly_topology_t topology_at(int64_t n, const StepArgs
   bfly_topology_t t{};
   const int w = n <= 1 ? 1 : 64 - __clzll((unsigned long long)(n - 1));
   const int count = s.rule == BFLY_RULE_BENES ? (2 * w - 2 > 1 ? 2 * w - 2 : 1) : w;
-  int64_t st = s.layer_idx % count;
-  if (st < 0) st += count;
+  int64_t st = dec_mod_layer(s.layer_idx, count);
   t.rule = s.rule;
   t.width = w;
   t.stage_idx = (int)st;
@@ -114,6 +119,155 @@ __device__ __forceinline__ float dec_wave_sum(float v) {
   return v;
 }
 
+
+// Non-negative 64-bit quotient / remainder by a positive int: one 32-bit
+// division when the dividend fits (always, for any realistic cache), else the
+// 64-bit routine.  The operands are workgroup-uniform.
+__device__ __forceinline__ int64_t dec_div(int64_t x, int64_t d) {
+  if (x >= 0 && x <= INT32_MAX && d <= INT32_MAX) return (int64_t)((uint32_t)x / (uint32_t)d);
+  return x / d;
+}
+__device__ __forceinline__ int64_t dec_mod(int64_t x, int64_t d) {
+  if (x >= 0 && x <= INT32_MAX && d <= INT32_MAX) return (int64_t)((uint32_t)x % (uint32_t)d);
+  return posmod(x, d);
+}
+
+// This step's cache counters: from the arguments, or (step mode) derived on the
+// device from the counter array with the reference's update rules.
+struct DecState {
+  int64_t kv_len, tail_start, nsum, nblocks;
+  int64_t sc0, so0, ts1, sc1, so1;   // step mode: counts before/after, tail size after
+  int n_new;                         // blocks that become due in this step
+  bool err;
+  bfly_topology_t topo;
+};
+
+template <bool kStep>
+__device__ __forceinline__ DecState dec_state(const DecodeArgs& a, const StepArgs& sa) {
+  DecState s{};
+  s.kv_len = a.kv_len;
+  s.tail_start = a.tail_start;
+  s.nsum = a.nsum;
+  s.nblocks = a.nblocks;
+  s.topo = a.topo;
+  if constexpr (kStep) {
+    const int64_t off0 = sa.state[kStOffset], ts0 = sa.state[kStTail];
+    s.sc0 = sa.state[kStCount];
+    s.so0 = sa.state[kStSumOff];
+    const int64_t off1 = off0 + 1;
+    s.ts1 = ts0 + 1;
+    bool err = s.ts1 > a.ring;                              // tail capacity (compressed_cache.py:105-110)
+    s.sc1 = s.sc0;
+    s.so1 = s.so0;
+    while (!err && s.so1 + a.bs <= off1 - a.W) {            // summarise (:120-149)
+      const int64_t bstart = s.so1 - (off1 - s.ts1);
+      if (bstart < 0 || bstart + a.bs > s.ts1) break;
+      if (s.sc1 >= a.pool_rows || s.n_new == kDecMaxNew) {  // pool capacity (:128-132)
+        err = true;
+        break;
+      }
+      ++s.n_new;
+      ++s.sc1;
+      s.so1 += a.bs;
+    }
+    while (s.ts1 - a.bs >= a.W) s.ts1 -= a.bs;              // trim: target max(W, step + W - 1) = W
+    s.err = err;
+    s.kv_len = off1;
+    s.tail_start = off1 - s.ts1;
+    s.nsum = s.sc1;
+    s.nblocks = dec_div(off1 + a.bs - 1, a.bs);
+    s.topo = topology_at(s.nblocks, sa);
+  }
+  return s;
+}
+
+// Step mode: pool the blocks that became due for this (batch, kv head) into the
+// pool and into `newrow` (K, V per block), in the summation order of
+// block_mean_kernel (slot s sums tokens s, s+RS, ...; the slots are added in
+// order; divided by BS; rounded once).
+template <typename T, int D>
+__device__ __forceinline__ void dec_pool(const DecodeArgs& a, const DecState& s, const T* rk, const T* rv, T* pk,
+                                         T* pv, float* part, T (*newrow)[D], int tid) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  constexpr int LPR = D / VEC;
+  constexpr int RS = 256 / LPR;
+  for (int j = 0; j < s.n_new; ++j) {
+    const int64_t pos0 = s.so0 + (int64_t)j * a.bs;
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      const T* src = kv ? rv : rk;
+      T* dst = (kv ? pv : pk) + (s.sc0 + j) * D;
+      const int c = tid % LPR, sl = tid / LPR;
+      float acc[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+      for (int tok = sl; tok < a.bs; tok += RS) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(src + dec_mod(pos0 + tok, a.ring) * D + c * VEC);
+        const T* x = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += to_f32(x[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) part[sl * D + c * VEC + e] = acc[e];
+      __syncthreads();
+      for (int col = tid; col < D; col += 256) {
+        float tot = 0.f;
+        for (int k = 0; k < RS; ++k) tot += part[k * D + col];
+        const T val = from_f32<T>(tot / (float)a.bs);
+        dst[col] = val;
+        newrow[2 * j + kv][col] = val;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Routed summaries of the query block (token-level cut-off), computed by one
+// wave on its own: lane j < kc holds entry j of the ordered row
+// [b, b-1..b-lwb, partners, sinks] (-1 where the reference pushes nothing),
+// keeps it at its first occurrence, and the ballot of the entries that pass the
+// filter gives their slots in row order (written to sel).  Returns the count.
+__device__ __forceinline__ int dec_select(int64_t p, const DecodeArgs& a, const DecState& s, int lane, int* sel) {
+  int64_t blk = dec_div(p, a.bs);
+  if (blk > s.nblocks - 1) blk = s.nblocks - 1;
+  int64_t cut = p - a.W + 1;
+  if (cut < 0) cut = 0;
+  const bfly_topology_t& topo = s.topo;
+  const int lwb = topo.local_window_blocks, npart = topo.partner_count;
+  const int64_t nsink = topo.sink_count < s.nblocks ? topo.sink_count : s.nblocks;
+  const int kc = 1 + lwb + npart + topo.sink_count;
+  int64_t cand = -1;
+  if (lane < kc) {
+    if (lane == 0) {
+      cand = blk;
+    } else if (lane <= lwb) {
+      cand = blk - lane >= 0 ? blk - lane : -1;
+    } else if (lane <= lwb + npart) {
+      const int j = lane - 1 - lwb;
+      int bit = 0;
+#pragma unroll
+      for (int jj = 0; jj < BFLY_MAX_PARTNERS; ++jj)
+        if (jj == j) bit = topo.partner_bits[jj];
+      cand = partner_block(blk, bit, s.nblocks, topo.rule, topo.width);
+    } else {
+      const int64_t sk = lane - 1 - lwb - npart;
+      cand = sk < nsink ? sk : -1;
+    }
+    if (cand >= s.nblocks) cand = -1;
+  }
+  const int c32 = (int)cand;
+  bool keep = cand >= 0;
+  for (int i = 0; i < kDecMaxSum; ++i) {
+    const int ci = __shfl(c32, i);
+    if (i < lane && ci == c32) keep = false;
+  }
+  const bool take = keep && cand < blk && cand < s.nsum && (cand + 1) * a.bs <= cut;
+  const unsigned long long mask = __ballot(take);
+  if (take) sel[__popcll(mask & ((1ull << lane) - 1ull))] = c32;
+  __builtin_amdgcn_wave_barrier();
+  return __popcll(mask);
+}
+
 template <typename T, int D, bool kStep>
 __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs sa) {
   constexpr int VEC = 16 / (int)sizeof(T);     // elements per 16-byte piece
@@ -135,41 +289,12 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
   const int gsz = a.hq / a.hkv;
 
   // ---- this step's counters: from the arguments, or (step mode) derived on the device
-  int64_t kv_len = a.kv_len, tail_start = a.tail_start, nsum = a.nsum, nblocks = a.nblocks;
-  bfly_topology_t topo = a.topo;
-  int64_t sc0 = 0, so0 = 0, ts1 = 0, sc1 = 0, so1 = 0;
-  int n_new = 0;
-  if constexpr (kStep) {
-    const int64_t off0 = sa.state[kStOffset], ts0 = sa.state[kStTail];
-    sc0 = sa.state[kStCount];
-    so0 = sa.state[kStSumOff];
-    const int64_t off1 = off0 + 1;
-    ts1 = ts0 + 1;
-    bool err = ts1 > a.ring;                              // tail capacity (compressed_cache.py:105-110)
-    sc1 = sc0;
-    so1 = so0;
-    while (!err && so1 + a.bs <= off1 - a.W) {            // summarise (:120-149)
-      const int64_t bstart = so1 - (off1 - ts1);
-      if (bstart < 0 || bstart + a.bs > ts1) break;
-      if (sc1 >= a.pool_rows || n_new == kDecMaxNew) {    // pool capacity (:128-132)
-        err = true;
-        break;
-      }
-      ++n_new;
-      ++sc1;
-      so1 += a.bs;
-    }
-    while (ts1 - a.bs >= a.W) ts1 -= a.bs;                // trim: target max(W, step + W - 1) = W
-    if (err) {
-      if (tid == 0) sa.state[kStError] = 1;               // the host raises at its next synchronisation
-      return;                                             // uniform: every workgroup sees the same counters
-    }
-    kv_len = off1;
-    tail_start = off1 - ts1;
-    nsum = sc1;
-    nblocks = (off1 + a.bs - 1) / a.bs;
-    topo = topology_at(nblocks, sa);
+  const DecState st = dec_state<kStep>(a, sa);
+  if (kStep && st.err) {
+    if (tid == 0) sa.state[kStError] = 1;                 // the host raises at its next synchronisation
+    return;                                               // uniform: every workgroup sees the same counters
   }
+  const int64_t kv_len = st.kv_len, tail_start = st.tail_start;
   const int64_t p = kv_len - 1;
   int64_t lo = p - a.W + 1;
   if (lo < tail_start) lo = tail_start;
@@ -191,87 +316,14 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
 #pragma unroll
     for (int e = 0; e < DPL; ++e) qv[e] = to_f32(qrow[e]);
   }
-  // ---- step mode: pool the newly due blocks of this (batch, kv head) (the
-  // summation order of block_mean_kernel: slot s sums tokens s, s+RS, ...; the
-  // slots are added in order; divided by BS; rounded once)
+  // ---- step mode: pool the newly due blocks of this (batch, kv head)
   __shared__ __attribute__((aligned(16))) T newrow[kStep ? kDecMaxNew * 2 : 1][kStep ? D : 1];
   if constexpr (kStep) {
     __shared__ float part[RS * D];
-    for (int j = 0; j < n_new; ++j) {
-      const int64_t pos0 = so0 + (int64_t)j * a.bs;
-#pragma unroll
-      for (int kv = 0; kv < 2; ++kv) {
-        const T* src = kv ? rv : rk;
-        T* dst = (kv ? pv : pk) + (sc0 + j) * D;
-        const int c = tid % LPR, sl = tid / LPR;
-        float acc[VEC];
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
-        for (int tok = sl; tok < a.bs; tok += RS) {
-          const uint4 raw = *reinterpret_cast<const uint4*>(src + posmod(pos0 + tok, a.ring) * D + c * VEC);
-          const T* x = reinterpret_cast<const T*>(&raw);
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) acc[e] += to_f32(x[e]);
-        }
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) part[sl * D + c * VEC + e] = acc[e];
-        __syncthreads();
-        for (int col = tid; col < D; col += 256) {
-          float tot = 0.f;
-          for (int k = 0; k < RS; ++k) tot += part[k * D + col];
-          const T val = from_f32<T>(tot / (float)a.bs);
-          dst[col] = val;
-          newrow[2 * j + kv][col] = val;
-        }
-        __syncthreads();
-      }
-    }
+    dec_pool<T, D>(a, st, rk, rv, pk, pv, part, newrow, tid);
   }
-  // ---- routed summaries of block p/BS (token-level cut-off), computed by every
-  // wave on its own: lane j < kc holds entry j of the ordered row
-  // [b, b-1..b-lwb, partners, sinks] (-1 where the reference pushes nothing),
-  // keeps it at its first occurrence, and the ballot of the entries that pass
-  // the filter gives their slots in row order.  No thread waits on another.
-  int ns;
-  {
-    int64_t blk = p / a.bs;
-    if (blk > nblocks - 1) blk = nblocks - 1;
-    int64_t cut = p - a.W + 1;
-    if (cut < 0) cut = 0;
-    const int lwb = topo.local_window_blocks, npart = topo.partner_count;
-    const int64_t nsink = topo.sink_count < nblocks ? topo.sink_count : nblocks;
-    const int kc = 1 + lwb + npart + topo.sink_count;
-    int64_t cand = -1;
-    if (lane < kc) {
-      if (lane == 0) {
-        cand = blk;
-      } else if (lane <= lwb) {
-        cand = blk - lane >= 0 ? blk - lane : -1;
-      } else if (lane <= lwb + npart) {
-        const int j = lane - 1 - lwb;
-        int bit = 0;
-#pragma unroll
-        for (int jj = 0; jj < BFLY_MAX_PARTNERS; ++jj)
-          if (jj == j) bit = topo.partner_bits[jj];
-        cand = partner_block(blk, bit, nblocks, topo.rule, topo.width);
-      } else {
-        const int64_t sk = lane - 1 - lwb - npart;
-        cand = sk < nsink ? sk : -1;
-      }
-      if (cand >= nblocks) cand = -1;
-    }
-    const int c32 = (int)cand;
-    bool keep = cand >= 0;
-    for (int i = 0; i < kDecMaxSum; ++i) {
-      const int ci = __shfl(c32, i);
-      if (i < lane && ci == c32) keep = false;
-    }
-    const bool take = keep && cand < blk && cand < nsum && (cand + 1) * a.bs <= cut;
-    const unsigned long long mask = __ballot(take);
-    ns = __popcll(mask);
-    if (take) selw[wave][__popcll(mask & ((1ull << lane) - 1ull))] = c32;
-    __builtin_amdgcn_wave_barrier();
-  }
+  // ---- routed summaries of the query block, computed by every wave on its own
+  const int ns = dec_select(p, a, st, lane, selw[wave]);
   const int nk = nw + ns;
 
   // ---- window rows (the newest from k_new/v_new when given, also appended to the
@@ -279,7 +331,7 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
   constexpr int kStage = (kDecMaxKeys * PIECES + 255) / 256;
   {
     uint4 kx[kStage], vx[kStage];
-    const int64_t slot_lo = a.ring ? posmod(lo, a.ring) : lo - tail_start;
+    const int64_t slot_lo = a.ring ? dec_mod(lo, a.ring) : lo - tail_start;
 #pragma unroll
     for (int it = 0; it < kStage; ++it) {
       const int i = tid + it * 256;
@@ -301,9 +353,9 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
           }
         } else {
           const int64_t n = selw[wave][r - nw];
-          if (kStep && n >= sc0) {           // pooled in this step: take the LDS copy
-            kx[it] = *reinterpret_cast<const uint4*>(&newrow[2 * (n - sc0)][pc * VEC]);
-            vx[it] = *reinterpret_cast<const uint4*>(&newrow[2 * (n - sc0) + 1][pc * VEC]);
+          if (kStep && n >= st.sc0) {        // pooled in this step: take the LDS copy
+            kx[it] = *reinterpret_cast<const uint4*>(&newrow[2 * (n - st.sc0)][pc * VEC]);
+            vx[it] = *reinterpret_cast<const uint4*>(&newrow[2 * (n - st.sc0) + 1][pc * VEC]);
           } else {
             kx[it] = *reinterpret_cast<const uint4*>(pk + n * D + pc * VEC);
             vx[it] = *reinterpret_cast<const uint4*>(pv + n * D + pc * VEC);
@@ -415,10 +467,231 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
       const unsigned long long prev =
           atomicAdd(reinterpret_cast<unsigned long long*>(sa.state + kStDone), 1ull);
       if (prev == (unsigned long long)gridDim.x - 1) {
-        sa.state[kStOffset] = kv_len;
-        sa.state[kStTail] = ts1;
-        sa.state[kStCount] = sc1;
-        sa.state[kStSumOff] = so1;
+        sa.state[kStOffset] = st.kv_len;
+        sa.state[kStTail] = st.ts1;
+        sa.state[kStCount] = st.sc1;
+        sa.state[kStSumOff] = st.so1;
+        sa.state[kStDone] = 0;
+      }
+    }
+  }
+}
+
+
+// ---------------------------------------------------------------------------------------------
+// bf16 decode on MFMA.  The GQA group's query heads are the 16 columns of one
+// v_mfma_f32_16x16x32_bf16 tile (heads 16g..16g+15 per pass; one pass up to 16
+// heads), so each wave computes the scores of every head at once:
+//   S^T = K Q^T over 6 tiles of 16 keys (window <= 64 + summaries <= 16, zero-padded),
+//   fp32 softmax per column (shuffles between the 4 lane groups),
+//   O^T = V^T P^T with V transposed in LDS; wave w takes output d-tiles w, w+4, ...
+// Staging, selection, pooling and counters are those of decode_kernel.
+constexpr int kDecMfmaKeys = 96;
+
+template <int D, bool kStep>
+__global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) decode_mfma_kernel(DecodeArgs a, StepArgs sa) {
+  using T = __bf16;
+  constexpr int VEC = 8;
+  constexpr int PIECES = D / VEC;
+  constexpr int KSTEPS = D / 32;
+  constexpr int MTILES = D / 32;                 // output tiles of 32 d (two 16-row halves each)
+  constexpr int NT = kDecMfmaKeys / 16;          // key tiles
+  constexpr int KP = D + VEC;                    // K row pitch (bf16)
+  constexpr int VTP = kDecMfmaKeys + 8;          // V^T row pitch (bf16)
+  constexpr int LPR = D / VEC;
+  constexpr int RS = 256 / LPR;
+  constexpr int KITEMS = kDecMfmaKeys * PIECES;          // K pieces
+  constexpr int VITEMS = (kDecMfmaKeys / 2) * PIECES;    // V row pairs x pieces
+  constexpr int KIT = (KITEMS + 255) / 256, VIT = (VITEMS + 255) / 256;
+  __shared__ __attribute__((aligned(16))) T Ks[kDecMfmaKeys * KP];
+  __shared__ __attribute__((aligned(16))) T Vt[D * VTP];
+  __shared__ int selw[4][kDecMaxSum];
+  __shared__ __attribute__((aligned(16))) T newrow[kStep ? kDecMaxNew * 2 : 1][kStep ? D : 1];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lg = lane >> 4, lq = lane & 15;
+  const int64_t bh = blockIdx.x;
+  const int64_t bi = bh / a.hkv;
+  const int kvh = (int)(bh - bi * a.hkv);
+  const int gsz = a.hq / a.hkv;
+  const T* qhead = reinterpret_cast<const T*>(a.q) + (bi * a.hq + (int64_t)kvh * gsz) * D;
+
+  // Q^T fragments of heads 16*hg + lq (B operand: d = lg*(D/4) + 8*ks + [0, 8)); the
+  // first pass is issued before anything else so its latency hides behind the rest
+  bf16x8 qf[KSTEPS];
+  auto load_q = [&](int hg) {
+    const int head = 16 * hg + lq;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      qf[ks] = head < gsz ? *reinterpret_cast<const bf16x8*>(qhead + (int64_t)head * D + lg * (D / 4) + 8 * ks)
+                          : bf16x8{};
+  };
+  load_q(0);
+
+  const DecState st = dec_state<kStep>(a, sa);
+  if (kStep && st.err) {
+    if (tid == 0) sa.state[kStError] = 1;
+    return;
+  }
+  const int64_t p = st.kv_len - 1;
+  int64_t lo = p - a.W + 1;
+  if (lo < st.tail_start) lo = st.tail_start;
+  if (lo < 0) lo = 0;
+  const int nw = (int)(p - lo + 1);
+
+  const T* knew = a.k_new ? reinterpret_cast<const T*>(a.k_new) + bh * D : nullptr;
+  const T* vnew = a.v_new ? reinterpret_cast<const T*>(a.v_new) + bh * D : nullptr;
+  T* rk = reinterpret_cast<T*>(a.ring_k) + bh * a.kv_rows * D;
+  T* rv = reinterpret_cast<T*>(a.ring_v) + bh * a.kv_rows * D;
+  T* pk = reinterpret_cast<T*>(const_cast<void*>(a.pool_k)) + bh * a.pool_rows * D;
+  T* pv = reinterpret_cast<T*>(const_cast<void*>(a.pool_v)) + bh * a.pool_rows * D;
+
+  if constexpr (kStep) {
+    __shared__ float part[RS * D];
+    dec_pool<T, D>(a, st, rk, rv, pk, pv, part, newrow, tid);
+  }
+  const int ns = dec_select(p, a, st, lane, selw[wave]);
+  const int nk = nw + ns;
+  const int64_t slot_lo = a.ring ? dec_mod(lo, a.ring) : lo - st.tail_start;
+
+  // ---- append the new token to its ring slot (read back from k_new/v_new below)
+  if (knew != nullptr && tid < 2 * PIECES) {
+    int64_t row = slot_lo + (p - lo);
+    if (a.ring && row >= a.ring) row -= a.ring;
+    const int pc = tid % PIECES;
+    const T* src = tid < PIECES ? knew : vnew;
+    T* dst = tid < PIECES ? rk : rv;
+    *reinterpret_cast<uint4*>(dst + row * D + pc * VEC) = *reinterpret_cast<const uint4*>(src + pc * VEC);
+  }
+
+  // ---- stage keys row-major and values transposed; rows >= nk are zero
+  auto src_row = [&](int r, bool vside) -> const T* {
+    if (r < nw) {
+      if (knew != nullptr && lo + r == p) return vside ? vnew : knew;
+      int64_t row = slot_lo + r;
+      if (a.ring && row >= a.ring) row -= a.ring;
+      return (vside ? rv : rk) + row * D;
+    }
+    const int64_t n = selw[wave][r - nw];
+    if (kStep && n >= st.sc0) return &newrow[2 * (n - st.sc0) + (vside ? 1 : 0)][0];
+    return (vside ? pv : pk) + n * D;
+  };
+  {
+    uint4 kx[KIT], v0[VIT], v1[VIT];
+#pragma unroll
+    for (int it = 0; it < KIT; ++it) {
+      const int i = tid + it * 256;
+      const int r = i / PIECES, pc = i % PIECES;
+      kx[it] = i < KITEMS && r < nk ? *reinterpret_cast<const uint4*>(src_row(r, false) + pc * VEC)
+                                    : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+      const int i = tid + it * 256;
+      const int kp = i % (kDecMfmaKeys / 2), pc = i / (kDecMfmaKeys / 2);
+      const int r0 = 2 * kp;
+      const bool in = i < VITEMS;
+      v0[it] = in && r0 < nk ? *reinterpret_cast<const uint4*>(src_row(r0, true) + pc * VEC) : make_uint4(0, 0, 0, 0);
+      v1[it] = in && r0 + 1 < nk ? *reinterpret_cast<const uint4*>(src_row(r0 + 1, true) + pc * VEC)
+                                 : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int it = 0; it < KIT; ++it) {
+      const int i = tid + it * 256;
+      const int r = i / PIECES, pc = i % PIECES;
+      if (i < KITEMS) *reinterpret_cast<uint4*>(Ks + r * KP + pc * VEC) = kx[it];
+    }
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+      const int i = tid + it * 256;
+      const int kp = i % (kDecMfmaKeys / 2), pc = i / (kDecMfmaKeys / 2);
+      if (i >= VITEMS) continue;
+      const uint16_t* e0 = reinterpret_cast<const uint16_t*>(&v0[it]);
+      const uint16_t* e1 = reinterpret_cast<const uint16_t*>(&v1[it]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        *reinterpret_cast<uint32_t*>(Vt + (pc * 8 + j) * VTP + 2 * kp) = (uint32_t)e0[j] | ((uint32_t)e1[j] << 16);
+    }
+  }
+  __syncthreads();
+
+  const float sl2 = a.scale * 1.4426950408889634f;   // host guarantees scale > 0 on this path
+  for (int hg = 0; 16 * hg < gsz; ++hg) {
+    if (hg > 0) load_q(hg);
+    // S^T: lane (lg, lq) holds keys 16t + 4lg + i of head 16hg + lq
+    f32x4 sc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      bf16x8 kf[KSTEPS];
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks)
+        kf[ks] = *reinterpret_cast<const bf16x8*>(Ks + (16 * t + lq) * KP + lg * (D / 4) + 8 * ks);
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[ks], acc, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[t][i] = 16 * t + 4 * lg + i < nk ? acc[i] : -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) mx = fmaxf(mx, fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float nm = -mx * sl2;                      // nk >= 1: every column has a finite max
+    float lsum = 0.f;
+    bf16x8 pf[NT / 2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = __builtin_amdgcn_exp2f(fmaf(sc[t][i], sl2, nm));
+        lsum += e;
+        pf[t / 2][(t % 2) * 4 + i] = (__bf16)e;
+      }
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    const float inv = 1.f / fmaxf(lsum, 1e-30f);
+    const int head = 16 * hg + lq;
+    __bf16* orow = reinterpret_cast<__bf16*>(a.out) + (bi * a.hq + (int64_t)kvh * gsz + head) * D;
+    // O^T = V^T P^T: tile (mt, half) row r holds d = mt*32 + (r/4)*8 + half*4 + r%4, and its
+    // k index runs over keys (tile 2pr, 4lg..4lg+3) then (tile 2pr+1, 4lg..4lg+3), the
+    // order of this lane's P fragment, so no lane exchange is needed.
+    for (int mt = wave; mt < MTILES; mt += 4) {
+      f32x4 o[2];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const T* vrow = Vt + (mt * 32 + (lq >> 2) * 8 + half * 4 + (lq & 3)) * VTP;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int pr = 0; pr < NT / 2; ++pr) {
+          const bf16x4 va = *reinterpret_cast<const bf16x4*>(vrow + 16 * (2 * pr) + 4 * lg);
+          const bf16x4 vb = *reinterpret_cast<const bf16x4*>(vrow + 16 * (2 * pr + 1) + 4 * lg);
+          const bf16x8 vf = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[pr], acc, 0, 0, 0);
+        }
+        o[half] = acc;
+      }
+      if (head < gsz) {
+        bf16x8 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          w[i] = (__bf16)(o[0][i] * inv);
+          w[4 + i] = (__bf16)(o[1][i] * inv);
+        }
+        *reinterpret_cast<bf16x8*>(orow + mt * 32 + lg * 8) = w;
+      }
+    }
+  }
+  if constexpr (kStep) {
+    // the last workgroup to finish publishes the counters (see decode_kernel)
+    if (tid == 0) {
+      const unsigned long long prev =
+          atomicAdd(reinterpret_cast<unsigned long long*>(sa.state + kStDone), 1ull);
+      if (prev == (unsigned long long)gridDim.x - 1) {
+        sa.state[kStOffset] = st.kv_len;
+        sa.state[kStTail] = st.ts1;
+        sa.state[kStCount] = st.sc1;
+        sa.state[kStSumOff] = st.so1;
         sa.state[kStDone] = 0;
       }
     }
@@ -427,6 +700,22 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
 
 template <typename T, bool kStep>
 static void launch_decode(const DecodeArgs& a, const StepArgs& sa, int d, int64_t grid, hipStream_t stream) {
+  // bf16 with a positive scale (folded into exp2) runs on MFMA; fp32 on the lane-per-key kernel
+  if constexpr (sizeof(T) == 2) {
+    if (a.scale > 0.f) {
+      switch (d) {
+        case 64:
+          hipLaunchKernelGGL((decode_mfma_kernel<64, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, a, sa);
+          return;
+        case 128:
+          hipLaunchKernelGGL((decode_mfma_kernel<128, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, a, sa);
+          return;
+        default:
+          hipLaunchKernelGGL((decode_mfma_kernel<256, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, a, sa);
+          return;
+      }
+    }
+  }
   switch (d) {
     case 64:
       hipLaunchKernelGGL((decode_kernel<T, 64, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, a, sa);

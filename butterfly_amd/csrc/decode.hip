@@ -257,8 +257,8 @@ __device__ __forceinline__ int dec_select(int64_t p, const DecodeArgs& a, const 
   }
   const int c32 = (int)cand;
   bool keep = cand >= 0;
-  for (int i = 0; i < kDecMaxSum; ++i) {
-    const int ci = __shfl(c32, i);
+  for (int i = 0; i < kc; ++i) {                  // kc is uniform: lane i's entry as a scalar
+    const int ci = __builtin_amdgcn_readlane(c32, i);
     if (i < lane && ci == c32) keep = false;
   }
   const bool take = keep && cand < blk && cand < s.nsum && (cand + 1) * a.bs <= cut;
@@ -550,8 +550,6 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) decode_mfma_kernel(Deco
     __shared__ float part[RS * D];
     dec_pool<T, D>(a, st, rk, rv, pk, pv, part, newrow, tid);
   }
-  const int ns = dec_select(p, a, st, lane, selw[wave]);
-  const int nk = nw + ns;
   const int64_t slot_lo = a.ring ? dec_mod(lo, a.ring) : lo - st.tail_start;
 
   // ---- append the new token to its ring slot (read back from k_new/v_new below)
@@ -564,25 +562,28 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) decode_mfma_kernel(Deco
     *reinterpret_cast<uint4*>(dst + row * D + pc * VEC) = *reinterpret_cast<const uint4*>(src + pc * VEC);
   }
 
-  // ---- stage keys row-major and values transposed; rows >= nk are zero
-  auto src_row = [&](int r, bool vside) -> const T* {
-    if (r < nw) {
-      if (knew != nullptr && lo + r == p) return vside ? vnew : knew;
-      int64_t row = slot_lo + r;
-      if (a.ring && row >= a.ring) row -= a.ring;
-      return (vside ? rv : rk) + row * D;
-    }
-    const int64_t n = selw[wave][r - nw];
+  // ---- stage keys row-major and values transposed; rows >= nk are zero.  The
+  // window rows are requested first; the routed selection runs while they are
+  // in flight, then the summary rows are requested.
+  auto win_row = [&](int r, bool vside) -> const T* {
+    if (knew != nullptr && lo + r == p) return vside ? vnew : knew;
+    int64_t row = slot_lo + r;
+    if (a.ring && row >= a.ring) row -= a.ring;
+    return (vside ? rv : rk) + row * D;
+  };
+  auto sum_row = [&](int j, bool vside) -> const T* {
+    const int64_t n = selw[wave][j];
     if (kStep && n >= st.sc0) return &newrow[2 * (n - st.sc0) + (vside ? 1 : 0)][0];
     return (vside ? pv : pk) + n * D;
   };
+  int nk;
   {
     uint4 kx[KIT], v0[VIT], v1[VIT];
 #pragma unroll
     for (int it = 0; it < KIT; ++it) {
       const int i = tid + it * 256;
       const int r = i / PIECES, pc = i % PIECES;
-      kx[it] = i < KITEMS && r < nk ? *reinterpret_cast<const uint4*>(src_row(r, false) + pc * VEC)
+      kx[it] = i < KITEMS && r < nw ? *reinterpret_cast<const uint4*>(win_row(r, false) + pc * VEC)
                                     : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
@@ -591,9 +592,27 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) decode_mfma_kernel(Deco
       const int kp = i % (kDecMfmaKeys / 2), pc = i / (kDecMfmaKeys / 2);
       const int r0 = 2 * kp;
       const bool in = i < VITEMS;
-      v0[it] = in && r0 < nk ? *reinterpret_cast<const uint4*>(src_row(r0, true) + pc * VEC) : make_uint4(0, 0, 0, 0);
-      v1[it] = in && r0 + 1 < nk ? *reinterpret_cast<const uint4*>(src_row(r0 + 1, true) + pc * VEC)
+      v0[it] = in && r0 < nw ? *reinterpret_cast<const uint4*>(win_row(r0, true) + pc * VEC) : make_uint4(0, 0, 0, 0);
+      v1[it] = in && r0 + 1 < nw ? *reinterpret_cast<const uint4*>(win_row(r0 + 1, true) + pc * VEC)
                                  : make_uint4(0, 0, 0, 0);
+    }
+    const int ns = dec_select(p, a, st, lane, selw[wave]);
+    nk = nw + ns;
+#pragma unroll
+    for (int it = 0; it < KIT; ++it) {
+      const int i = tid + it * 256;
+      const int r = i / PIECES, pc = i % PIECES;
+      if (i < KITEMS && r >= nw && r < nk) kx[it] = *reinterpret_cast<const uint4*>(sum_row(r - nw, false) + pc * VEC);
+    }
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+      const int i = tid + it * 256;
+      const int kp = i % (kDecMfmaKeys / 2), pc = i / (kDecMfmaKeys / 2);
+      const int r0 = 2 * kp;
+      const bool in = i < VITEMS;
+      if (in && r0 >= nw && r0 < nk) v0[it] = *reinterpret_cast<const uint4*>(sum_row(r0 - nw, true) + pc * VEC);
+      if (in && r0 + 1 >= nw && r0 + 1 < nk)
+        v1[it] = *reinterpret_cast<const uint4*>(sum_row(r0 + 1 - nw, true) + pc * VEC);
     }
 #pragma unroll
     for (int it = 0; it < KIT; ++it) {

@@ -323,6 +323,53 @@ def bench_decode(torch, bf, batches=(1, 8, 32), steps=64, seed=0):
     return out
 
 
+def bench_decode_sweep(torch, bf, batches=(128, 512, 1024), steps=64, seed=1):
+    """cfg3 shapes at batch sizes beyond the config (labelled as such): the same
+    device-counter decode step, 64 steps in one HIP graph, to show where the
+    per-step latency floor gives way to HBM bandwidth."""
+    hq, hkv, d, bs, W, ctx = 8, 2, 128, 128, 64, 131072
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    out = {}
+    for B in batches:
+        tk = torch.randn(B, hkv, 256, d, generator=g, device=dev).bfloat16()
+        tv = torch.randn(B, hkv, 256, d, generator=g, device=dev).bfloat16()
+        sk = torch.randn(B, hkv, 1023, d, generator=g, device=dev).bfloat16()
+        sv = torch.randn(B, hkv, 1023, d, generator=g, device=dev).bfloat16()
+        c = bf.CompressedKVCache(block_size=bs, local_window_tokens=W, max_kv_size=131328, max_chunk_size=512)
+        c.state = (tk, tv, sk, sv)
+        c.meta_state = (str(bs), str(W), str(ctx), str(1023 * bs))
+        c.ring_state()
+        del tk, tv, sk, sv
+        c.use_device_counters()
+        qn = torch.randn(steps, B, hq, 1, d, generator=g, device=dev).bfloat16()
+        kn = torch.randn(steps, B, hkv, 1, d, generator=g, device=dev).bfloat16()
+        vn = torch.randn(steps, B, hkv, 1, d, generator=g, device=dev).bfloat16()
+        outs = torch.empty(steps, B, hq, 1, d, dtype=torch.bfloat16, device=dev)
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for s in range(steps):
+                    c.decode_step(qn[s], kn[s], vn[s], layer_idx=3, local_window_tokens=W, out=outs[s])
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        graph.replay()
+        torch.cuda.synchronize()
+        gdt = (time.perf_counter() - t0) / steps
+        c.sync()
+        assert c.summary_count == 1024 and torch.isfinite(outs[-1].float()).all()
+        bytes_step = B * (2 * hq * d * 2 + 2 * hkv * W * d * 2 + 2 * hkv * 2 * d * 2 + 2 * hkv * d * 2)
+        out[str(B)] = {"ms_per_step": gdt * 1e3, "tok_s": B / gdt, "alg_bytes_per_step": bytes_step,
+                       "wall_gbs": bytes_step / gdt / 1e9, "mode": "device counters, 64 steps in one HIP graph",
+                       "note": "batch beyond the config: bandwidth ramp, not a config result"}
+        del c, graph, qn, kn, vn, outs
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_stream(torch, bf, seed=0, T=262144, chunk=384, layer=5):
     """cfg4: streaming chunked prefill, Hq=16, Hkv=4, d=256, bf16, 384-token chunks.
 
@@ -529,6 +576,7 @@ def main():
     pre = bench_prefill(args, torch, bf, tp)
     q, k, v, ref_lays = pre.pop("inputs")
     decode = None if args.no_decode else bench_decode(torch, bf)
+    decode_sweep = None if args.no_decode else bench_decode_sweep(torch, bf)
     stream = None if args.no_stream else bench_stream(torch, bf)
     model = None if args.no_model else bench_decoder(torch, bf, cpu_agreement=not args.no_cpu_baseline)
     cpu = None if args.no_cpu_baseline else cpu_baseline(q, k, v, ref_lays)
@@ -563,6 +611,7 @@ def main():
                   "prefill_event_ms_in_step_avg": pre["prefill_event_ms_in_step_avg"],
                   "prefill_event_ms_in_step_min": pre["prefill_event_ms_in_step_min"],
                   "compress_alg_bytes": pre["compress_bytes"], "decode_cfg3": decode,
+                  "decode_batch_sweep": decode_sweep,
                   "stream_cfg4": stream, "model_cfg5": model},
     }
     print(json.dumps(line), flush=True)

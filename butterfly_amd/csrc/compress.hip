@@ -43,17 +43,34 @@ __global__ void __launch_bounds__(256) block_mean_kernel(PoolJob j0, PoolJob j1,
   float acc[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+  // row of token 0 of the block; tokens are < bs <= ring, so one wrap at most
+  const int64_t r0 = job.ring ? posmod(job.base_pos + first, job.ring) : job.base_pos + first;
+  auto tok_row = [&](int64_t tok) {
+    int64_t r = r0 + tok;
+    if (job.ring && r >= job.ring) r -= job.ring;
+    return r;
+  };
   if (s < rs) {
-    for (int64_t tok = s; tok < cnt; tok += rs) {
-      int64_t p = job.base_pos + first + tok;
-      int64_t r = job.ring ? posmod(p, job.ring) : p;
-      const T* ptr = src + r * d + c * VEC;
-      if constexpr (VEC * sizeof(T) == 16) {
-        uint4 raw = *reinterpret_cast<const uint4*>(ptr);
-        const T* v = reinterpret_cast<const T*>(&raw);
+    if constexpr (VEC * sizeof(T) == 16) {
+      // eight loads in flight per thread, then the adds in token order
+      for (int64_t base = s; base < cnt; base += 8 * (int64_t)rs) {
+        uint4 raw[8];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[e] += to_f32(v[e]);
-      } else {
+        for (int u = 0; u < 8; ++u) {
+          const int64_t tok = base + (int64_t)u * rs;
+          raw[u] = tok < cnt ? *reinterpret_cast<const uint4*>(src + tok_row(tok) * d + c * VEC) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (base + (int64_t)u * rs >= cnt) continue;
+          const T* v = reinterpret_cast<const T*>(&raw[u]);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[e] += to_f32(v[e]);
+        }
+      }
+    } else {
+      for (int64_t tok = s; tok < cnt; tok += rs) {
+        const T* ptr = src + tok_row(tok) * d + c * VEC;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc[e] += to_f32(ptr[e]);
       }

@@ -41,7 +41,10 @@ def _check(got, want, dtype):
 
 @pytest.mark.parametrize("dtype,d,hq,hkv,b", [(torch.bfloat16, 128, 8, 2, 2), (torch.float32, 128, 8, 2, 1),
                                               (torch.bfloat16, 256, 16, 4, 1), (torch.bfloat16, 64, 4, 1, 3),
-                                              (torch.float32, 64, 6, 3, 2)])
+                                              (torch.float32, 64, 6, 3, 2),
+                                              # GQA groups of 20 (two 16-head MFMA passes), 3 and 1
+                                              (torch.bfloat16, 128, 40, 2, 1), (torch.bfloat16, 128, 3, 1, 2),
+                                              (torch.bfloat16, 64, 5, 5, 1)])
 def test_decode_steps_across_block_boundaries(dtype, d, hq, hkv, b):
     bs, W, prompt, ndec, layer = 128, 64, 300, 300, 6
     total = prompt + ndec
@@ -127,3 +130,29 @@ def test_single_row_entries_use_decode_kernel(dtype):
     want2 = oa.from_cache(q, rep(k[:, :, ts:]), rep(v[:, :, ts:]), rep(ksum), rep(vsum), layout=ref_lay,
                           query_positions=qp, W=W, tail_start=ts, kv_len=T)
     _check(y2, want2, dtype)
+
+
+@pytest.mark.parametrize("rule,lwb,sinks,partners,bs,W", [("xor", 2, 2, 2, 64, 17), ("benes", 1, 3, 2, 96, 64),
+                                                          ("bit_reversal", 0, 1, 3, 64, 40),
+                                                          ("random", 3, 0, 1, 128, 1)])
+def test_decode_routing_variants(rule, lwb, sinks, partners, bs, W):
+    """Other partner rules, sink/partner counts, block sizes and windows through the
+    decode kernel's in-kernel routed selection (lane per row entry, first-occurrence dedup)."""
+    b, hq, hkv, d, prompt, ndec, layer = 2, 8, 2, 128, 5 * bs + 7, 2 * bs + 3, 7
+    total = prompt + ndec
+    q = _rand(31, (b, hq, total, d), torch.bfloat16)
+    k = _rand(32, (b, hkv, total, d), torch.bfloat16)
+    v = _rand(33, (b, hkv, total, d), torch.bfloat16)
+    cache = bf.CompressedKVCache(block_size=bs, local_window_tokens=W, max_kv_size=total)
+    cache.update(k[:, :, :prompt].cuda(), v[:, :, :prompt].cuda())
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    for pos in range(prompt, total):
+        kw = dict(seq_len=pos + 1, block_size=bs, num_key_value_heads=hkv, num_key_value_groups=hq // hkv,
+                  layer_idx=layer, local_window_blocks=lwb, sink_count=sinks, partner_count=partners,
+                  partner_rule=rule)
+        lay, ref_lay = bf.build_block_butterfly_layout(**kw), tp.build_layout(**kw)
+        got = cache.update_and_attend(qd[:, :, pos:pos + 1], kd[:, :, pos:pos + 1], vd[:, :, pos:pos + 1],
+                                      layout=lay, local_window_tokens=W)
+        want = oa.active(q[:, :, pos:pos + 1], k[:, :, :pos + 1], v[:, :, :pos + 1], layout=ref_lay,
+                         query_positions=torch.tensor([pos]), W=W)
+        _check(got, want, torch.bfloat16)

@@ -93,20 +93,26 @@ class CompressedKVCache:
         if self._ring_k is None:
             raise ValueError("allocate the cache with a first update before enabling device counters")
         self._apply_realign()
-        self._dev = torch.zeros(6, dtype=torch.int64, device=self._ring_k.device)
+        b, h = int(self._ring_k.shape[0]), int(self._ring_k.shape[1])
+        words = int(_native.lib().bfly_decode_state_words(b, h))
+        self._dev = torch.zeros(words, dtype=torch.int64, device=self._ring_k.device)
         self._dev_dirty = False
         self._push()
 
     @property
     def device_counters(self) -> Optional[torch.Tensor]:
-        """The device int64[6] {offset, tail_size, summary_count, summary_offset, error, done}, or None."""
+        """The device counter array, or None: word 4 is the error flag; sequence g
+        (= batch * Hkv + kv head) keeps {offset, tail_size, summary_count,
+        summary_offset} at words 8 + 4g .. 8 + 4g + 3 (all copies equal)."""
         return self._dev
 
     def sync(self) -> None:
         """Read device counters back; raise the capacity error a device step recorded."""
         if self._dev is None or not self._dev_dirty:
             return
-        off, ts, sc, so, err, _ = (int(x) for x in self._dev.tolist())
+        head = self._dev[:12].tolist()
+        err = int(head[4])
+        off, ts, sc, so = (int(x) for x in head[8:12])
         self._dev_dirty = False
         if err:
             self._push()
@@ -118,8 +124,10 @@ class CompressedKVCache:
 
     def _push(self) -> None:
         if self._dev is not None:
-            self._dev.copy_(torch.tensor([self.offset, self.tail_size, self.summary_count, self.summary_offset, 0, 0],
-                                         dtype=torch.int64))
+            g = (self._dev.numel() - 8) // 4
+            counters = torch.tensor([self.offset, self.tail_size, self.summary_count, self.summary_offset],
+                                    dtype=torch.int64)
+            self._dev.copy_(torch.cat([torch.zeros(8, dtype=torch.int64), counters.repeat(g)]))
             self._dev_dirty = False
 
     def decode_step(self, q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, *, layer_idx: int,

@@ -30,9 +30,9 @@
 // (append one token, summarise every block with end + W <= offset, trim whole
 // blocks while tail_size - BS >= W; compressed_cache.py:94-172), pools a newly
 // due block itself (same summation order as bfly_cache_compress), computes the
-// layer's topology at the live block count, and attends; the last workgroup to
-// finish writes the new counters.  A step then has fixed arguments and can be
-// captured in a HIP graph.
+// layer's topology at the live block count, and attends; each workgroup keeps
+// its own copy of the counters and writes it back.  A step then has fixed
+// arguments and can be captured in a HIP graph.
 #include "bfly_topology.h"
 
 namespace bfly {
@@ -42,9 +42,15 @@ constexpr int kDecMaxSum = 16;
 constexpr int kDecMaxKeys = kDecMaxWin + kDecMaxSum;
 constexpr int kDecMaxNew = 2;   // blocks pooled in one step (one per 128 steps in steady state)
 
-// Device cache counters of step mode: {offset, tail_size, summary_count,
-// summary_offset, error, done}.
-enum { kStOffset = 0, kStTail = 1, kStCount = 2, kStSumOff = 3, kStError = 4, kStDone = 5 };
+// Device cache counters of step mode: state[4] is the error word; workgroup g
+// (= batch * Hkv + kv head) keeps its own copy of {offset, tail_size,
+// summary_count, summary_offset} at state[8 + 4g ...] and advances it itself,
+// so a step needs no cross-workgroup synchronisation (every copy evolves
+// identically; the host reads copy 0).
+enum { kStOffset = 0, kStTail = 1, kStCount = 2, kStSumOff = 3 };
+constexpr int kStError = 4;
+constexpr int kStHeader = 8;
+__device__ __forceinline__ int64_t* dec_slot(int64_t* state) { return state + kStHeader + 4 * (int64_t)blockIdx.x; }
 
 struct StepArgs {
   int64_t* state;
@@ -151,9 +157,10 @@ __device__ __forceinline__ DecState dec_state(const DecodeArgs& a, const StepArg
   s.nblocks = a.nblocks;
   s.topo = a.topo;
   if constexpr (kStep) {
-    const int64_t off0 = sa.state[kStOffset], ts0 = sa.state[kStTail];
-    s.sc0 = sa.state[kStCount];
-    s.so0 = sa.state[kStSumOff];
+    const int64_t* slot = dec_slot(sa.state);
+    const int64_t off0 = slot[kStOffset], ts0 = slot[kStTail];
+    s.sc0 = slot[kStCount];
+    s.so0 = slot[kStSumOff];
     const int64_t off1 = off0 + 1;
     s.ts1 = ts0 + 1;
     bool err = s.ts1 > a.ring;                              // tail capacity (compressed_cache.py:105-110)
@@ -459,20 +466,15 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
     __builtin_amdgcn_wave_barrier();   // qs/ps reused by this wave's next head
   }
   if constexpr (kStep) {
-    // The last workgroup to finish publishes the counters.  Every workgroup read
-    // the old counters at its start and used them before its increment, and no
-    // workgroup reads another's pool, ring or output within the step, so no
-    // fence is needed: the next launch sees everything at the kernel boundary.
+    // Each workgroup advances its own counter copy; no workgroup reads another's
+    // copy, pool, ring or output within the step, so no atomic or fence is
+    // needed: the next launch sees everything at the kernel boundary.
     if (tid == 0) {
-      const unsigned long long prev =
-          atomicAdd(reinterpret_cast<unsigned long long*>(sa.state + kStDone), 1ull);
-      if (prev == (unsigned long long)gridDim.x - 1) {
-        sa.state[kStOffset] = st.kv_len;
-        sa.state[kStTail] = st.ts1;
-        sa.state[kStCount] = st.sc1;
-        sa.state[kStSumOff] = st.so1;
-        sa.state[kStDone] = 0;
-      }
+      int64_t* slot = dec_slot(sa.state);
+      slot[kStOffset] = st.kv_len;
+      slot[kStTail] = st.ts1;
+      slot[kStCount] = st.sc1;
+      slot[kStSumOff] = st.so1;
     }
   }
 }
@@ -486,16 +488,17 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
 //   fp32 softmax per column (shuffles between the 4 lane groups),
 //   O^T = V^T P^T with V transposed in LDS; wave w takes output d-tiles w, w+4, ...
 // Staging, selection, pooling and counters are those of decode_kernel.
-constexpr int kDecMfmaKeys = 96;
+constexpr int kDecMfmaKeys = kDecMaxKeys;   // 80 keys staged: 5 score tiles, PV k-steps padded to 96 in registers
 
 template <int D, bool kStep>
-__global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) decode_mfma_kernel(DecodeArgs a, StepArgs sa) {
+__global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(DecodeArgs a, StepArgs sa) {
   using T = __bf16;
   constexpr int VEC = 8;
   constexpr int PIECES = D / VEC;
   constexpr int KSTEPS = D / 32;
   constexpr int MTILES = D / 32;                 // output tiles of 32 d (two 16-row halves each)
-  constexpr int NT = kDecMfmaKeys / 16;          // key tiles
+  constexpr int NT = kDecMfmaKeys / 16;          // key tiles (5)
+  constexpr int NPR = (NT + 1) / 2;              // PV k-steps of 32 keys (3, the last half zero)
   constexpr int KP = D + VEC;                    // K row pitch (bf16)
   constexpr int VTP = kDecMfmaKeys + 8;          // V^T row pitch (bf16)
   constexpr int LPR = D / VEC;
@@ -503,8 +506,13 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) decode_mfma_kernel(Deco
   constexpr int KITEMS = kDecMfmaKeys * PIECES;          // K pieces
   constexpr int VITEMS = (kDecMfmaKeys / 2) * PIECES;    // V row pairs x pieces
   constexpr int KIT = (KITEMS + 255) / 256, VIT = (VITEMS + 255) / 256;
-  __shared__ __attribute__((aligned(16))) T Ks[kDecMfmaKeys * KP];
-  __shared__ __attribute__((aligned(16))) T Vt[D * VTP];
+  // K rows and V^T share one LDS block with the pooling scratch (pooling ends
+  // with a barrier before the staging writes)
+  constexpr int KS_BYTES = kDecMfmaKeys * KP * 2, VT_BYTES = D * VTP * 2;
+  constexpr int STAGE_BYTES = KS_BYTES + VT_BYTES > RS * D * 4 ? KS_BYTES + VT_BYTES : RS * D * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char stage_lds[STAGE_BYTES];
+  T* Ks = reinterpret_cast<T*>(stage_lds);
+  T* Vt = reinterpret_cast<T*>(stage_lds + KS_BYTES);
   __shared__ int selw[4][kDecMaxSum];
   __shared__ __attribute__((aligned(16))) T newrow[kStep ? kDecMaxNew * 2 : 1][kStep ? D : 1];
 
@@ -547,7 +555,7 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) decode_mfma_kernel(Deco
   T* pv = reinterpret_cast<T*>(const_cast<void*>(a.pool_v)) + bh * a.pool_rows * D;
 
   if constexpr (kStep) {
-    __shared__ float part[RS * D];
+    float* part = reinterpret_cast<float*>(stage_lds);
     dec_pool<T, D>(a, st, rk, rv, pk, pv, part, newrow, tid);
   }
   const int64_t slot_lo = a.ring ? dec_mod(lo, a.ring) : lo - st.tail_start;
@@ -658,7 +666,8 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) decode_mfma_kernel(Deco
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float nm = -mx * sl2;                      // nk >= 1: every column has a finite max
     float lsum = 0.f;
-    bf16x8 pf[NT / 2];
+    bf16x8 pf[NPR];
+    pf[NPR - 1] = bf16x8{};
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -682,9 +691,10 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) decode_mfma_kernel(Deco
         const T* vrow = Vt + (mt * 32 + (lq >> 2) * 8 + half * 4 + (lq & 3)) * VTP;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int pr = 0; pr < NT / 2; ++pr) {
+        for (int pr = 0; pr < NPR; ++pr) {
           const bf16x4 va = *reinterpret_cast<const bf16x4*>(vrow + 16 * (2 * pr) + 4 * lg);
-          const bf16x4 vb = *reinterpret_cast<const bf16x4*>(vrow + 16 * (2 * pr + 1) + 4 * lg);
+          const bf16x4 vb = 2 * pr + 1 < NT ? *reinterpret_cast<const bf16x4*>(vrow + 16 * (2 * pr + 1) + 4 * lg)
+                                            : bf16x4{};
           const bf16x8 vf = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
           acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[pr], acc, 0, 0, 0);
         }
@@ -702,17 +712,13 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) decode_mfma_kernel(Deco
     }
   }
   if constexpr (kStep) {
-    // the last workgroup to finish publishes the counters (see decode_kernel)
+    // each workgroup advances its own counter copy (see decode_kernel)
     if (tid == 0) {
-      const unsigned long long prev =
-          atomicAdd(reinterpret_cast<unsigned long long*>(sa.state + kStDone), 1ull);
-      if (prev == (unsigned long long)gridDim.x - 1) {
-        sa.state[kStOffset] = st.kv_len;
-        sa.state[kStTail] = st.ts1;
-        sa.state[kStCount] = st.sc1;
-        sa.state[kStSumOff] = st.so1;
-        sa.state[kStDone] = 0;
-      }
+      int64_t* slot = dec_slot(sa.state);
+      slot[kStOffset] = st.kv_len;
+      slot[kStTail] = st.ts1;
+      slot[kStCount] = st.sc1;
+      slot[kStSumOff] = st.so1;
     }
   }
 }
@@ -798,6 +804,11 @@ extern "C" int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int 
     launch_decode<__bf16, false>(a, none, head_dim, batch * hkv, stream);
   BFLY_CHECK_LAUNCH("bfly_decode");
   return BFLY_OK;
+}
+
+extern "C" int64_t bfly_decode_state_words(int64_t batch, int hkv) {
+  if (batch <= 0 || hkv <= 0) return 0;
+  return kStHeader + 4 * batch * hkv;
 }
 
 extern "C" int bfly_decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,

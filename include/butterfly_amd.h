@@ -249,6 +249,13 @@ int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int hkv, int he
                 float scale, void* out, hipStream_t stream);
 
 /*
+ * Length in int64 words of the bfly_decode_step counter array for batch*hkv
+ * sequences: an 8-word header (word 4: error) and one 4-word copy per sequence.
+ * No counterpart in the reference (its counters are host attributes).
+ */
+int64_t bfly_decode_state_words(int64_t batch, int hkv);
+
+/*
  * Device: one decode step with the cache counters held on the device, so a
  * step has fixed arguments and can be captured in a HIP graph.  Same result as
  * CompressedKVCache.update_and_fetch of one token (bna/mlx/compressed_cache.py:94-172:
@@ -256,8 +263,10 @@ int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int hkv, int he
  * tail_size - BS >= W) followed by compressed_butterfly_attention_from_cache for
  * that token (bna/mlx/attention.py:1816-1876), with the layout of the live
  * kv_len (stage = layer_idx mod stage_count at ceil(kv_len / BS) blocks).
- * state: device int64[6] = {offset, tail_size, summary_count, summary_offset,
- * error, done}; `done` must be 0 between steps (the kernel leaves it so).  On a
+ * state: device int64[bfly_decode_state_words(batch, hkv)]: state[4] is the
+ * error word; workgroup g = b*Hkv + kv head keeps its own copy of
+ * {offset, tail_size, summary_count, summary_offset} at state[8 + 4g .. 8 + 4g + 3]
+ * and advances it itself (all copies stay equal; initialise every copy).  On a
  * capacity overflow the step changes nothing and sets state[4] = 1 (the
  * reference's RuntimeError; read it back to raise).
  * Other arguments as bfly_decode; ring_k/ring_v is the ring (capacity > 0).

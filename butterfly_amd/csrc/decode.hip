@@ -560,16 +560,6 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
   }
   const int64_t slot_lo = a.ring ? dec_mod(lo, a.ring) : lo - st.tail_start;
 
-  // ---- append the new token to its ring slot (read back from k_new/v_new below)
-  if (knew != nullptr && tid < 2 * PIECES) {
-    int64_t row = slot_lo + (p - lo);
-    if (a.ring && row >= a.ring) row -= a.ring;
-    const int pc = tid % PIECES;
-    const T* src = tid < PIECES ? knew : vnew;
-    T* dst = tid < PIECES ? rk : rv;
-    *reinterpret_cast<uint4*>(dst + row * D + pc * VEC) = *reinterpret_cast<const uint4*>(src + pc * VEC);
-  }
-
   // ---- stage keys row-major and values transposed; rows >= nk are zero.  The
   // window rows are requested first; the routed selection runs while they are
   // in flight, then the summary rows are requested.
@@ -621,6 +611,16 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
       if (in && r0 >= nw && r0 < nk) v0[it] = *reinterpret_cast<const uint4*>(sum_row(r0 - nw, true) + pc * VEC);
       if (in && r0 + 1 >= nw && r0 + 1 < nk)
         v1[it] = *reinterpret_cast<const uint4*>(sum_row(r0 + 1 - nw, true) + pc * VEC);
+    }
+    // append the new token to its ring slot; requested after every staging load so
+    // that its wait coincides with theirs (the staging reads it from k_new/v_new)
+    if (knew != nullptr && tid < 2 * PIECES) {
+      int64_t row = slot_lo + (p - lo);
+      if (a.ring && row >= a.ring) row -= a.ring;
+      const int pc = tid % PIECES;
+      const T* src = tid < PIECES ? knew : vnew;
+      T* dst = tid < PIECES ? rk : rv;
+      *reinterpret_cast<uint4*>(dst + row * D + pc * VEC) = *reinterpret_cast<const uint4*>(src + pc * VEC);
     }
 #pragma unroll
     for (int it = 0; it < KIT; ++it) {

@@ -22,6 +22,7 @@ from typing import Optional
 import torch
 
 from . import _native
+from ._device import on, stream_of
 
 
 def _dtype_code(t: torch.Tensor) -> int:
@@ -33,7 +34,11 @@ def _dtype_code(t: torch.Tensor) -> int:
 
 
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """Handle of the current stream of t's device (the launch stream of every call)."""
+    return stream_of(t)
+
+
+_on = on
 
 
 def _require_cuda(*ts: torch.Tensor) -> None:
@@ -78,7 +83,7 @@ def block_mean_summaries(x: torch.Tensor, *, seq_len: int, block_size: int, num_
             raise ValueError("x2 must match x in shape and dtype")
         x2 = _c(x2)
         out2 = torch.empty_like(out)
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         _native.call("bfly_block_mean", x.data_ptr(), out.data_ptr(),
                      x2.data_ptr() if x2 is not None else None, out2.data_ptr() if out2 is not None else None,
                      _dtype_code(x), b * h, int(t), d, int(block_size), int(num_blocks), _stream(x))
@@ -104,7 +109,7 @@ def compressed_butterfly_block_index_tensors(layout, *, T: int, local_window_tok
     raw_mask = torch.empty((n, bs, slots), dtype=torch.uint8, device=dev)
     sidx = torch.empty((n, k), dtype=torch.int32, device=dev)
     smask = torch.empty((n, bs, k), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _on(dev):
         _native.call("bfly_prefill_tables", nb.data_ptr(), n, k, bs, int(T), int(local_window_tokens),
                      raw_idx.data_ptr(), raw_mask.data_ptr(), sidx.data_ptr(), smask.data_ptr(), _stream(nb))
     return raw_idx, raw_mask.bool(), sidx, smask.bool()
@@ -129,7 +134,7 @@ def compressed_butterfly_active_index_tensors(layout, *, kv_len: int, query_posi
     sidx = torch.empty((tq, k), dtype=torch.int32, device=dev)
     smask = torch.empty((tq, k), dtype=torch.uint8, device=dev)
     tail = tail_len is not None
-    with torch.cuda.device(dev):
+    with _on(dev):
         _native.call("bfly_active_tables", nb.data_ptr(), n, k, bs, int(kv_len), w, qp.data_ptr(), tq,
                      int(tail_start or 0), int(tail_len) if tail else -1,
                      int(num_summary_blocks) if num_summary_blocks is not None else n,
@@ -170,7 +175,7 @@ def compressed_butterfly_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Te
     ksum, vsum = block_mean_summaries(k, seq_len=t, block_size=bs, num_blocks=n, x2=v)
     out = torch.empty_like(q)
     nb = layout.neighbors
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         _native.call("bfly_prefill", q.data_ptr(), k.data_ptr(), v.data_ptr(), ksum.data_ptr(), vsum.data_ptr(),
                      _dtype_code(q), b, hq, hk, t, d, nb.data_ptr(), n, nb.shape[1], bs,
                      int(local_window_tokens), _scale(scale, d), out.data_ptr(), _stream(q))
@@ -210,14 +215,14 @@ def _attend(q, tail_k, tail_v, pool_k, pool_v, *, layout, q_pos0, qpos_dev, ring
             and int(local_window_tokens) <= 64 and nb.shape[1] <= 16 and pool_k.shape[2] > 0
             and (d in (64, 128) or (d == 256 and q.dtype == torch.bfloat16))):
         # a single row at the newest position: the decode kernel
-        with torch.cuda.device(q.device):
+        with _on(q.device):
             _native.call("bfly_decode", q.data_ptr(), _dtype_code(q), b, hq, hk, d, None, None,
                          tail_k.data_ptr(), tail_v.data_ptr(), int(ring_capacity), int(tail_start), int(kv_len),
                          pool_k.data_ptr(), pool_v.data_ptr(), pool_k.shape[2], int(summary_count),
                          layout.table.topology, nb.shape[0], layout.block_size, int(local_window_tokens),
                          _scale(scale, d), out.data_ptr(), _stream(q))
         return out
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         _native.call("bfly_attend_cache", q.data_ptr(), _dtype_code(q), b, hq, hk, tq, d,
                      qpos_dev.data_ptr() if qpos_dev is not None else None, int(q_pos0),
                      tail_k.data_ptr(), tail_v.data_ptr(), int(ring_capacity), int(tail_start), int(kv_len),

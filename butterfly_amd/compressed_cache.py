@@ -24,7 +24,7 @@ from typing import Any, Optional
 import torch
 
 from . import _native
-from .attention import _c, _dtype_code, _stream
+from .attention import _c, _dtype_code, _on, _stream
 
 
 @dataclass(frozen=True)
@@ -207,7 +207,7 @@ class CompressedKVCache:
         """Pool the due blocks (they predate the new tokens) and raise on overflow."""
         b, h, _, d = self._ring_k.shape
         if n_new:
-            with torch.cuda.device(self._ring_k.device):
+            with _on(self._ring_k.device):
                 _native.call("bfly_cache_compress", self._ring_k.data_ptr(), self._ring_v.data_ptr(),
                              _dtype_code(self._ring_k), b, h, d, self.tail_capacity, first_pos, n_new,
                              self.block_size, self._pool_k.data_ptr(), self._pool_v.data_ptr(),
@@ -233,7 +233,7 @@ class CompressedKVCache:
         b, h, d = int(keys.shape[0]), int(keys.shape[1]), int(keys.shape[3])
         keys, values = _c(keys), _c(values)
         st = _stream(keys)
-        with torch.cuda.device(keys.device):
+        with _on(keys.device):
             _native.call("bfly_cache_append", keys.data_ptr(), values.data_ptr(), _dtype_code(keys), b, h, step, d,
                          self._ring_k.data_ptr(), self._ring_v.data_ptr(), self.tail_capacity, offset0, st)
         self._compress(first_pos, first_slot, n_new, overflow, st)
@@ -275,7 +275,7 @@ class CompressedKVCache:
         b, hq = int(q.shape[0]), int(q.shape[1])
         out = torch.empty_like(q)
         nb = layout.neighbors
-        with torch.cuda.device(q.device):
+        with _on(q.device):
             _native.call("bfly_decode", q.data_ptr(), _dtype_code(q), b, hq, int(keys.shape[1]), d,
                          keys.data_ptr(), values.data_ptr(), self._ring_k.data_ptr(), self._ring_v.data_ptr(),
                          self.tail_capacity, self.offset - self.tail_size, self.offset, self._pool_k.data_ptr(),

@@ -237,7 +237,7 @@ struct MfmaArgs {
 // so HBM traffic of chunk c+1 overlaps the MFMA/softmax work of chunk c.
 template <int D>
 __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1)
-attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunks) {
+attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunks, int hsplit) {
   using C = MfmaCfg<D>;
   __shared__ __attribute__((aligned(16))) unsigned char smem[C::LDS];
   __shared__ int cand_n[kSumSlots], cand_b[kSumSlots];
@@ -249,10 +249,14 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
   const int wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
   const int seg = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = blockIdx.y;
+  // small grids split a GQA group's head pairs over hsplit workgroups
+  const int bh = blockIdx.y / hsplit, hpart = blockIdx.y - bh * hsplit;
   const int bi = bh / a.hkv;
   const int kvh = bh - bi * a.hkv;
   const int gsz = a.hq / a.hkv;
+  const int hper = ((gsz + hsplit - 1) / hsplit + 1) & ~1;     // heads per workgroup, whole pairs
+  const int hlo = hpart * hper;
+  const int hhi = min(gsz, hlo + hper);
   const int cbeg = c_first + seg * seg_chunks;
   const int cend = min(cbeg + seg_chunks, c_first + nchunks);
 
@@ -414,8 +418,8 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
   // (chunk, head) that uses the slot.
   auto refill_q = [&](int u, int c, int hh) {
     int nh = hh + kQPipe, nc = c;
-    if (nh >= gsz) {
-      nh = u;
+    if (nh >= hhi) {
+      nh = hlo + u;
       nc = c + 1;
     }
     if (nc < cend) load_q(u, nc, nh);
@@ -423,7 +427,7 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
 
 #pragma unroll
   for (int u = 0; u < kQPipe; ++u)
-    if (u < gsz) load_q(u, cbeg, u);
+    if (hlo + u < hhi) load_q(u, cbeg, hlo + u);
   fetch_page(cbeg - 1);
   store_page(cbeg - 1);
   fetch_page(cbeg);
@@ -491,12 +495,12 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
       inv = 1.f / fmaxf(lsum, 1e-30f);
     };
 
-    for (int hb = 0; hb < gsz; hb += kQPipe) {
+    for (int hb = hlo; hb < hhi; hb += kQPipe) {
 #pragma unroll
       for (int pp = 0; pp < kQPipe / 2; ++pp) {
         const int h0 = hb + 2 * pp;
-        if (h0 >= gsz) break;
-        const bool two = h0 + 1 < gsz;
+        if (h0 >= hhi) break;
+        const bool two = h0 + 1 < hhi;
         const int u0 = 2 * pp, u1 = 2 * pp + 1;
         if (!wave_active) {
           refill_q(u0, c, h0);
@@ -639,11 +643,20 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
     m.bs = a.bs;
     m.W = a.W;
     m.token_cutoff = a.token_cutoff;
-    dim3 grid((unsigned)nseg, (unsigned)groups);
+    // Head split: a grid far below the resident capacity (e.g. one 384-query chunk)
+    // spreads the group's head pairs over more workgroups (each reloads the small
+    // K/V pages); results are unchanged, every head is computed the same way.
+    const int64_t capacity = a.d <= 128 ? 512 : 256;
+    const int npairs = (a.hq / a.hkv + 1) / 2;
+    int hsplit = 1;
+    while (hsplit < npairs && nseg * groups * hsplit * 2 <= capacity) hsplit *= 2;
+    if (hsplit > npairs) hsplit = npairs;
+    BFLY_CHECK_ARG(groups * hsplit <= 65535, "%s: grid too large", what);
+    dim3 grid((unsigned)nseg, (unsigned)(groups * hsplit));
     switch (a.d) {
-      case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks); break;
-      case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks); break;
-      default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks); break;
+      case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hsplit); break;
+      case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hsplit); break;
+      default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hsplit); break;
     }
   } else {
     BFLY_CHECK_ARG(a.d <= kGenericMaxD, "%s: head_dim=%d > %d", what, a.d, kGenericMaxD);

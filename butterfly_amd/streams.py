@@ -24,7 +24,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _native
-from .attention import _c, _check_heads, _dtype_code, _require_cuda, _stream
+from .attention import _c, _check_heads, _dtype_code, _on, _require_cuda, _stream
 
 Stream = Tuple[torch.Tensor, torch.Tensor, torch.Tensor]
 NEG = -1e30
@@ -66,7 +66,7 @@ def swa_stream_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, n
         return _empty(q)
     q, k, v = _c(q), _c(k), _c(v)
     o, l, m = _outputs(q)
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         _native.call("bfly_swa_stream", q.data_ptr(), k.data_ptr(), v.data_ptr(), _dtype_code(q), b, hq, hk, t, d,
                      max(1, int(n_win)), float(scale), o.data_ptr(), l.data_ptr(), m.data_ptr(), _stream(q))
     return o, l, m
@@ -110,7 +110,7 @@ def compressed_stream_attention(q: torch.Tensor, k_summary: torch.Tensor, v_summ
         routed = ri.to(device=q.device, dtype=torch.int32).contiguous()
         rblocks, kcap = int(ri.shape[1]), int(ri.shape[2])
     o, l, m = _outputs(q)
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         _native.call("bfly_compressed_stream", q.data_ptr(), ks.data_ptr(), vs.data_ptr(), _dtype_code(q), b, hq, hk,
                      t, d, nsum, int(block_size), routed.data_ptr() if routed is not None else None, rblocks, kcap,
                      float(scale), o.data_ptr(), l.data_ptr(), m.data_ptr(), _stream(q))
@@ -136,7 +136,7 @@ def online_softmax_merge(a: Stream, b: Stream) -> torch.Tensor:
     out = torch.empty((bsz, h, t, d), dtype=torch.float32, device=oa.device)
     if rows == 0:
         return out
-    with torch.cuda.device(oa.device):
+    with _on(oa.device):
         _native.call("bfly_softmax_merge", oa_c.data_ptr(), _dtype_code(oa_c), stats[0].data_ptr(),
                      stats[1].data_ptr(), ob_c.data_ptr(), _dtype_code(ob_c), stats[2].data_ptr(),
                      stats[3].data_ptr(), rows, d, out.data_ptr(), _stream(oa))

@@ -14,6 +14,7 @@ from typing import Literal
 import torch
 
 from . import _native
+from ._device import on as _on, stream_of as _stream_of
 
 ButterflyPartnerRule = Literal["xor", "bit_reversal", "benes", "causal_shift", "fixed_stride", "random"]
 ROLE_ORDER = ("self", "local", "partner", "sink")
@@ -113,10 +114,10 @@ def block_neighbor_table_padded(*, num_blocks: int, layer_idx: int, partner_rule
     kcap = 1 + int(local_window_blocks) + int(partner_count) + int(sink_count)
     table = torch.empty((int(num_blocks), kcap), dtype=torch.int32, device=dev)
     degree = torch.empty((int(num_blocks),), dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
+    with _on(dev):
         _native.call("bfly_block_neighbors", int(num_blocks), int(layer_idx), _rule_code(partner_rule),
                      int(local_window_blocks), int(sink_count), int(partner_count), table.data_ptr(), kcap,
-                     degree.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+                     degree.data_ptr(), _stream_of(dev))
     return table, degree
 
 

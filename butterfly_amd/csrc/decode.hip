@@ -484,11 +484,200 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
 // bf16 decode on MFMA.  The GQA group's query heads are the 16 columns of one
 // v_mfma_f32_16x16x32_bf16 tile (heads 16g..16g+15 per pass; one pass up to 16
 // heads), so each wave computes the scores of every head at once:
-//   S^T = K Q^T over 6 tiles of 16 keys (window <= 64 + summaries <= 16, zero-padded),
+//   S^T = K Q^T over 5 tiles of 16 keys (window <= 64 + summaries <= 16, zero-padded),
 //   fp32 softmax per column (shuffles between the 4 lane groups),
 //   O^T = V^T P^T with V transposed in LDS; wave w takes output d-tiles w, w+4, ...
-// Staging, selection, pooling and counters are those of decode_kernel.
+// Staging, selection, pooling and counters follow decode_kernel, in 32-bit
+// arithmetic: the host sends a cache here only when every position, row and
+// element offset stays below 2^30 (else decode_kernel runs), and in step mode
+// the kernel flags counters outside that range as an error.
 constexpr int kDecMfmaKeys = kDecMaxKeys;   // 80 keys staged: 5 score tiles, PV k-steps padded to 96 in registers
+constexpr int kDecPosLimit = 1 << 30;
+
+struct DecState32 {
+  int kv_len, tail_start, nsum, nblocks;
+  int sc0, so0, ts1, sc1, so1;   // step mode: counts before/after, tail size after
+  int n_new;                     // blocks that become due in this step
+  int stage, count, width;       // step mode: topology at nblocks
+  bool err;
+};
+
+// Step-mode counter update of dec_state (compressed_cache.py:94-172) and the
+// topology of bfly_topology_init at the live block count (butterfly.py:39-105).
+template <bool kStep>
+__device__ __forceinline__ DecState32 dec_state32(const DecodeArgs& a, const StepArgs& sa) {
+  DecState32 s{};
+  if constexpr (kStep) {
+    const int64_t* slot = dec_slot(sa.state);
+    const int64_t off0 = slot[kStOffset], ts0 = slot[kStTail], sc0 = slot[kStCount], so0 = slot[kStSumOff];
+    const bool range = (uint64_t)off0 < (uint64_t)kDecPosLimit && (uint64_t)ts0 < (uint64_t)kDecPosLimit &&
+                       (uint64_t)sc0 < (uint64_t)kDecPosLimit && (uint64_t)so0 < (uint64_t)kDecPosLimit;
+    const int ring = (int)a.ring, bs = a.bs, W = a.W, pool_rows = (int)a.pool_rows;
+    const int off1 = (int)off0 + 1;
+    int ts1 = (int)ts0 + 1, sc1 = (int)sc0, so1 = (int)so0, n_new = 0;
+    bool err = !range || ts1 > ring;                        // tail capacity (compressed_cache.py:105-110)
+    while (!err && so1 + bs <= off1 - W) {                  // summarise (:120-149)
+      const int bstart = so1 - (off1 - ts1);
+      if (bstart < 0 || bstart + bs > ts1) break;
+      if (sc1 >= pool_rows || n_new == kDecMaxNew) {        // pool capacity (:128-132)
+        err = true;
+        break;
+      }
+      ++n_new;
+      ++sc1;
+      so1 += bs;
+    }
+    while (ts1 - bs >= W) ts1 -= bs;                        // trim: target max(W, step + W - 1) = W
+    s.err = err;
+    s.sc0 = (int)sc0;
+    s.so0 = (int)so0;
+    s.ts1 = ts1;
+    s.sc1 = sc1;
+    s.so1 = so1;
+    s.n_new = n_new;
+    s.kv_len = off1;
+    s.tail_start = off1 - ts1;
+    s.nsum = sc1;
+    s.nblocks = (int)(((uint32_t)off1 + (uint32_t)bs - 1u) / (uint32_t)bs);
+    const int w = s.nblocks <= 1 ? 1 : 32 - __clz(s.nblocks - 1);
+    s.width = w;
+    s.count = sa.rule == BFLY_RULE_BENES ? (2 * w - 2 > 1 ? 2 * w - 2 : 1) : w;
+    s.stage = (int)dec_mod_layer(sa.layer_idx, s.count);
+  } else {
+    s.kv_len = (int)a.kv_len;
+    s.tail_start = (int)a.tail_start;
+    s.nsum = (int)a.nsum;
+    s.nblocks = (int)a.nblocks;
+    s.width = a.topo.width;
+  }
+  return s;
+}
+
+// partner_block (bfly_topology.h) for blocks below 2^30.
+__device__ __forceinline__ int partner32(int block, int bit, int nblocks, int rule, int width) {
+  if (bit < 0 || bit >= (width > 1 ? width : 1)) return -1;
+  int p;
+  switch (rule) {
+    case BFLY_RULE_CAUSAL_SHIFT: p = block - (1 << bit); break;
+    case BFLY_RULE_XOR:
+    case BFLY_RULE_BENES: p = block ^ (1 << bit); break;
+    case BFLY_RULE_FIXED_STRIDE: p = block - 1; break;
+    case BFLY_RULE_RANDOM: {
+      if (block <= 0) return -1;
+      const uint32_t seed = (uint32_t)block * 2654435761u + (uint32_t)bit * 374761393u;
+      p = (int)(seed % (uint32_t)block);
+      break;
+    }
+    default: {   // bit reversal over `width` bits (block < 2^width)
+      const int sh = 32 - width;
+      const uint32_t rev = __builtin_bitreverse32((uint32_t)block) >> sh;
+      p = (int)(__builtin_bitreverse32(rev ^ (1u << bit)) >> sh);
+      break;
+    }
+  }
+  if (p < 0 || p >= nblocks || p > block) return -1;
+  return p;
+}
+
+// dec_select in 32-bit; in step mode lane j derives its partner bit from the
+// stage (bfly_topology_init's rule) instead of reading a bit array.
+template <bool kStep>
+__device__ __forceinline__ int dec_select32(int p, int blk, const DecodeArgs& a, const StepArgs& sa,
+                                            const DecState32& s, int lane, int* sel) {
+  const int cut = max(p - a.W + 1, 0);
+  const int rule = kStep ? sa.rule : a.topo.rule;
+  const int lwb = kStep ? sa.lwb : a.topo.local_window_blocks;
+  const int npart = kStep ? sa.partners : a.topo.partner_count;
+  const int sinks = kStep ? sa.sinks : a.topo.sink_count;
+  const int nsink = min(sinks, s.nblocks);
+  const int kc = 1 + lwb + npart + sinks;
+  int cand = -1;
+  if (lane < kc) {
+    if (lane == 0) {
+      cand = blk;
+    } else if (lane <= lwb) {
+      cand = blk - lane;
+    } else if (lane <= lwb + npart) {
+      const int j = lane - 1 - lwb;
+      int bit = 0;
+      if constexpr (kStep) {
+        int ph = s.stage + j;
+        if (rule == BFLY_RULE_BENES) {
+          while (ph >= s.count) ph -= s.count;
+          bit = s.width <= 1 ? 0 : (ph < s.width ? ph : 2 * s.width - 2 - ph);
+        } else {
+          while (ph >= s.width) ph -= s.width;
+          bit = ph;
+        }
+      } else {
+#pragma unroll
+        for (int jj = 0; jj < BFLY_MAX_PARTNERS; ++jj)
+          if (jj == j) bit = a.topo.partner_bits[jj];
+      }
+      cand = partner32(blk, bit, s.nblocks, rule, s.width);
+    } else {
+      const int sk = lane - 1 - lwb - npart;
+      cand = sk < nsink ? sk : -1;
+    }
+    if (cand < 0 || cand >= s.nblocks) cand = -1;
+  }
+  bool keep = cand >= 0;
+  for (int i = 0; i < kc; ++i) {                  // kc is uniform: lane i's entry as a scalar
+    const int ci = __builtin_amdgcn_readlane(cand, i);
+    if (i < lane && ci == cand) keep = false;
+  }
+  const bool take = keep && cand < blk && cand < s.nsum && (cand + 1) * a.bs <= cut;
+  const unsigned long long mask = __ballot(take);
+  if (take) sel[__popcll(mask & ((1ull << lane) - 1ull))] = cand;
+  __builtin_amdgcn_wave_barrier();
+  return __popcll(mask);
+}
+
+// x where c holds, else zero (a value select: no branch, no memory)
+__device__ __forceinline__ uint4 keep_if(bool c, uint4 x) {
+  return make_uint4(c ? x.x : 0u, c ? x.y : 0u, c ? x.z : 0u, c ? x.w : 0u);
+}
+
+// dec_pool with 32-bit ring offsets (same summation order).
+template <int D>
+__device__ __forceinline__ void dec_pool32(const DecodeArgs& a, const DecState32& s, const __bf16* rk,
+                                        const __bf16* rv, __bf16* pk, __bf16* pv, float* part, int tid) {
+  constexpr int VEC = 8;
+  constexpr int LPR = D / VEC;
+  constexpr int RS = 256 / LPR;
+  const int ring = (int)a.ring;
+  for (int j = 0; j < s.n_new; ++j) {
+    const int pos0 = s.so0 + j * a.bs;
+    int row0 = (int)((uint32_t)pos0 % (uint32_t)ring);
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      const __bf16* src = kv ? rv : rk;
+      __bf16* dst = (kv ? pv : pk) + (uint32_t)(s.sc0 + j) * D;
+      const int c = tid % LPR, sl = tid / LPR;
+      float acc[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+      for (int tok = sl; tok < a.bs; tok += RS) {
+        int row = row0 + tok;
+        while (row >= ring) row -= ring;
+        const uint4 raw = *reinterpret_cast<const uint4*>(src + (uint32_t)row * D + c * VEC);
+        const __bf16* x = reinterpret_cast<const __bf16*>(&raw);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += (float)x[e];
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) part[sl * D + c * VEC + e] = acc[e];
+      __syncthreads();
+      for (int col = tid; col < D; col += 256) {
+        float tot = 0.f;
+        for (int k = 0; k < RS; ++k) tot += part[k * D + col];
+        const __bf16 val = (__bf16)(tot / (float)a.bs);
+        dst[col] = val;
+      }
+      __syncthreads();
+    }
+  }
+}
 
 template <int D, bool kStep>
 __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(DecodeArgs a, StepArgs sa) {
@@ -514,130 +703,153 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
   T* Ks = reinterpret_cast<T*>(stage_lds);
   T* Vt = reinterpret_cast<T*>(stage_lds + KS_BYTES);
   __shared__ int selw[4][kDecMaxSum];
-  __shared__ __attribute__((aligned(16))) T newrow[kStep ? kDecMaxNew * 2 : 1][kStep ? D : 1];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
-  const int64_t bh = blockIdx.x;
-  const int64_t bi = bh / a.hkv;
-  const int kvh = (int)(bh - bi * a.hkv);
+  const int bh = blockIdx.x;
+  const int bi = bh / a.hkv;
+  const int kvh = bh - bi * a.hkv;
   const int gsz = a.hq / a.hkv;
-  const T* qhead = reinterpret_cast<const T*>(a.q) + (bi * a.hq + (int64_t)kvh * gsz) * D;
+  const T* qhead = reinterpret_cast<const T*>(a.q) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz) * D;
 
-  // Q^T fragments of heads 16*hg + lq (B operand: d = lg*(D/4) + 8*ks + [0, 8)); the
-  // first pass is issued before anything else so its latency hides behind the rest
+  // Q^T fragments of heads 16*hg + lq (B operand: d = lg*(D/4) + 8*ks + [0, 8)).
+  // Columns past the group read its last head: they are computed and never
+  // stored.  The loads are unconditional, so nothing waits on them before the
+  // scores.
   bf16x8 qf[KSTEPS];
   auto load_q = [&](int hg) {
-    const int head = 16 * hg + lq;
+    const int head = min(16 * hg + lq, gsz - 1);
+    const T* qrow = qhead + (uint32_t)head * D + lg * (D / 4);
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks)
-      qf[ks] = head < gsz ? *reinterpret_cast<const bf16x8*>(qhead + (int64_t)head * D + lg * (D / 4) + 8 * ks)
-                          : bf16x8{};
+    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 8 * ks);
   };
   load_q(0);
 
-  const DecState st = dec_state<kStep>(a, sa);
+  const DecState32 st = dec_state32<kStep>(a, sa);
   if (kStep && st.err) {
     if (tid == 0) sa.state[kStError] = 1;
     return;
   }
-  const int64_t p = st.kv_len - 1;
-  int64_t lo = p - a.W + 1;
-  if (lo < st.tail_start) lo = st.tail_start;
-  if (lo < 0) lo = 0;
-  const int nw = (int)(p - lo + 1);
+  const int p = st.kv_len - 1;
+  const int lo = max(max(p - a.W + 1, st.tail_start), 0);
+  const int nw = p - lo + 1;
+  const int ring = (int)a.ring;
 
-  const T* knew = a.k_new ? reinterpret_cast<const T*>(a.k_new) + bh * D : nullptr;
-  const T* vnew = a.v_new ? reinterpret_cast<const T*>(a.v_new) + bh * D : nullptr;
-  T* rk = reinterpret_cast<T*>(a.ring_k) + bh * a.kv_rows * D;
-  T* rv = reinterpret_cast<T*>(a.ring_v) + bh * a.kv_rows * D;
-  T* pk = reinterpret_cast<T*>(const_cast<void*>(a.pool_k)) + bh * a.pool_rows * D;
-  T* pv = reinterpret_cast<T*>(const_cast<void*>(a.pool_v)) + bh * a.pool_rows * D;
+  const T* knew = a.k_new ? reinterpret_cast<const T*>(a.k_new) + (int64_t)bh * D : nullptr;
+  const T* vnew = a.v_new ? reinterpret_cast<const T*>(a.v_new) + (int64_t)bh * D : nullptr;
+  T* rk = reinterpret_cast<T*>(a.ring_k) + (int64_t)bh * a.kv_rows * D;
+  T* rv = reinterpret_cast<T*>(a.ring_v) + (int64_t)bh * a.kv_rows * D;
+  T* pk = reinterpret_cast<T*>(const_cast<void*>(a.pool_k)) + (int64_t)bh * a.pool_rows * D;
+  T* pv = reinterpret_cast<T*>(const_cast<void*>(a.pool_v)) + (int64_t)bh * a.pool_rows * D;
 
   if constexpr (kStep) {
-    float* part = reinterpret_cast<float*>(stage_lds);
-    dec_pool<T, D>(a, st, rk, rv, pk, pv, part, newrow, tid);
+    if (st.n_new > 0) dec_pool32<D>(a, st, rk, rv, pk, pv, reinterpret_cast<float*>(stage_lds), tid);
   }
-  const int64_t slot_lo = a.ring ? dec_mod(lo, a.ring) : lo - st.tail_start;
+  const int slot_lo = ring ? (int)((uint32_t)lo % (uint32_t)ring) : lo - st.tail_start;
+  const int r_new = knew != nullptr ? nw - 1 : -1;   // row of position p: read from k_new/v_new
 
-  // ---- stage keys row-major and values transposed; rows >= nk are zero.  The
-  // window rows are requested first; the routed selection runs while they are
-  // in flight, then the summary rows are requested.
+  // element offset of window row r (< nw) in the ring or linear tail
+  auto ring_off = [&](int r) -> uint32_t {
+    int row = slot_lo + r;
+    if (ring && row >= ring) row -= ring;
+    return (uint32_t)row * D;
+  };
+  // Window row r, clamped to the last one: every load is issued unconditionally
+  // from valid memory, and rows r >= nw are zeroed when they are written to LDS.
   auto win_row = [&](int r, bool vside) -> const T* {
-    if (knew != nullptr && lo + r == p) return vside ? vnew : knew;
-    int64_t row = slot_lo + r;
-    if (a.ring && row >= a.ring) row -= a.ring;
-    return (vside ? rv : rk) + row * D;
+    r = min(r, nw - 1);
+    if (r == r_new) return vside ? vnew : knew;
+    return (vside ? rv : rk) + ring_off(r);
   };
-  auto sum_row = [&](int j, bool vside) -> const T* {
-    const int64_t n = selw[wave][j];
-    if (kStep && n >= st.sc0) return &newrow[2 * (n - st.sc0) + (vside ? 1 : 0)][0];
-    return (vside ? pv : pk) + n * D;
-  };
-  int nk;
+
+  // ---- staging: keys 0..63 are the window rows (lo + r), keys 64..79 the routed
+  // summaries in row order; unused keys are zero rows and masked in the scores.
+  // K is stored row-major, V transposed (pairs of keys per 32-bit LDS word).
+  // Window rows are requested first, the routed selection runs while they are in
+  // flight, then the summary rows are requested.
+  constexpr int WK = kDecMaxWin * PIECES / 256;                   // window K pieces per thread
+  constexpr int SKN = kDecMaxSum * PIECES;                         // summary K pieces
+  constexpr int SK = (SKN + 255) / 256;
+  constexpr int WV = (kDecMaxWin / 2) * PIECES / 256;              // window V row pairs per thread
+  constexpr int SVN = (kDecMaxSum / 2) * PIECES;                   // summary V row pairs
+  constexpr int SV = (SVN + 255) / 256;
+  static_assert(kDecMaxWin * PIECES % 256 == 0 && (kDecMaxWin / 2) * PIECES % 256 == 0, "staging split");
+  static_assert(kDecMaxWin + kDecMaxSum == kDecMfmaKeys, "key layout");
+  int ns;
   {
-    uint4 kx[KIT], v0[VIT], v1[VIT];
+    uint4 kx[WK], v0[WV], v1[WV], skx[SK], sv0[SV], sv1[SV];
 #pragma unroll
-    for (int it = 0; it < KIT; ++it) {
+    for (int it = 0; it < WK; ++it) {
       const int i = tid + it * 256;
-      const int r = i / PIECES, pc = i % PIECES;
-      kx[it] = i < KITEMS && r < nw ? *reinterpret_cast<const uint4*>(win_row(r, false) + pc * VEC)
-                                    : make_uint4(0, 0, 0, 0);
+      kx[it] = *reinterpret_cast<const uint4*>(win_row(i / PIECES, false) + (i % PIECES) * VEC);
     }
 #pragma unroll
-    for (int it = 0; it < VIT; ++it) {
+    for (int it = 0; it < WV; ++it) {
       const int i = tid + it * 256;
-      const int kp = i % (kDecMfmaKeys / 2), pc = i / (kDecMfmaKeys / 2);
-      const int r0 = 2 * kp;
-      const bool in = i < VITEMS;
-      v0[it] = in && r0 < nw ? *reinterpret_cast<const uint4*>(win_row(r0, true) + pc * VEC) : make_uint4(0, 0, 0, 0);
-      v1[it] = in && r0 + 1 < nw ? *reinterpret_cast<const uint4*>(win_row(r0 + 1, true) + pc * VEC)
-                                 : make_uint4(0, 0, 0, 0);
+      const int kp = i % (kDecMaxWin / 2), pc = i / (kDecMaxWin / 2);
+      v0[it] = *reinterpret_cast<const uint4*>(win_row(2 * kp, true) + pc * VEC);
+      v1[it] = *reinterpret_cast<const uint4*>(win_row(2 * kp + 1, true) + pc * VEC);
     }
-    const int ns = dec_select(p, a, st, lane, selw[wave]);
-    nk = nw + ns;
+    const int blk = min((int)((uint32_t)p / (uint32_t)a.bs), st.nblocks - 1);
+    ns = dec_select32<kStep>(p, blk, a, sa, st, lane, selw[wave]);
+    // summary j: pool row selw[j] (row 0 stands in for j >= ns; zeroed below)
+    auto sum_row = [&](int j, bool vside) -> const T* {
+      const int n = j < ns ? selw[wave][j] : 0;
+      return (vside ? pv : pk) + (uint32_t)n * D;
+    };
 #pragma unroll
-    for (int it = 0; it < KIT; ++it) {
-      const int i = tid + it * 256;
-      const int r = i / PIECES, pc = i % PIECES;
-      if (i < KITEMS && r >= nw && r < nk) kx[it] = *reinterpret_cast<const uint4*>(sum_row(r - nw, false) + pc * VEC);
+    for (int it = 0; it < SK; ++it) {
+      const int i = min(tid + it * 256, SKN - 1);
+      skx[it] = *reinterpret_cast<const uint4*>(sum_row(i / PIECES, false) + (i % PIECES) * VEC);
     }
 #pragma unroll
-    for (int it = 0; it < VIT; ++it) {
-      const int i = tid + it * 256;
-      const int kp = i % (kDecMfmaKeys / 2), pc = i / (kDecMfmaKeys / 2);
-      const int r0 = 2 * kp;
-      const bool in = i < VITEMS;
-      if (in && r0 >= nw && r0 < nk) v0[it] = *reinterpret_cast<const uint4*>(sum_row(r0 - nw, true) + pc * VEC);
-      if (in && r0 + 1 >= nw && r0 + 1 < nk)
-        v1[it] = *reinterpret_cast<const uint4*>(sum_row(r0 + 1 - nw, true) + pc * VEC);
+    for (int it = 0; it < SV; ++it) {
+      const int i = min(tid + it * 256, SVN - 1);
+      const int kp = i % (kDecMaxSum / 2), pc = i / (kDecMaxSum / 2);
+      sv0[it] = *reinterpret_cast<const uint4*>(sum_row(2 * kp, true) + pc * VEC);
+      sv1[it] = *reinterpret_cast<const uint4*>(sum_row(2 * kp + 1, true) + pc * VEC);
     }
     // append the new token to its ring slot; requested after every staging load so
     // that its wait coincides with theirs (the staging reads it from k_new/v_new)
     if (knew != nullptr && tid < 2 * PIECES) {
-      int64_t row = slot_lo + (p - lo);
-      if (a.ring && row >= a.ring) row -= a.ring;
       const int pc = tid % PIECES;
       const T* src = tid < PIECES ? knew : vnew;
       T* dst = tid < PIECES ? rk : rv;
-      *reinterpret_cast<uint4*>(dst + row * D + pc * VEC) = *reinterpret_cast<const uint4*>(src + pc * VEC);
+      *reinterpret_cast<uint4*>(dst + ring_off(nw - 1) + pc * VEC) = *reinterpret_cast<const uint4*>(src + pc * VEC);
     }
+    // V^T words of keys key0, key0 + 1 (bf16 pairs) for the 8 d of piece pc
+    auto put_vt = [&](int key0, int pc, uint4 a0, uint4 a1) {
+      const uint32_t w0[4] = {a0.x, a0.y, a0.z, a0.w}, w1[4] = {a1.x, a1.y, a1.z, a1.w};
 #pragma unroll
-    for (int it = 0; it < KIT; ++it) {
+      for (int j = 0; j < 4; ++j) {
+        T* col = Vt + (pc * 8 + 2 * j) * VTP + key0;
+        *reinterpret_cast<uint32_t*>(col) = (w0[j] & 0xffffu) | (w1[j] << 16);
+        *reinterpret_cast<uint32_t*>(col + VTP) = (w0[j] >> 16) | (w1[j] & 0xffff0000u);
+      }
+    };
+#pragma unroll
+    for (int it = 0; it < WK; ++it) {
       const int i = tid + it * 256;
       const int r = i / PIECES, pc = i % PIECES;
-      if (i < KITEMS) *reinterpret_cast<uint4*>(Ks + r * KP + pc * VEC) = kx[it];
+      *reinterpret_cast<uint4*>(Ks + r * KP + pc * VEC) = keep_if(r < nw, kx[it]);
     }
 #pragma unroll
-    for (int it = 0; it < VIT; ++it) {
+    for (int it = 0; it < WV; ++it) {
       const int i = tid + it * 256;
-      const int kp = i % (kDecMfmaKeys / 2), pc = i / (kDecMfmaKeys / 2);
-      if (i >= VITEMS) continue;
-      const uint16_t* e0 = reinterpret_cast<const uint16_t*>(&v0[it]);
-      const uint16_t* e1 = reinterpret_cast<const uint16_t*>(&v1[it]);
+      const int kp = i % (kDecMaxWin / 2), pc = i / (kDecMaxWin / 2);
+      put_vt(2 * kp, pc, keep_if(2 * kp < nw, v0[it]), keep_if(2 * kp + 1 < nw, v1[it]));
+    }
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        *reinterpret_cast<uint32_t*>(Vt + (pc * 8 + j) * VTP + 2 * kp) = (uint32_t)e0[j] | ((uint32_t)e1[j] << 16);
+    for (int it = 0; it < SK; ++it) {
+      const int i = tid + it * 256;
+      const int j = i / PIECES, pc = i % PIECES;
+      if (i < SKN) *reinterpret_cast<uint4*>(Ks + (kDecMaxWin + j) * KP + pc * VEC) = keep_if(j < ns, skx[it]);
+    }
+#pragma unroll
+    for (int it = 0; it < SV; ++it) {
+      const int i = tid + it * 256;
+      const int kp = i % (kDecMaxSum / 2), pc = i / (kDecMaxSum / 2);
+      if (i < SVN) put_vt(kDecMaxWin + 2 * kp, pc, keep_if(2 * kp < ns, sv0[it]), keep_if(2 * kp + 1 < ns, sv1[it]));
     }
   }
   __syncthreads();
@@ -657,14 +869,17 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[ks], acc, 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sc[t][i] = 16 * t + 4 * lg + i < nk ? acc[i] : -INFINITY;
+      for (int i = 0; i < 4; ++i) {
+        const int key = 16 * t + 4 * lg + i;
+        sc[t][i] = key < nw || (key >= kDecMaxWin && key < kDecMaxWin + ns) ? acc[i] : -INFINITY;
+      }
     }
     float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < NT; ++t) mx = fmaxf(mx, fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])));
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float nm = -mx * sl2;                      // nk >= 1: every column has a finite max
+    const float nm = -mx * sl2;                      // nw >= 1: every column has a finite max
     float lsum = 0.f;
     bf16x8 pf[NPR];
     pf[NPR - 1] = bf16x8{};
@@ -680,7 +895,7 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
     lsum += __shfl_xor(lsum, 32);
     const float inv = 1.f / fmaxf(lsum, 1e-30f);
     const int head = 16 * hg + lq;
-    __bf16* orow = reinterpret_cast<__bf16*>(a.out) + (bi * a.hq + (int64_t)kvh * gsz + head) * D;
+    __bf16* orow = reinterpret_cast<__bf16*>(a.out) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz + head) * D;
     // O^T = V^T P^T: tile (mt, half) row r holds d = mt*32 + (r/4)*8 + half*4 + r%4, and its
     // k index runs over keys (tile 2pr, 4lg..4lg+3) then (tile 2pr+1, 4lg..4lg+3), the
     // order of this lane's P fragment, so no lane exchange is needed.
@@ -725,9 +940,14 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
 
 template <typename T, bool kStep>
 static void launch_decode(const DecodeArgs& a, const StepArgs& sa, int d, int64_t grid, hipStream_t stream) {
-  // bf16 with a positive scale (folded into exp2) runs on MFMA; fp32 on the lane-per-key kernel
+  // bf16 with a positive scale (folded into exp2) runs on MFMA when its 32-bit
+  // positions and offsets suffice; fp32 and larger caches on the lane-per-key kernel
   if constexpr (sizeof(T) == 2) {
-    if (a.scale > 0.f) {
+    const int64_t lim = kDecPosLimit;
+    const bool fits = a.kv_rows * d < lim && a.pool_rows * d < lim && a.ring < lim &&
+                      (kStep ? (a.pool_rows + 2) * a.bs + a.ring + a.W < lim
+                             : a.kv_len < lim && a.nblocks < lim && a.nsum < lim);
+    if (a.scale > 0.f && fits) {
       switch (d) {
         case 64:
           hipLaunchKernelGGL((decode_mfma_kernel<64, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, a, sa);

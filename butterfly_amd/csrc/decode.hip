@@ -93,6 +93,27 @@ __device__ __forceinline__ bfly_topology_t topology_at(int64_t n, const StepArgs
   return t;
 }
 
+// Division of n < 2^31 by a fixed d >= 1 without a divide: with l = ceil(log2 d)
+// and m = ceil(2^(31+l) / d) (< 2^32), floor(n / d) = (n * m) >> (31 + l),
+// exact because m * d - 2^(31+l) < d <= 2^l (Granlund and Montgomery, "Division
+// by invariant integers using multiplication", PLDI 1994, theorem 4.2).
+struct FastDiv {
+  uint32_t m = 1u << 31;
+  int sh = 31;
+  uint32_t d = 1;
+  __host__ static FastDiv make(uint32_t d) {
+    FastDiv f;
+    int l = 0;
+    while (l < 32 && (1ull << l) < d) ++l;
+    f.m = (uint32_t)(((1ull << (31 + l)) + d - 1) / d);
+    f.sh = 31 + l;
+    f.d = d;
+    return f;
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const { return (uint32_t)(((uint64_t)n * m) >> sh); }
+  __device__ __forceinline__ uint32_t mod(uint32_t n) const { return n - div(n) * d; }
+};
+
 struct DecodeArgs {
   const void* q;          // [B, Hq, 1, d]
   void* out;              // [B, Hq, 1, d]
@@ -112,6 +133,7 @@ struct DecodeArgs {
   int64_t nblocks;
   int hq, hkv, bs, W;
   float scale;
+  FastDiv bs_div, ring_div, hkv_div;   // MFMA path: block_size, ring capacity, Hkv
 };
 
 __device__ __forceinline__ float dec_wave_max(float v) {
@@ -538,7 +560,7 @@ __device__ __forceinline__ DecState32 dec_state32(const DecodeArgs& a, const Ste
     s.kv_len = off1;
     s.tail_start = off1 - ts1;
     s.nsum = sc1;
-    s.nblocks = (int)(((uint32_t)off1 + (uint32_t)bs - 1u) / (uint32_t)bs);
+    s.nblocks = (int)a.bs_div.div((uint32_t)(off1 + bs - 1));
     const int w = s.nblocks <= 1 ? 1 : 32 - __clz(s.nblocks - 1);
     s.width = w;
     s.count = sa.rule == BFLY_RULE_BENES ? (2 * w - 2 > 1 ? 2 * w - 2 : 1) : w;
@@ -633,6 +655,24 @@ __device__ __forceinline__ int dec_select32(int p, int blk, const DecodeArgs& a,
   return __popcll(mask);
 }
 
+// Max / sum of v over lanes L, L^16, L^32, L^48 (the four lane groups that hold
+// one MFMA column), on the VALU: v_permlane16_swap / v_permlane32_swap exchange
+// rows of 16 / halves of 32 lanes, so max(a, b) of a swapped pair is the
+// reduction with lane ^ 16 (^ 32) in every lane.  Same order as two xor
+// shuffles (16, then 32), so the sums are bit-identical to that form.
+__device__ __forceinline__ float col_max4(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float col_sum4(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // x where c holds, else zero (a value select: no branch, no memory)
 __device__ __forceinline__ uint4 keep_if(bool c, uint4 x) {
   return make_uint4(c ? x.x : 0u, c ? x.y : 0u, c ? x.z : 0u, c ? x.w : 0u);
@@ -648,7 +688,7 @@ __device__ __forceinline__ void dec_pool32(const DecodeArgs& a, const DecState32
   const int ring = (int)a.ring;
   for (int j = 0; j < s.n_new; ++j) {
     const int pos0 = s.so0 + j * a.bs;
-    int row0 = (int)((uint32_t)pos0 % (uint32_t)ring);
+    int row0 = (int)a.ring_div.mod((uint32_t)pos0);
 #pragma unroll
     for (int kv = 0; kv < 2; ++kv) {
       const __bf16* src = kv ? rv : rk;
@@ -707,7 +747,7 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
   const int bh = blockIdx.x;
-  const int bi = bh / a.hkv;
+  const int bi = (int)a.hkv_div.div((uint32_t)bh);
   const int kvh = bh - bi * a.hkv;
   const int gsz = a.hq / a.hkv;
   const T* qhead = reinterpret_cast<const T*>(a.q) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz) * D;
@@ -745,7 +785,7 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
   if constexpr (kStep) {
     if (st.n_new > 0) dec_pool32<D>(a, st, rk, rv, pk, pv, reinterpret_cast<float*>(stage_lds), tid);
   }
-  const int slot_lo = ring ? (int)((uint32_t)lo % (uint32_t)ring) : lo - st.tail_start;
+  const int slot_lo = ring ? (int)a.ring_div.mod((uint32_t)lo) : lo - st.tail_start;
   const int r_new = knew != nullptr ? nw - 1 : -1;   // row of position p: read from k_new/v_new
 
   // element offset of window row r (< nw) in the ring or linear tail
@@ -790,7 +830,7 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
       v0[it] = *reinterpret_cast<const uint4*>(win_row(2 * kp, true) + pc * VEC);
       v1[it] = *reinterpret_cast<const uint4*>(win_row(2 * kp + 1, true) + pc * VEC);
     }
-    const int blk = min((int)((uint32_t)p / (uint32_t)a.bs), st.nblocks - 1);
+    const int blk = min((int)a.bs_div.div((uint32_t)p), st.nblocks - 1);
     ns = dec_select32<kStep>(p, blk, a, sa, st, lane, selw[wave]);
     // summary j: pool row selw[j] (row 0 stands in for j >= ns; zeroed below)
     auto sum_row = [&](int j, bool vside) -> const T* {
@@ -877,8 +917,7 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
     float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < NT; ++t) mx = fmaxf(mx, fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = col_max4(mx);
     const float nm = -mx * sl2;                      // nw >= 1: every column has a finite max
     float lsum = 0.f;
     bf16x8 pf[NPR];
@@ -891,9 +930,8 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
         lsum += e;
         pf[t / 2][(t % 2) * 4 + i] = (__bf16)e;
       }
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
-    const float inv = 1.f / fmaxf(lsum, 1e-30f);
+    lsum = col_sum4(lsum);
+    const float inv = __builtin_amdgcn_rcpf(fmaxf(lsum, 1e-30f));
     const int head = 16 * hg + lq;
     __bf16* orow = reinterpret_cast<__bf16*>(a.out) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz + head) * D;
     // O^T = V^T P^T: tile (mt, half) row r holds d = mt*32 + (r/4)*8 + half*4 + r%4, and its
@@ -948,15 +986,19 @@ static void launch_decode(const DecodeArgs& a, const StepArgs& sa, int d, int64_
                       (kStep ? (a.pool_rows + 2) * a.bs + a.ring + a.W < lim
                              : a.kv_len < lim && a.nblocks < lim && a.nsum < lim);
     if (a.scale > 0.f && fits) {
+      DecodeArgs m = a;
+      m.bs_div = FastDiv::make((uint32_t)a.bs);
+      m.ring_div = FastDiv::make(a.ring > 0 ? (uint32_t)a.ring : 1u);
+      m.hkv_div = FastDiv::make((uint32_t)a.hkv);
       switch (d) {
         case 64:
-          hipLaunchKernelGGL((decode_mfma_kernel<64, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, a, sa);
+          hipLaunchKernelGGL((decode_mfma_kernel<64, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, m, sa);
           return;
         case 128:
-          hipLaunchKernelGGL((decode_mfma_kernel<128, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, a, sa);
+          hipLaunchKernelGGL((decode_mfma_kernel<128, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, m, sa);
           return;
         default:
-          hipLaunchKernelGGL((decode_mfma_kernel<256, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, a, sa);
+          hipLaunchKernelGGL((decode_mfma_kernel<256, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, m, sa);
           return;
       }
     }

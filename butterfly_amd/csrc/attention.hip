@@ -197,13 +197,17 @@ struct MfmaCfg {
   static constexpr int LDS = K_BYTES + V_BYTES;
 };
 
-// Swap 16 bytes with lane ^ 8 (within each 16-lane row).
+// Swap 16 bytes with lane ^ 8 (within each 16-lane row): DPP row_ror:8 rotates
+// each row of 16 lanes by 8, which is lane ^ 8; a VALU move, no LDS traffic.
+__device__ __forceinline__ uint32_t ror8(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xf, 0xf, false);
+}
 __device__ __forceinline__ bf16x8 xchg8(bf16x8 v) {
   uint4 u = __builtin_bit_cast(uint4, v);
-  u.x = __shfl_xor(u.x, 8);
-  u.y = __shfl_xor(u.y, 8);
-  u.z = __shfl_xor(u.z, 8);
-  u.w = __shfl_xor(u.w, 8);
+  u.x = ror8(u.x);
+  u.y = ror8(u.y);
+  u.z = ror8(u.z);
+  u.w = ror8(u.w);
   return __builtin_bit_cast(bf16x8, u);
 }
 
@@ -478,8 +482,7 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
       float mx = -INFINITY;
 #pragma unroll
       for (int t = 0; t < 6; ++t) mx = fmaxf(mx, fmaxf(fmaxf(st[t][0], st[t][1]), fmaxf(st[t][2], st[t][3])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = col_max4(mx);
       const float nm = mx == -INFINITY ? 0.f : -mx * sl2;
       float lsum = 0.f;
 #pragma unroll
@@ -490,9 +493,8 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
           lsum += e;
           pf[t / 2][(t % 2) * 4 + i] = (__bf16)e;
         }
-      lsum += __shfl_xor(lsum, 16);
-      lsum += __shfl_xor(lsum, 32);
-      inv = 1.f / fmaxf(lsum, 1e-30f);
+      lsum = col_sum4(lsum);
+      inv = __builtin_amdgcn_rcpf(fmaxf(lsum, 1e-30f));
     };
 
     for (int hb = hlo; hb < hhi; hb += kQPipe) {

@@ -44,6 +44,24 @@ __device__ __forceinline__ float from_f32<float>(float x) { return x; }
 template <>
 __device__ __forceinline__ __bf16 from_f32<__bf16>(float x) { return (__bf16)x; }
 
+// Max / sum of v over lanes L, L^16, L^32, L^48 (the four lane groups that hold
+// one MFMA column), on the VALU: v_permlane16_swap / v_permlane32_swap exchange
+// rows of 16 / halves of 32 lanes, so max(a, b) of a swapped pair is the
+// reduction with lane ^ 16 (^ 32) in every lane.  Same order as two xor
+// shuffles (16, then 32), so the sums are bit-identical to that form.
+__device__ __forceinline__ float col_max4(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float col_sum4(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Vectorised paths issue 16-byte loads/stores: tensor base pointers must be 16-byte aligned.
 __host__ __forceinline__ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 

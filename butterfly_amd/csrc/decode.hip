@@ -655,24 +655,6 @@ __device__ __forceinline__ int dec_select32(int p, int blk, const DecodeArgs& a,
   return __popcll(mask);
 }
 
-// Max / sum of v over lanes L, L^16, L^32, L^48 (the four lane groups that hold
-// one MFMA column), on the VALU: v_permlane16_swap / v_permlane32_swap exchange
-// rows of 16 / halves of 32 lanes, so max(a, b) of a swapped pair is the
-// reduction with lane ^ 16 (^ 32) in every lane.  Same order as two xor
-// shuffles (16, then 32), so the sums are bit-identical to that form.
-__device__ __forceinline__ float col_max4(float v) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float col_sum4(float v) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
 // x where c holds, else zero (a value select: no branch, no memory)
 __device__ __forceinline__ uint4 keep_if(bool c, uint4 x) {
   return make_uint4(c ? x.x : 0u, c ? x.y : 0u, c ? x.z : 0u, c ? x.w : 0u);

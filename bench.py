@@ -534,6 +534,33 @@ def cpu_baseline(q, k, v, ref_lays, repeats=3, max_seconds=30.0):
                       f"{_cpu_model()}"}
 
 
+def hbm_ceiling(torch, nbytes: int = 1 << 30, reps: int = 10) -> dict:
+    """Streaming rates of torch's own kernels over buffers 4x the 256 MB MALL:
+    the practical ceilings the roofline fractions are read against."""
+    src = torch.ones(nbytes // 2, dtype=torch.bfloat16, device="cuda:0")
+    dst = torch.empty_like(src)
+    cases = {
+        "read_amax": (lambda: torch.amax(src), nbytes),
+        "read_sum": (lambda: src.sum(dtype=torch.float32), nbytes),
+        "write_fill": (lambda: dst.fill_(1.0), nbytes),
+        "copy": (lambda: dst.copy_(src), 2 * nbytes),
+    }
+    out = {"bytes_per_buffer": nbytes, "reps": reps}
+    for name, (fn, moved) in cases.items():
+        for _ in range(3):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        sec = e0.elapsed_time(e1) * 1e-3 / reps
+        out[name + "_tbs"] = moved / sec / 1e12
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -546,6 +573,8 @@ def main():
     ap.add_argument("--no-model", action="store_true", help="skip the cfg5 swapped-decoder leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--hbm-ceiling", action="store_true",
+                    help="only time torch's streaming kernels (read-only reductions, fill, copy) on 1 GiB tensors")
     ap.add_argument("--prefill-launches", type=int, default=0,
                     help="only run the cfg2 compressor once and this many prefill launches (counter collection)")
     args = ap.parse_args()
@@ -569,6 +598,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2,
                           "launches": args.steps}), flush=True)
+        return
+    if args.hbm_ceiling:
+        print(json.dumps(hbm_ceiling(torch)), flush=True)
         return
     if args.prefill_launches:
         prefill_launches(args, torch, bf)

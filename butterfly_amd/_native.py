@@ -71,6 +71,8 @@ SIGNATURES = {
     "bfly_cache_append": (_int, [_vp, _vp, _int, _i64, _int, _i64, _int, _vp, _vp, _i64, _i64, _vp]),
     "bfly_cache_compress": (_int, [_vp, _vp, _int, _i64, _int, _int, _i64, _i64, _i64, _int, _vp, _vp,
                                    _i64, _i64, _vp]),
+    "bfly_cache_update": (_int, [_vp, _vp, _int, _i64, _int, _i64, _int, _vp, _vp, _i64, _i64, _i64, _i64, _int,
+                                 _vp, _vp, _i64, _i64, _vp]),
 }
 
 _lib = None

@@ -226,17 +226,27 @@ class CompressedKVCache:
             self.tail_size -= bs
 
     def update(self, keys: torch.Tensor, values: torch.Tensor) -> None:
-        """Append, summarise completed blocks, trim (compressed_cache.py:94-172)."""
+        """Append, summarise completed blocks, trim (compressed_cache.py:94-172).
+
+        The append and the pooling of the blocks that became due run as one
+        launch (``bfly_cache_update``); an overflowing pool raises after the
+        blocks that fit were pooled, as the reference does.
+        """
         self.sync()
         offset0 = self.offset
         step, first_pos, first_slot, n_new, overflow = self._advance(keys, values)
         b, h, d = int(keys.shape[0]), int(keys.shape[1]), int(keys.shape[3])
         keys, values = _c(keys), _c(values)
-        st = _stream(keys)
         with _on(keys.device):
-            _native.call("bfly_cache_append", keys.data_ptr(), values.data_ptr(), _dtype_code(keys), b, h, step, d,
-                         self._ring_k.data_ptr(), self._ring_v.data_ptr(), self.tail_capacity, offset0, st)
-        self._compress(first_pos, first_slot, n_new, overflow, st)
+            _native.call("bfly_cache_update", keys.data_ptr(), values.data_ptr(), _dtype_code(keys), b, h, step, d,
+                         self._ring_k.data_ptr(), self._ring_v.data_ptr(), self.tail_capacity, offset0, first_pos,
+                         n_new, self.block_size, self._pool_k.data_ptr(), self._pool_v.data_ptr(),
+                         self.summary_capacity, first_slot, _stream(keys))
+        self.summary_count += n_new
+        if overflow:
+            raise RuntimeError(
+                f"CompressedKVCache.summary_capacity={self.summary_capacity} exhausted "
+                f"at offset={self.offset}; raise max_kv_size at construction time.")
         self._trim(step)
         self._push()
 

@@ -241,7 +241,7 @@ struct MfmaArgs {
 // so HBM traffic of chunk c+1 overlaps the MFMA/softmax work of chunk c.
 template <int D>
 __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1)
-attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunks, int hsplit) {
+attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunks, int hper) {
   using C = MfmaCfg<D>;
   __shared__ __attribute__((aligned(16))) unsigned char smem[C::LDS];
   __shared__ int cand_n[kSumSlots], cand_b[kSumSlots];
@@ -253,12 +253,12 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
   const int wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
   const int seg = xcd_remap(blockIdx.x, gridDim.x);
-  // small grids split a GQA group's head pairs over hsplit workgroups
-  const int bh = blockIdx.y / hsplit, hpart = blockIdx.y - bh * hsplit;
+  // small grids split a GQA group's heads over workgroups of hper heads each
+  const int gsz = a.hq / a.hkv;
+  const int nparts = (gsz + hper - 1) / hper;
+  const int bh = blockIdx.y / nparts, hpart = blockIdx.y - bh * nparts;
   const int bi = bh / a.hkv;
   const int kvh = bh - bi * a.hkv;
-  const int gsz = a.hq / a.hkv;
-  const int hper = ((gsz + hsplit - 1) / hsplit + 1) & ~1;     // heads per workgroup, whole pairs
   const int hlo = hpart * hper;
   const int hhi = min(gsz, hlo + hper);
   const int cbeg = c_first + seg * seg_chunks;
@@ -649,16 +649,20 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
     // spreads the group's head pairs over more workgroups (each reloads the small
     // K/V pages); results are unchanged, every head is computed the same way.
     const int64_t capacity = a.d <= 128 ? 512 : 256;
-    const int npairs = (a.hq / a.hkv + 1) / 2;
+    const int gsz = a.hq / a.hkv;
     int hsplit = 1;
-    while (hsplit < npairs && nseg * groups * hsplit * 2 <= capacity) hsplit *= 2;
-    if (hsplit > npairs) hsplit = npairs;
-    BFLY_CHECK_ARG(groups * hsplit <= 65535, "%s: grid too large", what);
-    dim3 grid((unsigned)nseg, (unsigned)(groups * hsplit));
+    while (hsplit < gsz && nseg * groups * hsplit * 2 <= capacity) hsplit *= 2;
+    // heads per workgroup: whole pairs while there are two or more, else one
+    // (the pair's second MFMA column then runs on a stale slot and is dropped)
+    const int hq_per = (gsz + hsplit - 1) / hsplit;
+    const int hper = hq_per >= 2 ? (hq_per + 1) & ~1 : 1;
+    const int nparts = (gsz + hper - 1) / hper;
+    BFLY_CHECK_ARG(groups * nparts <= 65535, "%s: grid too large", what);
+    dim3 grid((unsigned)nseg, (unsigned)(groups * nparts));
     switch (a.d) {
-      case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hsplit); break;
-      case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hsplit); break;
-      default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hsplit); break;
+      case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
+      case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
+      default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
     }
   } else {
     BFLY_CHECK_ARG(a.d <= kGenericMaxD, "%s: head_dim=%d > %d", what, a.d, kGenericMaxD);

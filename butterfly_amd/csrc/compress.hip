@@ -26,30 +26,17 @@ struct PoolJob {
   int64_t seq_len;      // valid tokens are positions < base_pos + seq_len
 };
 
-template <typename T, int VEC>
-__global__ void __launch_bounds__(256) block_mean_kernel(PoolJob j0, PoolJob j1, int d, int bs) {
-  const PoolJob& job = blockIdx.z == 0 ? j0 : j1;
-  const int64_t n = blockIdx.x;          // block index
-  const int64_t row = blockIdx.y;        // sequence (b*h)
+// Mean of `cnt` token rows into dst (one workgroup, 256 threads); tok_ptr(tok)
+// is the row of token tok.  The summation order is the one documented above.
+template <typename T, int VEC, class TokPtr>
+__device__ __forceinline__ void pool_rows(TokPtr tok_ptr, int64_t cnt, T* dst, int d) {
   const int lpr = d / VEC;               // lanes per token row
   const int rs = 256 / lpr;              // token slots
   const int t = threadIdx.x;
   const int c = t % lpr, s = t / lpr;
-  const int64_t first = n * bs;
-  int64_t cnt = job.seq_len - first;
-  cnt = cnt < bs ? cnt : bs;
-  if (cnt < 0) cnt = 0;
-  const T* src = reinterpret_cast<const T*>(job.src) + row * job.src_rows * d;
   float acc[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
-  // row of token 0 of the block; tokens are < bs <= ring, so one wrap at most
-  const int64_t r0 = job.ring ? posmod(job.base_pos + first, job.ring) : job.base_pos + first;
-  auto tok_row = [&](int64_t tok) {
-    int64_t r = r0 + tok;
-    if (job.ring && r >= job.ring) r -= job.ring;
-    return r;
-  };
   if (s < rs) {
     if constexpr (VEC * sizeof(T) == 16) {
       // eight loads in flight per thread, then the adds in token order
@@ -58,7 +45,7 @@ __global__ void __launch_bounds__(256) block_mean_kernel(PoolJob j0, PoolJob j1,
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           const int64_t tok = base + (int64_t)u * rs;
-          raw[u] = tok < cnt ? *reinterpret_cast<const uint4*>(src + tok_row(tok) * d + c * VEC) : make_uint4(0, 0, 0, 0);
+          raw[u] = tok < cnt ? *reinterpret_cast<const uint4*>(tok_ptr(tok) + c * VEC) : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -70,7 +57,7 @@ __global__ void __launch_bounds__(256) block_mean_kernel(PoolJob j0, PoolJob j1,
       }
     } else {
       for (int64_t tok = s; tok < cnt; tok += rs) {
-        const T* ptr = src + tok_row(tok) * d + c * VEC;
+        const T* ptr = tok_ptr(tok) + c * VEC;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc[e] += to_f32(ptr[e]);
       }
@@ -82,13 +69,82 @@ __global__ void __launch_bounds__(256) block_mean_kernel(PoolJob j0, PoolJob j1,
     for (int e = 0; e < VEC; ++e) part[s * d + c * VEC + e] = acc[e];
   }
   __syncthreads();
-  T* dst = reinterpret_cast<T*>(job.dst) + (row * job.dst_rows + job.dst_slot0 + n) * d;
   const float denom = cnt > 0 ? (float)cnt : 1.f;
   for (int col = t; col < d; col += 256) {
     float tot = 0.f;
     for (int k = 0; k < rs; ++k) tot += part[k * d + col];
     dst[col] = from_f32<T>(tot / denom);
   }
+}
+
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256) block_mean_kernel(PoolJob j0, PoolJob j1, int d, int bs) {
+  const PoolJob& job = blockIdx.z == 0 ? j0 : j1;
+  const int64_t n = blockIdx.x;          // block index
+  const int64_t row = blockIdx.y;        // sequence (b*h)
+  const int64_t first = n * bs;
+  int64_t cnt = job.seq_len - first;
+  cnt = cnt < bs ? cnt : bs;
+  if (cnt < 0) cnt = 0;
+  const T* src = reinterpret_cast<const T*>(job.src) + row * job.src_rows * d;
+  // row of token 0 of the block; tokens are < bs <= ring, so one wrap at most
+  const int64_t r0 = job.ring ? posmod(job.base_pos + first, job.ring) : job.base_pos + first;
+  auto tok_ptr = [&](int64_t tok) {
+    int64_t r = r0 + tok;
+    if (job.ring && r >= job.ring) r -= job.ring;
+    return src + r * d;
+  };
+  T* dst = reinterpret_cast<T*>(job.dst) + (row * job.dst_rows + job.dst_slot0 + n) * d;
+  pool_rows<T, VEC>(tok_ptr, cnt, dst, d);
+}
+
+// One chunk's cache update in one launch (compressed_cache.py:104-149): the
+// append of k_new/v_new to ring slots (offset + t) mod C, and the mean of every
+// block that became due, whose tokens are read where they are before the
+// update (the ring for positions < offset, k_new/v_new for the rest), so the
+// two parts are independent: the pooled blocks and the new tokens all lie in
+// the post-append tail, which holds at most C positions, so their ring slots
+// are distinct.  Grid: (n_blocks + append workgroups, rows, K|V).
+struct UpdateJob {
+  const void* k_new;
+  const void* v_new;     // [rows, step, d]
+  void* ring_k;
+  void* ring_v;          // [rows, ring, d]
+  void* pool_k;
+  void* pool_v;          // [rows, pool_rows, d]
+  int64_t step, ring, pool_rows, offset, first_pos, first_slot;
+  int n_blocks, bs, d;
+};
+
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256) cache_update_kernel(UpdateJob u) {
+  const int kv = blockIdx.z;
+  const int64_t row = blockIdx.y;
+  const int d = u.d;
+  const T* fresh = reinterpret_cast<const T*>(kv ? u.v_new : u.k_new) + row * u.step * d;
+  T* ring = reinterpret_cast<T*>(kv ? u.ring_v : u.ring_k) + row * u.ring * d;
+  if ((int)blockIdx.x >= u.n_blocks) {
+    // append: 256 / (d / VEC) tokens per workgroup, one 16-byte piece per thread
+    const int lpr = d / VEC, tpw = 256 / lpr;
+    const int t = threadIdx.x, c = t % lpr;
+    const int64_t tok = (int64_t)(blockIdx.x - u.n_blocks) * tpw + t / lpr;
+    if (t / lpr >= tpw || tok >= u.step) return;
+    const int64_t slot = posmod(u.offset + tok, u.ring);
+    *reinterpret_cast<uint4*>(ring + slot * d + c * VEC) = *reinterpret_cast<const uint4*>(fresh + tok * d + c * VEC);
+    return;
+  }
+  const int64_t n = blockIdx.x;
+  const int64_t p0 = u.first_pos + n * u.bs;
+  const int64_t r0 = posmod(p0, u.ring);   // tokens < bs <= ring: one wrap at most
+  auto tok_ptr = [&](int64_t tok) -> const T* {
+    const int64_t p = p0 + tok;
+    if (p >= u.offset) return fresh + (p - u.offset) * d;
+    int64_t r = r0 + tok;
+    if (r >= u.ring) r -= u.ring;
+    return ring + r * d;
+  };
+  T* dst = reinterpret_cast<T*>(kv ? u.pool_v : u.pool_k) + (row * u.pool_rows + u.first_slot + n) * d;
+  pool_rows<T, VEC>(tok_ptr, (int64_t)u.bs, dst, d);
 }
 
 template <typename T>
@@ -210,5 +266,53 @@ extern "C" int bfly_cache_compress(const void* ring_k, const void* ring_v, int d
                : launch_pool<__bf16>(a, &b, batch * hkv, head_dim, block_size, n_blocks, stream);
   if (rc) return rc;
   BFLY_CHECK_LAUNCH("bfly_cache_compress");
+  return BFLY_OK;
+}
+
+extern "C" int bfly_cache_update(const void* k_new, const void* v_new, int dtype, int64_t batch, int hkv,
+                                 int64_t step, int head_dim, void* ring_k, void* ring_v, int64_t ring_capacity,
+                                 int64_t offset, int64_t first_block_pos, int64_t n_blocks, int block_size,
+                                 void* pool_k, void* pool_v, int64_t pool_capacity, int64_t first_slot,
+                                 hipStream_t stream) {
+  BFLY_CHECK_ARG(dtype_ok(dtype), "unsupported dtype %d", dtype);
+  BFLY_CHECK_ARG(k_new && v_new && ring_k && ring_v && pool_k && pool_v, "null pointer");
+  BFLY_CHECK_ARG(aligned16(k_new) && aligned16(v_new) && aligned16(ring_k) && aligned16(ring_v) &&
+                     aligned16(pool_k) && aligned16(pool_v),
+                 "tensor pointers must be 16-byte aligned");
+  BFLY_CHECK_ARG(batch > 0 && hkv > 0 && head_dim > 0 && step >= 0 && block_size > 0, "bad shape");
+  BFLY_CHECK_ARG(batch * hkv <= 65535, "batch*hkv too large");
+  BFLY_CHECK_ARG(ring_capacity >= block_size && step <= ring_capacity, "step=%lld exceeds ring capacity %lld",
+                 (long long)step, (long long)ring_capacity);
+  BFLY_CHECK_ARG(offset >= 0, "negative offset");
+  BFLY_CHECK_ARG(n_blocks >= 0 && n_blocks <= INT32_MAX && first_slot >= 0 && first_slot + n_blocks <= pool_capacity,
+                 "summary pool overflow: slots [%lld, %lld) of %lld", (long long)first_slot,
+                 (long long)(first_slot + n_blocks), (long long)pool_capacity);
+  // the due blocks lie inside the post-append tail: [offset + step - ring, offset + step)
+  BFLY_CHECK_ARG(n_blocks == 0 || (first_block_pos >= 0 && first_block_pos >= offset + step - ring_capacity &&
+                                   first_block_pos + n_blocks * (int64_t)block_size <= offset + step),
+                 "due blocks [%lld, %lld) outside the tail after the append", (long long)first_block_pos,
+                 (long long)(first_block_pos + n_blocks * (int64_t)block_size));
+  if (step == 0 && n_blocks == 0) return BFLY_OK;
+  const int esz = dtype == BFLY_DTYPE_F32 ? 4 : 2;
+  const int vec = 16 / esz;
+  if ((head_dim * esz) % 16 != 0 || head_dim / vec > 256) {
+    // shapes without a 16-byte row split: the two separate launches
+    int rc = bfly_cache_append(k_new, v_new, dtype, batch, hkv, step, head_dim, ring_k, ring_v, ring_capacity,
+                               offset, stream);
+    if (rc) return rc;
+    return bfly_cache_compress(ring_k, ring_v, dtype, batch, hkv, head_dim, ring_capacity, first_block_pos,
+                               n_blocks, block_size, pool_k, pool_v, pool_capacity, first_slot, stream);
+  }
+  const int tpw = 256 / (head_dim / vec);
+  const int64_t app = (step + tpw - 1) / tpw;
+  BFLY_CHECK_ARG(n_blocks + app <= INT32_MAX, "grid too large");
+  UpdateJob u{k_new, v_new, ring_k, ring_v, pool_k, pool_v, step, ring_capacity, pool_capacity, offset,
+              first_block_pos, first_slot, (int)n_blocks, block_size, head_dim};
+  dim3 grid((unsigned)(n_blocks + app), (unsigned)(batch * hkv), 2);
+  if (dtype == BFLY_DTYPE_F32)
+    hipLaunchKernelGGL((cache_update_kernel<float, 4>), grid, dim3(256), 0, stream, u);
+  else
+    hipLaunchKernelGGL((cache_update_kernel<__bf16, 8>), grid, dim3(256), 0, stream, u);
+  BFLY_CHECK_LAUNCH("bfly_cache_update");
   return BFLY_OK;
 }

@@ -301,6 +301,23 @@ int bfly_cache_compress(const void* ring_k, const void* ring_v, int dtype, int64
                         int64_t n_blocks, int block_size, void* pool_k, void* pool_v,
                         int64_t pool_capacity, int64_t first_slot, hipStream_t stream);
 
+/*
+ * Device: one chunk's whole cache update in one launch -- bfly_cache_append of
+ * k_new/v_new at `offset`, then bfly_cache_compress of the `n_blocks` due blocks
+ * from first_block_pos into pool slots [first_slot, first_slot + n_blocks).
+ * The blocks' tokens are read where they are before the append (ring below
+ * `offset`, k_new/v_new from it), so the result equals the two calls in order,
+ * bit for bit.  The due blocks must lie in the post-append tail
+ * [offset + step - ring_capacity, offset + step).  Replaces the append and
+ * summarise steps of CompressedKVCache.update_and_fetch
+ * (bna/mlx/compressed_cache.py:104-149).
+ */
+int bfly_cache_update(const void* k_new, const void* v_new, int dtype, int64_t batch, int hkv,
+                      int64_t step, int head_dim, void* ring_k, void* ring_v, int64_t ring_capacity,
+                      int64_t offset, int64_t first_block_pos, int64_t n_blocks, int block_size,
+                      void* pool_k, void* pool_v, int64_t pool_capacity, int64_t first_slot,
+                      hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

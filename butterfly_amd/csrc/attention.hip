@@ -176,7 +176,6 @@ constexpr int kPage = 64;              // positions per chunk / ring page
 constexpr int kRing = 2 * kPage;       // ring slots (window <= 64 needs pages c-1, c)
 constexpr int kSumSlots = 16;          // one 16-row MFMA tile of routed summaries
 constexpr int kSlots = kRing + kSumSlots;
-constexpr int kVPitch = kSlots + 4;    // bf16 per V^T row (296 B): spreads 16 rows over banks
 constexpr int kMaxSegChunks = 8;       // chunks per workgroup (host picks 1, 2, 4 or 8)
 constexpr int kMaxKcap = kSumSlots / 2;
 constexpr int kMaxSegBlocks = kMaxSegChunks * kPage / kPage + 1;   // block_size >= kPage
@@ -188,14 +187,26 @@ struct MfmaCfg {
   static constexpr int KSTEPS = D / 32;            // MFMA k-steps over head_dim
   static constexpr int DTILES = D / 16;            // output d tiles
   static constexpr int PIECES = D / 8;             // 16-byte pieces per row
-  static constexpr int KLD = kPage * PIECES / 256;         // K pieces per thread per page
-  static constexpr int VLD = (kPage / 2) * PIECES / 256;   // V row pairs per thread per page
+  static constexpr int KLD = kPage * PIECES / 256;         // K (and V) pieces per thread per page
   static constexpr int SITEMS = kSumSlots * PIECES;        // summary pieces per chunk
   static constexpr int SLD = (SITEMS + 255) / 256;
   static constexpr int K_BYTES = kSlots * KP * 2;
-  static constexpr int V_BYTES = D * kVPitch * 2;
+  static constexpr int V_BYTES = kSlots * D * 2;           // V row-major, unpadded, swizzled
   static constexpr int LDS = K_BYTES + V_BYTES;
+  // V rows are stored with their 16-byte pieces XOR-swizzled by the row, so that
+  // the transposing reads of four consecutive rows (below) hit distinct banks.
+  __device__ static constexpr int vswz(int row) { return D == 64 ? ((row >> 1) & 1) * 4 : (row & 3) * 4; }
 };
+
+// Four bf16 of column-major data from row-major LDS: within each 16-lane group,
+// lane i receives element (i & 3) of the 8 bytes read by lanes 4j + (i >> 2),
+// j = 0..3, as its elements j (ds_read_b64_tr_b16).
+__device__ __forceinline__ bf16x4 read_tr(const __bf16* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16*)(const_cast<__bf16*>(p)));
+  return __builtin_bit_cast(bf16x4, v);
+}
 
 // Swap 16 bytes with lane ^ 8 (within each 16-lane row): DPP row_ror:8 rotates
 // each row of 16 lanes by 8, which is lane ^ 8; a VALU move, no LDS traffic.
@@ -247,7 +258,7 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
   __shared__ int cand_n[kSumSlots], cand_b[kSumSlots];
   __shared__ int s_nbr[kMaxSegBlocks * kMaxKcap];
   __bf16* Ks = reinterpret_cast<__bf16*>(smem);                 // [kSlots][KP]
-  __bf16* Vt = reinterpret_cast<__bf16*>(smem + C::K_BYTES);    // [D][kVPitch]
+  __bf16* Vs = reinterpret_cast<__bf16*>(smem + C::K_BYTES);    // [kSlots][D], pieces swizzled by row
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -288,7 +299,7 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
   }
 
   // ---- register staging of one page (K rows and V row pairs) and of the routed summaries
-  uint4 kst[C::KLD], vst[2 * C::VLD];
+  uint4 kst[C::KLD], vst[C::KLD];
   auto fetch_page = [&](int pg) {
     const int p0 = pg * kPage;
     // row of position p0 (+ r): linear, or ring slot (ring >= kPage, so one wrap at most)
@@ -318,11 +329,9 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
       kst[it] = ld(kbase, i / C::PIECES, i % C::PIECES);
     }
 #pragma unroll
-    for (int it = 0; it < C::VLD; ++it) {
+    for (int it = 0; it < C::KLD; ++it) {
       const int i = tid + it * 256;
-      const int kp = i % (kPage / 2), pc = i / (kPage / 2);
-      vst[2 * it] = ld(vbase, 2 * kp, pc);
-      vst[2 * it + 1] = ld(vbase, 2 * kp + 1, pc);
+      vst[it] = ld(vbase, i / C::PIECES, i % C::PIECES);
     }
   };
   auto store_page = [&](int pg) {
@@ -334,16 +343,10 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
       *reinterpret_cast<uint4*>(Ks + (sbase + r) * C::KP + pc * 8) = kst[it];
     }
 #pragma unroll
-    for (int it = 0; it < C::VLD; ++it) {
+    for (int it = 0; it < C::KLD; ++it) {
       const int i = tid + it * 256;
-      const int kp = i % (kPage / 2), pc = i / (kPage / 2);
-      const uint16_t* e0 = reinterpret_cast<const uint16_t*>(&vst[2 * it]);
-      const uint16_t* e1 = reinterpret_cast<const uint16_t*>(&vst[2 * it + 1]);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t pair = (uint32_t)e0[j] | ((uint32_t)e1[j] << 16);
-        *reinterpret_cast<uint32_t*>(Vt + (pc * 8 + j) * kVPitch + sbase + 2 * kp) = pair;
-      }
+      const int r = sbase + i / C::PIECES, pc = i % C::PIECES;
+      *reinterpret_cast<uint4*>(Vs + r * D + (pc ^ C::vswz(r)) * 8) = vst[it];
     }
   };
 
@@ -390,9 +393,7 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
       if (i >= C::SITEMS) continue;
       const int s = i / C::PIECES, pc = i % C::PIECES;
       *reinterpret_cast<uint4*>(Ks + (kRing + s) * C::KP + pc * 8) = skst[it];
-      const __bf16* ve = reinterpret_cast<const __bf16*>(&svst[it]);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) Vt[(pc * 8 + j) * kVPitch + kRing + s] = ve[j];
+      *reinterpret_cast<uint4*>(Vs + (kRing + s) * D + (pc ^ C::vswz(kRing + s)) * 8) = svst[it];
       if (pc == 0) {
         cand_n[s] = scn[it];
         cand_b[s] = scb[it];
@@ -539,6 +540,10 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
         softmax(s1, p1, inv1);
         // O^T = V^T P^T.  Tile (mt, half), row r holds d = mt*32 + (r/4)*8 + half*4 + r%4,
         // so the two halves give each lane 8 consecutive d (16 bytes) of its position.
+        // The V^T fragments come from row-major V by transposing reads: lane (lg, lq)
+        // reads the 4 d (8 bytes) mt*32 + (lq&3)*8 + half*4 of key row
+        // slot + 4lg + (lq>>2), so lane lq of the group receives d row lq's four keys
+        // slot + 4lg + 0..3, the order of its P fragment.
         // Tiles mt and mt+1 together hold d [mt*32, mt*32+64) = one 128-byte line per
         // position.  Lanes lq and lq^8 swap one 16-byte piece so that each store
         // instruction writes 8 whole lines (positions 0..7, then 8..15): whole-line
@@ -558,12 +563,13 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
             f32x4 o0[2], o1[2];
 #pragma unroll
             for (int half = 0; half < 2; ++half) {
-              const __bf16* vrow = Vt + (mt * 32 + (lq >> 2) * 8 + half * 4 + (lq & 3)) * kVPitch;
+              const int unit = mt * 8 + (lq & 3) * 2 + half;   // 8-byte unit of the row
               bf16x8 vf[3];
 #pragma unroll
               for (int pr = 0; pr < 3; ++pr) {
-                const bf16x4 va = *reinterpret_cast<const bf16x4*>(vrow + slot[2 * pr] + 4 * lg);
-                const bf16x4 vb = *reinterpret_cast<const bf16x4*>(vrow + slot[2 * pr + 1] + 4 * lg);
+                const int ra = slot[2 * pr] + 4 * lg + (lq >> 2), rb = slot[2 * pr + 1] + 4 * lg + (lq >> 2);
+                const bf16x4 va = read_tr(Vs + ra * D + (unit ^ (2 * C::vswz(ra))) * 4);
+                const bf16x4 vb = read_tr(Vs + rb * D + (unit ^ (2 * C::vswz(rb))) * 4);
                 vf[pr] = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
               }
               f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};

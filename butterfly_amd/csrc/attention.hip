@@ -193,20 +193,8 @@ struct MfmaCfg {
   static constexpr int K_BYTES = kSlots * KP * 2;
   static constexpr int V_BYTES = kSlots * D * 2;           // V row-major, unpadded, swizzled
   static constexpr int LDS = K_BYTES + V_BYTES;
-  // V rows are stored with their 16-byte pieces XOR-swizzled by the row, so that
-  // the transposing reads of four consecutive rows (below) hit distinct banks.
-  __device__ static constexpr int vswz(int row) { return D == 64 ? ((row >> 1) & 1) * 4 : (row & 3) * 4; }
+  __device__ static constexpr int vswz(int row) { return vrow_swizzle<D>(row); }
 };
-
-// Four bf16 of column-major data from row-major LDS: within each 16-lane group,
-// lane i receives element (i & 3) of the 8 bytes read by lanes 4j + (i >> 2),
-// j = 0..3, as its elements j (ds_read_b64_tr_b16).
-__device__ __forceinline__ bf16x4 read_tr(const __bf16* p) {
-  typedef short v4i16 __attribute__((ext_vector_type(4)));
-  const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) v4i16*)(const_cast<__bf16*>(p)));
-  return __builtin_bit_cast(bf16x4, v);
-}
 
 // Swap 16 bytes with lane ^ 8 (within each 16-lane row): DPP row_ror:8 rotates
 // each row of 16 lanes by 8, which is lane ^ 8; a VALU move, no LDS traffic.

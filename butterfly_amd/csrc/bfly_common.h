@@ -62,6 +62,24 @@ __device__ __forceinline__ float col_sum4(float v) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Four bf16 of column-major data from row-major LDS: within each 16-lane group,
+// lane i receives element (i & 3) of the 8 bytes read by lanes 4j + (i >> 2),
+// j = 0..3, as its elements j (ds_read_b64_tr_b16).
+__device__ __forceinline__ bf16x4 read_tr(const __bf16* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16*)(const_cast<__bf16*>(p)));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+// Row-major bf16 V tiles in LDS keep their 16-byte pieces XOR-swizzled by the
+// row (piece pc of row r at pc ^ vrow_swizzle<D>(r)), so that the transposing
+// reads of four consecutive rows (read_tr over rows 4k..4k+3) hit distinct banks.
+template <int D>
+__device__ __forceinline__ constexpr int vrow_swizzle(int row) {
+  return D == 64 ? ((row >> 1) & 1) * 4 : (row & 3) * 4;
+}
+
 // Vectorised paths issue 16-byte loads/stores: tensor base pointers must be 16-byte aligned.
 __host__ __forceinline__ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 

@@ -711,19 +711,16 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
   constexpr int NT = kDecMfmaKeys / 16;          // key tiles (5)
   constexpr int NPR = (NT + 1) / 2;              // PV k-steps of 32 keys (3, the last half zero)
   constexpr int KP = D + VEC;                    // K row pitch (bf16)
-  constexpr int VTP = kDecMfmaKeys + 8;          // V^T row pitch (bf16)
   constexpr int LPR = D / VEC;
   constexpr int RS = 256 / LPR;
   constexpr int KITEMS = kDecMfmaKeys * PIECES;          // K pieces
-  constexpr int VITEMS = (kDecMfmaKeys / 2) * PIECES;    // V row pairs x pieces
-  constexpr int KIT = (KITEMS + 255) / 256, VIT = (VITEMS + 255) / 256;
-  // K rows and V^T share one LDS block with the pooling scratch (pooling ends
-  // with a barrier before the staging writes)
-  constexpr int KS_BYTES = kDecMfmaKeys * KP * 2, VT_BYTES = D * VTP * 2;
+  // K rows and V rows share one LDS block with the pooling scratch (pooling ends
+  // with a barrier before the staging writes); V rows are unpadded and swizzled
+  constexpr int KS_BYTES = kDecMfmaKeys * KP * 2, VT_BYTES = kDecMfmaKeys * D * 2;
   constexpr int STAGE_BYTES = KS_BYTES + VT_BYTES > RS * D * 4 ? KS_BYTES + VT_BYTES : RS * D * 4;
   __shared__ __attribute__((aligned(16))) unsigned char stage_lds[STAGE_BYTES];
   T* Ks = reinterpret_cast<T*>(stage_lds);
-  T* Vt = reinterpret_cast<T*>(stage_lds + KS_BYTES);
+  T* Vs = reinterpret_cast<T*>(stage_lds + KS_BYTES);   // [80][D], pieces swizzled by row
   __shared__ int selw[4][kDecMaxSum];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -786,31 +783,22 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
 
   // ---- staging: keys 0..63 are the window rows (lo + r), keys 64..79 the routed
   // summaries in row order; unused keys are zero rows and masked in the scores.
-  // K is stored row-major, V transposed (pairs of keys per 32-bit LDS word).
+  // K and V are stored row-major (V with swizzled pieces, read back transposed).
   // Window rows are requested first, the routed selection runs while they are in
   // flight, then the summary rows are requested.
   constexpr int WK = kDecMaxWin * PIECES / 256;                   // window K pieces per thread
   constexpr int SKN = kDecMaxSum * PIECES;                         // summary K pieces
   constexpr int SK = (SKN + 255) / 256;
-  constexpr int WV = (kDecMaxWin / 2) * PIECES / 256;              // window V row pairs per thread
-  constexpr int SVN = (kDecMaxSum / 2) * PIECES;                   // summary V row pairs
-  constexpr int SV = (SVN + 255) / 256;
-  static_assert(kDecMaxWin * PIECES % 256 == 0 && (kDecMaxWin / 2) * PIECES % 256 == 0, "staging split");
+  static_assert(kDecMaxWin * PIECES % 256 == 0, "staging split");
   static_assert(kDecMaxWin + kDecMaxSum == kDecMfmaKeys, "key layout");
   int ns;
   {
-    uint4 kx[WK], v0[WV], v1[WV], skx[SK], sv0[SV], sv1[SV];
+    uint4 kx[WK], vx[WK], skx[SK], svx[SK];
 #pragma unroll
     for (int it = 0; it < WK; ++it) {
       const int i = tid + it * 256;
       kx[it] = *reinterpret_cast<const uint4*>(win_row(i / PIECES, false) + (i % PIECES) * VEC);
-    }
-#pragma unroll
-    for (int it = 0; it < WV; ++it) {
-      const int i = tid + it * 256;
-      const int kp = i % (kDecMaxWin / 2), pc = i / (kDecMaxWin / 2);
-      v0[it] = *reinterpret_cast<const uint4*>(win_row(2 * kp, true) + pc * VEC);
-      v1[it] = *reinterpret_cast<const uint4*>(win_row(2 * kp + 1, true) + pc * VEC);
+      vx[it] = *reinterpret_cast<const uint4*>(win_row(i / PIECES, true) + (i % PIECES) * VEC);
     }
     const int blk = min((int)a.bs_div.div((uint32_t)p), st.nblocks - 1);
     ns = dec_select32<kStep>(p, blk, a, sa, st, lane, selw[wave]);
@@ -823,13 +811,7 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
     for (int it = 0; it < SK; ++it) {
       const int i = min(tid + it * 256, SKN - 1);
       skx[it] = *reinterpret_cast<const uint4*>(sum_row(i / PIECES, false) + (i % PIECES) * VEC);
-    }
-#pragma unroll
-    for (int it = 0; it < SV; ++it) {
-      const int i = min(tid + it * 256, SVN - 1);
-      const int kp = i % (kDecMaxSum / 2), pc = i / (kDecMaxSum / 2);
-      sv0[it] = *reinterpret_cast<const uint4*>(sum_row(2 * kp, true) + pc * VEC);
-      sv1[it] = *reinterpret_cast<const uint4*>(sum_row(2 * kp + 1, true) + pc * VEC);
+      svx[it] = *reinterpret_cast<const uint4*>(sum_row(i / PIECES, true) + (i % PIECES) * VEC);
     }
     // append the new token to its ring slot; requested after every staging load so
     // that its wait coincides with theirs (the staging reads it from k_new/v_new)
@@ -839,39 +821,24 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
       T* dst = tid < PIECES ? rk : rv;
       *reinterpret_cast<uint4*>(dst + ring_off(nw - 1) + pc * VEC) = *reinterpret_cast<const uint4*>(src + pc * VEC);
     }
-    // V^T words of keys key0, key0 + 1 (bf16 pairs) for the 8 d of piece pc
-    auto put_vt = [&](int key0, int pc, uint4 a0, uint4 a1) {
-      const uint32_t w0[4] = {a0.x, a0.y, a0.z, a0.w}, w1[4] = {a1.x, a1.y, a1.z, a1.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        T* col = Vt + (pc * 8 + 2 * j) * VTP + key0;
-        *reinterpret_cast<uint32_t*>(col) = (w0[j] & 0xffffu) | (w1[j] << 16);
-        *reinterpret_cast<uint32_t*>(col + VTP) = (w0[j] >> 16) | (w1[j] & 0xffff0000u);
-      }
+    auto put_v = [&](int r, int pc, uint4 x) {
+      *reinterpret_cast<uint4*>(Vs + r * D + (pc ^ vrow_swizzle<D>(r)) * VEC) = x;
     };
 #pragma unroll
     for (int it = 0; it < WK; ++it) {
       const int i = tid + it * 256;
       const int r = i / PIECES, pc = i % PIECES;
       *reinterpret_cast<uint4*>(Ks + r * KP + pc * VEC) = keep_if(r < nw, kx[it]);
-    }
-#pragma unroll
-    for (int it = 0; it < WV; ++it) {
-      const int i = tid + it * 256;
-      const int kp = i % (kDecMaxWin / 2), pc = i / (kDecMaxWin / 2);
-      put_vt(2 * kp, pc, keep_if(2 * kp < nw, v0[it]), keep_if(2 * kp + 1 < nw, v1[it]));
+      put_v(r, pc, keep_if(r < nw, vx[it]));
     }
 #pragma unroll
     for (int it = 0; it < SK; ++it) {
       const int i = tid + it * 256;
       const int j = i / PIECES, pc = i % PIECES;
-      if (i < SKN) *reinterpret_cast<uint4*>(Ks + (kDecMaxWin + j) * KP + pc * VEC) = keep_if(j < ns, skx[it]);
-    }
-#pragma unroll
-    for (int it = 0; it < SV; ++it) {
-      const int i = tid + it * 256;
-      const int kp = i % (kDecMaxSum / 2), pc = i / (kDecMaxSum / 2);
-      if (i < SVN) put_vt(kDecMaxWin + 2 * kp, pc, keep_if(2 * kp < ns, sv0[it]), keep_if(2 * kp + 1 < ns, sv1[it]));
+      if (i < SKN) {
+        *reinterpret_cast<uint4*>(Ks + (kDecMaxWin + j) * KP + pc * VEC) = keep_if(j < ns, skx[it]);
+        put_v(kDecMaxWin + j, pc, keep_if(j < ns, svx[it]));
+      }
     }
   }
   __syncthreads();
@@ -923,13 +890,19 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
       f32x4 o[2];
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const T* vrow = Vt + (mt * 32 + (lq >> 2) * 8 + half * 4 + (lq & 3)) * VTP;
+        // transposing reads of row-major V: lane (lg, lq) reads the 4 d
+        // mt*32 + (lq&3)*8 + half*4 of key 16t + 4lg + (lq>>2), so lane lq receives
+        // d row lq's keys 16t + 4lg + 0..3
+        const int unit = mt * 8 + (lq & 3) * 2 + half;
+        auto vfrag = [&](int t) {
+          const int r = 16 * t + 4 * lg + (lq >> 2);
+          return read_tr(Vs + r * D + (unit ^ (2 * vrow_swizzle<D>(r))) * 4);
+        };
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int pr = 0; pr < NPR; ++pr) {
-          const bf16x4 va = *reinterpret_cast<const bf16x4*>(vrow + 16 * (2 * pr) + 4 * lg);
-          const bf16x4 vb = 2 * pr + 1 < NT ? *reinterpret_cast<const bf16x4*>(vrow + 16 * (2 * pr + 1) + 4 * lg)
-                                            : bf16x4{};
+          const bf16x4 va = vfrag(2 * pr);
+          const bf16x4 vb = 2 * pr + 1 < NT ? vfrag(2 * pr + 1) : bf16x4{};
           const bf16x8 vf = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
           acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[pr], acc, 0, 0, 0);
         }

@@ -229,10 +229,11 @@ struct MfmaArgs {
 };
 
 // Work unit = (batch, kv head, segment of seg_chunks 64-position chunks).
-// Software pipeline per chunk c:
-//   LDS <- staged page c (K rows, V transposed) and routed summary rows
+// Software pipeline per chunk c (even segments walk chunks upwards, odd ones
+// downwards; see `dir`):
+//   LDS <- staged page (K rows, V rows) and routed summary rows
 //   barrier
-//   issue global loads of page c+1 and its summaries into registers
+//   issue global loads of the next chunk's page and summaries into registers
 //   query heads in pairs: S^T = K Q^T for both heads from one K fragment read,
 //     softmax, O^T = V^T P^T for both heads from one V fragment read; after a
 //     head's scores its register Q slot is refilled with the next (chunk, head)
@@ -409,33 +410,42 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
   };
   // After head hh of chunk c used slot u = hh % kQPipe, refill it with the next
   // (chunk, head) that uses the slot.
+  // Odd segments walk their chunks backwards: the page a segment shares with its
+  // left neighbour (the neighbour's last page, the segment's halo) is then read by
+  // both at about the same time, and the second read hits the XCD's L2.  Chunk c
+  // needs pages c - 1 and c; the page it adds to the ring is c forwards, c - 1
+  // backwards.
+  const int dir = (seg & 1) ? -1 : 1;
+  const int cfirst = dir > 0 ? cbeg : cend - 1;
+  const int cstop = dir > 0 ? cend : cbeg - 1;
+  auto new_page = [&](int c) { return dir > 0 ? c : c - 1; };
   auto refill_q = [&](int u, int c, int hh) {
     int nh = hh + kQPipe, nc = c;
     if (nh >= hhi) {
       nh = hlo + u;
-      nc = c + 1;
+      nc = c + dir;
     }
-    if (nc < cend) load_q(u, nc, nh);
+    if (nc != cstop) load_q(u, nc, nh);
   };
 
 #pragma unroll
   for (int u = 0; u < kQPipe; ++u)
-    if (hlo + u < hhi) load_q(u, cbeg, hlo + u);
-  fetch_page(cbeg - 1);
-  store_page(cbeg - 1);
-  fetch_page(cbeg);
+    if (hlo + u < hhi) load_q(u, cfirst, hlo + u);
+  fetch_page(dir > 0 ? cbeg - 1 : cend - 1);
+  store_page(dir > 0 ? cbeg - 1 : cend - 1);
+  fetch_page(new_page(cfirst));
   __syncthreads();   // s_nbr visible
-  fetch_sum(cbeg);
+  fetch_sum(cfirst);
 
   __bf16* ohead0 = reinterpret_cast<__bf16*>(a.out) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz) * a.tq * D;
 
-  for (int c = cbeg; c < cend; ++c) {
-    store_page(c);
+  for (int c = cfirst; c != cstop; c += dir) {
+    store_page(new_page(c));
     store_sum();
     __syncthreads();
-    if (c + 1 < cend) {
-      fetch_page(c + 1);
-      fetch_sum(c + 1);
+    if (c + dir != cstop) {
+      fetch_page(new_page(c + dir));
+      fetch_sum(c + dir);
     }
 
     // ---------------- per-lane state shared by every head: wave owns positions [pw, pw+16)

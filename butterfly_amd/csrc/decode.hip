@@ -613,36 +613,30 @@ __device__ __forceinline__ int dec_select32(int p, int blk, const DecodeArgs& a,
   const int sinks = kStep ? sa.sinks : a.topo.sink_count;
   const int nsink = min(sinks, s.nblocks);
   const int kc = 1 + lwb + npart + sinks;
-  int cand = -1;
-  if (lane < kc) {
-    if (lane == 0) {
-      cand = blk;
-    } else if (lane <= lwb) {
-      cand = blk - lane;
-    } else if (lane <= lwb + npart) {
-      const int j = lane - 1 - lwb;
-      int bit = 0;
-      if constexpr (kStep) {
-        int ph = s.stage + j;
-        if (rule == BFLY_RULE_BENES) {
-          while (ph >= s.count) ph -= s.count;
-          bit = s.width <= 1 ? 0 : (ph < s.width ? ph : 2 * s.width - 2 - ph);
-        } else {
-          while (ph >= s.width) ph -= s.width;
-          bit = ph;
-        }
-      } else {
-#pragma unroll
-        for (int jj = 0; jj < BFLY_MAX_PARTNERS; ++jj)
-          if (jj == j) bit = a.topo.partner_bits[jj];
-      }
-      cand = partner32(blk, bit, s.nblocks, rule, s.width);
+  // Every lane evaluates each kind of entry and keeps its own by selects (no
+  // divergent branches: this runs on the decode's critical path).
+  const int jp = min(max(lane - 1 - lwb, 0), BFLY_MAX_PARTNERS - 1);   // partner index
+  int bit = 0;
+  if constexpr (kStep) {
+    // stage + j reduced mod count (benes) or width
+    const int ph0 = s.stage + jp;
+    if (rule == BFLY_RULE_BENES) {
+      const int ph = ph0 % s.count;
+      bit = s.width <= 1 ? 0 : (ph < s.width ? ph : 2 * s.width - 2 - ph);
     } else {
-      const int sk = lane - 1 - lwb - npart;
-      cand = sk < nsink ? sk : -1;
+      bit = ph0 % s.width;
     }
-    if (cand < 0 || cand >= s.nblocks) cand = -1;
+  } else {
+#pragma unroll
+    for (int jj = 0; jj < BFLY_MAX_PARTNERS; ++jj) bit = jj == jp ? a.topo.partner_bits[jj] : bit;
   }
+  const int c_part = partner32(blk, bit, s.nblocks, rule, s.width);
+  const int sk = lane - 1 - lwb - npart;
+  int cand = lane == 0 ? blk
+             : lane <= lwb ? blk - lane
+             : lane <= lwb + npart ? c_part
+             : sk < nsink ? sk : -1;
+  if (lane >= kc || cand < 0 || cand >= s.nblocks) cand = -1;
   bool keep = cand >= 0;
   for (int i = 0; i < kc; ++i) {                  // kc is uniform: lane i's entry as a scalar
     const int ci = __builtin_amdgcn_readlane(cand, i);

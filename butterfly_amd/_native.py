@@ -1,4 +1,4 @@
-"""ctypes binding of ``libbutterfly_amd.so`` (the C ABI in ``include/butterfly_amd.h``).
+"""ctypes binding of ``libbutterfly_amd.so`` (the C ABI in ``include/*.h``).
 
 The library is built in-tree by ``butterfly_amd.build``.  There is no fallback:
 if the library is missing every product entry point raises.
@@ -73,6 +73,11 @@ SIGNATURES = {
                                    _i64, _i64, _vp]),
     "bfly_cache_update": (_int, [_vp, _vp, _int, _i64, _int, _i64, _int, _vp, _vp, _i64, _i64, _i64, _i64, _int,
                                  _vp, _vp, _i64, _i64, _vp]),
+    # include/butterfly_amd_decoder.h
+    "bfly_add_rms_norm": (_int, [_vp, _vp, _vp, _i64, _int, _f32, _vp, _vp, _vp]),
+    "bfly_qk_norm_rope": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _int, _f32, _vp, _vp,
+                                 _vp, _vp]),
+    "bfly_silu_mul": (_int, [_vp, _vp, _i64, _vp, _vp]),
 }
 
 _lib = None

@@ -1,0 +1,229 @@
+// Elementwise and row-wise steps of the swapped decoder on gfx950 (bf16 in and
+// out, fp32 inside), each one launch where the PyTorch formulation takes five to
+// eight: residual add + RMSNorm, per-head q/k RMSNorm + rotate-half RoPE + the
+// [B, T, H*d] -> [B, H, T, d] layout change, and SiLU(gate) * up.
+//
+// Reference: the projection step of the swapped attention applies q_norm and
+// k_norm per head, transposes to heads-first and applies rotate-half RoPE
+// (bna/integrations/qwen_torch.py:550-562; qwen_mlx.py:288-357).  The rounding
+// points follow the PyTorch forms in butterfly_amd/decoder.py exactly (bf16
+// after the residual add, after each norm, after RoPE, after SiLU and after the
+// product), so results differ from them only by the fp32 summation order of the
+// mean square and by the last bit of rsqrt/exp.
+#include "bfly_common.h"
+#include "../../include/butterfly_amd_decoder.h"
+
+// products and sums are rounded one by one, as the PyTorch forms do
+#pragma clang fp contract(off)
+
+namespace bfly {
+
+__device__ __forceinline__ float dec_wave_sum64(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Any dim that is a multiple of 256: the sum of squares from global memory,
+// then the row is read again (it is in cache) for the output.
+__global__ void __launch_bounds__(256) add_rmsnorm_any_kernel(const __bf16* __restrict__ x,
+                                                              const __bf16* __restrict__ y,
+                                                              const __bf16* __restrict__ w, __bf16* __restrict__ h_out,
+                                                              __bf16* __restrict__ n_out, int dim, float eps) {
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x;
+  const int per = dim / 256;
+  const int64_t base = row * dim + (int64_t)t * per;
+  auto hval = [&](int e) {
+    float v = (float)x[base + e];
+    if (y != nullptr) v = (float)(__bf16)(v + (float)y[base + e]);
+    return v;
+  };
+  float ss = 0.f;
+  for (int e = 0; e < per; ++e) {
+    const float v = hval(e);
+    if (y != nullptr && h_out != nullptr) h_out[base + e] = (__bf16)v;
+    ss = fmaf(v, v, ss);
+  }
+  ss = dec_wave_sum64(ss);
+  __shared__ float part[4];
+  if ((t & 63) == 0) part[t >> 6] = ss;
+  __syncthreads();
+  const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+  const float r = rsqrtf(tot / (float)dim + eps);
+  for (int e = 0; e < per; ++e) n_out[base + e] = (__bf16)(hval(e) * r * (float)w[t * per + e]);
+}
+
+// One workgroup of 256 threads per row; each thread holds `PER` consecutive
+// elements (dim = 256 * PER).
+template <int PER>
+__global__ void __launch_bounds__(256) add_rmsnorm_kernel(const __bf16* __restrict__ x, const __bf16* __restrict__ y,
+                                                          const __bf16* __restrict__ w, __bf16* __restrict__ h_out,
+                                                          __bf16* __restrict__ n_out, int dim, float eps) {
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x;
+  const int64_t base = row * dim + (int64_t)t * PER;
+  float h[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    float v = (float)x[base + e];
+    if (y != nullptr) v = (float)(__bf16)(v + (float)y[base + e]);   // residual stream in bf16
+    h[e] = v;
+  }
+  if (y != nullptr && h_out != nullptr) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) h_out[base + e] = (__bf16)h[e];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) ss = fmaf(h[e], h[e], ss);
+  ss = dec_wave_sum64(ss);
+  __shared__ float part[4];
+  if ((t & 63) == 0) part[t >> 6] = ss;
+  __syncthreads();
+  const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+  const float r = rsqrtf(tot / (float)dim + eps);
+#pragma unroll
+  for (int e = 0; e < PER; ++e) n_out[base + e] = (__bf16)(h[e] * r * (float)w[t * PER + e]);
+}
+
+// One wave per (row of B*T, head): q/k heads are normed over d with their weight,
+// rounded to bf16, rotated with cos/sin of the row's position, rounded to bf16 and
+// written heads-first; v heads are only moved.  Lane l holds elements l and
+// l + d/2, the two halves rotate-half pairs.
+template <int D>
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ k,
+                                                           const __bf16* __restrict__ v, const __bf16* __restrict__ qw,
+                                                           const __bf16* __restrict__ kw, const float* __restrict__ cosv,
+                                                           const float* __restrict__ sinv, __bf16* __restrict__ qo,
+                                                           __bf16* __restrict__ ko, __bf16* __restrict__ vo, int64_t rows,
+                                                           int t_len, int hq, int hkv, float eps) {
+  constexpr int HALF = D / 2;
+  constexpr int PER = HALF / 64;   // elements per lane in each half
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nh = hq + 2 * hkv;
+  if (item >= rows * nh) return;
+  const int64_t row = item / nh;                  // b * T + t
+  const int head = (int)(item - row * nh);
+  const int64_t b = row / t_len;
+  const int tt = (int)(row - b * t_len);
+  const __bf16* src;
+  __bf16* dst;
+  const __bf16* w = nullptr;
+  if (head < hq) {
+    src = q + (row * hq + head) * D;
+    dst = qo + ((b * hq + head) * t_len + tt) * D;
+    w = qw;
+  } else if (head < hq + hkv) {
+    const int hk = head - hq;
+    src = k + (row * hkv + hk) * D;
+    dst = ko + ((b * hkv + hk) * t_len + tt) * D;
+    w = kw;
+  } else {
+    const int hv = head - hq - hkv;
+    src = v + (row * hkv + hv) * D;
+    dst = vo + ((b * hkv + hv) * t_len + tt) * D;
+  }
+  float lo[PER], hi[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    lo[e] = (float)src[lane * PER + e];
+    hi[e] = (float)src[HALF + lane * PER + e];
+  }
+  if (w == nullptr) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      dst[lane * PER + e] = (__bf16)lo[e];
+      dst[HALF + lane * PER + e] = (__bf16)hi[e];
+    }
+    return;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) ss = fmaf(lo[e], lo[e], fmaf(hi[e], hi[e], ss));
+  ss = dec_wave_sum64(ss);
+  const float r = rsqrtf(ss / (float)D + eps);
+  const float* c = cosv + (int64_t)tt * D;
+  const float* s = sinv + (int64_t)tt * D;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int i = lane * PER + e;
+    const float a = (float)(__bf16)(lo[e] * r * (float)w[i]);            // normed, rounded as the module does
+    const float bb = (float)(__bf16)(hi[e] * r * (float)w[HALF + i]);
+    dst[i] = (__bf16)(a * c[i] + (-bb) * s[i]);                         // x*cos + rotate_half(x)*sin
+    dst[HALF + i] = (__bf16)(bb * c[HALF + i] + a * s[HALF + i]);
+  }
+}
+
+__global__ void __launch_bounds__(256) silu_mul_kernel(const __bf16* __restrict__ g, const __bf16* __restrict__ u,
+                                                       __bf16* __restrict__ out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float x = (float)g[i];
+  const float sg = (float)(__bf16)(x / (1.f + expf(-x)));
+  out[i] = (__bf16)(sg * (float)u[i]);
+}
+
+}  // namespace bfly
+
+using namespace bfly;
+
+extern "C" int bfly_add_rms_norm(const void* x, const void* residual, const void* weight, int64_t rows, int dim,
+                                 float eps, void* h_out, void* norm_out, hipStream_t stream) {
+  BFLY_CHECK_ARG(x && weight && norm_out, "null pointer");
+  BFLY_CHECK_ARG((residual == nullptr) == (h_out == nullptr), "residual and h_out must both be given or both NULL");
+  BFLY_CHECK_ARG(rows > 0 && rows <= INT32_MAX, "rows=%lld out of range", (long long)rows);
+  BFLY_CHECK_ARG(dim > 0 && dim % 256 == 0 && dim <= 256 * 32, "dim=%d must be a multiple of 256 up to 8192", dim);
+  const __bf16* xp = static_cast<const __bf16*>(x);
+  const __bf16* yp = static_cast<const __bf16*>(residual);
+  const __bf16* wp = static_cast<const __bf16*>(weight);
+  __bf16* hp = static_cast<__bf16*>(h_out);
+  __bf16* np = static_cast<__bf16*>(norm_out);
+  dim3 grid((unsigned)rows);
+  switch (dim / 256) {
+    case 4: hipLaunchKernelGGL(add_rmsnorm_kernel<4>, grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); break;
+    case 8: hipLaunchKernelGGL(add_rmsnorm_kernel<8>, grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); break;
+    case 16: hipLaunchKernelGGL(add_rmsnorm_kernel<16>, grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); break;
+    case 24: hipLaunchKernelGGL(add_rmsnorm_kernel<24>, grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); break;
+    case 32: hipLaunchKernelGGL(add_rmsnorm_kernel<32>, grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); break;
+    default: hipLaunchKernelGGL(add_rmsnorm_any_kernel, grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); break;
+  }
+  BFLY_CHECK_LAUNCH("bfly_add_rms_norm");
+  return BFLY_OK;
+}
+
+extern "C" int bfly_qk_norm_rope(const void* q, const void* k, const void* v, const void* q_weight,
+                                 const void* k_weight, const float* cos, const float* sin, int64_t batch,
+                                 int64_t seq_len, int hq, int hkv, int head_dim, float eps, void* q_out, void* k_out,
+                                 void* v_out, hipStream_t stream) {
+  BFLY_CHECK_ARG(q && k && v && q_weight && k_weight && cos && sin && q_out && k_out && v_out, "null pointer");
+  BFLY_CHECK_ARG(batch > 0 && seq_len > 0 && hq > 0 && hkv > 0, "bad shape");
+  BFLY_CHECK_ARG(head_dim == 128 || head_dim == 256, "bfly_qk_norm_rope: head_dim=%d unsupported (128, 256)",
+                 head_dim);
+  const int64_t rows = batch * seq_len;
+  const int64_t items = rows * (hq + 2 * hkv);
+  BFLY_CHECK_ARG((items + 3) / 4 <= INT32_MAX && seq_len <= INT32_MAX, "too many rows");
+  dim3 grid((unsigned)((items + 3) / 4));
+  const __bf16 *qp = static_cast<const __bf16*>(q), *kp = static_cast<const __bf16*>(k),
+               *vp = static_cast<const __bf16*>(v), *qw = static_cast<const __bf16*>(q_weight),
+               *kw = static_cast<const __bf16*>(k_weight);
+  __bf16 *qo = static_cast<__bf16*>(q_out), *ko = static_cast<__bf16*>(k_out), *vo = static_cast<__bf16*>(v_out);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(qk_norm_rope_kernel<128>, grid, dim3(256), 0, stream, qp, kp, vp, qw, kw, cos, sin, qo, ko, vo,
+                       rows, (int)seq_len, hq, hkv, eps);
+  else
+    hipLaunchKernelGGL(qk_norm_rope_kernel<256>, grid, dim3(256), 0, stream, qp, kp, vp, qw, kw, cos, sin, qo, ko, vo,
+                       rows, (int)seq_len, hq, hkv, eps);
+  BFLY_CHECK_LAUNCH("bfly_qk_norm_rope");
+  return BFLY_OK;
+}
+
+extern "C" int bfly_silu_mul(const void* gate, const void* up, int64_t n, void* out, hipStream_t stream) {
+  BFLY_CHECK_ARG(gate && up && out, "null pointer");
+  BFLY_CHECK_ARG(n > 0 && (n + 255) / 256 <= INT32_MAX, "bad length");
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const __bf16*>(gate), static_cast<const __bf16*>(up), static_cast<__bf16*>(out), n);
+  BFLY_CHECK_LAUNCH("bfly_silu_mul");
+  return BFLY_OK;
+}

@@ -8,7 +8,12 @@ with q/k/v/o projections, per-head q/k RMSNorm and RoPE (qwen_mlx.py:260-357),
 SwiGLU MLP, RMSNorm, tied embeddings.  Linear weights are stored 4-bit affine
 (group 64 along the input dimension, bf16 scale and bias per group:
 w = q * scale + bias, q in [0, 15]) and dequantized once to bf16; the
-non-attention GEMMs run through PyTorch-ROCm.
+non-attention GEMMs run through PyTorch-ROCm.  On the GPU (bf16) the row-wise
+and elementwise steps -- residual add + RMSNorm, q/k norm + RoPE + the move to
+heads-first, SiLU * up -- run as single HIP launches
+(include/butterfly_amd_decoder.h) with the rounding points of the PyTorch
+forms written below, which are the model's definition and what a CPU copy of
+the model runs.
 
 ``swap_qwen_attention_with_butterfly(model, cfg=...)`` replaces every
 attention by :class:`ButterflyAttention`, which keeps the projections, norms
@@ -27,6 +32,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _native
+from ._device import on, stream_of
 from .integrations import ButterflyAttentionCore, QwenButterflyConfig
 
 
@@ -89,6 +96,26 @@ class QuantLinear(nn.Module):
         return F.linear(x, self.weight)
 
 
+def _hip(x: torch.Tensor) -> bool:
+    """bf16 tensors on the GPU take the HIP kernels of the decoder steps."""
+    return x.is_cuda and x.dtype == torch.bfloat16
+
+
+def add_rms_norm(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torch.Tensor, eps: float):
+    """``(h, n)``: ``h = x + residual`` (bf16; ``x`` when no residual) and ``n = RMSNorm(h) * weight``,
+    one launch of ``bfly_add_rms_norm``."""
+    xc = x.contiguous()
+    dim = int(xc.shape[-1])
+    n = torch.empty_like(xc)
+    rc = residual.contiguous() if residual is not None else None
+    h = torch.empty_like(xc) if rc is not None else None
+    with on(xc.device):
+        _native.call("bfly_add_rms_norm", xc.data_ptr(), rc.data_ptr() if rc is not None else None,
+                     weight.data_ptr(), xc.numel() // dim, dim, float(eps), h.data_ptr() if h is not None else None,
+                     n.data_ptr(), stream_of(xc))
+    return (h if h is not None else xc), n
+
+
 class RMSNorm(nn.Module):
     def __init__(self, dim: int, eps: float, device):
         super().__init__()
@@ -96,6 +123,8 @@ class RMSNorm(nn.Module):
         self.eps = eps
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if _hip(x) and x.shape[-1] % 256 == 0:
+            return add_rms_norm(x, None, self.weight, self.eps)[1]
         xf = x.float()
         y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
         return (y * self.weight.float()).to(x.dtype)
@@ -137,6 +166,19 @@ class Attention(nn.Module):
         ``rope`` is an optional precomputed ``(cos, sin)`` for ``positions``."""
         b, t, _ = x.shape
         c = self.cfg
+        if _hip(x) and c.head_dim in (128, 256):
+            qp, kp, vp = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+            cos, sin = rope if rope is not None else rope_cos_sin(positions, c.head_dim, c.rope_theta)
+            cos, sin = cos.float().contiguous(), sin.float().contiguous()
+            qo = torch.empty(b, c.num_heads, t, c.head_dim, dtype=x.dtype, device=x.device)
+            ko = torch.empty(b, c.num_kv_heads, t, c.head_dim, dtype=x.dtype, device=x.device)
+            vo = torch.empty_like(ko)
+            with on(x.device):
+                _native.call("bfly_qk_norm_rope", qp.data_ptr(), kp.data_ptr(), vp.data_ptr(),
+                             self.q_norm.weight.data_ptr(), self.k_norm.weight.data_ptr(), cos.data_ptr(),
+                             sin.data_ptr(), b, t, c.num_heads, c.num_kv_heads, c.head_dim, float(self.q_norm.eps),
+                             qo.data_ptr(), ko.data_ptr(), vo.data_ptr(), stream_of(x))
+            return qo, ko, vo
         q = self.q_proj(x).view(b, t, c.num_heads, c.head_dim).transpose(1, 2)
         k = self.k_proj(x).view(b, t, c.num_kv_heads, c.head_dim).transpose(1, 2)
         v = self.v_proj(x).view(b, t, c.num_kv_heads, c.head_dim).transpose(1, 2)
@@ -199,6 +241,12 @@ class MLP(nn.Module):
         self.down_proj = QuantLinear(f, h, generator=generator, device=device, group=cfg.quant_group)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if _hip(x):
+            g, u = self.gate_proj(x), self.up_proj(x)
+            s = torch.empty_like(g)
+            with on(x.device):
+                _native.call("bfly_silu_mul", g.data_ptr(), u.data_ptr(), g.numel(), s.data_ptr(), stream_of(x))
+            return self.down_proj(s)
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
 
 
@@ -211,6 +259,10 @@ class DecoderLayer(nn.Module):
         self.mlp = MLP(cfg, generator=generator, device=device)
 
     def forward(self, x: torch.Tensor, positions: torch.Tensor, cache=None, rope=None) -> torch.Tensor:
+        if _hip(x) and x.shape[-1] % 256 == 0:
+            a = self.self_attn(self.input_layernorm(x), positions, cache, rope)
+            h, n = add_rms_norm(x, a, self.post_attention_layernorm.weight, self.post_attention_layernorm.eps)
+            return h + self.mlp(n)
         x = x + self.self_attn(self.input_layernorm(x), positions, cache, rope)
         return x + self.mlp(self.post_attention_layernorm(x))
 
@@ -228,6 +280,11 @@ class Decoder(nn.Module):
             requires_grad=False)
         self.layers = nn.ModuleList(DecoderLayer(cfg, generator=g, device=device) for _ in range(cfg.num_layers))
         self.norm = RMSNorm(cfg.hidden_size, cfg.rms_eps, device)
+
+    def _logits(self, h: torch.Tensor) -> torch.Tensor:
+        """Tied lm_head for a few rows: embed @ h^T, which PyTorch-ROCm runs as a
+        GEMV at twice the rate of the F.linear form for one row."""
+        return torch.matmul(self.embed_tokens, h.t()).t()
 
     def _rope(self, start: int, t: int, device):
         """cos/sin rows for positions [start, start+t) from a table grown on demand."""
@@ -248,7 +305,7 @@ class Decoder(nn.Module):
         for layer, cache in zip(self.layers, caches):
             x = layer(x, positions, cache, rope)
         h = self.norm(x[:, -1])
-        return F.linear(h, self.embed_tokens).float()
+        return self._logits(h).float()
 
     @torch.no_grad()
     def greedy_graph(self, prompt: torch.Tensor, new_tokens: int, caches: List) -> torch.Tensor:
@@ -287,7 +344,7 @@ class Decoder(nn.Module):
             rope = (cos_tab.index_select(0, pos), sin_tab.index_select(0, pos))
             for layer, cache in zip(self.layers, caches):
                 x = layer(x, pos, cache, rope)
-            nxt = F.linear(self.norm(x[:, -1]), self.embed_tokens).argmax(-1, keepdim=True)
+            nxt = self._logits(self.norm(x[:, -1])).argmax(-1, keepdim=True)
             tok.copy_(nxt)
             out.index_copy_(1, step, nxt)
             pos.add_(1)

@@ -1,0 +1,54 @@
+/*
+ * butterfly_amd decoder steps -- C ABI of the row-wise and elementwise steps of
+ * the swapped decoder (bf16 in and out, fp32 inside), one launch each.
+ *
+ * Conventions are those of butterfly_amd.h (device pointers, 16-byte aligned
+ * contiguous tensors, work enqueued on `stream`, 0 or a negative BFLY_ERR_*).
+ * The rounding points are those of the PyTorch forms in butterfly_amd/decoder.py:
+ * bf16 after a residual add, after each norm, after RoPE, after SiLU and after
+ * the product.
+ */
+#ifndef BUTTERFLY_AMD_DECODER_H_
+#define BUTTERFLY_AMD_DECODER_H_
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Device: h = x + residual (bf16), norm_out = RMSNorm(h) * weight over `dim`
+ * (eps inside the square root), for `rows` rows.  With residual == NULL (and
+ * h_out == NULL) it is the plain RMSNorm of x.  dim a multiple of 256, at most
+ * 8192.  The decoder layers' input / post-attention norms and the final norm;
+ * no counterpart in the reference's own code (the decoders it swaps into keep
+ * their norms).
+ */
+int bfly_add_rms_norm(const void* x, const void* residual, const void* weight, int64_t rows, int dim,
+                      float eps, void* h_out, void* norm_out, hipStream_t stream);
+
+/*
+ * Device: the projection tail of the swapped attention -- per-head RMSNorm of q
+ * [B, T, Hq*d] and k [B, T, Hkv*d] with q_weight / k_weight [d], rotate-half RoPE
+ * with cos/sin [T, d] (fp32, row t = this call's t-th position), and the move to
+ * heads-first q_out [B, Hq, T, d], k_out and v_out [B, Hkv, T, d] (v unchanged).
+ * head_dim 128 or 256.  Replaces q_norm / k_norm / transpose / RoPE of
+ * bna/integrations/qwen_torch.py:550-562 (qwen_mlx.py:288-357).
+ */
+int bfly_qk_norm_rope(const void* q, const void* k, const void* v, const void* q_weight, const void* k_weight,
+                      const float* cos, const float* sin, int64_t batch, int64_t seq_len, int hq, int hkv,
+                      int head_dim, float eps, void* q_out, void* k_out, void* v_out, hipStream_t stream);
+
+/*
+ * Device: out = SiLU(gate) * up over n elements (the SwiGLU MLP's product); no
+ * counterpart in the reference's own code.
+ */
+int bfly_silu_mul(const void* gate, const void* up, int64_t n, void* out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BUTTERFLY_AMD_DECODER_H_ */

@@ -75,9 +75,10 @@ SIGNATURES = {
                                  _vp, _vp, _i64, _i64, _vp]),
     # include/butterfly_amd_decoder.h
     "bfly_add_rms_norm": (_int, [_vp, _vp, _vp, _i64, _int, _f32, _vp, _vp, _vp]),
-    "bfly_qk_norm_rope": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _int, _f32, _vp, _vp,
-                                 _vp, _vp]),
-    "bfly_silu_mul": (_int, [_vp, _vp, _i64, _vp, _vp]),
+    "bfly_qk_norm_rope": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _int,
+                                 _f32, _vp, _vp, _vp, _vp]),
+    "bfly_silu_mul": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "bfly_argmax_rows": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp]),
 }
 
 _lib = None

@@ -97,7 +97,8 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const __bf16* __restr
                                                            const __bf16* __restrict__ kw, const float* __restrict__ cosv,
                                                            const float* __restrict__ sinv, __bf16* __restrict__ qo,
                                                            __bf16* __restrict__ ko, __bf16* __restrict__ vo, int64_t rows,
-                                                           int t_len, int hq, int hkv, float eps) {
+                                                           int t_len, int hq, int hkv, int64_t sq, int64_t sk,
+                                                           int64_t sv, float eps) {
   constexpr int HALF = D / 2;
   constexpr int PER = HALF / 64;   // elements per lane in each half
   const int lane = threadIdx.x & 63;
@@ -112,17 +113,17 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const __bf16* __restr
   __bf16* dst;
   const __bf16* w = nullptr;
   if (head < hq) {
-    src = q + (row * hq + head) * D;
+    src = q + row * sq + (int64_t)head * D;
     dst = qo + ((b * hq + head) * t_len + tt) * D;
     w = qw;
   } else if (head < hq + hkv) {
     const int hk = head - hq;
-    src = k + (row * hkv + hk) * D;
+    src = k + row * sk + (int64_t)hk * D;
     dst = ko + ((b * hkv + hk) * t_len + tt) * D;
     w = kw;
   } else {
     const int hv = head - hq - hkv;
-    src = v + (row * hkv + hv) * D;
+    src = v + row * sv + (int64_t)hv * D;
     dst = vo + ((b * hkv + hv) * t_len + tt) * D;
   }
   float lo[PER], hi[PER];
@@ -156,13 +157,17 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const __bf16* __restr
   }
 }
 
+// rows x cols elements; gate and up rows are `stride` elements apart (a fused
+// gate|up projection output has stride 2 * cols), out is contiguous.
 __global__ void __launch_bounds__(256) silu_mul_kernel(const __bf16* __restrict__ g, const __bf16* __restrict__ u,
-                                                       __bf16* __restrict__ out, int64_t n) {
+                                                       __bf16* __restrict__ out, int64_t cols, int64_t stride,
+                                                       int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
-  const float x = (float)g[i];
+  const int64_t r = i / cols, c = i - r * cols;
+  const float x = (float)g[r * stride + c];
   const float sg = (float)(__bf16)(x / (1.f + expf(-x)));
-  out[i] = (__bf16)(sg * (float)u[i]);
+  out[i] = (__bf16)(sg * (float)u[r * stride + c]);
 }
 
 }  // namespace bfly
@@ -193,7 +198,8 @@ extern "C" int bfly_add_rms_norm(const void* x, const void* residual, const void
   return BFLY_OK;
 }
 
-extern "C" int bfly_qk_norm_rope(const void* q, const void* k, const void* v, const void* q_weight,
+extern "C" int bfly_qk_norm_rope(const void* q, const void* k, const void* v, int64_t q_row_stride,
+                                 int64_t k_row_stride, int64_t v_row_stride, const void* q_weight,
                                  const void* k_weight, const float* cos, const float* sin, int64_t batch,
                                  int64_t seq_len, int hq, int hkv, int head_dim, float eps, void* q_out, void* k_out,
                                  void* v_out, hipStream_t stream) {
@@ -201,6 +207,9 @@ extern "C" int bfly_qk_norm_rope(const void* q, const void* k, const void* v, co
   BFLY_CHECK_ARG(batch > 0 && seq_len > 0 && hq > 0 && hkv > 0, "bad shape");
   BFLY_CHECK_ARG(head_dim == 128 || head_dim == 256, "bfly_qk_norm_rope: head_dim=%d unsupported (128, 256)",
                  head_dim);
+  BFLY_CHECK_ARG(q_row_stride >= (int64_t)hq * head_dim && k_row_stride >= (int64_t)hkv * head_dim &&
+                     v_row_stride >= (int64_t)hkv * head_dim,
+                 "row strides must cover a row's heads");
   const int64_t rows = batch * seq_len;
   const int64_t items = rows * (hq + 2 * hkv);
   BFLY_CHECK_ARG((items + 3) / 4 <= INT32_MAX && seq_len <= INT32_MAX, "too many rows");
@@ -211,19 +220,149 @@ extern "C" int bfly_qk_norm_rope(const void* q, const void* k, const void* v, co
   __bf16 *qo = static_cast<__bf16*>(q_out), *ko = static_cast<__bf16*>(k_out), *vo = static_cast<__bf16*>(v_out);
   if (head_dim == 128)
     hipLaunchKernelGGL(qk_norm_rope_kernel<128>, grid, dim3(256), 0, stream, qp, kp, vp, qw, kw, cos, sin, qo, ko, vo,
-                       rows, (int)seq_len, hq, hkv, eps);
+                       rows, (int)seq_len, hq, hkv, q_row_stride, k_row_stride, v_row_stride, eps);
   else
     hipLaunchKernelGGL(qk_norm_rope_kernel<256>, grid, dim3(256), 0, stream, qp, kp, vp, qw, kw, cos, sin, qo, ko, vo,
-                       rows, (int)seq_len, hq, hkv, eps);
+                       rows, (int)seq_len, hq, hkv, q_row_stride, k_row_stride, v_row_stride, eps);
   BFLY_CHECK_LAUNCH("bfly_qk_norm_rope");
   return BFLY_OK;
 }
 
-extern "C" int bfly_silu_mul(const void* gate, const void* up, int64_t n, void* out, hipStream_t stream) {
+extern "C" int bfly_silu_mul(const void* gate, const void* up, int64_t rows, int64_t cols, int64_t in_row_stride,
+                             void* out, hipStream_t stream) {
   BFLY_CHECK_ARG(gate && up && out, "null pointer");
-  BFLY_CHECK_ARG(n > 0 && (n + 255) / 256 <= INT32_MAX, "bad length");
+  BFLY_CHECK_ARG(rows > 0 && cols > 0 && in_row_stride >= cols, "bad shape");
+  const int64_t n = rows * cols;
+  BFLY_CHECK_ARG((n + 255) / 256 <= INT32_MAX, "bad length");
   hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                     static_cast<const __bf16*>(gate), static_cast<const __bf16*>(up), static_cast<__bf16*>(out), n);
+                     static_cast<const __bf16*>(gate), static_cast<const __bf16*>(up), static_cast<__bf16*>(out), cols,
+                     in_row_stride, n);
   BFLY_CHECK_LAUNCH("bfly_silu_mul");
+  return BFLY_OK;
+}
+
+namespace bfly {
+
+// Greedy selection order of torch.argmax: NaN above every number, then larger
+// values, then the lower index among equals.
+__device__ __forceinline__ bool argmax_better(float v, int64_t i, float bv, int64_t bi) {
+  if (bi < 0) return true;
+  const bool vn = v != v, bn = bv != bv;
+  if (vn != bn) return vn;
+  if (!vn && v != bv) return v > bv;
+  return i < bi;
+}
+
+__device__ __forceinline__ void argmax_combine(float& bv, int64_t& bi, float v, int64_t i) {
+  if (i >= 0 && argmax_better(v, i, bv, bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+// Block-wide combine of every thread's (value, index) candidate (256 threads).
+__device__ __forceinline__ void argmax_block(float& bv, int64_t& bi) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int64_t oi = __shfl_xor(bi, o);
+    argmax_combine(bv, bi, ov, oi);
+  }
+  __shared__ float sv[4];
+  __shared__ int64_t si[4];
+  const int t = threadIdx.x;
+  if ((t & 63) == 0) {
+    sv[t >> 6] = bv;
+    si[t >> 6] = bi;
+  }
+  __syncthreads();
+  if (t == 0)
+    for (int w = 1; w < 4; ++w) argmax_combine(bv, bi, sv[w], si[w]);
+}
+
+// Pass 1: workgroup (p, r) scans elements [p * span, (p + 1) * span) of row r
+// (span a multiple of 8) and leaves its candidate in part_v / part_i [r * parts + p],
+// or, with a single part, the answer in out[r].  Rows that are contiguous with a
+// 16-byte aligned start are read 8 elements per load.
+__global__ void __launch_bounds__(256) argmax_part_kernel(const __bf16* __restrict__ x, int64_t n, int64_t row_stride,
+                                                          int64_t col_stride, bool vec, int64_t span, int parts,
+                                                          float* __restrict__ part_v, int64_t* __restrict__ part_i,
+                                                          int64_t* __restrict__ out) {
+  const int p = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
+  const __bf16* row = x + (int64_t)r * row_stride;
+  const int64_t lo = (int64_t)p * span, hi = lo + span < n ? lo + span : n;
+  float bv = 0.f;
+  int64_t bi = -1;
+  if (vec) {
+    const int64_t c_lo = lo >> 3, c_hi = hi >> 3;  // whole 8-element pieces; lo is a multiple of 8
+    const uint4* r4 = reinterpret_cast<const uint4*>(row);
+#pragma unroll 2
+    for (int64_t c = c_lo + t; c < c_hi; c += 256) {
+      const uint4 u = r4[c];
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float v = __uint_as_float((j & 1) ? (w[j >> 1] & 0xffff0000u) : (w[j >> 1] << 16));
+        argmax_combine(bv, bi, v, c * 8 + j);
+      }
+    }
+    for (int64_t i = (c_hi << 3) + t; i < hi; i += 256) argmax_combine(bv, bi, (float)row[i], i);
+  } else {
+#pragma unroll 4
+    for (int64_t i = lo + t; i < hi; i += 256) argmax_combine(bv, bi, (float)row[i * col_stride], i);
+  }
+  argmax_block(bv, bi);
+  if (t == 0) {
+    if (parts == 1) {
+      out[r] = bi;
+    } else {
+      part_v[(int64_t)r * parts + p] = bv;
+      part_i[(int64_t)r * parts + p] = bi;
+    }
+  }
+}
+
+// Pass 2: one workgroup per row combines its `parts` (at most 256) candidates.
+__global__ void __launch_bounds__(256) argmax_final_kernel(const float* __restrict__ part_v,
+                                                           const int64_t* __restrict__ part_i, int parts,
+                                                           int64_t* __restrict__ out) {
+  const int r = blockIdx.x, t = threadIdx.x;
+  float bv = 0.f;
+  int64_t bi = -1;
+  if (t < parts) {
+    bv = part_v[(int64_t)r * parts + t];
+    bi = part_i[(int64_t)r * parts + t];
+  }
+  argmax_block(bv, bi);
+  if (t == 0) out[r] = bi;
+}
+
+}  // namespace bfly
+
+extern "C" int bfly_argmax_rows(const void* x, int64_t rows, int64_t n, int64_t row_stride, int64_t col_stride,
+                                void* workspace, int64_t workspace_bytes, void* out, hipStream_t stream) {
+  BFLY_CHECK_ARG(x && out, "null pointer");
+  BFLY_CHECK_ARG(rows > 0 && rows <= 65535 && n > 0 && col_stride > 0 && row_stride >= 0, "bad shape");
+  BFLY_CHECK_ARG(workspace_bytes >= 0 && (workspace != nullptr || workspace_bytes == 0), "bad workspace");
+  if (rows == 1) row_stride = 0;  // a single row: its stride is never used (a [1, n] view may carry any)
+  const bool vec = col_stride == 1 && row_stride % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+  // about 4096 elements per workgroup, at most 256 parts, as many as the workspace holds
+  int64_t parts = (n + 4095) / 4096;
+  if (parts > 256) parts = 256;
+  // part_v (rows * parts floats), padding to 8 bytes, part_i (rows * parts int64)
+  const int64_t fit = reinterpret_cast<uintptr_t>(workspace) % 8 == 0 && workspace_bytes >= 8
+                          ? (workspace_bytes - 4) / (rows * (int64_t)(sizeof(float) + sizeof(int64_t)))
+                          : 0;
+  if (parts > fit) parts = fit > 1 ? fit : 1;
+  const int64_t span = ((n + parts - 1) / parts + 7) / 8 * 8;
+  float* part_v = static_cast<float*>(workspace);
+  int64_t* part_i = parts > 1 ? reinterpret_cast<int64_t*>(part_v + rows * parts + (rows * parts & 1)) : nullptr;
+  hipLaunchKernelGGL(bfly::argmax_part_kernel, dim3((unsigned)parts, (unsigned)rows), dim3(256), 0, stream,
+                     static_cast<const __bf16*>(x), n, row_stride, col_stride, vec, span, (int)parts, part_v, part_i,
+                     static_cast<int64_t*>(out));
+  if (parts > 1)
+    hipLaunchKernelGGL(bfly::argmax_final_kernel, dim3((unsigned)rows), dim3(256), 0, stream, part_v, part_i,
+                       (int)parts, static_cast<int64_t*>(out));
+  BFLY_CHECK_LAUNCH("bfly_argmax_rows");
   return BFLY_OK;
 }

@@ -8,7 +8,8 @@ with q/k/v/o projections, per-head q/k RMSNorm and RoPE (qwen_mlx.py:260-357),
 SwiGLU MLP, RMSNorm, tied embeddings.  Linear weights are stored 4-bit affine
 (group 64 along the input dimension, bf16 scale and bias per group:
 w = q * scale + bias, q in [0, 15]) and dequantized once to bf16; the
-non-attention GEMMs run through PyTorch-ROCm.  On the GPU (bf16) the row-wise
+non-attention GEMMs run through PyTorch-ROCm (q/k/v and gate/up as one GEMM
+each, a single activation row as a GEMV).  On the GPU (bf16) the row-wise
 and elementwise steps -- residual add + RMSNorm, q/k norm + RoPE + the move to
 heads-first, SiLU * up -- run as single HIP launches
 (include/butterfly_amd_decoder.h) with the rounding points of the PyTorch
@@ -93,7 +94,29 @@ class QuantLinear(nn.Module):
         self.register_buffer("weight", dequantize_affine(packed, scale, bias, group))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return F.linear(x, self.weight)
+        return _linear(x, self.weight)
+
+
+def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``x @ w^T``.  One row of activations on the GPU (a decode step at batch 1) runs as
+    ``w @ x^T``, which PyTorch-ROCm hands to a GEMV kernel that streams the weight at close
+    to HBM rate; its ``F.linear`` form is a skinny GEMM that spreads a small weight over too
+    few workgroups."""
+    if x.is_cuda and x.numel() == x.shape[-1]:
+        return torch.matmul(w, x.reshape(-1, 1)).view(*x.shape[:-1], w.shape[0])
+    return F.linear(x, w)
+
+
+def _fuse_rows(*linears: QuantLinear) -> torch.Tensor:
+    """One weight matrix holding the given layers' (dequantized) weights as consecutive row
+    ranges; each layer's ``weight`` becomes a view of its range, so the memory is not doubled."""
+    fused = torch.cat([m.weight for m in linears])
+    row = 0
+    for m in linears:
+        n = m.weight.shape[0]
+        m.weight = fused[row:row + n]
+        row += n
+    return fused
 
 
 def _hip(x: torch.Tensor) -> bool:
@@ -114,6 +137,20 @@ def add_rms_norm(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torc
                      weight.data_ptr(), xc.numel() // dim, dim, float(eps), h.data_ptr() if h is not None else None,
                      n.data_ptr(), stream_of(xc))
     return (h if h is not None else xc), n
+
+
+def argmax_rows(x: torch.Tensor, parallel: bool = True) -> torch.Tensor:
+    """``x.argmax(-1, keepdim=True)`` for a 2-D bf16 GPU tensor (any strides) through
+    ``bfly_argmax_rows``: torch's argmax reduction records a memset node when captured in a
+    graph, these kernels write their results directly.  ``parallel=False`` passes no
+    workspace (one workgroup per row)."""
+    rows, n = x.shape
+    out = torch.empty(rows, 1, dtype=torch.long, device=x.device)
+    ws = torch.empty(rows * 3072 + 8 if parallel else 0, dtype=torch.uint8, device=x.device)
+    with on(x.device):
+        _native.call("bfly_argmax_rows", x.data_ptr(), rows, n, x.stride(0), x.stride(1),
+                     ws.data_ptr() if parallel else None, ws.numel(), out.data_ptr(), stream_of(x))
+    return out
 
 
 class RMSNorm(nn.Module):
@@ -159,6 +196,9 @@ class Attention(nn.Module):
         self.o_proj = QuantLinear(cfg.num_heads * d, h, generator=generator, device=device, group=cfg.quant_group)
         self.q_norm = RMSNorm(d, cfg.rms_eps, device)
         self.k_norm = RMSNorm(d, cfg.rms_eps, device)
+        # q, k and v weights as row ranges of one [Hq*d + 2*Hkv*d, hidden] matrix: one GEMM per
+        # projection on the GPU path, whose kernels read q, k and v as column ranges of its output.
+        self.register_buffer("qkv_weight", _fuse_rows(self.q_proj, self.k_proj, self.v_proj))
 
     def project(self, x: torch.Tensor, positions: torch.Tensor, rope=None):
         """x [B, T, hidden] -> q [B, Hq, T, d], k/v [B, Hkv, T, d] (normed, RoPE applied).
@@ -167,14 +207,16 @@ class Attention(nn.Module):
         b, t, _ = x.shape
         c = self.cfg
         if _hip(x) and c.head_dim in (128, 256):
-            qp, kp, vp = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+            qkv = _linear(x, self.qkv_weight)
+            nq, nkv = c.num_heads * c.head_dim, c.num_kv_heads * c.head_dim
+            base, ld, es = qkv.data_ptr(), qkv.shape[-1], qkv.element_size()
             cos, sin = rope if rope is not None else rope_cos_sin(positions, c.head_dim, c.rope_theta)
             cos, sin = cos.float().contiguous(), sin.float().contiguous()
             qo = torch.empty(b, c.num_heads, t, c.head_dim, dtype=x.dtype, device=x.device)
             ko = torch.empty(b, c.num_kv_heads, t, c.head_dim, dtype=x.dtype, device=x.device)
             vo = torch.empty_like(ko)
             with on(x.device):
-                _native.call("bfly_qk_norm_rope", qp.data_ptr(), kp.data_ptr(), vp.data_ptr(),
+                _native.call("bfly_qk_norm_rope", base, base + nq * es, base + (nq + nkv) * es, ld, ld, ld,
                              self.q_norm.weight.data_ptr(), self.k_norm.weight.data_ptr(), cos.data_ptr(),
                              sin.data_ptr(), b, t, c.num_heads, c.num_kv_heads, c.head_dim, float(self.q_norm.eps),
                              qo.data_ptr(), ko.data_ptr(), vo.data_ptr(), stream_of(x))
@@ -239,13 +281,16 @@ class MLP(nn.Module):
         self.gate_proj = QuantLinear(h, f, generator=generator, device=device, group=cfg.quant_group)
         self.up_proj = QuantLinear(h, f, generator=generator, device=device, group=cfg.quant_group)
         self.down_proj = QuantLinear(f, h, generator=generator, device=device, group=cfg.quant_group)
+        self.register_buffer("gate_up_weight", _fuse_rows(self.gate_proj, self.up_proj))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if _hip(x):
-            g, u = self.gate_proj(x), self.up_proj(x)
-            s = torch.empty_like(g)
+            gu = _linear(x, self.gate_up_weight)           # [..., 2f]: gate columns, then up columns
+            f = gu.shape[-1] // 2
+            s = gu.new_empty(*gu.shape[:-1], f)
             with on(x.device):
-                _native.call("bfly_silu_mul", g.data_ptr(), u.data_ptr(), g.numel(), s.data_ptr(), stream_of(x))
+                _native.call("bfly_silu_mul", gu.data_ptr(), gu.data_ptr() + f * gu.element_size(),
+                             gu.numel() // (2 * f), f, 2 * f, s.data_ptr(), stream_of(x))
             return self.down_proj(s)
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
 
@@ -265,6 +310,17 @@ class DecoderLayer(nn.Module):
             return h + self.mlp(n)
         x = x + self.self_attn(self.input_layernorm(x), positions, cache, rope)
         return x + self.mlp(self.post_attention_layernorm(x))
+
+    def forward_split(self, x: torch.Tensor, pending: Optional[torch.Tensor], positions: torch.Tensor, cache=None,
+                      rope=None):
+        """The HIP form of ``forward`` with the last residual add left pending: returns ``(h, m)``
+        whose sum is the layer's output.  ``pending`` is the previous layer's ``m`` (or None); it
+        is added to ``x`` in the launch that computes the input RMSNorm, which rounds the sum to
+        bf16 before normalising it, as the separate add would."""
+        x, n = add_rms_norm(x, pending, self.input_layernorm.weight, self.input_layernorm.eps)
+        a = self.self_attn(n, positions, cache, rope)
+        h, n = add_rms_norm(x, a, self.post_attention_layernorm.weight, self.post_attention_layernorm.eps)
+        return h, self.mlp(n)
 
 
 class Decoder(nn.Module):
@@ -296,16 +352,26 @@ class Decoder(nn.Module):
             self._rope_tab = tab
         return tab[0][start:need], tab[1][start:need]
 
+    def _last_hidden(self, x: torch.Tensor, positions: torch.Tensor, caches: List, rope) -> torch.Tensor:
+        """Run every layer over the embedded ``x`` [B, T, hidden]; returns the final RMSNorm of
+        the last position, [B, hidden].  On the HIP path each layer's closing residual add is
+        folded into the next layer's (or the final) RMSNorm launch."""
+        if _hip(x) and x.shape[-1] % 256 == 0:
+            m = None
+            for layer, cache in zip(self.layers, caches):
+                x, m = layer.forward_split(x, m, positions, cache, rope)
+            return add_rms_norm(x[:, -1], m[:, -1] if m is not None else None, self.norm.weight, self.norm.eps)[1]
+        for layer, cache in zip(self.layers, caches):
+            x = layer(x, positions, cache, rope)
+        return self.norm(x[:, -1])
+
     @torch.no_grad()
     def forward(self, tokens: torch.Tensor, caches: List, start: int) -> torch.Tensor:
         """tokens [B, T] at positions [start, start+T); returns logits [B, vocab] of the last position."""
         x = F.embedding(tokens, self.embed_tokens)
         positions = torch.arange(start, start + tokens.shape[1], device=tokens.device)
         rope = self._rope(start, tokens.shape[1], tokens.device)
-        for layer, cache in zip(self.layers, caches):
-            x = layer(x, positions, cache, rope)
-        h = self.norm(x[:, -1])
-        return self._logits(h).float()
+        return self._logits(self._last_hidden(x, positions, caches, rope)).float()
 
     @torch.no_grad()
     def greedy_graph(self, prompt: torch.Tensor, new_tokens: int, caches: List) -> torch.Tensor:
@@ -342,9 +408,8 @@ class Decoder(nn.Module):
         def one_step():
             x = F.embedding(tok, self.embed_tokens)
             rope = (cos_tab.index_select(0, pos), sin_tab.index_select(0, pos))
-            for layer, cache in zip(self.layers, caches):
-                x = layer(x, pos, cache, rope)
-            nxt = self._logits(self.norm(x[:, -1])).argmax(-1, keepdim=True)
+            lg = self._logits(self._last_hidden(x, pos, caches, rope))
+            nxt = argmax_rows(lg) if _hip(lg) else lg.argmax(-1, keepdim=True)
             tok.copy_(nxt)
             out.index_copy_(1, step, nxt)
             pos.add_(1)

@@ -31,21 +31,41 @@ int bfly_add_rms_norm(const void* x, const void* residual, const void* weight, i
 
 /*
  * Device: the projection tail of the swapped attention -- per-head RMSNorm of q
- * [B, T, Hq*d] and k [B, T, Hkv*d] with q_weight / k_weight [d], rotate-half RoPE
+ * [B*T rows of Hq*d] and k [B*T rows of Hkv*d] (rows *_row_stride elements apart,
+ * so q, k and v may be column ranges of one fused projection output) with
+ * q_weight / k_weight [d], rotate-half RoPE
  * with cos/sin [T, d] (fp32, row t = this call's t-th position), and the move to
  * heads-first q_out [B, Hq, T, d], k_out and v_out [B, Hkv, T, d] (v unchanged).
  * head_dim 128 or 256.  Replaces q_norm / k_norm / transpose / RoPE of
  * bna/integrations/qwen_torch.py:550-562 (qwen_mlx.py:288-357).
  */
-int bfly_qk_norm_rope(const void* q, const void* k, const void* v, const void* q_weight, const void* k_weight,
+int bfly_qk_norm_rope(const void* q, const void* k, const void* v, int64_t q_row_stride, int64_t k_row_stride,
+                      int64_t v_row_stride, const void* q_weight, const void* k_weight,
                       const float* cos, const float* sin, int64_t batch, int64_t seq_len, int hq, int hkv,
                       int head_dim, float eps, void* q_out, void* k_out, void* v_out, hipStream_t stream);
 
 /*
- * Device: out = SiLU(gate) * up over n elements (the SwiGLU MLP's product); no
- * counterpart in the reference's own code.
+ * Device: out [rows, cols] = SiLU(gate) * up, the SwiGLU MLP's product; gate and
+ * up rows are in_row_stride elements apart (2 * cols for a fused gate|up
+ * projection output).  No counterpart in the reference's own code.
  */
-int bfly_silu_mul(const void* gate, const void* up, int64_t n, void* out, hipStream_t stream);
+int bfly_silu_mul(const void* gate, const void* up, int64_t rows, int64_t cols, int64_t in_row_stride, void* out,
+                  hipStream_t stream);
+
+/*
+ * Device: out[r] (int64) = index of the greedy pick of row r of x (bf16, `rows`
+ * rows of n elements, element (r, i) at x[r * row_stride + i * col_stride]),
+ * in torch.argmax's order: NaN first, then the largest value, then the lowest
+ * index among equals.  rows at most 65535.  `workspace` (device, 8-byte
+ * aligned, `workspace_bytes` long; rows * 3 KiB + 8 bytes is enough) holds per-workgroup
+ * candidates so that a row is scanned by up to 256 workgroups; a smaller or
+ * NULL workspace gives fewer workgroups per row (one at the least), never a
+ * different result.  The decoder's greedy step inside a captured decode graph
+ * (torch's argmax reduction records a memset node there); no counterpart in the
+ * reference's own code.
+ */
+int bfly_argmax_rows(const void* x, int64_t rows, int64_t n, int64_t row_stride, int64_t col_stride,
+                     void* workspace, int64_t workspace_bytes, void* out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@ import torch
 import torch.nn.functional as F
 
 from butterfly_amd import _native
-from butterfly_amd.decoder import RMSNorm, add_rms_norm, apply_rope, rope_cos_sin
+from butterfly_amd.decoder import RMSNorm, add_rms_norm, apply_rope, argmax_rows, rope_cos_sin
 
 pytestmark = pytest.mark.gpu
 
@@ -59,23 +59,61 @@ def test_qk_norm_rope(d):
     vo = torch.empty_like(ko)
     qc, kc, vc, cc, sc = qp.cuda(), kp.cuda(), vp.cuda(), cos.cuda().contiguous(), sin.cuda().contiguous()
     qw, kw = qn.weight.cuda(), kn.weight.cuda()
-    _native.call("bfly_qk_norm_rope", qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), qw.data_ptr(), kw.data_ptr(),
-                 cc.data_ptr(), sc.data_ptr(), B, T, hq, hkv, d, 1e-6, qo.data_ptr(), ko.data_ptr(), vo.data_ptr(),
-                 torch.cuda.current_stream().cuda_stream)
+    _native.call("bfly_qk_norm_rope", qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), hq * d, hkv * d, hkv * d,
+                 qw.data_ptr(), kw.data_ptr(), cc.data_ptr(), sc.data_ptr(), B, T, hq, hkv, d, 1e-6, qo.data_ptr(),
+                 ko.data_ptr(), vo.data_ptr(), torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     _close(qo.cpu(), want_q)
     _close(ko.cpu(), want_k)
     assert torch.equal(vo.cpu(), want_v)
+    # q, k and v as column ranges of one fused projection output [B, T, (hq + 2 hkv) d]
+    fused = torch.cat([qp, kp, vp], -1).cuda()
+    ld, es, base = fused.shape[-1], fused.element_size(), fused.data_ptr()
+    qo2, ko2, vo2 = torch.empty_like(qo), torch.empty_like(ko), torch.empty_like(vo)
+    _native.call("bfly_qk_norm_rope", base, base + hq * d * es, base + (hq + hkv) * d * es, ld, ld, ld,
+                 qw.data_ptr(), kw.data_ptr(), cc.data_ptr(), sc.data_ptr(), B, T, hq, hkv, d, 1e-6, qo2.data_ptr(),
+                 ko2.data_ptr(), vo2.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(qo2, qo) and torch.equal(ko2, ko) and torch.equal(vo2, vo)
 
 
 def test_silu_mul():
     g, u = _rand(9, 3, 6144, scale=3.0), _rand(10, 3, 6144)
     out = torch.empty(3, 6144, dtype=torch.bfloat16, device="cuda")
     gc, uc = g.cuda(), u.cuda()
-    _native.call("bfly_silu_mul", gc.data_ptr(), uc.data_ptr(), g.numel(), out.data_ptr(),
+    _native.call("bfly_silu_mul", gc.data_ptr(), uc.data_ptr(), 3, 6144, 6144, out.data_ptr(),
                  torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     _close(out.cpu(), F.silu(g) * u)
+    # gate and up as the two column halves of one fused [3, 2 * 6144] output
+    gu = torch.cat([g, u], -1).cuda()
+    out2 = torch.empty_like(out)
+    _native.call("bfly_silu_mul", gu.data_ptr(), gu.data_ptr() + 6144 * 2, 3, 6144, 2 * 6144, out2.data_ptr(),
+                 torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(out2, out)
+
+
+@pytest.mark.parametrize("rows,n", [(1, 151936), (3, 1000), (2, 7), (1, 8), (2, 4096 * 300 + 5)])
+def test_argmax_rows(rows, n):
+    x = _rand(11, rows, n)
+    x[:, n // 3] = 9.0                      # ties: the lower index wins
+    x[:, n // 2] = 9.0
+    if rows > 1:
+        x[1, n - 1] = float("nan")          # NaN above every number
+        x[1, n // 4] = float("nan")
+    want = torch.argmax(x, -1, keepdim=True)
+    assert torch.equal(argmax_rows(x.cuda()).cpu(), want)
+    assert torch.equal(argmax_rows(x.cuda(), parallel=False).cpu(), want)
+    # a column-major [rows, n] view, as the lm_head's GEMV form leaves its logits
+    xt = x.t().contiguous().cuda().t()
+    assert torch.equal(argmax_rows(xt).cpu(), want)
+    # one row whose view carries a row stride of 1 (the lm_head's GEMV output, transposed)
+    x1 = x[:1].t().contiguous().cuda().t()
+    assert torch.equal(argmax_rows(x1).cpu(), want[:1])
+    # a row start that is not 16-byte aligned (element path)
+    xo = torch.cat([torch.zeros(rows, 1, dtype=x.dtype), x], 1).cuda()[:, 1:]
+    assert torch.equal(argmax_rows(xo).cpu(), want)
 
 
 def test_decoder_ops_reject_bad_shapes():

@@ -26,6 +26,11 @@ import torch
 from . import _native
 from .attention import _c, _dtype_code, _on, _stream
 
+# int64 words per counter copy in the device counter array of bfly_decode_step:
+# an 8-word header, then one copy per sequence and eight for the step's route
+# workgroups, so bfly_decode_state_words(1, 1) == 8 + 9 * _DEV_SLOT.
+_DEV_SLOT = 32
+
 
 @dataclass(frozen=True)
 class RingState:
@@ -102,8 +107,10 @@ class CompressedKVCache:
     @property
     def device_counters(self) -> Optional[torch.Tensor]:
         """The device counter array, or None: word 4 is the error flag; sequence g
-        (= batch * Hkv + kv head) keeps {offset, tail_size, summary_count,
-        summary_offset} at words 8 + 4g .. 8 + 4g + 3 (all copies equal)."""
+        (= batch * Hkv + kv head) keeps a copy of ``_DEV_SLOT`` words at 8 + _DEV_SLOT*g
+        (and eight more copies follow for the kernel's route workgroups): {offset,
+        tail_size, summary_count, summary_offset} in its first four words (all copies
+        equal), then the kernel's cache of the next step's routed row."""
         return self._dev
 
     def sync(self) -> None:
@@ -123,11 +130,13 @@ class CompressedKVCache:
         self.offset, self.tail_size, self.summary_count, self.summary_offset = off, ts, sc, so
 
     def _push(self) -> None:
+        """Write the host counters into every copy; the kernel's routed-row cache is cleared."""
         if self._dev is not None:
-            g = (self._dev.numel() - 8) // 4
-            counters = torch.tensor([self.offset, self.tail_size, self.summary_count, self.summary_offset],
+            g = (self._dev.numel() - 8) // _DEV_SLOT
+            copy = torch.zeros(_DEV_SLOT, dtype=torch.int64)
+            copy[:4] = torch.tensor([self.offset, self.tail_size, self.summary_count, self.summary_offset],
                                     dtype=torch.int64)
-            self._dev.copy_(torch.cat([torch.zeros(8, dtype=torch.int64), counters.repeat(g)]))
+            self._dev.copy_(torch.cat([torch.zeros(8, dtype=torch.int64), copy.repeat(g)]))
             self._dev_dirty = False
 
     def decode_step(self, q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, *, layer_idx: int,

@@ -32,7 +32,11 @@
 // due block itself (same summation order as bfly_cache_compress), computes the
 // layer's topology at the live block count, and attends; each workgroup keeps
 // its own copy of the counters and writes it back.  A step then has fixed
-// arguments and can be captured in a HIP graph.
+// arguments and can be captured in a HIP graph.  The MFMA kernel runs eight
+// more workgroups (one per XCD) that keep counter copies of their own and
+// write the next step's routed row into the copies of the workgroups on their
+// XCD, so the next step reads it with its counters (an L2 hit) and issues its
+// summary loads together with the window loads instead of after the selection.
 #include "bfly_topology.h"
 
 namespace bfly {
@@ -43,14 +47,37 @@ constexpr int kDecMaxKeys = kDecMaxWin + kDecMaxSum;
 constexpr int kDecMaxNew = 2;   // blocks pooled in one step (one per 128 steps in steady state)
 
 // Device cache counters of step mode: state[4] is the error word; workgroup g
-// (= batch * Hkv + kv head) keeps its own copy of {offset, tail_size,
-// summary_count, summary_offset} at state[8 + 4g ...] and advances it itself,
-// so a step needs no cross-workgroup synchronisation (every copy evolves
-// identically; the host reads copy 0).
+// (= batch * Hkv + kv head) keeps its own copy of kStSlot words at
+// state[8 + kStSlot * g ...]: {offset, tail_size, summary_count,
+// summary_offset} in words 0..3, advanced by the workgroup itself, so a step
+// needs no cross-workgroup synchronisation (every copy evolves identically;
+// the host reads copy 0).  The MFMA kernel's kRouteGroups extra workgroups
+// (g = batch * Hkv + r, the route workgroups) advance their own copies the
+// same way, and route workgroup g writes two route buffers, at words 4 and 16
+// of the copies of attending workgroups g' with g' = g mod 8 (buffer 0 shares
+// the counters' cache line).  Workgroups are dispatched to the eight XCDs
+// round-robin, so those copies are written and read on one XCD.
+//
+// Route buffer b (12 words) holds the routed row of the step whose post-update
+// kv_len has parity b, written during the step before it: word 0 a key
+// (kv_len | ns << 32 | W << 40 | rule << 48 | 1 << 62), word 1 layer_idx,
+// word 2 block_size | ring << 32, word 3 pool_rows | lwb << 32 | sinks << 40 |
+// partners << 48, words 4..11 the ns pool rows as int32.  A step uses it only
+// when every word matches its own kv_len and arguments (anything else, a zero
+// key included, falls back to computing the row).  A launch reads the buffer
+// of its own parity and writes only the other one, so no word is read and
+// written within one launch.
 enum { kStOffset = 0, kStTail = 1, kStCount = 2, kStSumOff = 3 };
 constexpr int kStError = 4;
 constexpr int kStHeader = 8;
-__device__ __forceinline__ int64_t* dec_slot(int64_t* state) { return state + kStHeader + 4 * (int64_t)blockIdx.x; }
+constexpr int kStSlot = 32;
+constexpr int kStRoute = 4;
+constexpr int kRouteWords = 12;
+constexpr int kRouteGroups = 8;
+__device__ __forceinline__ int64_t* dec_slot(int64_t* state) {
+  return state + kStHeader + kStSlot * (int64_t)blockIdx.x;
+}
+
 
 struct StepArgs {
   int64_t* state;
@@ -497,6 +524,8 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
       slot[kStTail] = st.ts1;
       slot[kStCount] = st.sc1;
       slot[kStSumOff] = st.so1;
+      slot[kStRoute] = 0;                  // this kernel keeps no routed rows
+      slot[kStRoute + kRouteWords] = 0;
     }
   }
 }
@@ -524,14 +553,13 @@ struct DecState32 {
   bool err;
 };
 
-// Step-mode counter update of dec_state (compressed_cache.py:94-172) and the
-// topology of bfly_topology_init at the live block count (butterfly.py:39-105).
-template <bool kStep>
-__device__ __forceinline__ DecState32 dec_state32(const DecodeArgs& a, const StepArgs& sa) {
+// Step-mode counter update of dec_state (compressed_cache.py:94-172) from the
+// counters before the step, and the topology of bfly_topology_init at the live
+// block count (butterfly.py:39-105).
+__device__ __forceinline__ DecState32 dec_advance32(int64_t off0, int64_t ts0, int64_t sc0, int64_t so0,
+                                                    const DecodeArgs& a, const StepArgs& sa) {
   DecState32 s{};
-  if constexpr (kStep) {
-    const int64_t* slot = dec_slot(sa.state);
-    const int64_t off0 = slot[kStOffset], ts0 = slot[kStTail], sc0 = slot[kStCount], so0 = slot[kStSumOff];
+  {
     const bool range = (uint64_t)off0 < (uint64_t)kDecPosLimit && (uint64_t)ts0 < (uint64_t)kDecPosLimit &&
                        (uint64_t)sc0 < (uint64_t)kDecPosLimit && (uint64_t)so0 < (uint64_t)kDecPosLimit;
     const int ring = (int)a.ring, bs = a.bs, W = a.W, pool_rows = (int)a.pool_rows;
@@ -565,6 +593,16 @@ __device__ __forceinline__ DecState32 dec_state32(const DecodeArgs& a, const Ste
     s.width = w;
     s.count = sa.rule == BFLY_RULE_BENES ? (2 * w - 2 > 1 ? 2 * w - 2 : 1) : w;
     s.stage = (int)dec_mod_layer(sa.layer_idx, s.count);
+  }
+  return s;
+}
+
+template <bool kStep>
+__device__ __forceinline__ DecState32 dec_state32(const DecodeArgs& a, const StepArgs& sa) {
+  DecState32 s{};
+  if constexpr (kStep) {
+    const int64_t* slot = dec_slot(sa.state);
+    s = dec_advance32(slot[kStOffset], slot[kStTail], slot[kStCount], slot[kStSumOff], a, sa);
   } else {
     s.kv_len = (int)a.kv_len;
     s.tail_start = (int)a.tail_start;
@@ -649,6 +687,70 @@ __device__ __forceinline__ int dec_select32(int p, int blk, const DecodeArgs& a,
   return __popcll(mask);
 }
 
+// The four header words of a route buffer for the step that ends at kv_len.
+struct RouteKey {
+  int64_t key, layer, geom, shape;
+};
+__device__ __forceinline__ RouteKey route_key(int kv_len, int ns, const DecodeArgs& a, const StepArgs& sa) {
+  RouteKey r;
+  r.key = (int64_t)(uint32_t)kv_len | ((int64_t)ns << 32) | ((int64_t)a.W << 40) | ((int64_t)sa.rule << 48) |
+          (1ll << 62);
+  r.layer = sa.layer_idx;
+  r.geom = (int64_t)(uint32_t)a.bs | (a.ring << 32);
+  r.shape = (int64_t)(uint32_t)a.pool_rows | ((int64_t)sa.lwb << 32) | ((int64_t)sa.sinks << 40) |
+            ((int64_t)sa.partners << 48);
+  return r;
+}
+
+// A route workgroup of a step launch (one of the last kRouteGroups, 256
+// threads): it advances its own counter copy like every other workgroup,
+// computes the routed row of the NEXT step (whose counters are the ones this
+// step writes back) with the same functions and inputs as that step's own
+// dec_state32 + dec_select32, and writes it into the route buffer of that
+// step's kv_len parity in the copies of the attending workgroups g with
+// g = blockIdx.x mod 8.  It touches no q, cache row or output.
+__device__ __forceinline__ void dec_route_workgroup(const DecodeArgs& a, const StepArgs& sa, int tid) {
+  __shared__ int sel[kDecMaxSum];
+  __shared__ int64_t hdr[4];
+  const DecState32 st = dec_state32<true>(a, sa);
+  if (st.err) return;                          // uniform: the attending workgroups report it
+  const DecState32 nx = dec_advance32(st.kv_len, st.ts1, st.sc1, st.so1, a, sa);
+  if (!nx.err) {                               // uniform; else the next step computes its own row
+    if (tid < 64) {
+      const int p1 = nx.kv_len - 1;
+      const int blk1 = min((int)a.bs_div.div((uint32_t)p1), nx.nblocks - 1);
+      const int ns1 = dec_select32<true>(p1, blk1, a, sa, nx, tid, sel);
+      if (tid == 0) {
+        const RouteKey k = route_key(nx.kv_len, ns1, a, sa);
+        hdr[0] = k.key;
+        hdr[1] = k.layer;
+        hdr[2] = k.geom;
+        hdr[3] = k.shape;
+      }
+      if (tid >= ns1 && tid < kDecMaxSum) sel[tid] = 0;
+    }
+    __syncthreads();
+    const int rb = nx.kv_len & 1;
+    const int64_t g_count = (int64_t)gridDim.x - kRouteGroups, g0 = blockIdx.x % 8;
+    const int64_t mine = g_count > g0 ? (g_count - g0 + 7) / 8 : 0;    // attending workgroups g0, g0 + 8, ...
+    for (int64_t e = tid; e < mine * kRouteWords; e += 256) {
+      const int64_t m = e / kRouteWords;
+      const int64_t g = g0 + 8 * m;
+      const int w = (int)(e - m * kRouteWords);
+      const int64_t val =
+          w < 4 ? hdr[w] : (int64_t)(uint32_t)sel[2 * (w - 4)] | ((int64_t)sel[2 * (w - 4) + 1] << 32);
+      sa.state[kStHeader + kStSlot * g + kStRoute + kRouteWords * rb + w] = val;
+    }
+  }
+  if (tid == 0) {
+    int64_t* slot = dec_slot(sa.state);
+    slot[kStOffset] = st.kv_len;
+    slot[kStTail] = st.ts1;
+    slot[kStCount] = st.sc1;
+    slot[kStSumOff] = st.so1;
+  }
+}
+
 // x where c holds, else zero (a value select: no branch, no memory)
 __device__ __forceinline__ uint4 keep_if(bool c, uint4 x) {
   return make_uint4(c ? x.x : 0u, c ? x.y : 0u, c ? x.z : 0u, c ? x.w : 0u);
@@ -720,6 +822,12 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
   const int bh = blockIdx.x;
+  if constexpr (kStep) {
+    if (bh >= (int)gridDim.x - kRouteGroups) {
+      dec_route_workgroup(a, sa, tid);
+      return;
+    }
+  }
   const int bi = (int)a.hkv_div.div((uint32_t)bh);
   const int kvh = bh - bi * a.hkv;
   const int gsz = a.hq / a.hkv;
@@ -738,10 +846,32 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
   };
   load_q(0);
 
+  constexpr int SKN = kDecMaxSum * PIECES;                         // summary K pieces
+  constexpr int SK = (SKN + 255) / 256;
+  // step mode: both route buffers' headers of this workgroup's copy, requested
+  // with the counters (scalar); the kv_len parity picks one
+  int64_t rh[2][4] = {};
+  if constexpr (kStep) {
+    const int64_t* slot = dec_slot(sa.state);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) rh[b][w] = slot[kStRoute + kRouteWords * b + w];
+  }
+
   const DecState32 st = dec_state32<kStep>(a, sa);
   if (kStep && st.err) {
     if (tid == 0) sa.state[kStError] = 1;
     return;
+  }
+  // the row-list entries of this step's route buffer that this thread's summary
+  // pieces need, requested before the window loads so that waiting for them
+  // does not wait for those
+  int rsel[SK] = {};
+  if constexpr (kStep) {
+    const int* rl = reinterpret_cast<const int*>(dec_slot(sa.state) + kStRoute + kRouteWords * (st.kv_len & 1) + 4);
+#pragma unroll
+    for (int it = 0; it < SK; ++it) rsel[it] = rl[min(tid + it * 256, SKN - 1) / PIECES];
   }
   const int p = st.kv_len - 1;
   const int lo = max(max(p - a.W + 1, st.tail_start), 0);
@@ -781,8 +911,6 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
   // Window rows are requested first, the routed selection runs while they are in
   // flight, then the summary rows are requested.
   constexpr int WK = kDecMaxWin * PIECES / 256;                   // window K pieces per thread
-  constexpr int SKN = kDecMaxSum * PIECES;                         // summary K pieces
-  constexpr int SK = (SKN + 255) / 256;
   static_assert(kDecMaxWin * PIECES % 256 == 0, "staging split");
   static_assert(kDecMaxWin + kDecMaxSum == kDecMfmaKeys, "key layout");
   int ns;
@@ -794,18 +922,29 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
       kx[it] = *reinterpret_cast<const uint4*>(win_row(i / PIECES, false) + (i % PIECES) * VEC);
       vx[it] = *reinterpret_cast<const uint4*>(win_row(i / PIECES, true) + (i % PIECES) * VEC);
     }
-    const int blk = min((int)a.bs_div.div((uint32_t)p), st.nblocks - 1);
-    ns = dec_select32<kStep>(p, blk, a, sa, st, lane, selw[wave]);
-    // summary j: pool row selw[j] (row 0 stands in for j >= ns; zeroed below)
-    auto sum_row = [&](int j, bool vside) -> const T* {
-      const int n = j < ns ? selw[wave][j] : 0;
-      return (vside ? pv : pk) + (uint32_t)n * D;
-    };
+    bool pre = false;   // this step's routed row was left by the previous step
+    if constexpr (kStep) {
+      const int rb = st.kv_len & 1;
+      const RouteKey want = route_key(st.kv_len, 0, a, sa);
+      const int64_t k0 = rb ? rh[1][0] : rh[0][0];
+      pre = (k0 & ~(0x1fll << 32)) == want.key && (rb ? rh[1][1] : rh[0][1]) == want.layer &&
+            (rb ? rh[1][2] : rh[0][2]) == want.geom && (rb ? rh[1][3] : rh[0][3]) == want.shape;
+      if (pre) ns = min((int)((k0 >> 32) & 0x1f), kDecMaxSum);
+    }
+    if (!pre) {
+      const int blk = min((int)a.bs_div.div((uint32_t)p), st.nblocks - 1);
+      ns = dec_select32<kStep>(p, blk, a, sa, st, lane, selw[wave]);
+    }
+    // summary j: pool row n (row 0 stands in for j >= ns; zeroed below); a row
+    // left by the previous step is clamped to the pool, so no load leaves it
 #pragma unroll
     for (int it = 0; it < SK; ++it) {
       const int i = min(tid + it * 256, SKN - 1);
-      skx[it] = *reinterpret_cast<const uint4*>(sum_row(i / PIECES, false) + (i % PIECES) * VEC);
-      svx[it] = *reinterpret_cast<const uint4*>(sum_row(i / PIECES, true) + (i % PIECES) * VEC);
+      const int j = i / PIECES;
+      int n = 0;
+      if (j < ns) n = pre ? min(max(rsel[it], 0), (int)a.pool_rows - 1) : selw[wave][j];
+      skx[it] = *reinterpret_cast<const uint4*>(pk + (uint32_t)n * D + (i % PIECES) * VEC);
+      svx[it] = *reinterpret_cast<const uint4*>(pv + (uint32_t)n * D + (i % PIECES) * VEC);
     }
     // append the new token to its ring slot; requested after every staging load so
     // that its wait coincides with theirs (the staging reads it from k_new/v_new)
@@ -939,15 +1078,16 @@ static void launch_decode(const DecodeArgs& a, const StepArgs& sa, int d, int64_
       m.bs_div = FastDiv::make((uint32_t)a.bs);
       m.ring_div = FastDiv::make(a.ring > 0 ? (uint32_t)a.ring : 1u);
       m.hkv_div = FastDiv::make((uint32_t)a.hkv);
+      const int64_t mgrid = kStep ? grid + kRouteGroups : grid;   // step mode: plus the route workgroups
       switch (d) {
         case 64:
-          hipLaunchKernelGGL((decode_mfma_kernel<64, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, m, sa);
+          hipLaunchKernelGGL((decode_mfma_kernel<64, kStep>), dim3((unsigned)mgrid), dim3(256), 0, stream, m, sa);
           return;
         case 128:
-          hipLaunchKernelGGL((decode_mfma_kernel<128, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, m, sa);
+          hipLaunchKernelGGL((decode_mfma_kernel<128, kStep>), dim3((unsigned)mgrid), dim3(256), 0, stream, m, sa);
           return;
         default:
-          hipLaunchKernelGGL((decode_mfma_kernel<256, kStep>), dim3((unsigned)grid), dim3(256), 0, stream, m, sa);
+          hipLaunchKernelGGL((decode_mfma_kernel<256, kStep>), dim3((unsigned)mgrid), dim3(256), 0, stream, m, sa);
           return;
       }
     }
@@ -1019,7 +1159,7 @@ extern "C" int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int 
 
 extern "C" int64_t bfly_decode_state_words(int64_t batch, int hkv) {
   if (batch <= 0 || hkv <= 0) return 0;
-  return kStHeader + 4 * batch * hkv;
+  return kStHeader + kStSlot * (batch * hkv + kRouteGroups);
 }
 
 extern "C" int bfly_decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,
@@ -1035,7 +1175,7 @@ extern "C" int bfly_decode_step(const void* q, int dtype, int64_t batch, int hq,
                      (reinterpret_cast<uintptr_t>(state) & 7) == 0,
                  "tensor pointers must be 16-byte aligned (state 8-byte)");
   BFLY_CHECK_ARG(batch > 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "bad head counts hq=%d hkv=%d", hq, hkv);
-  BFLY_CHECK_ARG(batch * hkv <= INT32_MAX, "batch*hkv too large");
+  BFLY_CHECK_ARG(batch * hkv <= INT32_MAX - kRouteGroups, "batch*hkv too large");
   BFLY_CHECK_ARG(head_dim == 64 || head_dim == 128 || (head_dim == 256 && dtype == BFLY_DTYPE_BF16),
                  "bfly_decode_step: head_dim=%d unsupported (64, 128; 256 for bf16)", head_dim);
   BFLY_CHECK_ARG(window > 0 && window <= kDecMaxWin, "bfly_decode_step: window=%d must be in [1, %d]", window,

@@ -250,8 +250,9 @@ int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int hkv, int he
 
 /*
  * Length in int64 words of the bfly_decode_step counter array for batch*hkv
- * sequences: an 8-word header (word 4: error) and one 4-word copy per sequence.
- * No counterpart in the reference (its counters are host attributes).
+ * sequences: an 8-word header (word 4: error) and batch*hkv + 8 copies of 32
+ * words (one per sequence, eight for the step's route workgroups).  No
+ * counterpart in the reference (its counters are host attributes).
  */
 int64_t bfly_decode_state_words(int64_t batch, int hkv);
 
@@ -264,11 +265,15 @@ int64_t bfly_decode_state_words(int64_t batch, int hkv);
  * that token (bna/mlx/attention.py:1816-1876), with the layout of the live
  * kv_len (stage = layer_idx mod stage_count at ceil(kv_len / BS) blocks).
  * state: device int64[bfly_decode_state_words(batch, hkv)]: state[4] is the
- * error word; workgroup g = b*Hkv + kv head keeps its own copy of
- * {offset, tail_size, summary_count, summary_offset} at state[8 + 4g .. 8 + 4g + 3]
- * and advances it itself (all copies stay equal; initialise every copy).  On a
- * capacity overflow the step changes nothing and sets state[4] = 1 (the
- * reference's RuntimeError; read it back to raise).
+ * error word; copy g (32 words at state[8 + 32g ..], g = b*Hkv + kv head, and
+ * g = batch*Hkv + 0..7 for the route workgroups) holds {offset, tail_size,
+ * summary_count, summary_offset} in words 0..3, advanced by its workgroup (all
+ * copies stay equal; initialise every copy), and words 4..31 hold the kernel's
+ * own cache of the next step's routed row (initialise to zero: zero is "none";
+ * the kernel uses an entry only when it names the step's kv_len and
+ * arguments).  On a capacity
+ * overflow the step changes nothing and sets state[4] = 1 (the reference's
+ * RuntimeError; read it back to raise).
  * Other arguments as bfly_decode; ring_k/ring_v is the ring (capacity > 0).
  */
 int bfly_decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,

@@ -55,6 +55,35 @@ def test_device_counter_steps_equal_host_steps(dtype, d):
     assert torch.equal(dev.k_summary, host.k_summary) and torch.equal(dev.values, host.values)
 
 
+def test_device_counter_steps_follow_changing_arguments():
+    """Each step leaves the next step's routed row in the counter array; a step whose
+    layer or partner rule differs from the previous step's must not use it."""
+    b, hq, hkv, d, prompt, steps = 2, 8, 2, 128, 300, 120
+    total = prompt + steps
+    q = _rand(81, (b, hq, total, d), torch.bfloat16).cuda()
+    k = _rand(82, (b, hkv, total, d), torch.bfloat16).cuda()
+    v = _rand(83, (b, hkv, total, d), torch.bfloat16).cuda()
+    host = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=total)
+    dev = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=total)
+    host.update(k[:, :, :prompt], v[:, :, :prompt])
+    dev.update(k[:, :, :prompt], v[:, :, :prompt])
+    dev.use_device_counters()
+    for p in range(prompt, total):
+        layer = 4 if p % 3 == 0 else 1
+        rule = "xor" if p % 7 == 0 else "causal_shift"
+        lay = bf.build_block_butterfly_layout(seq_len=p + 1, block_size=128, num_key_value_heads=hkv,
+                                              num_key_value_groups=hq // hkv, layer_idx=layer, local_window_blocks=1,
+                                              sink_count=1, partner_count=1, partner_rule=rule)
+        a = host.update_and_attend(q[:, :, p:p + 1], k[:, :, p:p + 1], v[:, :, p:p + 1], layout=lay,
+                                   local_window_tokens=64)
+        c = dev.decode_step(q[:, :, p:p + 1], k[:, :, p:p + 1], v[:, :, p:p + 1], layer_idx=layer,
+                            partner_rule=rule, local_window_tokens=64)
+        assert torch.equal(a, c), (p, layer, rule)
+        if p == prompt + 50:            # host bookkeeping in between: counters pushed, cached rows cleared
+            dev.sync()
+            dev._push()
+
+
 def test_device_counter_overflow_raises_at_sync():
     cache = bf.CompressedKVCache(block_size=4, local_window_tokens=4, max_kv_size=12)   # 7 summary slots
     kv = torch.randn(1, 1, 8, 64, device="cuda").bfloat16()

@@ -81,3 +81,12 @@ def test_topology_init_matches_oracle(rule):
             assert (t.rule, t.local_window_blocks, t.sink_count, t.partner_count) == (_native.RULES[rule], 1, 1, 2)
     t = _native.Topology()
     assert lib.bfly_topology_init(8, 0, 3, 1, 1, 17, C.byref(t)) == _native.ERR_INVALID
+
+
+def test_decode_state_words_match_the_host_layout():
+    from butterfly_amd.compressed_cache import _DEV_SLOT
+
+    lib = _native.lib()
+    assert lib.bfly_decode_state_words(1, 1) == 8 + 9 * _DEV_SLOT     # one sequence + 8 route copies
+    assert lib.bfly_decode_state_words(32, 2) == 8 + 72 * _DEV_SLOT
+    assert lib.bfly_decode_state_words(0, 2) == 0

@@ -52,10 +52,11 @@ constexpr int kDecMaxNew = 2;   // blocks pooled in one step (one per 128 steps 
 // summary_offset} in words 0..3, advanced by the workgroup itself, so a step
 // needs no cross-workgroup synchronisation (every copy evolves identically;
 // the host reads copy 0).  The MFMA kernel's kRouteGroups extra workgroups
-// (g = batch * Hkv + r, the route workgroups) advance their own copies the
-// same way, and route workgroup g writes two route buffers, at words 4 and 16
-// of the copies of attending workgroups g' with g' = g mod 8 (buffer 0 shares
-// the counters' cache line).  Workgroups are dispatched to the eight XCDs
+// (route workgroup r is blockIdx r and keeps copy batch * Hkv + r; attending
+// workgroup g is blockIdx g + 8) advance their own copies the same way, and
+// route workgroup r writes two route buffers, at words 4 and 16 of the copies
+// of the attending workgroups g with g mod 8 = r (buffer 0 shares the
+// counters' cache line).  Workgroups are dispatched to the eight XCDs
 // round-robin, so those copies are written and read on one XCD.
 //
 // Route buffer b (12 words) holds the routed row of the step whose post-update
@@ -74,9 +75,7 @@ constexpr int kStSlot = 32;
 constexpr int kStRoute = 4;
 constexpr int kRouteWords = 12;
 constexpr int kRouteGroups = 8;
-__device__ __forceinline__ int64_t* dec_slot(int64_t* state) {
-  return state + kStHeader + kStSlot * (int64_t)blockIdx.x;
-}
+__device__ __forceinline__ int64_t* dec_slot(int64_t* state, int64_t g) { return state + kStHeader + kStSlot * g; }
 
 
 struct StepArgs {
@@ -161,6 +160,7 @@ struct DecodeArgs {
   int hq, hkv, bs, W;
   float scale;
   FastDiv bs_div, ring_div, hkv_div;   // MFMA path: block_size, ring capacity, Hkv
+  int gsz;                             // MFMA path: hq / hkv
 };
 
 __device__ __forceinline__ float dec_wave_max(float v) {
@@ -206,7 +206,7 @@ __device__ __forceinline__ DecState dec_state(const DecodeArgs& a, const StepArg
   s.nblocks = a.nblocks;
   s.topo = a.topo;
   if constexpr (kStep) {
-    const int64_t* slot = dec_slot(sa.state);
+    const int64_t* slot = dec_slot(sa.state, blockIdx.x);
     const int64_t off0 = slot[kStOffset], ts0 = slot[kStTail];
     s.sc0 = slot[kStCount];
     s.so0 = slot[kStSumOff];
@@ -519,7 +519,7 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
     // copy, pool, ring or output within the step, so no atomic or fence is
     // needed: the next launch sees everything at the kernel boundary.
     if (tid == 0) {
-      int64_t* slot = dec_slot(sa.state);
+      int64_t* slot = dec_slot(sa.state, blockIdx.x);
       slot[kStOffset] = st.kv_len;
       slot[kStTail] = st.ts1;
       slot[kStCount] = st.sc1;
@@ -598,10 +598,10 @@ __device__ __forceinline__ DecState32 dec_advance32(int64_t off0, int64_t ts0, i
 }
 
 template <bool kStep>
-__device__ __forceinline__ DecState32 dec_state32(const DecodeArgs& a, const StepArgs& sa) {
+__device__ __forceinline__ DecState32 dec_state32(const DecodeArgs& a, const StepArgs& sa, int64_t g) {
   DecState32 s{};
   if constexpr (kStep) {
-    const int64_t* slot = dec_slot(sa.state);
+    const int64_t* slot = dec_slot(sa.state, g);
     s = dec_advance32(slot[kStOffset], slot[kStTail], slot[kStCount], slot[kStSumOff], a, sa);
   } else {
     s.kv_len = (int)a.kv_len;
@@ -702,17 +702,19 @@ __device__ __forceinline__ RouteKey route_key(int kv_len, int ns, const DecodeAr
   return r;
 }
 
-// A route workgroup of a step launch (one of the last kRouteGroups, 256
-// threads): it advances its own counter copy like every other workgroup,
-// computes the routed row of the NEXT step (whose counters are the ones this
-// step writes back) with the same functions and inputs as that step's own
-// dec_state32 + dec_select32, and writes it into the route buffer of that
-// step's kv_len parity in the copies of the attending workgroups g with
-// g = blockIdx.x mod 8.  It touches no q, cache row or output.
+// Route workgroup r of a step launch (blockIdx.x = r < kRouteGroups, 256
+// threads; its counter copy is g_count + r): it advances its own counter copy
+// like every other workgroup, computes the routed row of the NEXT step (whose
+// counters are the ones this step writes back) with the same functions and
+// inputs as that step's own dec_state32 + dec_select32, and writes it into the
+// route buffer of that step's kv_len parity in the copies of the attending
+// workgroups g with g mod 8 = r (attending workgroup g is blockIdx g + 8, so it
+// runs on the same XCD).  It touches no q, cache row or output.
 __device__ __forceinline__ void dec_route_workgroup(const DecodeArgs& a, const StepArgs& sa, int tid) {
   __shared__ int sel[kDecMaxSum];
   __shared__ int64_t hdr[4];
-  const DecState32 st = dec_state32<true>(a, sa);
+  const int64_t g_count = (int64_t)gridDim.x - kRouteGroups, g0 = blockIdx.x;
+  const DecState32 st = dec_state32<true>(a, sa, g_count + g0);
   if (st.err) return;                          // uniform: the attending workgroups report it
   const DecState32 nx = dec_advance32(st.kv_len, st.ts1, st.sc1, st.so1, a, sa);
   if (!nx.err) {                               // uniform; else the next step computes its own row
@@ -731,7 +733,6 @@ __device__ __forceinline__ void dec_route_workgroup(const DecodeArgs& a, const S
     }
     __syncthreads();
     const int rb = nx.kv_len & 1;
-    const int64_t g_count = (int64_t)gridDim.x - kRouteGroups, g0 = blockIdx.x % 8;
     const int64_t mine = g_count > g0 ? (g_count - g0 + 7) / 8 : 0;    // attending workgroups g0, g0 + 8, ...
     for (int64_t e = tid; e < mine * kRouteWords; e += 256) {
       const int64_t m = e / kRouteWords;
@@ -743,7 +744,7 @@ __device__ __forceinline__ void dec_route_workgroup(const DecodeArgs& a, const S
     }
   }
   if (tid == 0) {
-    int64_t* slot = dec_slot(sa.state);
+    int64_t* slot = dec_slot(sa.state, g_count + g0);
     slot[kStOffset] = st.kv_len;
     slot[kStTail] = st.ts1;
     slot[kStCount] = st.sc1;
@@ -821,16 +822,18 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
-  const int bh = blockIdx.x;
+  // step mode: the route workgroups come first (no argument is needed to tell
+  // them apart), attending workgroup bh is blockIdx bh + kRouteGroups
   if constexpr (kStep) {
-    if (bh >= (int)gridDim.x - kRouteGroups) {
+    if (blockIdx.x < kRouteGroups) {
       dec_route_workgroup(a, sa, tid);
       return;
     }
   }
+  const int bh = kStep ? (int)blockIdx.x - kRouteGroups : (int)blockIdx.x;
   const int bi = (int)a.hkv_div.div((uint32_t)bh);
   const int kvh = bh - bi * a.hkv;
-  const int gsz = a.hq / a.hkv;
+  const int gsz = a.gsz;
   const T* qhead = reinterpret_cast<const T*>(a.q) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz) * D;
 
   // Q^T fragments of heads 16*hg + lq (B operand: d = lg*(D/4) + 8*ks + [0, 8)).
@@ -852,14 +855,14 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
   // with the counters (scalar); the kv_len parity picks one
   int64_t rh[2][4] = {};
   if constexpr (kStep) {
-    const int64_t* slot = dec_slot(sa.state);
+    const int64_t* slot = dec_slot(sa.state, bh);
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int w = 0; w < 4; ++w) rh[b][w] = slot[kStRoute + kRouteWords * b + w];
   }
 
-  const DecState32 st = dec_state32<kStep>(a, sa);
+  const DecState32 st = dec_state32<kStep>(a, sa, bh);
   if (kStep && st.err) {
     if (tid == 0) sa.state[kStError] = 1;
     return;
@@ -869,7 +872,7 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
   // does not wait for those
   int rsel[SK] = {};
   if constexpr (kStep) {
-    const int* rl = reinterpret_cast<const int*>(dec_slot(sa.state) + kStRoute + kRouteWords * (st.kv_len & 1) + 4);
+    const int* rl = reinterpret_cast<const int*>(dec_slot(sa.state, bh) + kStRoute + kRouteWords * (st.kv_len & 1) + 4);
 #pragma unroll
     for (int it = 0; it < SK; ++it) rsel[it] = rl[min(tid + it * 256, SKN - 1) / PIECES];
   }
@@ -1055,7 +1058,7 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
   if constexpr (kStep) {
     // each workgroup advances its own counter copy (see decode_kernel)
     if (tid == 0) {
-      int64_t* slot = dec_slot(sa.state);
+      int64_t* slot = dec_slot(sa.state, bh);
       slot[kStOffset] = st.kv_len;
       slot[kStTail] = st.ts1;
       slot[kStCount] = st.sc1;
@@ -1078,6 +1081,7 @@ static void launch_decode(const DecodeArgs& a, const StepArgs& sa, int d, int64_
       m.bs_div = FastDiv::make((uint32_t)a.bs);
       m.ring_div = FastDiv::make(a.ring > 0 ? (uint32_t)a.ring : 1u);
       m.hkv_div = FastDiv::make((uint32_t)a.hkv);
+      m.gsz = a.hq / a.hkv;
       const int64_t mgrid = kStep ? grid + kRouteGroups : grid;   // step mode: plus the route workgroups
       switch (d) {
         case 64:

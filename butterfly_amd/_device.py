@@ -21,9 +21,12 @@ def stream_of(device) -> int:
     return torch.cuda.current_stream(idx).cuda_stream
 
 
+_NULL = contextlib.nullcontext()   # stateless, so one instance serves every call
+
+
 def on(device):
     """Make ``device`` current for a native call; no switch when it already is."""
-    device = torch.device(device)
-    if device.index is None or device.index == _GET_DEVICE():
-        return contextlib.nullcontext()
-    return torch.cuda.device(device)
+    idx = device.index if isinstance(device, torch.device) else torch.device(device).index
+    if idx is None or idx == _GET_DEVICE():
+        return _NULL
+    return torch.cuda.device(idx)

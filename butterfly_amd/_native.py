@@ -15,6 +15,7 @@ OK = 0
 ERR_INVALID = -1
 ERR_UNSUPPORTED = -2
 ERR_HIP = -3
+ERR_CAPACITY = -4
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -63,6 +64,8 @@ SIGNATURES = {
                                  _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _int, _int, _int, _f32,
                                  _vp, _vp]),
     "bfly_topology_init": (_int, [_i64, _i64, _int, _int, _int, _int, C.POINTER(Topology)]),
+    "bfly_stream_chunks": (_int, [_i64, _vp, _vp, _vp, _vp, _vp, _int, _i64, _int, _int, _int, _vp, _vp, _i64, _vp,
+                                  _vp, _i64, _vp, _int, _i64, _int, _int, _int, _int, _int, _int, _f32, _vp, _vp]),
     "bfly_decode": (_int, [_vp, _int, _i64, _int, _int, _int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp,
                            _i64, _i64, C.POINTER(Topology), _i64, _int, _int, _f32, _vp, _vp]),
     "bfly_decode_state_words": (_i64, [_i64, _int]),
@@ -82,6 +85,7 @@ SIGNATURES = {
 }
 
 _lib = None
+_fns = {}   # name -> bound foreign function, filled when the library loads
 
 
 class NativeLibraryMissing(RuntimeError):
@@ -100,6 +104,7 @@ def lib() -> C.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
+            _fns[name] = fn
         _lib = handle
     return _lib
 
@@ -118,4 +123,9 @@ def check(rc: int, what: str = "") -> None:
 
 
 def call(name: str, *args) -> None:
-    check(getattr(lib(), name)(*args), name)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = getattr(lib(), name)
+    rc = fn(*args)
+    if rc:
+        check(rc, name)

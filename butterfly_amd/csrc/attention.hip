@@ -20,7 +20,7 @@
 //    (batch, kv head, query); lanes over keys for scores and over d for output.
 #include <stdlib.h>
 
-#include "bfly_common.h"
+#include "bfly_topology.h"
 
 namespace bfly {
 
@@ -31,7 +31,8 @@ struct AttnArgs {
   const void* v;
   const void* ks;         // summary pool [B, Hkv, pool_rows, d]
   const void* vs;
-  const int32_t* nbr;     // [nblocks, kcap]
+  const int32_t* nbr;     // [nblocks, kcap], or null: the MFMA kernel computes rows from topo
+  bfly_topology_t topo;   // the layout at nblocks blocks (used when nbr is null)
   const int32_t* qpos;    // optional [tq]
   int64_t batch;
   int hq, hkv;
@@ -282,9 +283,14 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
   int b_lo, b_hi, tmp;
   chunk_blocks(cbeg, b_lo, tmp);
   chunk_blocks(cend - 1, tmp, b_hi);
-  {
+  if (a.nbr != nullptr) {
     const int cnt = (b_hi - b_lo + 1) * m.kcap;
     for (int i = tid; i < cnt; i += 256) s_nbr[i] = a.nbr[(int64_t)b_lo * m.kcap + i];
+  } else if (tid <= b_hi - b_lo) {
+    // the table builder's row (bfly_block_neighbors): same function, -1 padding
+    int32_t* row = reinterpret_cast<int32_t*>(s_nbr) + tid * m.kcap;
+    const int len = neighbor_row(b_lo + tid, m.nblocks, a.topo, row, m.kcap);
+    for (int i = len; i < m.kcap; ++i) row[i] = -1;
   }
 
   // ---- register staging of one page (K rows and V row pairs) and of the routed summaries
@@ -619,6 +625,7 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
                        (a.ring == 0 || a.ring >= kPage) && a.kv_len + 2 * kPage < INT32_MAX &&
                        a.nblocks < INT32_MAX && a.kv_rows < INT32_MAX && a.pool_rows < INT32_MAX;
   if (a.tq == 0) return BFLY_OK;
+  BFLY_CHECK_ARG(mfma_ok || a.nbr != nullptr, "%s: neighbour rows from the topology need the MFMA path", what);
   if (mfma_ok) {
     const int64_t c_first = floordiv(a.q_pos0, kPage);
     const int64_t c_last = floordiv(a.q_pos0 + a.tq - 1, kPage);
@@ -744,4 +751,107 @@ extern "C" int bfly_attend_cache(const void* q, int dtype, int64_t batch, int hq
   a.pool_rows = pool_capacity; a.nsum = summary_count; a.nblocks = num_blocks;
   a.kcap = kcap; a.bs = block_size; a.W = window; a.scale = scale; a.token_cutoff = 1;
   return launch_attention(a, dtype, stream, "bfly_attend_cache");
+}
+
+// Streaming chunked prefill of one layer over a two-pool cache, host loop in C++
+// (the per-chunk work of ButterflyAttentionCore with a CompressedKVCache:
+// bna/integrations/qwen_mlx.py:1515-1581 over bna/mlx/compressed_cache.py:94-172).
+// Per chunk: the counter bookkeeping of update_and_fetch (append, summarise every
+// block with end + W_cache <= offset, trim whole blocks while
+// tail_size - BS >= max(W_cache, step + W_cache - 1)), one bfly_cache_update
+// launch, the layout of the live kv_len (bfly_topology_init; the attention kernel
+// builds the neighbour rows itself), and one attention launch for the chunk's
+// queries from the cache -- the same kernels and arguments as the per-chunk path.
+extern "C" int bfly_stream_chunks(int64_t n_chunks, const void* const* q, const void* const* k,
+                                  const void* const* v, void* const* out, const int64_t* chunk_len, int dtype,
+                                  int64_t batch, int hq, int hkv, int head_dim, void* ring_k, void* ring_v,
+                                  int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity,
+                                  int64_t* counters, int cache_window, int64_t layer_idx, int partner_rule,
+                                  int local_window_blocks, int sink_count, int partner_count, int block_size,
+                                  int window, float scale, int64_t* chunks_done, hipStream_t stream) {
+  BFLY_CHECK_ARG(n_chunks >= 0 && q && k && v && out && chunk_len && counters && chunks_done, "null pointer");
+  BFLY_CHECK_ARG(ring_k && ring_v && pool_k && pool_v, "null pointer");
+  BFLY_CHECK_ARG(batch > 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "bad head counts hq=%d hkv=%d", hq, hkv);
+  BFLY_CHECK_ARG(block_size > 0 && window > 0 && cache_window > 0, "bad block_size/window");
+  BFLY_CHECK_ARG(local_window_blocks >= 0 && sink_count >= 0 && partner_count >= 0 &&
+                     partner_count <= BFLY_MAX_PARTNERS,
+                 "bad topology parameters");
+  *chunks_done = 0;
+  int64_t offset = counters[0], tail = counters[1], count = counters[2], sum_off = counters[3];
+  BFLY_CHECK_ARG(offset > 0 && tail >= 0 && tail <= offset && count >= 0 && count <= pool_capacity && sum_off >= 0,
+                 "the cache must hold a first chunk (offset > 0) and valid counters");
+  int64_t total = offset;
+  for (int64_t c = 0; c < n_chunks; ++c) {
+    BFLY_CHECK_ARG(chunk_len[c] > 0 && q[c] && k[c] && v[c] && out[c], "chunk %lld: empty or null", (long long)c);
+    total += chunk_len[c];
+  }
+  const int kcap = 1 + local_window_blocks + partner_count + sink_count;
+  // the MFMA attention kernel is the one that builds neighbour rows from the topology
+  const bool mfma_ok = dtype == BFLY_DTYPE_BF16 && window <= kPage && block_size >= kPage && 2 * kcap <= kSumSlots &&
+                       (head_dim == 64 || head_dim == 128 || head_dim == 256) && scale > 0.f &&
+                       ring_capacity >= kPage && total + 2 * kPage < INT32_MAX && ring_capacity < INT32_MAX &&
+                       pool_capacity < INT32_MAX;
+  if (!mfma_ok) {
+    set_error("bfly_stream_chunks: configuration outside the MFMA attention path");
+    return BFLY_ERR_UNSUPPORTED;
+  }
+  auto publish = [&]() {
+    counters[0] = offset;
+    counters[1] = tail;
+    counters[2] = count;
+    counters[3] = sum_off;
+  };
+  for (int64_t c = 0; c < n_chunks; ++c) {
+    const int64_t step = chunk_len[c];
+    if (tail + step > ring_capacity) {
+      set_error("CompressedKVCache.tail_capacity=%lld too small to fit tail_size=%lld + step=%lld",
+                (long long)ring_capacity, (long long)tail, (long long)step);
+      return BFLY_ERR_CAPACITY;
+    }
+    const int64_t offset0 = offset;
+    tail += step;
+    offset += step;
+    const int64_t first_pos = sum_off, first_slot = count;
+    int64_t n_new = 0;
+    bool overflow = false;
+    while (sum_off + block_size <= offset - cache_window) {
+      const int64_t block_start = sum_off - (offset - tail);
+      if (block_start < 0 || block_start + block_size > tail) break;
+      if (count + n_new >= pool_capacity) {
+        overflow = true;
+        break;
+      }
+      ++n_new;
+      sum_off += block_size;
+    }
+    int rc = bfly_cache_update(k[c], v[c], dtype, batch, hkv, step, head_dim, ring_k, ring_v, ring_capacity, offset0,
+                               first_pos, n_new, block_size, pool_k, pool_v, pool_capacity, first_slot, stream);
+    if (rc) return rc;
+    count += n_new;
+    if (overflow) {
+      publish();
+      set_error("CompressedKVCache.summary_capacity=%lld exhausted at offset=%lld", (long long)pool_capacity,
+                (long long)offset);
+      return BFLY_ERR_CAPACITY;
+    }
+    const int64_t target = cache_window > step + cache_window - 1 ? cache_window : step + cache_window - 1;
+    while (tail - block_size >= target) tail -= block_size;
+    publish();
+
+    const int64_t nblocks = (offset + block_size - 1) / block_size;
+    AttnArgs a{};
+    rc = bfly_topology_init(nblocks, layer_idx, partner_rule, local_window_blocks, sink_count, partner_count, &a.topo);
+    if (rc) return rc;
+    a.q = q[c]; a.out = out[c]; a.k = ring_k; a.v = ring_v; a.ks = pool_k; a.vs = pool_v;
+    a.nbr = nullptr; a.qpos = nullptr;
+    a.batch = batch; a.hq = hq; a.hkv = hkv; a.tq = step; a.d = head_dim;
+    a.q_pos0 = offset - step; a.kv_rows = ring_capacity; a.ring = ring_capacity;
+    a.key_lo = offset - tail; a.kv_len = offset;
+    a.pool_rows = pool_capacity; a.nsum = count; a.nblocks = nblocks;
+    a.kcap = kcap; a.bs = block_size; a.W = window; a.scale = scale; a.token_cutoff = 1;
+    rc = launch_attention(a, dtype, stream, "bfly_stream_chunks");
+    if (rc) return rc;
+    *chunks_done = c + 1;
+  }
+  return BFLY_OK;
 }

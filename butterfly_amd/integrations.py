@@ -32,7 +32,7 @@ from typing import Any, Dict, List, Optional, Sequence
 
 import torch
 
-from .attention import _attend, _c, compressed_butterfly_attention
+from .attention import _attend, _c, _on, compressed_butterfly_attention
 from .compressed_cache import CompressedKVCache
 from .layout import build_block_butterfly_layout
 
@@ -98,6 +98,9 @@ def _now_ms() -> float:
     return time.perf_counter() * 1e3
 
 
+_DEVICE_STEP_NOTES = {"q_len": 1, "device_counters": True, "block_sparse_active_mode": True}
+
+
 class ButterflyAttentionCore:
     """Compressed Butterfly attention of one layer, after the q/k/v projections.
 
@@ -116,7 +119,29 @@ class ButterflyAttentionCore:
         self.cfg = cfg
         self.layer_idx = int(layer_idx)
         self.scale = scale
-        self.last_profile: Optional[AttentionProfile] = None
+        self._last: Any = None     # an AttentionProfile, or the raw fields it is built from on access
+
+    @property
+    def last_profile(self) -> Optional[AttentionProfile]:
+        """Profile of the last call (reference: bna/mlx/attention.py:144-162), built on
+        first access from the fields the call recorded (keeps the per-chunk path cheap)."""
+        r = self._last
+        if r is None or isinstance(r, AttentionProfile):
+            return r
+        t0, t1, graph_ms, path, notes, lay = r
+        notes = dict(notes)
+        if graph_ms is not None:
+            notes["graph_ms"] = graph_ms
+        if lay is not None:
+            notes["stage_idx"] = lay.stage_idx
+            notes["stage_count"] = lay.stage_count
+        prof = AttentionProfile(graph_build_ms=float(graph_ms or 0.0), total_ms=t1 - t0, path=path, notes=notes)
+        self._last = prof
+        return prof
+
+    @last_profile.setter
+    def last_profile(self, value: Optional[AttentionProfile]) -> None:
+        self._last = value
 
     def layout(self, kv_len: int, num_kv_heads: int, groups: int, device):
         c = self.cfg
@@ -143,14 +168,13 @@ class ButterflyAttentionCore:
                                     partner_rule=c.block_partner_rule, local_window_blocks=c.block_local_window_blocks,
                                     sink_count=c.block_sink_blocks, partner_count=c.block_partner_count,
                                     scale=self.scale)
-            self.last_profile = AttentionProfile(total_ms=_now_ms() - t0, path="block_sparse_compressed_active",
-                                                 notes={"q_len": 1, "device_counters": True,
-                                                        "block_sparse_active_mode": True})
+            self._last = (t0, _now_ms(), None, "block_sparse_compressed_active", _DEVICE_STEP_NOTES, None)
             return out
         if cache is not None:
             cache.sync()
         k_len = q_len + (cache.offset if cache is not None else 0)
         notes: Dict[str, Any] = {"seq_len": int(k_len), "q_len": int(q_len)}
+        graph_ms = None
         if cache is not None and q_len < k_len and q_len <= 2 and self.cfg.butterfly_decode_backend == "dense":
             # stock decode: dense attention over the trimmed tail only (qwen_mlx.py:1273-1293)
             cache.update(k, v)
@@ -166,7 +190,7 @@ class ButterflyAttentionCore:
             # one-shot prefill over this call's own tokens (q_len == k_len)
             tg = _now_ms()
             lay = self.layout(k_len, hkv, groups, q.device)
-            notes["graph_ms"] = _now_ms() - tg
+            graph_ms = _now_ms() - tg
             if cache is not None:
                 cache.update(k, v)
             out, _ = compressed_butterfly_attention(q, k, v, layout=lay, local_window_tokens=w, scale=self.scale)
@@ -176,14 +200,11 @@ class ButterflyAttentionCore:
                 raise TypeError("the active path needs a butterfly_amd.CompressedKVCache")
             tg = _now_ms()
             lay = self.layout(k_len, hkv, groups, q.device)
-            notes["graph_ms"] = _now_ms() - tg
+            graph_ms = _now_ms() - tg
             out = cache.update_and_attend(q, k, v, layout=lay, local_window_tokens=w, scale=self.scale)
             notes["block_sparse_active_mode"] = True
             path = "block_sparse_compressed_active"
-        notes["stage_idx"] = lay.stage_idx
-        notes["stage_count"] = lay.stage_count
-        self.last_profile = AttentionProfile(graph_build_ms=float(notes.get("graph_ms", 0.0)),
-                                             total_ms=_now_ms() - t0, path=path, notes=notes)
+        self._last = (t0, _now_ms(), graph_ms, path, notes, lay)
         return out
 
 
@@ -249,5 +270,83 @@ def chunked_prefill(core: ButterflyAttentionCore, chunks, cache: CompressedKVCac
     1515-1581: the first chunk is one-shot over its own tokens; each later
     chunk appends to the cache and attends from it with the layout of the live
     kv_len.  ``chunks`` yields contiguous ``(q, k, v)`` chunks in order.
+
+    After the first chunk, the remaining ones run through one ``bfly_stream_chunks``
+    call (the same kernels and arguments, with the per-chunk bookkeeping in C++)
+    whenever the configuration allows it; otherwise each chunk goes through ``core``.
     """
-    return [core(qc, kc, vc, cache) for qc, kc, vc in chunks]
+    chunks = list(chunks)
+    if not chunks:
+        return []
+    outs = [core(*chunks[0], cache)]
+    rest = chunks[1:]
+    if rest:
+        native = _stream_chunks(core, rest, cache)
+        outs += native if native is not None else [core(qc, kc, vc, cache) for qc, kc, vc in rest]
+    return outs
+
+
+def _stream_chunks(core: ButterflyAttentionCore, chunks, cache) -> Optional[List[torch.Tensor]]:
+    """``bfly_stream_chunks`` over ``chunks`` (the cache already holds the first chunk), or
+    None when the per-chunk path must run them: a cache with device counters, chunks of
+    one or two tokens (the per-chunk path sends those to the decode kernel or, with the
+    dense backend, to the stock fallback), or a configuration the loop does not cover."""
+    import ctypes as C
+
+    from . import _native
+    from .attention import _dtype_code, _scale, _stream
+
+    if not isinstance(cache, CompressedKVCache) or cache.device_counters is not None or cache.offset <= 0:
+        return None
+    q0, k0, _ = chunks[0]
+    b, hq, _, d = (int(x) for x in q0.shape)
+    hkv = int(k0.shape[1])
+    if q0.dtype != torch.bfloat16 or cache._ring_k is None:
+        return None
+    qs, ks, vs = [], [], []
+    for qc, kc, vc in chunks:
+        n = int(qc.shape[2])
+        if (n <= 2 or tuple(qc.shape) != (b, hq, n, d) or tuple(kc.shape) != (b, hkv, n, d) or kc.shape != vc.shape
+                or not (qc.dtype == kc.dtype == vc.dtype == torch.bfloat16) or not qc.is_cuda):
+            return None
+        qs.append(_c(qc))
+        ks.append(_c(kc))
+        vs.append(_c(vc))
+    cache.sync()
+    cache._apply_realign()
+    ring_k, ring_v, pool_k, pool_v = cache._ring_k, cache._ring_v, cache._pool_k, cache._pool_v
+    if tuple(ring_k.shape[:2]) != (b, hkv) or ring_k.shape[3] != d or ring_k.dtype != torch.bfloat16:
+        raise ValueError("keys do not match the cache's batch/head/dim/dtype")
+    # outputs: consecutive 16-byte aligned ranges of one allocation
+    sizes = [q.numel() for q in qs]
+    starts, off = [], 0
+    for n in sizes:
+        starts.append(off)
+        off += (n + 7) // 8 * 8
+    flat = torch.empty(off, dtype=torch.bfloat16, device=q0.device)
+    outs = [flat[s:s + n].view(q.shape) for s, n, q in zip(starts, sizes, qs)]
+    m = len(qs)
+    ptrs = lambda ts: (C.c_void_p * m)(*[t.data_ptr() for t in ts])
+    lens = (C.c_int64 * m)(*[int(q.shape[2]) for q in qs])
+    counters = (C.c_int64 * 4)(cache.offset, cache.tail_size, cache.summary_count, cache.summary_offset)
+    done = C.c_int64(0)
+    c = core.cfg
+    rule = _native.RULES.get(str(c.block_partner_rule))
+    w = int(c.compressed_local_window_tokens)
+    t0 = _now_ms()
+    with _on(q0.device):
+        rc = _native.lib().bfly_stream_chunks(
+            m, ptrs(qs), ptrs(ks), ptrs(vs), ptrs(outs), lens, _dtype_code(q0), b, hq, hkv, d, ring_k.data_ptr(),
+            ring_v.data_ptr(), cache.tail_capacity, pool_k.data_ptr(), pool_v.data_ptr(), cache.summary_capacity,
+            counters, int(cache.local_window_tokens), core.layer_idx, rule, int(c.block_local_window_blocks),
+            int(c.block_sink_blocks), int(c.block_partner_count), cache.block_size, w, _scale(core.scale, d),
+            C.byref(done), _stream(q0))
+    cache.offset, cache.tail_size, cache.summary_count, cache.summary_offset = (int(x) for x in counters)
+    if rc == _native.ERR_UNSUPPORTED and done.value == 0:
+        return None
+    _native.check(rc, "bfly_stream_chunks")
+    lay = core.layout(cache.offset, hkv, hq // hkv, q0.device)
+    core._last = (t0, _now_ms(), None, "block_sparse_compressed_active",
+                  {"seq_len": cache.offset, "q_len": int(qs[-1].shape[2]), "block_sparse_active_mode": True,
+                   "native_chunk_loop": m}, lay)
+    return outs

@@ -30,6 +30,7 @@ extern "C" {
 #define BFLY_ERR_INVALID (-1)     /* bad shape / argument: ValueError in the reference */
 #define BFLY_ERR_UNSUPPORTED (-2) /* valid but not implemented on this path */
 #define BFLY_ERR_HIP (-3)         /* HIP runtime failure */
+#define BFLY_ERR_CAPACITY (-4)    /* cache capacity exhausted: RuntimeError in the reference */
 
 #define BFLY_DTYPE_F32 0
 #define BFLY_DTYPE_BF16 1
@@ -222,6 +223,32 @@ int bfly_attend_cache(const void* q, int dtype, int64_t batch, int hq, int hkv, 
                       int64_t pool_capacity, int64_t summary_count, const int32_t* neighbors,
                       int64_t num_blocks, int kcap, int block_size, int window, float scale,
                       void* out, hipStream_t stream);
+
+/*
+ * Device (host loop): a streaming chunked prefill of one layer over a two-pool
+ * cache that already holds a first chunk.  For chunk c (q[c]: [B, Hq, len_c, d],
+ * k[c]/v[c]: [B, Hkv, len_c, d], out[c]: [B, Hq, len_c, d], host pointer arrays):
+ * the counter bookkeeping and append + block pooling of
+ * CompressedKVCache.update_and_fetch (bna/mlx/compressed_cache.py:94-172, with
+ * the cache's own window cache_window), then the chunk's queries attend from the
+ * cache as compressed_butterfly_attention_from_cache does with the layout of the
+ * live kv_len (bna/mlx/attention.py:1816-1876; stage = layer_idx mod stage count)
+ * -- the per-chunk schedule of the Qwen layer swap (bna/integrations/
+ * qwen_mlx.py:1515-1581) with no host round trip between chunks.
+ * counters (host int64[4], in/out): {offset, tail_size, summary_count,
+ * summary_offset}; they are left at the last completed chunk, and *chunks_done
+ * counts the chunks whose work was enqueued.  ring_k/ring_v: [B, Hkv,
+ * ring_capacity, d] (position p at slot p mod ring_capacity); pool_k/pool_v:
+ * [B, Hkv, pool_capacity, d].  bf16 with head_dim 64/128/256 and window <= 64
+ * only (BFLY_ERR_UNSUPPORTED otherwise, before any work); BFLY_ERR_CAPACITY when
+ * the tail or the pool overflows (the reference's RuntimeError).
+ */
+int bfly_stream_chunks(int64_t n_chunks, const void* const* q, const void* const* k, const void* const* v,
+                       void* const* out, const int64_t* chunk_len, int dtype, int64_t batch, int hq, int hkv,
+                       int head_dim, void* ring_k, void* ring_v, int64_t ring_capacity, void* pool_k, void* pool_v,
+                       int64_t pool_capacity, int64_t* counters, int cache_window, int64_t layer_idx,
+                       int partner_rule, int local_window_blocks, int sink_count, int partner_count, int block_size,
+                       int window, float scale, int64_t* chunks_done, hipStream_t stream);
 
 /*
  * Device: one decode step -- a single new query per sequence at position

@@ -128,3 +128,59 @@ def test_stock_decode_fallback_is_dense_over_the_tail():
     vv = v[:, :, ts:T + 1].float().repeat_interleave(4, 1)
     want = torch.softmax(q[:, :, T:].float() @ kk.transpose(-1, -2) / d ** 0.5, -1) @ vv
     _check(o, want, dtype)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,hq,hkv,d", [(1, 16, 4, 256), (2, 8, 2, 128)])
+def test_native_chunk_loop_equals_per_chunk_calls(b, hq, hkv, d):
+    """chunked_prefill runs chunks 2.. through bfly_stream_chunks: outputs, counters,
+    ring and pool must equal those of one ButterflyAttentionCore call per chunk."""
+    layer, lens = 6, [384, 384, 200, 384, 130, 3, 384, 257]
+    total = sum(lens)
+    q = _rand(91, (b, hq, total, d), torch.bfloat16).cuda()
+    k = _rand(92, (b, hkv, total, d), torch.bfloat16).cuda()
+    v = _rand(93, (b, hkv, total, d), torch.bfloat16).cuda()
+    chunks, pos = [], 0
+    for n in lens:
+        chunks.append(tuple(t[:, :, pos:pos + n].contiguous() for t in (q, k, v)))
+        pos += n
+    cfg = bf.QwenButterflyConfig()
+    runs = []
+    for native in (True, False):
+        core = bf.ButterflyAttentionCore(cfg, layer)
+        cache = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=total, max_chunk_size=512)
+        outs = bf.chunked_prefill(core, chunks, cache) if native else [core(*c, cache) for c in chunks]
+        runs.append((core, cache, outs))
+    (ca, a, oa_), (cb, bb, ob) = runs
+    assert ca.last_profile.notes.get("native_chunk_loop") == len(lens) - 1
+    assert (a.offset, a.tail_size, a.summary_count, a.summary_offset) == \
+           (bb.offset, bb.tail_size, bb.summary_count, bb.summary_offset)
+    for x, y in zip(oa_, ob):
+        assert torch.equal(x, y)
+    assert torch.equal(a.k_summary, bb.k_summary) and torch.equal(a.v_summary, bb.v_summary)
+    assert torch.equal(a.keys, bb.keys) and torch.equal(a.values, bb.values)
+
+
+@pytest.mark.gpu
+def test_native_chunk_loop_capacity_error_matches_per_chunk_calls():
+    b, hq, hkv, d, layer = 1, 8, 2, 128, 2
+    lens = [384] * 6
+    total = sum(lens)
+    q = _rand(94, (b, hq, total, d), torch.bfloat16).cuda()
+    k = _rand(95, (b, hkv, total, d), torch.bfloat16).cuda()
+    v = _rand(96, (b, hkv, total, d), torch.bfloat16).cuda()
+    chunks = [tuple(t[:, :, i * 384:(i + 1) * 384].contiguous() for t in (q, k, v)) for i in range(6)]
+    caches = []
+    for native in (True, False):
+        core = bf.ButterflyAttentionCore(bf.QwenButterflyConfig(), layer)
+        cache = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=1200, max_chunk_size=512)
+        with pytest.raises(RuntimeError):
+            if native:
+                bf.chunked_prefill(core, chunks, cache)
+            else:
+                for c in chunks:
+                    core(*c, cache)
+        caches.append(cache)
+    a, bb = caches
+    assert (a.offset, a.tail_size, a.summary_count, a.summary_offset) == \
+           (bb.offset, bb.tail_size, bb.summary_count, bb.summary_offset)

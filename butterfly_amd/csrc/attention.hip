@@ -21,6 +21,7 @@
 #include <stdlib.h>
 
 #include "bfly_topology.h"
+#include "cache_update.h"
 
 namespace bfly {
 
@@ -227,6 +228,11 @@ struct MfmaArgs {
   int ring;              // 0: linear rows (row = p - key_lo); else row = p mod ring (ring >= kPage)
   int nblocks, nsum, kcap, bs, W;
   int token_cutoff;
+  // fused launch (kUpd): grid rows >= attn_y run a cache update instead
+  // (cache_update_body over upd_x x upd_rows x K|V work items, upd_wgs in all)
+  UpdateJob upd;
+  int attn_y, upd_x, upd_rows;
+  int64_t upd_wgs;
 };
 
 // Work unit = (batch, kv head, segment of seg_chunks 64-position chunks).
@@ -240,7 +246,12 @@ struct MfmaArgs {
 //     head's scores its register Q slot is refilled with the next (chunk, head)
 //   barrier
 // so HBM traffic of chunk c+1 overlaps the MFMA/softmax work of chunk c.
-template <int D>
+//
+// kUpd (the streaming prefill's fused launch): the grid carries extra rows of
+// workgroups that run the NEXT chunk's cache update (append + pooling) while
+// the attention workgroups run this chunk; the host fuses only when the update
+// writes no ring slot or pool row that this chunk's attention reads.
+template <int D, bool kUpd = false>
 __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1)
 attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunks, int hper) {
   using C = MfmaCfg<D>;
@@ -249,6 +260,19 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
   __shared__ int s_nbr[kMaxSegBlocks * kMaxKcap];
   __bf16* Ks = reinterpret_cast<__bf16*>(smem);                 // [kSlots][KP]
   __bf16* Vs = reinterpret_cast<__bf16*>(smem + C::K_BYTES);    // [kSlots][D], pieces swizzled by row
+  static_assert(C::LDS >= 256 * 8 * 4, "pooling scratch aliases the staging tiles");
+  if constexpr (kUpd) {
+    if ((int)blockIdx.y >= m.attn_y) {
+      const int64_t lin = (int64_t)(blockIdx.y - m.attn_y) * gridDim.x + blockIdx.x;
+      if (lin >= m.upd_wgs) return;
+      const int64_t per_kv = (int64_t)m.upd_x * m.upd_rows;
+      const int kv = (int)(lin / per_kv);
+      const int64_t r = lin - kv * per_kv;
+      const int64_t row = r / m.upd_x;
+      cache_update_body<__bf16, 8>(m.upd, r - row * m.upd_x, row, kv, reinterpret_cast<float*>(smem));
+      return;
+    }
+  }
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -613,7 +637,10 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
   }
 }
 
-static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, const char* what) {
+// upd (optional, bf16 MFMA path only): a cache update to run in the same
+// launch on extra grid rows (see attn_mfma_kernel's kUpd).
+static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, const char* what,
+                            const UpdateJob* upd = nullptr, int64_t upd_rows = 0) {
   BFLY_CHECK_ARG(aligned16(a.q) && aligned16(a.out) && aligned16(a.k) && aligned16(a.v) && aligned16(a.ks) &&
                      aligned16(a.vs),
                  "%s: tensor pointers must be 16-byte aligned", what);
@@ -626,6 +653,7 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
                        a.nblocks < INT32_MAX && a.kv_rows < INT32_MAX && a.pool_rows < INT32_MAX;
   if (a.tq == 0) return BFLY_OK;
   BFLY_CHECK_ARG(mfma_ok || a.nbr != nullptr, "%s: neighbour rows from the topology need the MFMA path", what);
+  BFLY_CHECK_ARG(mfma_ok || upd == nullptr, "%s: a fused cache update needs the MFMA path", what);
   if (mfma_ok) {
     const int64_t c_first = floordiv(a.q_pos0, kPage);
     const int64_t c_last = floordiv(a.q_pos0 + a.tq - 1, kPage);
@@ -670,10 +698,27 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
     const int nparts = (gsz + hper - 1) / hper;
     BFLY_CHECK_ARG(groups * nparts <= 65535, "%s: grid too large", what);
     dim3 grid((unsigned)nseg, (unsigned)(groups * nparts));
-    switch (a.d) {
-      case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
-      case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
-      default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
+    if (upd != nullptr) {
+      const int64_t ux = update_x(upd->n_blocks, upd->step, upd->d, 8);
+      m.upd = *upd;
+      m.attn_y = (int)grid.y;
+      m.upd_x = (int)ux;
+      m.upd_rows = (int)upd_rows;
+      m.upd_wgs = ux * upd_rows * 2;
+      const int64_t extra = (m.upd_wgs + nseg - 1) / nseg;
+      BFLY_CHECK_ARG(ux <= INT32_MAX && upd_rows <= 65535 && grid.y + extra <= 65535, "%s: grid too large", what);
+      grid.y += (unsigned)extra;
+      switch (a.d) {
+        case 64: hipLaunchKernelGGL((attn_mfma_kernel<64, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
+        case 128: hipLaunchKernelGGL((attn_mfma_kernel<128, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
+        default: hipLaunchKernelGGL((attn_mfma_kernel<256, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
+      }
+    } else {
+      switch (a.d) {
+        case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
+        case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
+        default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
+      }
     }
   } else {
     BFLY_CHECK_ARG(a.d <= kGenericMaxD, "%s: head_dim=%d > %d", what, a.d, kGenericMaxD);
@@ -758,10 +803,75 @@ extern "C" int bfly_attend_cache(const void* q, int dtype, int64_t batch, int hq
 // bna/integrations/qwen_mlx.py:1515-1581 over bna/mlx/compressed_cache.py:94-172).
 // Per chunk: the counter bookkeeping of update_and_fetch (append, summarise every
 // block with end + W_cache <= offset, trim whole blocks while
-// tail_size - BS >= max(W_cache, step + W_cache - 1)), one bfly_cache_update
-// launch, the layout of the live kv_len (bfly_topology_init; the attention kernel
-// builds the neighbour rows itself), and one attention launch for the chunk's
-// queries from the cache -- the same kernels and arguments as the per-chunk path.
+// tail_size - BS >= max(W_cache, step + W_cache - 1)), the cache update (append +
+// pooling of the due blocks), the layout of the live kv_len (bfly_topology_init;
+// the attention kernel builds the neighbour rows itself), and the attention of the
+// chunk's queries from the cache -- the same kernels and arguments as the
+// per-chunk path.  Chunk c's attention and chunk c+1's update share one launch
+// when they touch disjoint ring slots and pool rows: the update writes positions
+// [P, P + len_{c+1}) (P = end of chunk c) and pool rows >= the summaries chunk c
+// reads, while chunk c's attention reads pages no lower than P - len_c - 2*64,
+// so len_c + len_{c+1} + 2*64 <= ring capacity keeps them apart.
+namespace {
+
+struct StreamCounters {
+  int64_t offset, tail, count, sum_off;
+};
+
+struct PlannedUpdate {
+  UpdateJob job;
+  int64_t n_new;
+  bool overflow;
+};
+
+// _advance of the cache for one chunk (counters move; the update is described, not launched)
+int plan_update(StreamCounters& s, int64_t step, const void* k, const void* v, void* ring_k, void* ring_v,
+                int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity, int block_size,
+                int cache_window, int head_dim, PlannedUpdate* out) {
+  if (s.tail + step > ring_capacity) {
+    set_error("CompressedKVCache.tail_capacity=%lld too small to fit tail_size=%lld + step=%lld",
+              (long long)ring_capacity, (long long)s.tail, (long long)step);
+    return BFLY_ERR_CAPACITY;
+  }
+  const int64_t offset0 = s.offset;
+  s.tail += step;
+  s.offset += step;
+  const int64_t first_pos = s.sum_off, first_slot = s.count;
+  int64_t n_new = 0;
+  bool overflow = false;
+  while (s.sum_off + block_size <= s.offset - cache_window) {
+    const int64_t block_start = s.sum_off - (s.offset - s.tail);
+    if (block_start < 0 || block_start + block_size > s.tail) break;
+    if (s.count + n_new >= pool_capacity) {
+      overflow = true;
+      break;
+    }
+    ++n_new;
+    s.sum_off += block_size;
+  }
+  out->job = UpdateJob{k, v, ring_k, ring_v, pool_k, pool_v, step, ring_capacity, pool_capacity, offset0,
+                       first_pos, first_slot, (int)n_new, block_size, head_dim};
+  out->n_new = n_new;
+  out->overflow = overflow;
+  return BFLY_OK;
+}
+
+// after the update's launch: pooled count, then the trim (or the overflow error)
+int finish_update(StreamCounters& s, const PlannedUpdate& u, int64_t step, int64_t pool_capacity, int block_size,
+                  int cache_window) {
+  s.count += u.n_new;
+  if (u.overflow) {
+    set_error("CompressedKVCache.summary_capacity=%lld exhausted at offset=%lld", (long long)pool_capacity,
+              (long long)s.offset);
+    return BFLY_ERR_CAPACITY;
+  }
+  const int64_t target = cache_window > step + cache_window - 1 ? cache_window : step + cache_window - 1;
+  while (s.tail - block_size >= target) s.tail -= block_size;
+  return BFLY_OK;
+}
+
+}  // namespace
+
 extern "C" int bfly_stream_chunks(int64_t n_chunks, const void* const* q, const void* const* k,
                                   const void* const* v, void* const* out, const int64_t* chunk_len, int dtype,
                                   int64_t batch, int hq, int hkv, int head_dim, void* ring_k, void* ring_v,
@@ -772,86 +882,102 @@ extern "C" int bfly_stream_chunks(int64_t n_chunks, const void* const* q, const 
   BFLY_CHECK_ARG(n_chunks >= 0 && q && k && v && out && chunk_len && counters && chunks_done, "null pointer");
   BFLY_CHECK_ARG(ring_k && ring_v && pool_k && pool_v, "null pointer");
   BFLY_CHECK_ARG(batch > 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "bad head counts hq=%d hkv=%d", hq, hkv);
+  BFLY_CHECK_ARG(batch * hkv <= 65535, "batch*hkv too large");
   BFLY_CHECK_ARG(block_size > 0 && window > 0 && cache_window > 0, "bad block_size/window");
   BFLY_CHECK_ARG(local_window_blocks >= 0 && sink_count >= 0 && partner_count >= 0 &&
                      partner_count <= BFLY_MAX_PARTNERS,
                  "bad topology parameters");
+  BFLY_CHECK_ARG(aligned16(ring_k) && aligned16(ring_v) && aligned16(pool_k) && aligned16(pool_v),
+                 "tensor pointers must be 16-byte aligned");
   *chunks_done = 0;
-  int64_t offset = counters[0], tail = counters[1], count = counters[2], sum_off = counters[3];
-  BFLY_CHECK_ARG(offset > 0 && tail >= 0 && tail <= offset && count >= 0 && count <= pool_capacity && sum_off >= 0,
+  StreamCounters s{counters[0], counters[1], counters[2], counters[3]};
+  BFLY_CHECK_ARG(s.offset > 0 && s.tail >= 0 && s.tail <= s.offset && s.count >= 0 && s.count <= pool_capacity &&
+                     s.sum_off >= 0,
                  "the cache must hold a first chunk (offset > 0) and valid counters");
-  int64_t total = offset;
+  int64_t total = s.offset;
   for (int64_t c = 0; c < n_chunks; ++c) {
     BFLY_CHECK_ARG(chunk_len[c] > 0 && q[c] && k[c] && v[c] && out[c], "chunk %lld: empty or null", (long long)c);
+    BFLY_CHECK_ARG(aligned16(k[c]) && aligned16(v[c]), "chunk %lld: k/v must be 16-byte aligned", (long long)c);
     total += chunk_len[c];
   }
   const int kcap = 1 + local_window_blocks + partner_count + sink_count;
   // the MFMA attention kernel is the one that builds neighbour rows from the topology
   const bool mfma_ok = dtype == BFLY_DTYPE_BF16 && window <= kPage && block_size >= kPage && 2 * kcap <= kSumSlots &&
                        (head_dim == 64 || head_dim == 128 || head_dim == 256) && scale > 0.f &&
-                       ring_capacity >= kPage && total + 2 * kPage < INT32_MAX && ring_capacity < INT32_MAX &&
-                       pool_capacity < INT32_MAX;
+                       ring_capacity >= kPage && ring_capacity >= block_size && total + 2 * kPage < INT32_MAX &&
+                       ring_capacity < INT32_MAX && pool_capacity < INT32_MAX;
   if (!mfma_ok) {
     set_error("bfly_stream_chunks: configuration outside the MFMA attention path");
     return BFLY_ERR_UNSUPPORTED;
   }
+  const int64_t rows = batch * hkv;
   auto publish = [&]() {
-    counters[0] = offset;
-    counters[1] = tail;
-    counters[2] = count;
-    counters[3] = sum_off;
+    counters[0] = s.offset;
+    counters[1] = s.tail;
+    counters[2] = s.count;
+    counters[3] = s.sum_off;
   };
+  auto launch_update = [&](const PlannedUpdate& u) -> int {
+    const UpdateJob& j = u.job;
+    return bfly_cache_update(j.k_new, j.v_new, dtype, batch, hkv, j.step, head_dim, ring_k, ring_v, ring_capacity,
+                             j.offset, j.first_pos, j.n_blocks, block_size, pool_k, pool_v, pool_capacity,
+                             j.first_slot, stream);
+  };
+  if (n_chunks == 0) return BFLY_OK;
+  // the first chunk's update runs alone; every later one rides with the previous attention
+  PlannedUpdate cur{};
+  int rc = plan_update(s, chunk_len[0], k[0], v[0], ring_k, ring_v, ring_capacity, pool_k, pool_v, pool_capacity,
+                       block_size, cache_window, head_dim, &cur);
+  if (rc) return rc;
+  rc = launch_update(cur);
+  if (rc) return rc;
+  rc = finish_update(s, cur, chunk_len[0], pool_capacity, block_size, cache_window);
+  publish();
+  if (rc) return rc;
   for (int64_t c = 0; c < n_chunks; ++c) {
     const int64_t step = chunk_len[c];
-    if (tail + step > ring_capacity) {
-      set_error("CompressedKVCache.tail_capacity=%lld too small to fit tail_size=%lld + step=%lld",
-                (long long)ring_capacity, (long long)tail, (long long)step);
-      return BFLY_ERR_CAPACITY;
-    }
-    const int64_t offset0 = offset;
-    tail += step;
-    offset += step;
-    const int64_t first_pos = sum_off, first_slot = count;
-    int64_t n_new = 0;
-    bool overflow = false;
-    while (sum_off + block_size <= offset - cache_window) {
-      const int64_t block_start = sum_off - (offset - tail);
-      if (block_start < 0 || block_start + block_size > tail) break;
-      if (count + n_new >= pool_capacity) {
-        overflow = true;
-        break;
-      }
-      ++n_new;
-      sum_off += block_size;
-    }
-    int rc = bfly_cache_update(k[c], v[c], dtype, batch, hkv, step, head_dim, ring_k, ring_v, ring_capacity, offset0,
-                               first_pos, n_new, block_size, pool_k, pool_v, pool_capacity, first_slot, stream);
-    if (rc) return rc;
-    count += n_new;
-    if (overflow) {
-      publish();
-      set_error("CompressedKVCache.summary_capacity=%lld exhausted at offset=%lld", (long long)pool_capacity,
-                (long long)offset);
-      return BFLY_ERR_CAPACITY;
-    }
-    const int64_t target = cache_window > step + cache_window - 1 ? cache_window : step + cache_window - 1;
-    while (tail - block_size >= target) tail -= block_size;
-    publish();
-
-    const int64_t nblocks = (offset + block_size - 1) / block_size;
+    const int64_t nblocks = (s.offset + block_size - 1) / block_size;
     AttnArgs a{};
     rc = bfly_topology_init(nblocks, layer_idx, partner_rule, local_window_blocks, sink_count, partner_count, &a.topo);
     if (rc) return rc;
     a.q = q[c]; a.out = out[c]; a.k = ring_k; a.v = ring_v; a.ks = pool_k; a.vs = pool_v;
     a.nbr = nullptr; a.qpos = nullptr;
     a.batch = batch; a.hq = hq; a.hkv = hkv; a.tq = step; a.d = head_dim;
-    a.q_pos0 = offset - step; a.kv_rows = ring_capacity; a.ring = ring_capacity;
-    a.key_lo = offset - tail; a.kv_len = offset;
-    a.pool_rows = pool_capacity; a.nsum = count; a.nblocks = nblocks;
+    a.q_pos0 = s.offset - step; a.kv_rows = ring_capacity; a.ring = ring_capacity;
+    a.key_lo = s.offset - s.tail; a.kv_len = s.offset;
+    a.pool_rows = pool_capacity; a.nsum = s.count; a.nblocks = nblocks;
     a.kcap = kcap; a.bs = block_size; a.W = window; a.scale = scale; a.token_cutoff = 1;
-    rc = launch_attention(a, dtype, stream, "bfly_stream_chunks");
-    if (rc) return rc;
+    if (c + 1 == n_chunks) {
+      rc = launch_attention(a, dtype, stream, "bfly_stream_chunks");
+      if (rc) return rc;
+      *chunks_done = c + 1;
+      break;
+    }
+    const int64_t next = chunk_len[c + 1];
+    PlannedUpdate nu{};
+    StreamCounters s_next = s;
+    const int prc = plan_update(s_next, next, k[c + 1], v[c + 1], ring_k, ring_v, ring_capacity, pool_k, pool_v,
+                                pool_capacity, block_size, cache_window, head_dim, &nu);
+    if (prc) {   // chunk c+1 does not fit: chunk c completes, the error is chunk c+1's
+      rc = launch_attention(a, dtype, stream, "bfly_stream_chunks");
+      if (rc) return rc;
+      *chunks_done = c + 1;
+      return prc;
+    }
+    if (step + next + 2 * kPage <= ring_capacity) {
+      rc = launch_attention(a, dtype, stream, "bfly_stream_chunks", &nu.job, rows);
+      if (rc) return rc;
+    } else {
+      rc = launch_attention(a, dtype, stream, "bfly_stream_chunks");
+      if (rc) return rc;
+      rc = launch_update(nu);
+      if (rc) return rc;
+    }
     *chunks_done = c + 1;
+    s = s_next;
+    rc = finish_update(s, nu, next, pool_capacity, block_size, cache_window);
+    publish();
+    if (rc) return rc;
   }
   return BFLY_OK;
 }

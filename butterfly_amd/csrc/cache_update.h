@@ -1,0 +1,125 @@
+// Block mean pooling and the one-launch cache update (append + pooling of the
+// due blocks), as device functions shared by the compressor kernels and the
+// streaming prefill's fused launch.
+//
+// Reference semantics: _block_mean_summaries_torch
+// (bna/torch/attention_wayfinder_permute.py:1022-1043) and the summarise and
+// append steps of CompressedKVCache.update_and_fetch
+// (bna/mlx/compressed_cache.py:104-149).
+//
+// Fixed summation order (documented so results are reproducible): thread slot
+// s (of RS slots) sums tokens s, s+RS, s+2RS, ... sequentially; the RS partial
+// sums are then added in slot order 0..RS-1; the total is divided by the
+// valid-token count and rounded (RNE) to the storage type.
+#pragma once
+
+#include "bfly_common.h"
+
+namespace bfly {
+
+// Mean of `cnt` token rows into dst (one workgroup, 256 threads); tok_ptr(tok)
+// is the row of token tok; `part` is 256 * 8 floats of LDS scratch.
+template <typename T, int VEC, class TokPtr>
+__device__ __forceinline__ void pool_rows(TokPtr tok_ptr, int64_t cnt, T* dst, int d, float* part) {
+  const int lpr = d / VEC;               // lanes per token row
+  const int rs = 256 / lpr;              // token slots
+  const int t = threadIdx.x;
+  const int c = t % lpr, s = t / lpr;
+  float acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+  if (s < rs) {
+    if constexpr (VEC * sizeof(T) == 16) {
+      // eight loads in flight per thread, then the adds in token order
+      for (int64_t base = s; base < cnt; base += 8 * (int64_t)rs) {
+        uint4 raw[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int64_t tok = base + (int64_t)u * rs;
+          raw[u] = tok < cnt ? *reinterpret_cast<const uint4*>(tok_ptr(tok) + c * VEC) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (base + (int64_t)u * rs >= cnt) continue;
+          const T* v = reinterpret_cast<const T*>(&raw[u]);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[e] += to_f32(v[e]);
+        }
+      }
+    } else {
+      for (int64_t tok = s; tok < cnt; tok += rs) {
+        const T* ptr = tok_ptr(tok) + c * VEC;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += to_f32(ptr[e]);
+      }
+    }
+  }
+  if (s < rs) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) part[s * d + c * VEC + e] = acc[e];
+  }
+  __syncthreads();
+  const float denom = cnt > 0 ? (float)cnt : 1.f;
+  for (int col = t; col < d; col += 256) {
+    float tot = 0.f;
+    for (int k = 0; k < rs; ++k) tot += part[k * d + col];
+    dst[col] = from_f32<T>(tot / denom);
+  }
+}
+
+// One chunk's cache update (compressed_cache.py:104-149): the append of
+// k_new/v_new to ring slots (offset + t) mod C, and the mean of every block
+// that became due, whose tokens are read where they are before the update (the
+// ring for positions < offset, k_new/v_new for the rest), so the two parts are
+// independent: the pooled blocks and the new tokens all lie in the post-append
+// tail, which holds at most C positions, so their ring slots are distinct.
+// Work: x in [0, n_blocks + append workgroups), rows, K|V.
+struct UpdateJob {
+  const void* k_new;
+  const void* v_new;     // [rows, step, d]
+  void* ring_k;
+  void* ring_v;          // [rows, ring, d]
+  void* pool_k;
+  void* pool_v;          // [rows, pool_rows, d]
+  int64_t step, ring, pool_rows, offset, first_pos, first_slot;
+  int n_blocks, bs, d;
+};
+
+// Work item (bx, row, kv) of an update: workgroup-uniform, 256 threads.
+template <typename T, int VEC>
+__device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx, int64_t row, int kv, float* part) {
+  const int d = u.d;
+  const T* fresh = reinterpret_cast<const T*>(kv ? u.v_new : u.k_new) + row * u.step * d;
+  T* ring = reinterpret_cast<T*>(kv ? u.ring_v : u.ring_k) + row * u.ring * d;
+  if (bx >= u.n_blocks) {
+    // append: 256 / (d / VEC) tokens per workgroup, one 16-byte piece per thread
+    const int lpr = d / VEC, tpw = 256 / lpr;
+    const int t = threadIdx.x, c = t % lpr;
+    const int64_t tok = (bx - u.n_blocks) * tpw + t / lpr;
+    if (t / lpr >= tpw || tok >= u.step) return;
+    const int64_t slot = posmod(u.offset + tok, u.ring);
+    *reinterpret_cast<uint4*>(ring + slot * d + c * VEC) = *reinterpret_cast<const uint4*>(fresh + tok * d + c * VEC);
+    return;
+  }
+  const int64_t n = bx;
+  const int64_t p0 = u.first_pos + n * u.bs;
+  const int64_t r0 = posmod(p0, u.ring);   // tokens < bs <= ring: one wrap at most
+  auto tok_ptr = [&](int64_t tok) -> const T* {
+    const int64_t p = p0 + tok;
+    if (p >= u.offset) return fresh + (p - u.offset) * d;
+    int64_t r = r0 + tok;
+    if (r >= u.ring) r -= u.ring;
+    return ring + r * d;
+  };
+  T* dst = reinterpret_cast<T*>(kv ? u.pool_v : u.pool_k) + (row * u.pool_rows + u.first_slot + n) * d;
+  pool_rows<T, VEC>(tok_ptr, (int64_t)u.bs, dst, d, part);
+}
+
+// Workgroups along x of an update with a 16-byte row split (VEC elements per
+// 16 bytes): the due blocks, then the append workgroups.
+inline int64_t update_x(int64_t n_blocks, int64_t step, int head_dim, int vec) {
+  const int tpw = 256 / (head_dim / vec);
+  return n_blocks + (step + tpw - 1) / tpw;
+}
+
+}  // namespace bfly

@@ -11,7 +11,7 @@
 // s (of RS slots) sums tokens s, s+RS, s+2RS, ... sequentially; the RS partial
 // sums are then added in slot order 0..RS-1; the total is divided by the
 // valid-token count and rounded (RNE) to the storage type.
-#include "bfly_common.h"
+#include "cache_update.h"
 
 namespace bfly {
 
@@ -25,57 +25,6 @@ struct PoolJob {
   int64_t dst_slot0;    // dst row of block 0
   int64_t seq_len;      // valid tokens are positions < base_pos + seq_len
 };
-
-// Mean of `cnt` token rows into dst (one workgroup, 256 threads); tok_ptr(tok)
-// is the row of token tok.  The summation order is the one documented above.
-template <typename T, int VEC, class TokPtr>
-__device__ __forceinline__ void pool_rows(TokPtr tok_ptr, int64_t cnt, T* dst, int d) {
-  const int lpr = d / VEC;               // lanes per token row
-  const int rs = 256 / lpr;              // token slots
-  const int t = threadIdx.x;
-  const int c = t % lpr, s = t / lpr;
-  float acc[VEC];
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
-  if (s < rs) {
-    if constexpr (VEC * sizeof(T) == 16) {
-      // eight loads in flight per thread, then the adds in token order
-      for (int64_t base = s; base < cnt; base += 8 * (int64_t)rs) {
-        uint4 raw[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int64_t tok = base + (int64_t)u * rs;
-          raw[u] = tok < cnt ? *reinterpret_cast<const uint4*>(tok_ptr(tok) + c * VEC) : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          if (base + (int64_t)u * rs >= cnt) continue;
-          const T* v = reinterpret_cast<const T*>(&raw[u]);
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) acc[e] += to_f32(v[e]);
-        }
-      }
-    } else {
-      for (int64_t tok = s; tok < cnt; tok += rs) {
-        const T* ptr = tok_ptr(tok) + c * VEC;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[e] += to_f32(ptr[e]);
-      }
-    }
-  }
-  __shared__ float part[256 * 8];
-  if (s < rs) {
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) part[s * d + c * VEC + e] = acc[e];
-  }
-  __syncthreads();
-  const float denom = cnt > 0 ? (float)cnt : 1.f;
-  for (int col = t; col < d; col += 256) {
-    float tot = 0.f;
-    for (int k = 0; k < rs; ++k) tot += part[k * d + col];
-    dst[col] = from_f32<T>(tot / denom);
-  }
-}
 
 template <typename T, int VEC>
 __global__ void __launch_bounds__(256) block_mean_kernel(PoolJob j0, PoolJob j1, int d, int bs) {
@@ -95,56 +44,16 @@ __global__ void __launch_bounds__(256) block_mean_kernel(PoolJob j0, PoolJob j1,
     return src + r * d;
   };
   T* dst = reinterpret_cast<T*>(job.dst) + (row * job.dst_rows + job.dst_slot0 + n) * d;
-  pool_rows<T, VEC>(tok_ptr, cnt, dst, d);
+  __shared__ float part[256 * 8];
+  pool_rows<T, VEC>(tok_ptr, cnt, dst, d, part);
 }
 
-// One chunk's cache update in one launch (compressed_cache.py:104-149): the
-// append of k_new/v_new to ring slots (offset + t) mod C, and the mean of every
-// block that became due, whose tokens are read where they are before the
-// update (the ring for positions < offset, k_new/v_new for the rest), so the
-// two parts are independent: the pooled blocks and the new tokens all lie in
-// the post-append tail, which holds at most C positions, so their ring slots
-// are distinct.  Grid: (n_blocks + append workgroups, rows, K|V).
-struct UpdateJob {
-  const void* k_new;
-  const void* v_new;     // [rows, step, d]
-  void* ring_k;
-  void* ring_v;          // [rows, ring, d]
-  void* pool_k;
-  void* pool_v;          // [rows, pool_rows, d]
-  int64_t step, ring, pool_rows, offset, first_pos, first_slot;
-  int n_blocks, bs, d;
-};
-
+// One chunk's cache update in one launch: cache_update_body over the grid
+// (n_blocks + append workgroups, rows, K|V).
 template <typename T, int VEC>
 __global__ void __launch_bounds__(256) cache_update_kernel(UpdateJob u) {
-  const int kv = blockIdx.z;
-  const int64_t row = blockIdx.y;
-  const int d = u.d;
-  const T* fresh = reinterpret_cast<const T*>(kv ? u.v_new : u.k_new) + row * u.step * d;
-  T* ring = reinterpret_cast<T*>(kv ? u.ring_v : u.ring_k) + row * u.ring * d;
-  if ((int)blockIdx.x >= u.n_blocks) {
-    // append: 256 / (d / VEC) tokens per workgroup, one 16-byte piece per thread
-    const int lpr = d / VEC, tpw = 256 / lpr;
-    const int t = threadIdx.x, c = t % lpr;
-    const int64_t tok = (int64_t)(blockIdx.x - u.n_blocks) * tpw + t / lpr;
-    if (t / lpr >= tpw || tok >= u.step) return;
-    const int64_t slot = posmod(u.offset + tok, u.ring);
-    *reinterpret_cast<uint4*>(ring + slot * d + c * VEC) = *reinterpret_cast<const uint4*>(fresh + tok * d + c * VEC);
-    return;
-  }
-  const int64_t n = blockIdx.x;
-  const int64_t p0 = u.first_pos + n * u.bs;
-  const int64_t r0 = posmod(p0, u.ring);   // tokens < bs <= ring: one wrap at most
-  auto tok_ptr = [&](int64_t tok) -> const T* {
-    const int64_t p = p0 + tok;
-    if (p >= u.offset) return fresh + (p - u.offset) * d;
-    int64_t r = r0 + tok;
-    if (r >= u.ring) r -= u.ring;
-    return ring + r * d;
-  };
-  T* dst = reinterpret_cast<T*>(kv ? u.pool_v : u.pool_k) + (row * u.pool_rows + u.first_slot + n) * d;
-  pool_rows<T, VEC>(tok_ptr, (int64_t)u.bs, dst, d);
+  __shared__ float part[256 * 8];
+  cache_update_body<T, VEC>(u, blockIdx.x, blockIdx.y, blockIdx.z, part);
 }
 
 template <typename T>
@@ -303,12 +212,11 @@ extern "C" int bfly_cache_update(const void* k_new, const void* v_new, int dtype
     return bfly_cache_compress(ring_k, ring_v, dtype, batch, hkv, head_dim, ring_capacity, first_block_pos,
                                n_blocks, block_size, pool_k, pool_v, pool_capacity, first_slot, stream);
   }
-  const int tpw = 256 / (head_dim / vec);
-  const int64_t app = (step + tpw - 1) / tpw;
-  BFLY_CHECK_ARG(n_blocks + app <= INT32_MAX, "grid too large");
+  const int64_t ux = update_x(n_blocks, step, head_dim, vec);
+  BFLY_CHECK_ARG(ux <= INT32_MAX, "grid too large");
   UpdateJob u{k_new, v_new, ring_k, ring_v, pool_k, pool_v, step, ring_capacity, pool_capacity, offset,
               first_block_pos, first_slot, (int)n_blocks, block_size, head_dim};
-  dim3 grid((unsigned)(n_blocks + app), (unsigned)(batch * hkv), 2);
+  dim3 grid((unsigned)ux, (unsigned)(batch * hkv), 2);
   if (dtype == BFLY_DTYPE_F32)
     hipLaunchKernelGGL((cache_update_kernel<float, 4>), grid, dim3(256), 0, stream, u);
   else

@@ -271,24 +271,42 @@ def chunked_prefill(core: ButterflyAttentionCore, chunks, cache: CompressedKVCac
     chunk appends to the cache and attends from it with the layout of the live
     kv_len.  ``chunks`` yields contiguous ``(q, k, v)`` chunks in order.
 
-    After the first chunk, the remaining ones run through one ``bfly_stream_chunks``
-    call (the same kernels and arguments, with the per-chunk bookkeeping in C++)
-    whenever the configuration allows it; otherwise each chunk goes through ``core``.
+    After the first chunk, runs of chunks go through ``bfly_stream_chunks`` (the same
+    kernels and arguments, with the per-chunk bookkeeping in C++; a small first run
+    so the GPU starts while the host prepares the next) whenever the configuration
+    allows it; a chunk the loop does not cover goes through ``core``.
     """
     chunks = list(chunks)
     if not chunks:
         return []
     outs = [core(*chunks[0], cache)]
-    rest = chunks[1:]
-    if rest:
-        native = _stream_chunks(core, rest, cache)
-        outs += native if native is not None else [core(qc, kc, vc, cache) for qc, kc, vc in rest]
+    i, native, run = 1, True, 8
+    while i < len(chunks):
+        got = _stream_chunks(core, chunks, i, run, cache) if native else None
+        if got is None:
+            native = native and _stream_possible(core, cache, chunks[i])
+            outs.append(core(*chunks[i], cache))
+            i += 1
+            continue
+        outs += got
+        i += len(got)
+        run = 64
     return outs
 
 
-def _stream_chunks(core: ButterflyAttentionCore, chunks, cache) -> Optional[List[torch.Tensor]]:
-    """``bfly_stream_chunks`` over ``chunks`` (the cache already holds the first chunk), or
-    None when the per-chunk path must run them: a cache with device counters, chunks of
+def _stream_possible(core: ButterflyAttentionCore, cache, chunk) -> bool:
+    """False once the native loop cannot take any chunk of this call (cache mode or
+    configuration); True when only this chunk's shape kept it out."""
+    q = chunk[0]
+    return (isinstance(cache, CompressedKVCache) and cache.device_counters is None and q.dtype == torch.bfloat16
+            and int(q.shape[3]) in (64, 128, 256))
+
+
+def _stream_chunks(core: ButterflyAttentionCore, chunks, start: int, run: int,
+                   cache) -> Optional[List[torch.Tensor]]:
+    """Outputs of up to ``run`` chunks from ``chunks[start]`` on, through one
+    ``bfly_stream_chunks`` call (the cache already holds the first chunk), or None when
+    ``chunks[start]`` must go through ``core``: a cache with device counters, a chunk of
     one or two tokens (the per-chunk path sends those to the decode kernel or, with the
     dense backend, to the stock fallback), or a configuration the loop does not cover."""
     import ctypes as C
@@ -296,22 +314,23 @@ def _stream_chunks(core: ButterflyAttentionCore, chunks, cache) -> Optional[List
     from . import _native
     from .attention import _dtype_code, _scale, _stream
 
-    if not isinstance(cache, CompressedKVCache) or cache.device_counters is not None or cache.offset <= 0:
+    if not isinstance(cache, CompressedKVCache) or cache.device_counters is not None or cache.offset <= 0 \
+            or cache._ring_k is None:
         return None
-    q0, k0, _ = chunks[0]
+    q0, k0, _ = chunks[start]
     b, hq, _, d = (int(x) for x in q0.shape)
     hkv = int(k0.shape[1])
-    if q0.dtype != torch.bfloat16 or cache._ring_k is None:
-        return None
     qs, ks, vs = [], [], []
-    for qc, kc, vc in chunks:
+    for qc, kc, vc in chunks[start:start + run]:
         n = int(qc.shape[2])
         if (n <= 2 or tuple(qc.shape) != (b, hq, n, d) or tuple(kc.shape) != (b, hkv, n, d) or kc.shape != vc.shape
                 or not (qc.dtype == kc.dtype == vc.dtype == torch.bfloat16) or not qc.is_cuda):
-            return None
+            break
         qs.append(_c(qc))
         ks.append(_c(kc))
         vs.append(_c(vc))
+    if not qs:
+        return None
     cache.sync()
     cache._apply_realign()
     ring_k, ring_v, pool_k, pool_v = cache._ring_k, cache._ring_v, cache._pool_k, cache._pool_v
@@ -348,5 +367,5 @@ def _stream_chunks(core: ButterflyAttentionCore, chunks, cache) -> Optional[List
     lay = core.layout(cache.offset, hkv, hq // hkv, q0.device)
     core._last = (t0, _now_ms(), None, "block_sparse_compressed_active",
                   {"seq_len": cache.offset, "q_len": int(qs[-1].shape[2]), "block_sparse_active_mode": True,
-                   "native_chunk_loop": m}, lay)
+                   "native_chunk_loop": m}, lay)     # chunks of the last native call
     return outs

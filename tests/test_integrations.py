@@ -184,3 +184,31 @@ def test_native_chunk_loop_capacity_error_matches_per_chunk_calls():
     a, bb = caches
     assert (a.offset, a.tail_size, a.summary_count, a.summary_offset) == \
            (bb.offset, bb.tail_size, bb.summary_count, bb.summary_offset)
+
+
+@pytest.mark.gpu
+def test_native_chunk_runs_mix_with_per_chunk_calls():
+    """A run of native chunks stops at a chunk the loop does not take (two tokens): that
+    chunk goes through the core, and the next run continues from the same cache."""
+    b, hq, hkv, d, layer = 1, 8, 2, 128, 4
+    lens = [300] + [200] * 12 + [2] + [150] * 70
+    total = sum(lens)
+    q = _rand(97, (b, hq, total, d), torch.bfloat16).cuda()
+    k = _rand(98, (b, hkv, total, d), torch.bfloat16).cuda()
+    v = _rand(99, (b, hkv, total, d), torch.bfloat16).cuda()
+    chunks, pos = [], 0
+    for n in lens:
+        chunks.append(tuple(t[:, :, pos:pos + n].contiguous() for t in (q, k, v)))
+        pos += n
+    runs = []
+    for native in (True, False):
+        core = bf.ButterflyAttentionCore(bf.QwenButterflyConfig(), layer)
+        cache = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=total, max_chunk_size=512)
+        outs = bf.chunked_prefill(core, chunks, cache) if native else [core(*c, cache) for c in chunks]
+        runs.append((cache, outs))
+    (a, oa_), (bb, ob) = runs
+    assert len(oa_) == len(ob) == len(lens)
+    for x, y in zip(oa_, ob):
+        assert torch.equal(x, y)
+    assert (a.offset, a.tail_size, a.summary_count, a.summary_offset) == \
+           (bb.offset, bb.tail_size, bb.summary_count, bb.summary_offset)

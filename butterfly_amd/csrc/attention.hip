@@ -538,98 +538,115 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
           if (two) refill_q(u1, c, h0 + 1);
           continue;
         }
-        // S^T for both heads; one K fragment read feeds two MFMAs.
-        // (With an odd group the second head of the last pair is computed on a
-        // stale Q slot and discarded: no branch sits between the MFMAs.)
-        f32x4 s0[6], s1[6];
-#pragma unroll
-        for (int t = 0; t < 6; ++t) {
-          bf16x8 kf[C::KSTEPS];
-#pragma unroll
-          for (int ks = 0; ks < C::KSTEPS; ++ks)
-            kf[ks] = *reinterpret_cast<const bf16x8*>(Ks + (slot[t] + lq) * C::KP + lg * (D / 4) + 8 * ks);
-          f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int ks = 0; ks < C::KSTEPS; ++ks) {
-            a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qbuf[u0][ks], a0, 0, 0, 0);
-            a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qbuf[u1][ks], a1, 0, 0, 0);
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            s0[t][i] = ok[t][i] ? a0[i] : -INFINITY;
-            s1[t][i] = ok[t][i] ? a1[i] : -INFINITY;
-          }
-        }
-        refill_q(u0, c, h0);
-        if (two) refill_q(u1, c, h0 + 1);
-        bf16x8 p0[3], p1[3];
-        float inv0, inv1;
-        softmax(s0, p0, inv0);
-        softmax(s1, p1, inv1);
-        // O^T = V^T P^T.  Tile (mt, half), row r holds d = mt*32 + (r/4)*8 + half*4 + r%4,
-        // so the two halves give each lane 8 consecutive d (16 bytes) of its position.
-        // The V^T fragments come from row-major V by transposing reads: lane (lg, lq)
-        // reads the 4 d (8 bytes) mt*32 + (lq&3)*8 + half*4 of key row
-        // slot + 4lg + (lq>>2), so lane lq of the group receives d row lq's four keys
-        // slot + 4lg + 0..3, the order of its P fragment.
-        // Tiles mt and mt+1 together hold d [mt*32, mt*32+64) = one 128-byte line per
-        // position.  Lanes lq and lq^8 swap one 16-byte piece so that each store
-        // instruction writes 8 whole lines (positions 0..7, then 8..15): whole-line
-        // non-temporal stores stream to HBM at full rate, half lines do not.
-        const bool lo8 = lq < 8;
-        const int pA = pw + (lq & 7), pB = pA + 8;        // positions of the two store passes
-        const bool okA = pA >= m.qlo && pA < m.qhi, okB = pB >= m.qlo && pB < m.qhi;
-        __bf16* oA0 = ohead0 + ((int64_t)h0 * a.tq + (okA ? pA - m.qlo : 0)) * D;
-        __bf16* oB0 = ohead0 + ((int64_t)h0 * a.tq + (okB ? pB - m.qlo : 0)) * D;
-        const int64_t hstride = (int64_t)a.tq * D;
-#pragma unroll
-        for (int mp = 0; mp < C::DTILES / 4; ++mp) {
-          bf16x8 w0[2], w1[2];
-#pragma unroll
-          for (int sub = 0; sub < 2; ++sub) {
-            const int mt = 2 * mp + sub;
-            f32x4 o0[2], o1[2];
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-              const int unit = mt * 8 + (lq & 3) * 2 + half;   // 8-byte unit of the row
-              bf16x8 vf[3];
-#pragma unroll
-              for (int pr = 0; pr < 3; ++pr) {
-                const int ra = slot[2 * pr] + 4 * lg + (lq >> 2), rb = slot[2 * pr + 1] + 4 * lg + (lq >> 2);
-                const bf16x4 va = read_tr(Vs + ra * D + (unit ^ (2 * C::vswz(ra))) * 4);
-                const bf16x4 vb = read_tr(Vs + rb * D + (unit ^ (2 * C::vswz(rb))) * 4);
-                vf[pr] = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
-              }
-              f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-              for (int pr = 0; pr < 3; ++pr) {
-                a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[pr], p0[pr], a0, 0, 0, 0);
-                a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[pr], p1[pr], a1, 0, 0, 0);
-              }
-              o0[half] = a0;
-              o1[half] = a1;
+        auto pair_body = [&](auto two_tag) {
+          constexpr bool kTwo = decltype(two_tag)::value;
+          // S^T for both heads; one K fragment read feeds two MFMAs.  For d = 256 a
+          // pair with one head (an odd group, or one head per workgroup) runs the
+          // kTwo = false copy of this body, which issues no MFMA for the missing
+          // head; smaller d keep one copy (registers), where the second head of
+          // such a pair is computed on a stale Q slot and discarded.
+          f32x4 s0[6], s1[6];
+  #pragma unroll
+          for (int t = 0; t < 6; ++t) {
+            bf16x8 kf[C::KSTEPS];
+  #pragma unroll
+            for (int ks = 0; ks < C::KSTEPS; ++ks)
+              kf[ks] = *reinterpret_cast<const bf16x8*>(Ks + (slot[t] + lq) * C::KP + lg * (D / 4) + 8 * ks);
+            f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+            for (int ks = 0; ks < C::KSTEPS; ++ks) {
+              a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qbuf[u0][ks], a0, 0, 0, 0);
+              if constexpr (kTwo) a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qbuf[u1][ks], a1, 0, 0, 0);
             }
-#pragma unroll
+  #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              w0[sub][i] = (__bf16)(o0[0][i] * inv0);
-              w0[sub][4 + i] = (__bf16)(o0[1][i] * inv0);
-              w1[sub][i] = (__bf16)(o1[0][i] * inv1);
-              w1[sub][4 + i] = (__bf16)(o1[1][i] * inv1);
+              s0[t][i] = ok[t][i] ? a0[i] : -INFINITY;
+              if constexpr (kTwo) s1[t][i] = ok[t][i] ? a1[i] : -INFINITY;
             }
           }
-          // lanes lq < 8 keep tile mt (sub 0) and receive the partner's tile mt;
-          // lanes lq >= 8 keep tile mt+1 (sub 1) and receive the partner's tile mt+1
-          const bf16x8 x0 = xchg8(lo8 ? w0[1] : w0[0]);
-          const bf16x8 x1 = xchg8(lo8 ? w1[1] : w1[0]);
-          const int dA = (2 * mp + (lo8 ? 0 : 1)) * 32 + lg * 8;   // d of this lane's piece
-          const bf16x8 a0 = lo8 ? w0[0] : x0, b0 = lo8 ? x0 : w0[1];
-          const bf16x8 a1 = lo8 ? w1[0] : x1, b1 = lo8 ? x1 : w1[1];
-          // O is written once and never re-read here: non-temporal stores keep it
-          // from evicting the K/V pages and Q rows still in flight from L2.
-          if (okA) __builtin_nontemporal_store(a0, reinterpret_cast<bf16x8*>(oA0 + dA));
-          if (okB) __builtin_nontemporal_store(b0, reinterpret_cast<bf16x8*>(oB0 + dA));
-          if (two && okA) __builtin_nontemporal_store(a1, reinterpret_cast<bf16x8*>(oA0 + hstride + dA));
-          if (two && okB) __builtin_nontemporal_store(b1, reinterpret_cast<bf16x8*>(oB0 + hstride + dA));
+          refill_q(u0, c, h0);
+          if (kTwo && two) refill_q(u1, c, h0 + 1);
+          bf16x8 p0[3], p1[3];
+          float inv0, inv1 = 0.f;
+          softmax(s0, p0, inv0);
+          if constexpr (kTwo) softmax(s1, p1, inv1);
+          // O^T = V^T P^T.  Tile (mt, half), row r holds d = mt*32 + (r/4)*8 + half*4 + r%4,
+          // so the two halves give each lane 8 consecutive d (16 bytes) of its position.
+          // The V^T fragments come from row-major V by transposing reads: lane (lg, lq)
+          // reads the 4 d (8 bytes) mt*32 + (lq&3)*8 + half*4 of key row
+          // slot + 4lg + (lq>>2), so lane lq of the group receives d row lq's four keys
+          // slot + 4lg + 0..3, the order of its P fragment.
+          // Tiles mt and mt+1 together hold d [mt*32, mt*32+64) = one 128-byte line per
+          // position.  Lanes lq and lq^8 swap one 16-byte piece so that each store
+          // instruction writes 8 whole lines (positions 0..7, then 8..15): whole-line
+          // non-temporal stores stream to HBM at full rate, half lines do not.
+          const bool lo8 = lq < 8;
+          const int pA = pw + (lq & 7), pB = pA + 8;        // positions of the two store passes
+          const bool okA = pA >= m.qlo && pA < m.qhi, okB = pB >= m.qlo && pB < m.qhi;
+          __bf16* oA0 = ohead0 + ((int64_t)h0 * a.tq + (okA ? pA - m.qlo : 0)) * D;
+          __bf16* oB0 = ohead0 + ((int64_t)h0 * a.tq + (okB ? pB - m.qlo : 0)) * D;
+          const int64_t hstride = (int64_t)a.tq * D;
+  #pragma unroll
+          for (int mp = 0; mp < C::DTILES / 4; ++mp) {
+            bf16x8 w0[2], w1[2];
+  #pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+              const int mt = 2 * mp + sub;
+              f32x4 o0[2], o1[2];
+  #pragma unroll
+              for (int half = 0; half < 2; ++half) {
+                const int unit = mt * 8 + (lq & 3) * 2 + half;   // 8-byte unit of the row
+                bf16x8 vf[3];
+  #pragma unroll
+                for (int pr = 0; pr < 3; ++pr) {
+                  const int ra = slot[2 * pr] + 4 * lg + (lq >> 2), rb = slot[2 * pr + 1] + 4 * lg + (lq >> 2);
+                  const bf16x4 va = read_tr(Vs + ra * D + (unit ^ (2 * C::vswz(ra))) * 4);
+                  const bf16x4 vb = read_tr(Vs + rb * D + (unit ^ (2 * C::vswz(rb))) * 4);
+                  vf[pr] = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
+                }
+                f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+                for (int pr = 0; pr < 3; ++pr) {
+                  a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[pr], p0[pr], a0, 0, 0, 0);
+                  if constexpr (kTwo) a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[pr], p1[pr], a1, 0, 0, 0);
+                }
+                o0[half] = a0;
+                o1[half] = a1;
+              }
+  #pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                w0[sub][i] = (__bf16)(o0[0][i] * inv0);
+                w0[sub][4 + i] = (__bf16)(o0[1][i] * inv0);
+                if constexpr (kTwo) {
+                  w1[sub][i] = (__bf16)(o1[0][i] * inv1);
+                  w1[sub][4 + i] = (__bf16)(o1[1][i] * inv1);
+                }
+              }
+            }
+            // lanes lq < 8 keep tile mt (sub 0) and receive the partner's tile mt;
+            // lanes lq >= 8 keep tile mt+1 (sub 1) and receive the partner's tile mt+1
+            const bf16x8 x0 = xchg8(lo8 ? w0[1] : w0[0]);
+            const int dA = (2 * mp + (lo8 ? 0 : 1)) * 32 + lg * 8;   // d of this lane's piece
+            const bf16x8 a0 = lo8 ? w0[0] : x0, b0 = lo8 ? x0 : w0[1];
+            // O is written once and never re-read here: non-temporal stores keep it
+            // from evicting the K/V pages and Q rows still in flight from L2.
+            if (okA) __builtin_nontemporal_store(a0, reinterpret_cast<bf16x8*>(oA0 + dA));
+            if (okB) __builtin_nontemporal_store(b0, reinterpret_cast<bf16x8*>(oB0 + dA));
+            if constexpr (kTwo) {
+              const bf16x8 x1 = xchg8(lo8 ? w1[1] : w1[0]);
+              const bf16x8 a1 = lo8 ? w1[0] : x1, b1 = lo8 ? x1 : w1[1];
+              if (two && okA) __builtin_nontemporal_store(a1, reinterpret_cast<bf16x8*>(oA0 + hstride + dA));
+              if (two && okB) __builtin_nontemporal_store(b1, reinterpret_cast<bf16x8*>(oB0 + hstride + dA));
+            }
+          }
+        };
+        if constexpr (D == 256) {
+          if (two)
+            pair_body(std::true_type{});
+          else
+            pair_body(std::false_type{});
+        } else {
+          pair_body(std::true_type{});
         }
       }
     }

@@ -56,7 +56,9 @@ __global__ void __launch_bounds__(256) add_rmsnorm_any_kernel(const __bf16* __re
 
 // One workgroup of 256 threads per row; each thread holds `PER` consecutive
 // elements (dim = 256 * PER).
-template <int PER>
+// kVec: every pointer is 16-byte aligned and PER a multiple of 8, so each
+// thread moves its elements as 16-byte pieces.
+template <int PER, bool kVec>
 __global__ void __launch_bounds__(256) add_rmsnorm_kernel(const __bf16* __restrict__ x, const __bf16* __restrict__ y,
                                                           const __bf16* __restrict__ w, __bf16* __restrict__ h_out,
                                                           __bf16* __restrict__ n_out, int dim, float eps) {
@@ -64,15 +66,39 @@ __global__ void __launch_bounds__(256) add_rmsnorm_kernel(const __bf16* __restri
   const int t = threadIdx.x;
   const int64_t base = row * dim + (int64_t)t * PER;
   float h[PER];
+  if constexpr (kVec) {
 #pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    float v = (float)x[base + e];
-    if (y != nullptr) v = (float)(__bf16)(v + (float)y[base + e]);   // residual stream in bf16
-    h[e] = v;
-  }
-  if (y != nullptr && h_out != nullptr) {
+    for (int c = 0; c < PER / 8; ++c) {
+      const bf16x8 xv = *reinterpret_cast<const bf16x8*>(x + base + 8 * c);
+      bf16x8 yv{};
+      if (y != nullptr) yv = *reinterpret_cast<const bf16x8*>(y + base + 8 * c);
 #pragma unroll
-    for (int e = 0; e < PER; ++e) h_out[base + e] = (__bf16)h[e];
+      for (int e = 0; e < 8; ++e) {
+        float v = (float)xv[e];
+        if (y != nullptr) v = (float)(__bf16)(v + (float)yv[e]);   // residual stream in bf16
+        h[8 * c + e] = v;
+      }
+    }
+    if (y != nullptr && h_out != nullptr) {
+#pragma unroll
+      for (int c = 0; c < PER / 8; ++c) {
+        bf16x8 hv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) hv[e] = (__bf16)h[8 * c + e];
+        *reinterpret_cast<bf16x8*>(h_out + base + 8 * c) = hv;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      float v = (float)x[base + e];
+      if (y != nullptr) v = (float)(__bf16)(v + (float)y[base + e]);   // residual stream in bf16
+      h[e] = v;
+    }
+    if (y != nullptr && h_out != nullptr) {
+#pragma unroll
+      for (int e = 0; e < PER; ++e) h_out[base + e] = (__bf16)h[e];
+    }
   }
   float ss = 0.f;
 #pragma unroll
@@ -83,8 +109,19 @@ __global__ void __launch_bounds__(256) add_rmsnorm_kernel(const __bf16* __restri
   __syncthreads();
   const float tot = (part[0] + part[1]) + (part[2] + part[3]);
   const float r = rsqrtf(tot / (float)dim + eps);
+  if constexpr (kVec) {
 #pragma unroll
-  for (int e = 0; e < PER; ++e) n_out[base + e] = (__bf16)(h[e] * r * (float)w[t * PER + e]);
+    for (int c = 0; c < PER / 8; ++c) {
+      const bf16x8 wv = *reinterpret_cast<const bf16x8*>(w + t * PER + 8 * c);
+      bf16x8 nv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) nv[e] = (__bf16)(h[8 * c + e] * r * (float)wv[e]);
+      *reinterpret_cast<bf16x8*>(n_out + base + 8 * c) = nv;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) n_out[base + e] = (__bf16)(h[e] * r * (float)w[t * PER + e]);
+  }
 }
 
 // One wave per (row of B*T, head): q/k heads are normed over d with their weight,
@@ -157,8 +194,108 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const __bf16* __restr
   }
 }
 
+// The same step with 16-byte accesses: a group of HALF / 8 lanes per (row,
+// head) item, lane j of the group holding elements [8j, 8j + 8) of both halves
+// (the rotate-half partners).  Same rounding points; the sum of squares runs
+// over the group with shuffles.  Needs 16-byte aligned rows (strides multiples
+// of 8, aligned base pointers).
+template <int D>
+__global__ void __launch_bounds__(256) qk_norm_rope_vec_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const __bf16* __restrict__ qw, const __bf16* __restrict__ kw, const float* __restrict__ cosv,
+    const float* __restrict__ sinv, __bf16* __restrict__ qo, __bf16* __restrict__ ko, __bf16* __restrict__ vo,
+    int64_t rows, int t_len, int hq, int hkv, int64_t sq, int64_t sk, int64_t sv, float eps) {
+  constexpr int HALF = D / 2;
+  constexpr int G = HALF / 8;    // lanes per item: 8 (d = 128) or 16 (d = 256)
+  const int gl = threadIdx.x % G;
+  const int64_t item = ((int64_t)blockIdx.x * 256 + threadIdx.x) / G;
+  const int nh = hq + 2 * hkv;
+  if (item >= rows * nh) return;   // whole groups: items are group-uniform
+  const int64_t row = item / nh;   // b * T + t
+  const int head = (int)(item - row * nh);
+  const int64_t b = row / t_len;
+  const int tt = (int)(row - b * t_len);
+  const __bf16* src;
+  __bf16* dst;
+  const __bf16* w = nullptr;
+  if (head < hq) {
+    src = q + row * sq + (int64_t)head * D;
+    dst = qo + ((b * hq + head) * t_len + tt) * D;
+    w = qw;
+  } else if (head < hq + hkv) {
+    const int hk = head - hq;
+    src = k + row * sk + (int64_t)hk * D;
+    dst = ko + ((b * hkv + hk) * t_len + tt) * D;
+    w = kw;
+  } else {
+    const int hv = head - hq - hkv;
+    src = v + row * sv + (int64_t)hv * D;
+    dst = vo + ((b * hkv + hv) * t_len + tt) * D;
+  }
+  const int i0 = 8 * gl;
+  const bf16x8 lov = *reinterpret_cast<const bf16x8*>(src + i0);
+  const bf16x8 hiv = *reinterpret_cast<const bf16x8*>(src + HALF + i0);
+  if (w == nullptr) {
+    *reinterpret_cast<bf16x8*>(dst + i0) = lov;
+    *reinterpret_cast<bf16x8*>(dst + HALF + i0) = hiv;
+    return;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss = fmaf((float)lov[e], (float)lov[e], fmaf((float)hiv[e], (float)hiv[e], ss));
+#pragma unroll
+  for (int o = 1; o < G; o <<= 1) ss += __shfl_xor(ss, o);
+  const float r = rsqrtf(ss / (float)D + eps);
+  const bf16x8 wlo = *reinterpret_cast<const bf16x8*>(w + i0);
+  const bf16x8 whi = *reinterpret_cast<const bf16x8*>(w + HALF + i0);
+  const float* c = cosv + (int64_t)tt * D;
+  const float* sn = sinv + (int64_t)tt * D;
+  float clo[8], chi[8], slo[8], shi[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float4 a = *reinterpret_cast<const float4*>(c + i0 + 4 * h);
+    const float4 bq = *reinterpret_cast<const float4*>(c + HALF + i0 + 4 * h);
+    const float4 cc = *reinterpret_cast<const float4*>(sn + i0 + 4 * h);
+    const float4 d = *reinterpret_cast<const float4*>(sn + HALF + i0 + 4 * h);
+    clo[4 * h] = a.x; clo[4 * h + 1] = a.y; clo[4 * h + 2] = a.z; clo[4 * h + 3] = a.w;
+    chi[4 * h] = bq.x; chi[4 * h + 1] = bq.y; chi[4 * h + 2] = bq.z; chi[4 * h + 3] = bq.w;
+    slo[4 * h] = cc.x; slo[4 * h + 1] = cc.y; slo[4 * h + 2] = cc.z; slo[4 * h + 3] = cc.w;
+    shi[4 * h] = d.x; shi[4 * h + 1] = d.y; shi[4 * h + 2] = d.z; shi[4 * h + 3] = d.w;
+  }
+  bf16x8 olo, ohi;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float a = (float)(__bf16)((float)lov[e] * r * (float)wlo[e]);    // normed, rounded as the module does
+    const float bb = (float)(__bf16)((float)hiv[e] * r * (float)whi[e]);
+    olo[e] = (__bf16)(a * clo[e] + (-bb) * slo[e]);                        // x*cos + rotate_half(x)*sin
+    ohi[e] = (__bf16)(bb * chi[e] + a * shi[e]);
+  }
+  *reinterpret_cast<bf16x8*>(dst + i0) = olo;
+  *reinterpret_cast<bf16x8*>(dst + HALF + i0) = ohi;
+}
+
 // rows x cols elements; gate and up rows are `stride` elements apart (a fused
-// gate|up projection output has stride 2 * cols), out is contiguous.
+// gate|up projection output has stride 2 * cols), out is contiguous.  The
+// vector form moves 8 consecutive elements of a row per thread (cols and
+// stride multiples of 8, pointers 16-byte aligned), with the same arithmetic.
+__global__ void __launch_bounds__(256) silu_mul_vec_kernel(const __bf16* __restrict__ g, const __bf16* __restrict__ u,
+                                                           __bf16* __restrict__ out, int64_t cols8, int64_t stride8,
+                                                           int64_t n8) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const int64_t r = i / cols8, c = i - r * cols8;
+  const bf16x8 gv = reinterpret_cast<const bf16x8*>(g)[r * stride8 + c];
+  const bf16x8 uv = reinterpret_cast<const bf16x8*>(u)[r * stride8 + c];
+  bf16x8 ov;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float x = (float)gv[e];
+    const float sg = (float)(__bf16)(x / (1.f + expf(-x)));
+    ov[e] = (__bf16)(sg * (float)uv[e]);
+  }
+  reinterpret_cast<bf16x8*>(out)[i] = ov;
+}
+
 __global__ void __launch_bounds__(256) silu_mul_kernel(const __bf16* __restrict__ g, const __bf16* __restrict__ u,
                                                        __bf16* __restrict__ out, int64_t cols, int64_t stride,
                                                        int64_t n) {
@@ -186,14 +323,21 @@ extern "C" int bfly_add_rms_norm(const void* x, const void* residual, const void
   __bf16* hp = static_cast<__bf16*>(h_out);
   __bf16* np = static_cast<__bf16*>(norm_out);
   dim3 grid((unsigned)rows);
+  const bool vec = aligned16(x) && aligned16(residual) && aligned16(weight) && aligned16(h_out) && aligned16(norm_out);
+#define BFLY_ADD_RMS(P)                                                                                    \
+  if (vec)                                                                                                 \
+    hipLaunchKernelGGL((add_rmsnorm_kernel<P, true>), grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); \
+  else                                                                                                     \
+    hipLaunchKernelGGL((add_rmsnorm_kernel<P, false>), grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps);
   switch (dim / 256) {
-    case 4: hipLaunchKernelGGL(add_rmsnorm_kernel<4>, grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); break;
-    case 8: hipLaunchKernelGGL(add_rmsnorm_kernel<8>, grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); break;
-    case 16: hipLaunchKernelGGL(add_rmsnorm_kernel<16>, grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); break;
-    case 24: hipLaunchKernelGGL(add_rmsnorm_kernel<24>, grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); break;
-    case 32: hipLaunchKernelGGL(add_rmsnorm_kernel<32>, grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); break;
+    case 4: hipLaunchKernelGGL((add_rmsnorm_kernel<4, false>), grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); break;
+    case 8: BFLY_ADD_RMS(8) break;
+    case 16: BFLY_ADD_RMS(16) break;
+    case 24: BFLY_ADD_RMS(24) break;
+    case 32: BFLY_ADD_RMS(32) break;
     default: hipLaunchKernelGGL(add_rmsnorm_any_kernel, grid, dim3(256), 0, stream, xp, yp, wp, hp, np, dim, eps); break;
   }
+#undef BFLY_ADD_RMS
   BFLY_CHECK_LAUNCH("bfly_add_rms_norm");
   return BFLY_OK;
 }
@@ -218,7 +362,20 @@ extern "C" int bfly_qk_norm_rope(const void* q, const void* k, const void* v, in
                *vp = static_cast<const __bf16*>(v), *qw = static_cast<const __bf16*>(q_weight),
                *kw = static_cast<const __bf16*>(k_weight);
   __bf16 *qo = static_cast<__bf16*>(q_out), *ko = static_cast<__bf16*>(k_out), *vo = static_cast<__bf16*>(v_out);
-  if (head_dim == 128)
+  const bool vec = q_row_stride % 8 == 0 && k_row_stride % 8 == 0 && v_row_stride % 8 == 0 && aligned16(q) &&
+                   aligned16(k) && aligned16(v) && aligned16(q_weight) && aligned16(k_weight) && aligned16(cos) &&
+                   aligned16(sin) && aligned16(q_out) && aligned16(k_out) && aligned16(v_out);
+  if (vec) {
+    const int64_t threads = items * (head_dim / 16);
+    BFLY_CHECK_ARG((threads + 255) / 256 <= INT32_MAX, "too many rows");
+    dim3 vgrid((unsigned)((threads + 255) / 256));
+    if (head_dim == 128)
+      hipLaunchKernelGGL(qk_norm_rope_vec_kernel<128>, vgrid, dim3(256), 0, stream, qp, kp, vp, qw, kw, cos, sin, qo,
+                         ko, vo, rows, (int)seq_len, hq, hkv, q_row_stride, k_row_stride, v_row_stride, eps);
+    else
+      hipLaunchKernelGGL(qk_norm_rope_vec_kernel<256>, vgrid, dim3(256), 0, stream, qp, kp, vp, qw, kw, cos, sin, qo,
+                         ko, vo, rows, (int)seq_len, hq, hkv, q_row_stride, k_row_stride, v_row_stride, eps);
+  } else if (head_dim == 128)
     hipLaunchKernelGGL(qk_norm_rope_kernel<128>, grid, dim3(256), 0, stream, qp, kp, vp, qw, kw, cos, sin, qo, ko, vo,
                        rows, (int)seq_len, hq, hkv, q_row_stride, k_row_stride, v_row_stride, eps);
   else
@@ -234,9 +391,16 @@ extern "C" int bfly_silu_mul(const void* gate, const void* up, int64_t rows, int
   BFLY_CHECK_ARG(rows > 0 && cols > 0 && in_row_stride >= cols, "bad shape");
   const int64_t n = rows * cols;
   BFLY_CHECK_ARG((n + 255) / 256 <= INT32_MAX, "bad length");
-  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                     static_cast<const __bf16*>(gate), static_cast<const __bf16*>(up), static_cast<__bf16*>(out), cols,
-                     in_row_stride, n);
+  if (cols % 8 == 0 && in_row_stride % 8 == 0 && aligned16(gate) && aligned16(up) && aligned16(out)) {
+    const int64_t n8 = n / 8;
+    hipLaunchKernelGGL(silu_mul_vec_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<const __bf16*>(gate), static_cast<const __bf16*>(up), static_cast<__bf16*>(out),
+                       cols / 8, in_row_stride / 8, n8);
+  } else {
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<const __bf16*>(gate), static_cast<const __bf16*>(up), static_cast<__bf16*>(out),
+                       cols, in_row_stride, n);
+  }
   BFLY_CHECK_LAUNCH("bfly_silu_mul");
   return BFLY_OK;
 }

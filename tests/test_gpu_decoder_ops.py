@@ -41,6 +41,12 @@ def test_add_rms_norm(dim, rows):
     _close(n.cpu(), norm(x + y))
     _, n0 = add_rms_norm(x.cuda(), None, norm.weight.cuda(), 1e-6)
     _close(n0.cpu(), norm(x))
+    # rows that start 2 bytes off a 16-byte boundary take the element-wise path
+    xo = torch.cat([torch.zeros(rows, 1, dtype=x.dtype), x], 1).cuda()[:, 1:]
+    yo = torch.cat([torch.zeros(rows, 1, dtype=x.dtype), y], 1).cuda()[:, 1:]
+    h2, n2 = add_rms_norm(xo, yo, norm.weight.cuda(), 1e-6)
+    assert torch.equal(h2.cpu(), x + y)
+    _close(n2.cpu(), norm(x + y))
 
 
 @pytest.mark.parametrize("d", [128, 256])
@@ -75,6 +81,20 @@ def test_qk_norm_rope(d):
                  ko2.data_ptr(), vo2.data_ptr(), torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert torch.equal(qo2, qo) and torch.equal(ko2, ko) and torch.equal(vo2, vo)
+    # a fused output whose row stride is not a multiple of 8 takes the element-wise kernel
+    ld3 = ld + 1
+    fused3 = torch.zeros(B, T, ld3, dtype=torch.bfloat16)
+    fused3[..., :ld] = torch.cat([qp, kp, vp], -1)
+    fused3 = fused3.cuda()
+    base3 = fused3.data_ptr()
+    qo3, ko3, vo3 = torch.empty_like(qo), torch.empty_like(ko), torch.empty_like(vo)
+    _native.call("bfly_qk_norm_rope", base3, base3 + hq * d * es, base3 + (hq + hkv) * d * es, ld3, ld3, ld3,
+                 qw.data_ptr(), kw.data_ptr(), cc.data_ptr(), sc.data_ptr(), B, T, hq, hkv, d, 1e-6, qo3.data_ptr(),
+                 ko3.data_ptr(), vo3.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    _close(qo3.cpu(), want_q)
+    _close(ko3.cpu(), want_k)
+    assert torch.equal(vo3.cpu(), want_v)
 
 
 def test_silu_mul():
@@ -92,6 +112,12 @@ def test_silu_mul():
                  torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert torch.equal(out2, out)
+    # columns that are not a multiple of 8: the element-wise kernel, same values
+    out3 = torch.empty(3, 6141, dtype=torch.bfloat16, device="cuda")
+    _native.call("bfly_silu_mul", gc.data_ptr(), uc.data_ptr(), 3, 6141, 6144, out3.data_ptr(),
+                 torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(out3.cpu(), out.cpu()[:, :6141])
 
 
 @pytest.mark.parametrize("rows,n", [(1, 151936), (3, 1000), (2, 7), (1, 8), (2, 4096 * 300 + 5)])

@@ -27,6 +27,9 @@ FLAGS = [
     # Keep hipcc from forming packed fp32 ops: some of their forms have given
     # silently wrong results on the target boxes.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Leading pointer arguments of a kernel arrive preloaded in SGPRs (the decode
+    # step reads its counters through the first one without a kernel-argument load).
+    "-mllvm", "-amdgpu-kernarg-preload-count=2",
     "-Wno-unused-result",
 ]
 

@@ -798,8 +798,14 @@ __device__ __forceinline__ void dec_pool32(const DecodeArgs& a, const DecState32
   }
 }
 
+// `state` and `q` lead the argument list: the hardware preloads leading pointer
+// arguments into SGPRs (the library is built with a kernarg preload count), so
+// the counter read needs no kernel-argument load first.
 template <int D, bool kStep>
-__global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(DecodeArgs a, StepArgs sa) {
+__global__ void __launch_bounds__(256, D <= 128 ? 3 : 1)
+decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) {
+  StepArgs sa = sa_in;
+  sa.state = state;
   using T = __bf16;
   constexpr int VEC = 8;
   constexpr int PIECES = D / VEC;
@@ -831,10 +837,26 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
     }
   }
   const int bh = kStep ? (int)blockIdx.x - kRouteGroups : (int)blockIdx.x;
+  // step mode: this workgroup's counter copy and both route buffers' headers,
+  // requested first (the state pointer needs no argument load); the kv_len
+  // parity picks a route buffer below
+  int64_t cnt[4] = {}, rh[2][4] = {};
+  if constexpr (kStep) {
+    const int64_t* slot = dec_slot(sa.state, bh);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) cnt[w] = slot[w];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) rh[b][w] = slot[kStRoute + kRouteWords * b + w];
+    // keep these loads ahead of the first use of an argument: both round trips
+    // then overlap instead of following each other
+    __builtin_amdgcn_sched_barrier(0);
+  }
   const int bi = (int)a.hkv_div.div((uint32_t)bh);
   const int kvh = bh - bi * a.hkv;
   const int gsz = a.gsz;
-  const T* qhead = reinterpret_cast<const T*>(a.q) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz) * D;
+  const T* qhead = reinterpret_cast<const T*>(q) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz) * D;
 
   // Q^T fragments of heads 16*hg + lq (B operand: d = lg*(D/4) + 8*ks + [0, 8)).
   // Columns past the group read its last head: they are computed and never
@@ -851,18 +873,8 @@ __global__ void __launch_bounds__(256, D <= 128 ? 3 : 1) decode_mfma_kernel(Deco
 
   constexpr int SKN = kDecMaxSum * PIECES;                         // summary K pieces
   constexpr int SK = (SKN + 255) / 256;
-  // step mode: both route buffers' headers of this workgroup's copy, requested
-  // with the counters (scalar); the kv_len parity picks one
-  int64_t rh[2][4] = {};
-  if constexpr (kStep) {
-    const int64_t* slot = dec_slot(sa.state, bh);
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) rh[b][w] = slot[kStRoute + kRouteWords * b + w];
-  }
-
-  const DecState32 st = dec_state32<kStep>(a, sa, bh);
+  const DecState32 st =
+      kStep ? dec_advance32(cnt[kStOffset], cnt[kStTail], cnt[kStCount], cnt[kStSumOff], a, sa) : dec_state32<false>(a, sa, bh);
   if (kStep && st.err) {
     if (tid == 0) sa.state[kStError] = 1;
     return;
@@ -1085,13 +1097,16 @@ static void launch_decode(const DecodeArgs& a, const StepArgs& sa, int d, int64_
       const int64_t mgrid = kStep ? grid + kRouteGroups : grid;   // step mode: plus the route workgroups
       switch (d) {
         case 64:
-          hipLaunchKernelGGL((decode_mfma_kernel<64, kStep>), dim3((unsigned)mgrid), dim3(256), 0, stream, m, sa);
+          hipLaunchKernelGGL((decode_mfma_kernel<64, kStep>), dim3((unsigned)mgrid), dim3(256), 0, stream, sa.state,
+                             m.q, m, sa);
           return;
         case 128:
-          hipLaunchKernelGGL((decode_mfma_kernel<128, kStep>), dim3((unsigned)mgrid), dim3(256), 0, stream, m, sa);
+          hipLaunchKernelGGL((decode_mfma_kernel<128, kStep>), dim3((unsigned)mgrid), dim3(256), 0, stream, sa.state,
+                             m.q, m, sa);
           return;
         default:
-          hipLaunchKernelGGL((decode_mfma_kernel<256, kStep>), dim3((unsigned)mgrid), dim3(256), 0, stream, m, sa);
+          hipLaunchKernelGGL((decode_mfma_kernel<256, kStep>), dim3((unsigned)mgrid), dim3(256), 0, stream, sa.state,
+                             m.q, m, sa);
           return;
       }
     }

@@ -310,11 +310,43 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
   if (a.nbr != nullptr) {
     const int cnt = (b_hi - b_lo + 1) * m.kcap;
     for (int i = tid; i < cnt; i += 256) s_nbr[i] = a.nbr[(int64_t)b_lo * m.kcap + i];
-  } else if (tid <= b_hi - b_lo) {
-    // the table builder's row (bfly_block_neighbors): same function, -1 padding
-    int32_t* row = reinterpret_cast<int32_t*>(s_nbr) + tid * m.kcap;
-    const int len = neighbor_row(b_lo + tid, m.nblocks, a.topo, row, m.kcap);
-    for (int i = len; i < m.kcap; ++i) row[i] = -1;
+  } else {
+    // the table builder's row (neighbor_row, bfly_block_neighbors), one wave per
+    // block and one lane per row entry: lane j holds the j-th candidate of
+    // [b, b-1..b-lwb, partners, sinks], a lane keeps it if no lower lane holds
+    // the same block, and a ballot gives the kept entries their slots (first
+    // occurrences in candidate order, cut at kcap, -1 padding)
+    const bfly_topology_t& t = a.topo;
+    const int lwb = t.local_window_blocks, np = t.partner_count;
+    const int nsk = t.sink_count < m.nblocks ? t.sink_count : m.nblocks;
+    const int kc = min(1 + lwb + np + nsk, 64);   // candidates past lane 63 lie beyond kcap (<= 8 here)
+    const int jp = min(max(lane - 1 - lwb, 0), BFLY_MAX_PARTNERS - 1);
+    int bit = 0;
+#pragma unroll
+    for (int jj = 0; jj < BFLY_MAX_PARTNERS; ++jj) bit = jj == jp ? t.partner_bits[jj] : bit;
+    for (int bb = b_lo + wave; bb <= b_hi; bb += 4) {
+      int cand = -1;
+      if (lane == 0) {
+        cand = bb;
+      } else if (lane <= lwb) {
+        cand = bb - lane;
+      } else if (lane <= lwb + np) {
+        cand = (int)partner_block(bb, bit, m.nblocks, t.rule, t.width);
+      } else if (lane < kc) {
+        cand = lane - 1 - lwb - np;
+      }
+      if (cand < 0 || cand >= m.nblocks) cand = -1;
+      bool keep = cand >= 0;
+      for (int i = 0; i < kc; ++i) {
+        const int ci = __builtin_amdgcn_readlane(cand, i);
+        if (i < lane && ci == cand) keep = false;
+      }
+      const unsigned long long mask = __ballot(keep);
+      const int slot = __popcll(mask & ((1ull << lane) - 1ull));
+      int* row = s_nbr + (bb - b_lo) * m.kcap;
+      if (keep && slot < m.kcap) row[slot] = cand;
+      if (lane >= __popcll(mask) && lane < m.kcap) row[lane] = -1;
+    }
   }
 
   // ---- register staging of one page (K rows and V row pairs) and of the routed summaries

@@ -14,7 +14,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OUT_DIR = PKG / "_lib"
 LIB = OUT_DIR / "libbutterfly_amd.so"
-SOURCES = ["topology.hip", "compress.hip", "attention.hip", "decode.hip", "streams.hip", "decoder_ops.hip"]
+SOURCES = ["topology.hip", "compress.hip", "attention.hip", "decode.hip", "streams.hip", "decoder_ops.hip", "qgemv.hip"]
 ARCH = os.environ.get("BFLY_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

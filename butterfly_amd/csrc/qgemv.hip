@@ -1,0 +1,218 @@
+// One-row projections over 4-bit affine weights on gfx950 (a decode step at
+// batch 1): y = W x, with W stored as two 4-bit codes per byte (low nibble
+// first) and one bf16 (scale, bias) pair per group of G codes along the input
+// dimension, w = code * scale + bias.
+//
+// Reference: the swapped decoder's projections are quantized linear layers with
+// 4-bit affine weights, group 64, bf16 scales and biases
+// (bna/integrations/qwen_mlx.py:1115-1157 builds them as mlx.nn.QuantizedLinear
+// with weight / scales / biases).  The product is taken group by group in the
+// factorised form of w = code * scale + bias:
+//   y_n = sum_g ( scale_ng * sum_{i in g} x_i code_ni + bias_ng * sum_{i in g} x_i ),
+// so the kernel streams half a byte per weight and never expands W in memory.
+// fp32 throughout; y is rounded once to bf16.  The results equal the product
+// with the fp32 weights code * scale + bias up to the fp32 summation order.
+#include "bfly_common.h"
+#include "../../include/butterfly_amd_decoder.h"
+
+namespace bfly {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kQ4PieceCodes = 32;      // codes in one 16-byte piece of a row
+constexpr int kQ4MaxPieces = 4;        // pieces per lane: in_features <= 64 * 4 * 32 = 8192
+constexpr int64_t kQ4MaxWaves = 8192;  // grid cap; the waves stride over the row sets
+
+// v summed over the 64 lanes, the total in every lane: halves and rows of 16 by
+// v_permlane32/16_swap, then rotations by 8 and 4 inside each row of 16 and two
+// quad permutations (DPP); no LDS traffic.
+__device__ __forceinline__ float q4_wave_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));  // row_ror:8
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, false));  // row_ror:4
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+  return v;
+}
+
+// SiLU(gate) * up with the rounding points of the separate steps: the projection
+// outputs are bf16, SiLU is rounded to bf16, then the product (the formula of
+// decoder_ops.hip's silu_mul kernels).
+__device__ __forceinline__ __bf16 q4_silu_times(float g, float u) {
+#pragma clang fp contract(off)
+  const float x = (float)(__bf16)g;
+  const float sg = (float)(__bf16)(x / (1.f + expf(-x)));
+  return (__bf16)(sg * (float)(__bf16)u);
+}
+
+// x: in_features bf16.  w: [rows][pieces] 16-byte pieces.  sb: [rows][groups]
+// words, bf16 scale in the low half and bf16 bias in the high half.
+// One wave per row set at a time (the grid strides over the sets).  A set is R
+// rows, or with kSilu R/2 gate rows and the R/2 up rows up_off further.  Lane l
+// owns the pieces p = l + 64 j (j < NP) of every row; each piece lies in one
+// group, so a lane needs one (scale, bias) word per piece.  The lane's x values
+// stay in registers for all its sets, the odd (high-nibble) ones divided by 16:
+// masking the high nibbles in place gives 16 * code, and (x / 16) * (16 * code)
+// is x * code exactly.
+template <int NP, int R, bool kSilu>
+__global__ void __launch_bounds__(64) q4_gemv_kernel(const __bf16* __restrict__ x, const u32x4* __restrict__ w,
+                                                     const uint32_t* __restrict__ sb, int64_t n_sets,
+                                                     int64_t n_out, int pieces, int groups, int pieces_per_group,
+                                                     int64_t up_off, __bf16* __restrict__ y) {
+  const int lane = threadIdx.x;
+  float xq[NP][kQ4PieceCodes];
+  float xs[NP];
+  int pc[NP], gi[NP];
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const int p = lane + 64 * j;
+    const bool valid = p < pieces;
+    pc[j] = valid ? p : 0;   // a lane past the row reads piece 0 and weighs it by zeros
+    gi[j] = pc[j] / pieces_per_group;
+    const bf16x8* xp = reinterpret_cast<const bf16x8*>(x) + (int64_t)pc[j] * 4;
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bf16x8 v = xp[c];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = valid ? (float)v[e] : 0.f;
+        s += f;
+        xq[j][8 * c + e] = (e & 1) ? f * 0.0625f : f;
+      }
+    }
+    xs[j] = s;
+  }
+
+  constexpr int OUTS = kSilu ? R / 2 : R;   // outputs per set
+  for (int64_t set = blockIdx.x; set < n_sets; set += gridDim.x) {
+    const int64_t o0 = set * OUTS;
+    u32x4 wv[R][NP];
+    uint32_t sv[R][NP];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t o = o0 + (kSilu ? r % OUTS : r);
+      const int64_t row = (o < n_out ? o : 0) + (kSilu && r >= OUTS ? up_off : 0);
+#pragma unroll
+      for (int j = 0; j < NP; ++j) {
+        wv[r][j] = __builtin_nontemporal_load(w + row * pieces + pc[j]);
+        sv[r][j] = sb[row * groups + gi[j]];
+      }
+    }
+    float tot[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < NP; ++j) {
+        const uint32_t dw[4] = {wv[r][j][0], wv[r][j][1], wv[r][j][2], wv[r][j][3]};
+        float lo_sum = 0.f, hi_sum = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          uint32_t lo = dw[t] & 0x0F0F0F0Fu, hi = dw[t] & 0xF0F0F0F0u;
+          // opaque to the combiner, so each byte converts with v_cvt_f32_ubyte{0..3}
+          // instead of a bit-field extract of the unmasked word and a conversion
+          asm volatile("" : "+v"(lo), "+v"(hi));
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            lo_sum += xq[j][8 * t + 2 * b] * (float)((lo >> (8 * b)) & 0xFFu);
+            hi_sum += xq[j][8 * t + 2 * b + 1] * (float)((hi >> (8 * b)) & 0xFFu);
+          }
+        }
+        const float scale = __uint_as_float(sv[r][j] << 16);
+        const float bias = __uint_as_float(sv[r][j] & 0xFFFF0000u);
+        acc += scale * (lo_sum + hi_sum) + bias * xs[j];
+      }
+      tot[r] = q4_wave_sum(acc);
+    }
+    float mine = 0.f, mate = 0.f;
+#pragma unroll
+    for (int r = 0; r < OUTS; ++r) {
+      if (lane == r) {
+        mine = tot[r];
+        if constexpr (kSilu) mate = tot[r + OUTS];
+      }
+    }
+    const int64_t o = o0 + lane;
+    if (lane < OUTS && o < n_out) y[o] = kSilu ? q4_silu_times(mine, mate) : (__bf16)mine;
+  }
+}
+
+template <int NP, int R, bool kSilu>
+void q4_launch(const void* x, const void* w, const void* sb, int64_t n_out, int pieces, int groups, int ppg,
+               int64_t up_off, void* y, hipStream_t stream) {
+  constexpr int OUTS = kSilu ? R / 2 : R;
+  const int64_t n_sets = (n_out + OUTS - 1) / OUTS;
+  const int64_t iters = (n_sets + kQ4MaxWaves - 1) / kQ4MaxWaves;
+  const int64_t grid = (n_sets + iters - 1) / iters;
+  hipLaunchKernelGGL((q4_gemv_kernel<NP, R, kSilu>), dim3((unsigned)grid), dim3(64), 0, stream,
+                     static_cast<const __bf16*>(x), static_cast<const u32x4*>(w), static_cast<const uint32_t*>(sb),
+                     n_sets, n_out, pieces, groups, ppg, up_off, static_cast<__bf16*>(y));
+}
+
+// Rows per set: four when the sets still cover the chip twice over, else two
+// (small projections want more waves; two rows keep two pieces in flight).
+template <bool kSilu>
+int q4_dispatch(const void* x, const void* w, const void* sb, int64_t n_out, int64_t in_features, int group,
+                int64_t up_off, void* y, hipStream_t stream) {
+  const int pieces = (int)(in_features / kQ4PieceCodes);
+  const int groups = (int)(in_features / group);
+  const int ppg = group / kQ4PieceCodes;
+  const int np = (pieces + 63) / 64;
+  const int64_t sets4 = (n_out + (kSilu ? 1 : 3)) / (kSilu ? 2 : 4);
+  const bool four = np == 1 && sets4 >= 2048;
+  switch (np) {
+    case 1:
+      if (four)
+        q4_launch<1, 4, kSilu>(x, w, sb, n_out, pieces, groups, ppg, up_off, y, stream);
+      else
+        q4_launch<1, 2, kSilu>(x, w, sb, n_out, pieces, groups, ppg, up_off, y, stream);
+      break;
+    case 2: q4_launch<2, 2, kSilu>(x, w, sb, n_out, pieces, groups, ppg, up_off, y, stream); break;
+    case 3: q4_launch<3, 2, kSilu>(x, w, sb, n_out, pieces, groups, ppg, up_off, y, stream); break;
+    default: q4_launch<4, 2, kSilu>(x, w, sb, n_out, pieces, groups, ppg, up_off, y, stream); break;
+  }
+  return BFLY_OK;
+}
+
+int q4_check(const void* x, const void* packed, const void* scale_bias, int64_t out_features, int64_t in_features,
+             int group, const void* out) {
+  BFLY_CHECK_ARG(x && packed && scale_bias && out, "null pointer");
+  BFLY_CHECK_ARG(group > 0 && group % kQ4PieceCodes == 0, "group=%d must be a positive multiple of 32", group);
+  BFLY_CHECK_ARG(in_features > 0 && in_features % group == 0, "in_features=%lld must be a multiple of group=%d",
+                 (long long)in_features, group);
+  BFLY_CHECK_ARG(in_features <= 64LL * kQ4MaxPieces * kQ4PieceCodes, "in_features=%lld above the supported 8192",
+                 (long long)in_features);
+  BFLY_CHECK_ARG(out_features > 0, "bad out_features=%lld", (long long)out_features);
+  BFLY_CHECK_ARG(aligned16(x) && aligned16(packed), "x and the packed codes must be 16-byte aligned");
+  BFLY_CHECK_ARG(((uintptr_t)scale_bias & 3) == 0 && ((uintptr_t)out & 1) == 0, "misaligned scale_bias or out");
+  return BFLY_OK;
+}
+
+}  // namespace bfly
+
+using namespace bfly;
+
+extern "C" int bfly_q4_gemv(const void* x, const void* packed, const void* scale_bias, int64_t out_features,
+                            int64_t in_features, int group, void* out, hipStream_t stream) {
+  const int rc = q4_check(x, packed, scale_bias, out_features, in_features, group, out);
+  if (rc) return rc;
+  q4_dispatch<false>(x, packed, scale_bias, out_features, in_features, group, 0, out, stream);
+  BFLY_CHECK_LAUNCH("bfly_q4_gemv");
+  return BFLY_OK;
+}
+
+extern "C" int bfly_q4_gemv_silu(const void* x, const void* packed, const void* scale_bias, int64_t out_features,
+                                 int64_t in_features, int group, int64_t up_row_offset, void* out,
+                                 hipStream_t stream) {
+  const int rc = q4_check(x, packed, scale_bias, out_features, in_features, group, out);
+  if (rc) return rc;
+  BFLY_CHECK_ARG(up_row_offset >= out_features, "up_row_offset=%lld overlaps the gate rows",
+                 (long long)up_row_offset);
+  q4_dispatch<true>(x, packed, scale_bias, out_features, in_features, group, up_row_offset, out, stream);
+  BFLY_CHECK_LAUNCH("bfly_q4_gemv_silu");
+  return BFLY_OK;
+}

@@ -5,11 +5,14 @@ transformers Qwen models, bna/integrations/qwen_mlx.py:1822-1846,
 qwen_torch.py:1652-1700); none can be downloaded here, so this module
 provides the same structure with random weights: ``model.layers[i].self_attn``
 with q/k/v/o projections, per-head q/k RMSNorm and RoPE (qwen_mlx.py:260-357),
-SwiGLU MLP, RMSNorm, tied embeddings.  Linear weights are stored 4-bit affine
-(group 64 along the input dimension, bf16 scale and bias per group:
-w = q * scale + bias, q in [0, 15]) and dequantized once to bf16; the
-non-attention GEMMs run through PyTorch-ROCm (q/k/v and gate/up as one GEMM
-each, a single activation row as a GEMV).  On the GPU (bf16) the row-wise
+SwiGLU MLP, RMSNorm, tied embeddings.  Linear weights and the tied embedding
+are stored 4-bit affine (group 64 along the input dimension, bf16 scale and
+bias per group: w = q * scale + bias, q in [0, 15]).  A single activation row
+on the GPU (a decode step, the prefill's last-position logits) is multiplied
+straight from the 4-bit codes by ``bfly_q4_gemv`` (``bfly_q4_gemv_silu`` for
+the gate|up projection with SiLU * up); larger products run through
+PyTorch-ROCm's GEMMs over the weights dequantized once to bf16 (q/k/v and
+gate/up as one GEMM each).  On the GPU (bf16) the row-wise
 and elementwise steps -- residual add + RMSNorm, q/k norm + RoPE + the move to
 heads-first, SiLU * up -- run as single HIP launches
 (include/butterfly_amd_decoder.h) with the rounding points of the PyTorch
@@ -80,21 +83,97 @@ def dequantize_affine(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Ten
     return w.view(out_f, -1).to(torch.bfloat16)
 
 
-class QuantLinear(nn.Module):
-    """Linear layer with 4-bit affine weights, dequantized once to bf16 for the GEMM."""
+_Q4_TENSORS = ("packed", "scale", "bias", "scale_bias", "weight")
 
-    def __init__(self, in_features: int, out_features: int, *, generator: torch.Generator, device, group: int = 64):
+
+class QuantLinear(nn.Module):
+    """Linear layer with 4-bit affine weights.
+
+    Buffers: ``packed`` (two codes per byte, low nibble first), ``scale`` and ``bias``
+    (bf16 per group), ``scale_bias`` (the same pairs interleaved, [out, in/group, 2], the
+    layout ``bfly_q4_gemv`` reads) and ``weight`` (dequantized once to bf16, for the
+    multi-row GEMMs and for CPU copies of the model)."""
+
+    def __init__(self, in_features: int, out_features: int, *, generator: Optional[torch.Generator] = None,
+                 device=None, group: int = 64, weight: Optional[torch.Tensor] = None):
         super().__init__()
-        w = torch.randn(out_features, in_features, generator=generator, device=device) / math.sqrt(in_features)
-        packed, scale, bias = quantize_affine(w, group)
+        if weight is None:
+            weight = torch.randn(out_features, in_features, generator=generator, device=device) / math.sqrt(in_features)
+        self.group = group
+        self._set(*quantize_affine(weight, group))
+
+    def _set(self, packed, scale, bias):
         self.register_buffer("packed", packed)
         self.register_buffer("scale", scale)
         self.register_buffer("bias", bias)
-        self.group = group
-        self.register_buffer("weight", dequantize_affine(packed, scale, bias, group))
+        self.register_buffer("scale_bias", torch.stack([scale, bias], -1).contiguous())
+        self.register_buffer("weight", dequantize_affine(packed, scale, bias, self.group))
+
+    @property
+    def in_features(self) -> int:
+        return int(self.packed.shape[1]) * 2
+
+    @property
+    def out_features(self) -> int:
+        return int(self.packed.shape[0])
+
+    @classmethod
+    def fuse_rows(cls, *parts: "QuantLinear") -> "QuantLinear":
+        """One layer whose output rows are the given layers' rows in order (q|k|v, gate|up):
+        each part's tensors become views of their row range, so memory is not doubled."""
+        fused = cls.__new__(cls)
+        nn.Module.__init__(fused)
+        fused.group = parts[0].group
+        for name in _Q4_TENSORS:
+            fused.register_buffer(name, torch.cat([getattr(m, name) for m in parts]))
+        row = 0
+        for m in parts:
+            n = m.out_features
+            for name in _Q4_TENSORS:
+                setattr(m, name, getattr(fused, name)[row:row + n])
+            row += n
+        return fused
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if _one_row(x):
+            return q4_gemv(x, self)
         return _linear(x, self.weight)
+
+
+def _one_row(x: torch.Tensor) -> bool:
+    """A single bf16 activation row on the GPU: the product runs from the 4-bit codes."""
+    return x.is_cuda and x.dtype == torch.bfloat16 and x.numel() == x.shape[-1]
+
+
+def _row16(x: torch.Tensor) -> torch.Tensor:
+    x = x.reshape(-1)
+    if not x.is_contiguous() or x.data_ptr() % 16:
+        x = x.clone()
+    return x
+
+
+def q4_gemv(x: torch.Tensor, layer: QuantLinear) -> torch.Tensor:
+    """``layer(x)`` for one bf16 row ``x`` [..., in] through ``bfly_q4_gemv`` (reads the
+    4-bit codes and the (scale, bias) pairs; fp32 accumulation, bf16 out)."""
+    xr = _row16(x)
+    out = torch.empty(*x.shape[:-1], layer.out_features, dtype=torch.bfloat16, device=x.device)
+    with on(x.device):
+        _native.call("bfly_q4_gemv", xr.data_ptr(), layer.packed.data_ptr(), layer.scale_bias.data_ptr(),
+                     layer.out_features, layer.in_features, layer.group, out.data_ptr(), stream_of(x))
+    return out
+
+
+def q4_gemv_silu(x: torch.Tensor, gate_up: QuantLinear) -> torch.Tensor:
+    """``SiLU(gate(x)) * up(x)`` for one bf16 row through ``bfly_q4_gemv_silu``; ``gate_up``
+    holds the gate rows, then as many up rows.  Same rounding points as the two projections'
+    bf16 outputs followed by ``bfly_silu_mul``."""
+    xr = _row16(x)
+    f = gate_up.out_features // 2
+    out = torch.empty(*x.shape[:-1], f, dtype=torch.bfloat16, device=x.device)
+    with on(x.device):
+        _native.call("bfly_q4_gemv_silu", xr.data_ptr(), gate_up.packed.data_ptr(), gate_up.scale_bias.data_ptr(),
+                     f, gate_up.in_features, gate_up.group, f, out.data_ptr(), stream_of(x))
+    return out
 
 
 def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
@@ -105,18 +184,6 @@ def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     if x.is_cuda and x.numel() == x.shape[-1]:
         return torch.matmul(w, x.reshape(-1, 1)).view(*x.shape[:-1], w.shape[0])
     return F.linear(x, w)
-
-
-def _fuse_rows(*linears: QuantLinear) -> torch.Tensor:
-    """One weight matrix holding the given layers' (dequantized) weights as consecutive row
-    ranges; each layer's ``weight`` becomes a view of its range, so the memory is not doubled."""
-    fused = torch.cat([m.weight for m in linears])
-    row = 0
-    for m in linears:
-        n = m.weight.shape[0]
-        m.weight = fused[row:row + n]
-        row += n
-    return fused
 
 
 def _hip(x: torch.Tensor) -> bool:
@@ -196,9 +263,9 @@ class Attention(nn.Module):
         self.o_proj = QuantLinear(cfg.num_heads * d, h, generator=generator, device=device, group=cfg.quant_group)
         self.q_norm = RMSNorm(d, cfg.rms_eps, device)
         self.k_norm = RMSNorm(d, cfg.rms_eps, device)
-        # q, k and v weights as row ranges of one [Hq*d + 2*Hkv*d, hidden] matrix: one GEMM per
+        # q, k and v weights as row ranges of one [Hq*d + 2*Hkv*d, hidden] layer: one product per
         # projection on the GPU path, whose kernels read q, k and v as column ranges of its output.
-        self.register_buffer("qkv_weight", _fuse_rows(self.q_proj, self.k_proj, self.v_proj))
+        self.qkv = QuantLinear.fuse_rows(self.q_proj, self.k_proj, self.v_proj)
 
     def project(self, x: torch.Tensor, positions: torch.Tensor, rope=None):
         """x [B, T, hidden] -> q [B, Hq, T, d], k/v [B, Hkv, T, d] (normed, RoPE applied).
@@ -207,7 +274,7 @@ class Attention(nn.Module):
         b, t, _ = x.shape
         c = self.cfg
         if _hip(x) and c.head_dim in (128, 256):
-            qkv = _linear(x, self.qkv_weight)
+            qkv = self.qkv(x)
             nq, nkv = c.num_heads * c.head_dim, c.num_kv_heads * c.head_dim
             base, ld, es = qkv.data_ptr(), qkv.shape[-1], qkv.element_size()
             cos, sin = rope if rope is not None else rope_cos_sin(positions, c.head_dim, c.rope_theta)
@@ -281,11 +348,13 @@ class MLP(nn.Module):
         self.gate_proj = QuantLinear(h, f, generator=generator, device=device, group=cfg.quant_group)
         self.up_proj = QuantLinear(h, f, generator=generator, device=device, group=cfg.quant_group)
         self.down_proj = QuantLinear(f, h, generator=generator, device=device, group=cfg.quant_group)
-        self.register_buffer("gate_up_weight", _fuse_rows(self.gate_proj, self.up_proj))
+        self.gate_up = QuantLinear.fuse_rows(self.gate_proj, self.up_proj)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if _one_row(x):
+            return self.down_proj(q4_gemv_silu(x, self.gate_up))
         if _hip(x):
-            gu = _linear(x, self.gate_up_weight)           # [..., 2f]: gate columns, then up columns
+            gu = self.gate_up(x)                           # [..., 2f]: gate columns, then up columns
             f = gu.shape[-1] // 2
             s = gu.new_empty(*gu.shape[:-1], f)
             with on(x.device):
@@ -331,15 +400,19 @@ class Decoder(nn.Module):
         device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         g = torch.Generator(device=device).manual_seed(seed)
         self.cfg = cfg
-        self.embed_tokens = nn.Parameter(
-            (torch.randn(cfg.vocab_size, cfg.hidden_size, generator=g, device=device) * 0.02).to(torch.bfloat16),
-            requires_grad=False)
+        # tied embedding, 4-bit like every other weight: the lookup reads the dequantized
+        # table, the lm_head the same layer (from the codes for one row on the GPU)
+        self.lm_head = QuantLinear(cfg.hidden_size, cfg.vocab_size, group=cfg.quant_group,
+                                   weight=torch.randn(cfg.vocab_size, cfg.hidden_size, generator=g, device=device) * 0.02)
+        self.embed_tokens = nn.Parameter(self.lm_head.weight, requires_grad=False)
         self.layers = nn.ModuleList(DecoderLayer(cfg, generator=g, device=device) for _ in range(cfg.num_layers))
         self.norm = RMSNorm(cfg.hidden_size, cfg.rms_eps, device)
 
     def _logits(self, h: torch.Tensor) -> torch.Tensor:
-        """Tied lm_head for a few rows: embed @ h^T, which PyTorch-ROCm runs as a
-        GEMV at twice the rate of the F.linear form for one row."""
+        """Tied lm_head for a few rows [B, hidden]: one row on the GPU from the 4-bit codes,
+        else embed @ h^T over the dequantized table."""
+        if _one_row(h):
+            return q4_gemv(h, self.lm_head)
         return torch.matmul(self.embed_tokens, h.t()).t()
 
     def _rope(self, start: int, t: int, device):

@@ -67,6 +67,31 @@ int bfly_silu_mul(const void* gate, const void* up, int64_t rows, int64_t cols, 
 int bfly_argmax_rows(const void* x, int64_t rows, int64_t n, int64_t row_stride, int64_t col_stride,
                      void* workspace, int64_t workspace_bytes, void* out, hipStream_t stream);
 
+/*
+ * Device: out[n] (bf16) = sum_i x_i * (code_ni * scale_ng + bias_ng) for one row x
+ * (in_features bf16, 16-byte aligned): a quantized linear layer's product at
+ * batch 1, read from the 4-bit codes.  packed: [out_features][in_features / 2]
+ * bytes, two codes per byte, low nibble first (16-byte aligned).  scale_bias:
+ * [out_features][in_features / group] pairs of bf16 (scale, bias), 4-byte
+ * aligned.  group a multiple of 32; in_features a multiple of group and at most
+ * 8192.  fp32 accumulation.  Replaces the 4-bit affine quantized matmul of the
+ * reference's quantized projections (mlx.nn.QuantizedLinear as used at
+ * bna/integrations/qwen_mlx.py:1115-1157).
+ */
+int bfly_q4_gemv(const void* x, const void* packed, const void* scale_bias, int64_t out_features,
+                 int64_t in_features, int group, void* out, hipStream_t stream);
+
+/*
+ * Device: the SwiGLU MLP's first half at batch 1 in one launch: out[n] (bf16) =
+ * SiLU(g_n) * u_n with g_n the bfly_q4_gemv product of weight row n and u_n that
+ * of row n + up_row_offset (a fused gate|up weight: up_row_offset =
+ * out_features), each rounded to bf16 first, as bfly_silu_mul over the two
+ * projections' outputs computes it.  Same weight layout and limits as
+ * bfly_q4_gemv.  No counterpart in the reference's own code.
+ */
+int bfly_q4_gemv_silu(const void* x, const void* packed, const void* scale_bias, int64_t out_features,
+                      int64_t in_features, int group, int64_t up_row_offset, void* out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

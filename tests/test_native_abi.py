@@ -68,6 +68,26 @@ def test_errors_are_reported():
     assert rc == _native.ERR_INVALID and b"kcap" in lib.bfly_last_error()
 
 
+@pytest.mark.parametrize("args,msg", [
+    ((256, 1024, 256, 8, 2048, 48, 512, None), b"group"),             # group not a multiple of 32
+    ((256, 1024, 256, 8, 8256, 64, 512, None), b"8192"),              # in_features above the limit
+    ((256, 1024, 256, 8, 2000, 64, 512, None), b"multiple of group"),
+    ((264, 1024, 256, 8, 2048, 64, 512, None), b"16-byte"),           # x not 16-byte aligned
+    ((256, 1024, 258, 8, 2048, 64, 512, None), b"scale_bias"),
+    ((256, 1024, 256, 0, 2048, 64, 512, None), b"out_features"),
+])
+def test_q4_gemv_validates_before_launch(args, msg):
+    """Fake, never dereferenced addresses: every case fails its checks before a launch."""
+    lib = _native.lib()
+    assert lib.bfly_q4_gemv(*args) == _native.ERR_INVALID
+    assert msg in lib.bfly_last_error()
+    x, w, sb, n, k, g, out, st = args
+    assert lib.bfly_q4_gemv_silu(x, w, sb, n, k, g, n, out, st) == _native.ERR_INVALID
+    if n > 0:   # up rows overlapping the gate rows
+        assert lib.bfly_q4_gemv_silu(256, 1024, 256, 8, 2048, 64, 4, 512, None) == _native.ERR_INVALID
+        assert b"up_row_offset" in lib.bfly_last_error()
+
+
 @pytest.mark.parametrize("rule", list(tp.RULES))
 def test_topology_init_matches_oracle(rule):
     lib = _native.lib()

@@ -57,51 +57,75 @@ __device__ __forceinline__ __bf16 q4_silu_times(float g, float u) {
 // stay in registers for all its sets, the odd (high-nibble) ones divided by 16:
 // masking the high nibbles in place gives 16 * code, and (x / 16) * (16 * code)
 // is x * code exactly.
+struct Q4Args {
+  const __bf16* x;
+  const u32x4* w;
+  const uint32_t* sb;
+  __bf16* y;
+  int64_t n_sets, n_out, up_off;
+  int pieces, groups, pieces_per_group;
+};
+
 template <int NP, int R, bool kSilu>
-__global__ void __launch_bounds__(64) q4_gemv_kernel(const __bf16* __restrict__ x, const u32x4* __restrict__ w,
-                                                     const uint32_t* __restrict__ sb, int64_t n_sets,
-                                                     int64_t n_out, int pieces, int groups, int pieces_per_group,
-                                                     int64_t up_off, __bf16* __restrict__ y) {
+__global__ void __launch_bounds__(64) q4_gemv_kernel(Q4Args a) {
   const int lane = threadIdx.x;
+  const int pieces = a.pieces, groups = a.groups;
+  const u32x4* __restrict__ w = a.w;
+  const uint32_t* __restrict__ sb = a.sb;
+  constexpr int OUTS = kSilu ? R / 2 : R;   // outputs per set
+  const int64_t n_out = a.n_out;
   float xq[NP][kQ4PieceCodes];
   float xs[NP];
   int pc[NP], gi[NP];
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
     const int p = lane + 64 * j;
-    const bool valid = p < pieces;
-    pc[j] = valid ? p : 0;   // a lane past the row reads piece 0 and weighs it by zeros
-    gi[j] = pc[j] / pieces_per_group;
-    const bf16x8* xp = reinterpret_cast<const bf16x8*>(x) + (int64_t)pc[j] * 4;
-    float s = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const bf16x8 v = xp[c];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float f = valid ? (float)v[e] : 0.f;
-        s += f;
-        xq[j][8 * c + e] = (e & 1) ? f * 0.0625f : f;
-      }
-    }
-    xs[j] = s;
+    pc[j] = p < pieces ? p : 0;   // a lane past the row reads piece 0 and weighs it by zeros
+    gi[j] = pc[j] / a.pieces_per_group;
   }
-
-  constexpr int OUTS = kSilu ? R / 2 : R;   // outputs per set
-  for (int64_t set = blockIdx.x; set < n_sets; set += gridDim.x) {
+  // The weights of a set are requested one set ahead: the first set's before the
+  // row is formed, the next set's before the current one is reduced.
+  u32x4 wv[R][NP];
+  uint32_t sv[R][NP];
+  auto load_set = [&](int64_t set) {
     const int64_t o0 = set * OUTS;
-    u32x4 wv[R][NP];
-    uint32_t sv[R][NP];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t o = o0 + (kSilu ? r % OUTS : r);
-      const int64_t row = (o < n_out ? o : 0) + (kSilu && r >= OUTS ? up_off : 0);
+      const int64_t row = (o < n_out ? o : 0) + (kSilu && r >= OUTS ? a.up_off : 0);
 #pragma unroll
       for (int j = 0; j < NP; ++j) {
         wv[r][j] = __builtin_nontemporal_load(w + row * pieces + pc[j]);
         sv[r][j] = sb[row * groups + gi[j]];
       }
     }
+  };
+  load_set(blockIdx.x);   // the grid never exceeds the number of sets
+
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const bool valid = lane + 64 * j < pieces;
+    const bf16x8* xp = reinterpret_cast<const bf16x8*>(a.x) + (int64_t)pc[j] * 4;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bf16x8 v = xp[c];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xq[j][8 * c + e] = valid ? (float)v[e] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kQ4PieceCodes; ++i) {
+      s += xq[j][i];
+      if (i & 1) xq[j][i] *= 0.0625f;
+    }
+    xs[j] = s;
+  }
+
+  for (int64_t set = blockIdx.x; set < a.n_sets; set += gridDim.x) {
+    const int64_t o0 = set * OUTS;
     float tot[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -126,8 +150,11 @@ __global__ void __launch_bounds__(64) q4_gemv_kernel(const __bf16* __restrict__ 
         const float bias = __uint_as_float(sv[r][j] & 0xFFFF0000u);
         acc += scale * (lo_sum + hi_sum) + bias * xs[j];
       }
-      tot[r] = q4_wave_sum(acc);
+      tot[r] = acc;
     }
+    if (set + gridDim.x < a.n_sets) load_set(set + gridDim.x);
+#pragma unroll
+    for (int r = 0; r < R; ++r) tot[r] = q4_wave_sum(tot[r]);
     float mine = 0.f, mate = 0.f;
 #pragma unroll
     for (int r = 0; r < OUTS; ++r) {
@@ -137,45 +164,50 @@ __global__ void __launch_bounds__(64) q4_gemv_kernel(const __bf16* __restrict__ 
       }
     }
     const int64_t o = o0 + lane;
-    if (lane < OUTS && o < n_out) y[o] = kSilu ? q4_silu_times(mine, mate) : (__bf16)mine;
+    if (lane < OUTS && o < n_out) a.y[o] = kSilu ? q4_silu_times(mine, mate) : (__bf16)mine;
   }
 }
 
 template <int NP, int R, bool kSilu>
-void q4_launch(const void* x, const void* w, const void* sb, int64_t n_out, int pieces, int groups, int ppg,
-               int64_t up_off, void* y, hipStream_t stream) {
+void q4_launch(Q4Args a, hipStream_t stream) {
   constexpr int OUTS = kSilu ? R / 2 : R;
-  const int64_t n_sets = (n_out + OUTS - 1) / OUTS;
-  const int64_t iters = (n_sets + kQ4MaxWaves - 1) / kQ4MaxWaves;
-  const int64_t grid = (n_sets + iters - 1) / iters;
-  hipLaunchKernelGGL((q4_gemv_kernel<NP, R, kSilu>), dim3((unsigned)grid), dim3(64), 0, stream,
-                     static_cast<const __bf16*>(x), static_cast<const u32x4*>(w), static_cast<const uint32_t*>(sb),
-                     n_sets, n_out, pieces, groups, ppg, up_off, static_cast<__bf16*>(y));
+  a.n_sets = (a.n_out + OUTS - 1) / OUTS;
+  const int64_t iters = (a.n_sets + kQ4MaxWaves - 1) / kQ4MaxWaves;
+  const int64_t grid = (a.n_sets + iters - 1) / iters;
+  hipLaunchKernelGGL((q4_gemv_kernel<NP, R, kSilu>), dim3((unsigned)grid), dim3(64), 0, stream, a);
 }
 
 // Rows per set: four when the sets still cover the chip twice over, else two
 // (small projections want more waves; two rows keep two pieces in flight).
 template <bool kSilu>
-int q4_dispatch(const void* x, const void* w, const void* sb, int64_t n_out, int64_t in_features, int group,
-                int64_t up_off, void* y, hipStream_t stream) {
-  const int pieces = (int)(in_features / kQ4PieceCodes);
-  const int groups = (int)(in_features / group);
-  const int ppg = group / kQ4PieceCodes;
-  const int np = (pieces + 63) / 64;
-  const int64_t sets4 = (n_out + (kSilu ? 1 : 3)) / (kSilu ? 2 : 4);
+void q4_dispatch(Q4Args a, int64_t in_features, int group, hipStream_t stream) {
+  a.pieces = (int)(in_features / kQ4PieceCodes);
+  a.groups = (int)(in_features / group);
+  a.pieces_per_group = group / kQ4PieceCodes;
+  const int np = (a.pieces + 63) / 64;
+  const int64_t sets4 = (a.n_out + (kSilu ? 1 : 3)) / (kSilu ? 2 : 4);
   const bool four = np == 1 && sets4 >= 2048;
   switch (np) {
     case 1:
       if (four)
-        q4_launch<1, 4, kSilu>(x, w, sb, n_out, pieces, groups, ppg, up_off, y, stream);
+        q4_launch<1, 4, kSilu>(a, stream);
       else
-        q4_launch<1, 2, kSilu>(x, w, sb, n_out, pieces, groups, ppg, up_off, y, stream);
+        q4_launch<1, 2, kSilu>(a, stream);
       break;
-    case 2: q4_launch<2, 2, kSilu>(x, w, sb, n_out, pieces, groups, ppg, up_off, y, stream); break;
-    case 3: q4_launch<3, 2, kSilu>(x, w, sb, n_out, pieces, groups, ppg, up_off, y, stream); break;
-    default: q4_launch<4, 2, kSilu>(x, w, sb, n_out, pieces, groups, ppg, up_off, y, stream); break;
+    case 2: q4_launch<2, 2, kSilu>(a, stream); break;
+    case 3: q4_launch<3, 2, kSilu>(a, stream); break;
+    default: q4_launch<4, 2, kSilu>(a, stream); break;
   }
-  return BFLY_OK;
+}
+
+Q4Args q4_args(const void* x, const void* packed, const void* scale_bias, int64_t out_features, void* out) {
+  Q4Args a{};
+  a.x = static_cast<const __bf16*>(x);
+  a.w = static_cast<const u32x4*>(packed);
+  a.sb = static_cast<const uint32_t*>(scale_bias);
+  a.y = static_cast<__bf16*>(out);
+  a.n_out = out_features;
+  return a;
 }
 
 int q4_check(const void* x, const void* packed, const void* scale_bias, int64_t out_features, int64_t in_features,
@@ -200,7 +232,7 @@ extern "C" int bfly_q4_gemv(const void* x, const void* packed, const void* scale
                             int64_t in_features, int group, void* out, hipStream_t stream) {
   const int rc = q4_check(x, packed, scale_bias, out_features, in_features, group, out);
   if (rc) return rc;
-  q4_dispatch<false>(x, packed, scale_bias, out_features, in_features, group, 0, out, stream);
+  q4_dispatch<false>(q4_args(x, packed, scale_bias, out_features, out), in_features, group, stream);
   BFLY_CHECK_LAUNCH("bfly_q4_gemv");
   return BFLY_OK;
 }
@@ -212,7 +244,9 @@ extern "C" int bfly_q4_gemv_silu(const void* x, const void* packed, const void* 
   if (rc) return rc;
   BFLY_CHECK_ARG(up_row_offset >= out_features, "up_row_offset=%lld overlaps the gate rows",
                  (long long)up_row_offset);
-  q4_dispatch<true>(x, packed, scale_bias, out_features, in_features, group, up_row_offset, out, stream);
+  Q4Args a = q4_args(x, packed, scale_bias, out_features, out);
+  a.up_off = up_row_offset;
+  q4_dispatch<true>(a, in_features, group, stream);
   BFLY_CHECK_LAUNCH("bfly_q4_gemv_silu");
   return BFLY_OK;
 }

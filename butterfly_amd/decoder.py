@@ -274,26 +274,32 @@ class Attention(nn.Module):
         b, t, _ = x.shape
         c = self.cfg
         if _hip(x) and c.head_dim in (128, 256):
-            qkv = self.qkv(x)
-            nq, nkv = c.num_heads * c.head_dim, c.num_kv_heads * c.head_dim
-            base, ld, es = qkv.data_ptr(), qkv.shape[-1], qkv.element_size()
-            cos, sin = rope if rope is not None else rope_cos_sin(positions, c.head_dim, c.rope_theta)
-            cos, sin = cos.float().contiguous(), sin.float().contiguous()
-            qo = torch.empty(b, c.num_heads, t, c.head_dim, dtype=x.dtype, device=x.device)
-            ko = torch.empty(b, c.num_kv_heads, t, c.head_dim, dtype=x.dtype, device=x.device)
-            vo = torch.empty_like(ko)
-            with on(x.device):
-                _native.call("bfly_qk_norm_rope", base, base + nq * es, base + (nq + nkv) * es, ld, ld, ld,
-                             self.q_norm.weight.data_ptr(), self.k_norm.weight.data_ptr(), cos.data_ptr(),
-                             sin.data_ptr(), b, t, c.num_heads, c.num_kv_heads, c.head_dim, float(self.q_norm.eps),
-                             qo.data_ptr(), ko.data_ptr(), vo.data_ptr(), stream_of(x))
-            return qo, ko, vo
+            return self.heads(self.qkv(x), positions, rope)
         q = self.q_proj(x).view(b, t, c.num_heads, c.head_dim).transpose(1, 2)
         k = self.k_proj(x).view(b, t, c.num_kv_heads, c.head_dim).transpose(1, 2)
         v = self.v_proj(x).view(b, t, c.num_kv_heads, c.head_dim).transpose(1, 2)
         q, k = self.q_norm(q), self.k_norm(k)
         cos, sin = rope if rope is not None else rope_cos_sin(positions, c.head_dim, c.rope_theta)
         return apply_rope(q, cos, sin).contiguous(), apply_rope(k, cos, sin).contiguous(), v.contiguous()
+
+    def heads(self, qkv: torch.Tensor, positions: torch.Tensor, rope=None):
+        """The fused projection output [B, T, (Hq + 2 Hkv) d] (bf16, GPU, d in {128, 256}) ->
+        q [B, Hq, T, d], k/v [B, Hkv, T, d]: q/k RMSNorm and RoPE in one ``bfly_qk_norm_rope``."""
+        b, t, _ = qkv.shape
+        c = self.cfg
+        nq, nkv = c.num_heads * c.head_dim, c.num_kv_heads * c.head_dim
+        base, ld, es = qkv.data_ptr(), qkv.shape[-1], qkv.element_size()
+        cos, sin = rope if rope is not None else rope_cos_sin(positions, c.head_dim, c.rope_theta)
+        cos, sin = cos.float().contiguous(), sin.float().contiguous()
+        qo = torch.empty(b, c.num_heads, t, c.head_dim, dtype=qkv.dtype, device=qkv.device)
+        ko = torch.empty(b, c.num_kv_heads, t, c.head_dim, dtype=qkv.dtype, device=qkv.device)
+        vo = torch.empty_like(ko)
+        with on(qkv.device):
+            _native.call("bfly_qk_norm_rope", base, base + nq * es, base + (nq + nkv) * es, ld, ld, ld,
+                         self.q_norm.weight.data_ptr(), self.k_norm.weight.data_ptr(), cos.data_ptr(),
+                         sin.data_ptr(), b, t, c.num_heads, c.num_kv_heads, c.head_dim, float(self.q_norm.eps),
+                         qo.data_ptr(), ko.data_ptr(), vo.data_ptr(), stream_of(qkv))
+        return qo, ko, vo
 
     def output(self, o: torch.Tensor) -> torch.Tensor:
         b, _, t, _ = o.shape

@@ -31,23 +31,27 @@ def test_quantize_affine_round_trip_and_packing():
 
 SMALL = DecoderConfig(vocab_size=2048, hidden_size=512, num_layers=4, num_heads=8, num_kv_heads=2, head_dim=64,
                       intermediate_size=1024)
+# head_dim 128: decode steps take the fused one-row path (add + RMSNorm inside the projections)
+SMALL128 = DecoderConfig(vocab_size=2048, hidden_size=512, num_layers=4, num_heads=4, num_kv_heads=2, head_dim=128,
+                         intermediate_size=1024)
 
 
 @pytest.mark.gpu
-def test_swapped_decoder_tracks_cpu_reference_teacher_forced():
+@pytest.mark.parametrize("cfg_", [SMALL, SMALL128], ids=["d64", "d128"])
+def test_swapped_decoder_tracks_cpu_reference_teacher_forced(cfg_):
     """Same tokens into both paths (the CPU reference's greedy continuation): the
     HIP path's logits stay within bf16 noise of the reference's at every step, and
     the argmax agrees wherever the reference's top-2 margin exceeds that noise."""
-    model = Decoder(SMALL, seed=7)
+    model = Decoder(cfg_, seed=7)
     cpu_model = copy.deepcopy(model).to("cpu")
     cfg = bf.QwenButterflyConfig()
     assert bf.swap_qwen_attention_with_butterfly(model, cfg=cfg) == [0, 1, 2, 3]
     swap_to_oracle(cpu_model, cfg)
-    prompt = torch.randint(0, SMALL.vocab_size, (1, 700), generator=torch.Generator().manual_seed(3))
+    prompt = torch.randint(0, cfg_.vocab_size, (1, 700), generator=torch.Generator().manual_seed(3))
     steps = 12
-    caches = [None] * SMALL.num_layers
+    caches = [None] * cfg_.num_layers
     bf.install_compressed_kv_caches(model, caches, block_size=128, local_window_tokens=64, max_kv_size=800)
-    ref_caches = [[] for _ in range(SMALL.num_layers)]
+    ref_caches = [[] for _ in range(cfg_.num_layers)]
     lc = cpu_model.forward(prompt, ref_caches, 0)
     lg = model.forward(prompt.cuda(), caches, 0).cpu()
     pos, diffs, checked = 700, [], 0

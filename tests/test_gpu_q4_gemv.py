@@ -13,7 +13,7 @@ import torch
 import torch.nn.functional as F
 
 from butterfly_amd import _native
-from butterfly_amd.decoder import QuantLinear, q4_gemv, q4_gemv_silu, quantize_affine
+from butterfly_amd.decoder import QuantLinear, q4_gemv, q4_gemv_silu
 
 pytestmark = pytest.mark.gpu
 
@@ -95,3 +95,4 @@ def test_q4_gemv_unaligned_row_is_copied():
     assert x.data_ptr() % 16
     y = q4_gemv(x, layer)
     assert torch.equal(y, q4_gemv(x.clone(), layer))
+

@@ -142,12 +142,15 @@ class CompressedKVCache:
     def decode_step(self, q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, *, layer_idx: int,
                     local_window_tokens: int, partner_rule: str = "causal_shift", local_window_blocks: int = 1,
                     sink_count: int = 1, partner_count: int = 1, scale: Optional[float] = None,
-                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                    out: Optional[torch.Tensor] = None, qk_norm=None) -> torch.Tensor:
         """One token per sequence with device counters: ``update_and_attend`` of one step,
         with the layer's layout at the live kv_len computed on the device.
 
         q [B, Hq, 1, d]; keys/values [B, Hkv, 1, d].  One kernel launch, fixed
-        arguments; the host counters are stale until ``sync()``.
+        arguments; the host counters are stale until ``sync()``.  ``qk_norm`` =
+        ``(q_norm_weight, k_norm_weight, rope_cos, rope_sin, eps)``: q and keys are raw
+        projection rows, normed and rotated at position ``offset`` inside the launch
+        (``bfly_decode_step_qk_norm``: bf16, d = 128; rope tables [rows, 128] fp32).
         """
         from .attention import _scale
 
@@ -165,6 +168,20 @@ class CompressedKVCache:
         q, keys, values = _c(q), _c(keys), _c(values)
         if out is None:
             out = torch.empty_like(q)
+        if qk_norm is not None:
+            qw, kw, cos, sin, eps = qk_norm
+            if cos.dtype != torch.float32 or cos.shape != sin.shape or cos.shape[-1] != d or not cos.is_contiguous() \
+                    or not sin.is_contiguous():
+                raise ValueError("rope tables must be contiguous fp32 [rows, head_dim]")
+            _native.call("bfly_decode_step_qk_norm", q.data_ptr(), _dtype_code(q), b, hq, int(keys.shape[1]), d,
+                         keys.data_ptr(), values.data_ptr(), self._ring_k.data_ptr(), self._ring_v.data_ptr(),
+                         self.tail_capacity, self._pool_k.data_ptr(), self._pool_v.data_ptr(), self.summary_capacity,
+                         self._dev.data_ptr(), int(layer_idx), rule, int(local_window_blocks), int(sink_count),
+                         int(partner_count), self.block_size, int(local_window_tokens), _scale(scale, d),
+                         qw.data_ptr(), kw.data_ptr(), cos.data_ptr(), sin.data_ptr(), int(cos.shape[0]), float(eps),
+                         out.data_ptr(), _stream(q))
+            self._dev_dirty = True
+            return out
         _native.call("bfly_decode_step", q.data_ptr(), _dtype_code(q), b, hq, int(keys.shape[1]), d, keys.data_ptr(),
                      values.data_ptr(), self._ring_k.data_ptr(), self._ring_v.data_ptr(), self.tail_capacity,
                      self._pool_k.data_ptr(), self._pool_v.data_ptr(), self.summary_capacity, self._dev.data_ptr(),

@@ -161,6 +161,15 @@ struct DecodeArgs {
   float scale;
   FastDiv bs_div, ring_div, hkv_div;   // MFMA path: block_size, ring capacity, Hkv
   int gsz;                             // MFMA path: hq / hkv
+  // MFMA step path, d = 128: when qn_w is set, q and k_new are the raw projection
+  // rows and the kernel applies the per-head q/k RMSNorm and rotate-half RoPE at
+  // position kv_len - 1 itself (rope_cos / rope_sin: [rope_rows][128] fp32)
+  const __bf16* qn_w;
+  const __bf16* kn_w;
+  const float* rope_cos;
+  const float* rope_sin;
+  int64_t rope_rows;
+  float qk_eps;
 };
 
 __device__ __forceinline__ float dec_wave_max(float v) {
@@ -753,6 +762,151 @@ __device__ __forceinline__ void dec_route_workgroup(const DecodeArgs& a, const S
 }
 
 // x where c holds, else zero (a value select: no branch, no memory)
+// ---- q/k RMSNorm + rotate-half RoPE of the new token (d = 128) inside the step.
+// Rounding points and the summation order of the mean square are those of
+// decoder_ops.hip's qk_norm_rope_vec_kernel<128>: chunk gl pairs d in
+// [8 gl, 8 gl + 8) with d + 64, summed as fma(lo, lo, fma(hi, hi, s)) element
+// by element, and the eight chunk sums are added in xor-butterfly order (1, 2,
+// 4); the norm is ((x * r) * w) and the rotation x * cos -+ partner * sin, each
+// product and sum rounded on its own, with bf16 after the norm and after RoPE.
+// So the rows are bit-identical to that kernel's.
+__device__ __forceinline__ float dec_qkn_chunk(const float* lo, const float* hi) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s = fmaf(lo[e], lo[e], fmaf(hi[e], hi[e], s));
+  return s;
+}
+__device__ __forceinline__ float dec_qkn_norm(float x, float r, float w) {
+#pragma clang fp contract(off)
+  return (float)(__bf16)(x * r * w);
+}
+__device__ __forceinline__ __bf16 dec_qkn_rope(float own, float par, float c, float sn, bool lo) {
+#pragma clang fp contract(off)
+  return lo ? (__bf16)(own * c + (-par) * sn) : (__bf16)(own * c + par * sn);
+}
+__device__ __forceinline__ float dec_bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float dec_bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+typedef unsigned int dec_u32x4 __attribute__((ext_vector_type(4)));
+
+// q fragments of one head group: lane (lg, lq) holds d = 32 lg + 8 ks + e of its
+// head, so the partner d ^ 64 sits in lane ^ 32 (v_permlane32_swap), and lanes
+// lg and lg ^ 2 together hold chunks 4 (lg & 1) .. 4 (lg & 1) + 3; the other four
+// chunks' sum is in lane ^ 16.
+__device__ __forceinline__ void dec_qkn_swap(const bf16x8& f, float* own, float* par) {
+  const dec_u32x4 u = __builtin_bit_cast(dec_u32x4, f);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    // one of the two results is this lane's own word, the other lane ^ 32's (when
+    // both equal the own word, so does the partner's)
+    const auto sw = __builtin_amdgcn_permlane32_swap(u[t], u[t], false, false);
+    const uint32_t pw = sw[0] == u[t] ? sw[1] : sw[0];
+    own[2 * t] = dec_bf_lo(u[t]);
+    own[2 * t + 1] = dec_bf_hi(u[t]);
+    par[2 * t] = dec_bf_lo(pw);
+    par[2 * t + 1] = dec_bf_hi(pw);
+  }
+}
+// Norm weights and the RoPE row of one lane, requested as soon as the position is
+// known so that their latency overlaps the staging loads: q lanes d = 32 lg + 8 ks
+// + e (and the partners' weights), k lanes d = 8 pc + e.
+struct DecQknQ {
+  bf16x8 w[4], wp[4];
+  f32x4 c[8], s[8];
+};
+struct DecQknK {
+  bf16x8 w, wp;
+  f32x4 c[2], s[2];
+};
+__device__ __forceinline__ DecQknQ dec_qkn_q_load(const DecodeArgs& a, int p, int lg) {
+  DecQknQ o;
+  const float* cr = a.rope_cos + (int64_t)p * 128;
+  const float* sr = a.rope_sin + (int64_t)p * 128;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int d0 = 32 * lg + 8 * ks;
+    o.w[ks] = *reinterpret_cast<const bf16x8*>(a.qn_w + d0);
+    o.wp[ks] = *reinterpret_cast<const bf16x8*>(a.qn_w + (d0 ^ 64));
+    o.c[2 * ks] = *reinterpret_cast<const f32x4*>(cr + d0);
+    o.c[2 * ks + 1] = *reinterpret_cast<const f32x4*>(cr + d0 + 4);
+    o.s[2 * ks] = *reinterpret_cast<const f32x4*>(sr + d0);
+    o.s[2 * ks + 1] = *reinterpret_cast<const f32x4*>(sr + d0 + 4);
+  }
+  return o;
+}
+__device__ __forceinline__ DecQknK dec_qkn_k_load(const DecodeArgs& a, int p, int pc) {
+  DecQknK o;
+  const int d0 = 8 * pc;
+  o.w = *reinterpret_cast<const bf16x8*>(a.kn_w + d0);
+  o.wp = *reinterpret_cast<const bf16x8*>(a.kn_w + (d0 ^ 64));
+  const float* cr = a.rope_cos + (int64_t)p * 128 + d0;
+  const float* sr = a.rope_sin + (int64_t)p * 128 + d0;
+  o.c[0] = *reinterpret_cast<const f32x4*>(cr);
+  o.c[1] = *reinterpret_cast<const f32x4*>(cr + 4);
+  o.s[0] = *reinterpret_cast<const f32x4*>(sr);
+  o.s[1] = *reinterpret_cast<const f32x4*>(sr + 4);
+  return o;
+}
+
+// Two passes over the fragments (the partner values are swapped in again for the
+// second), so that no more than one fragment's values are live at a time.
+__device__ __forceinline__ void dec_qkn_q(bf16x8 (&qf)[4], const DecQknQ& pq, float eps, int lg) {
+  const bool lo = lg < 2;   // lanes 0..31 hold d < 64
+  float cs[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    float own[8], par[8];
+    dec_qkn_swap(qf[ks], own, par);
+    cs[ks] = lo ? dec_qkn_chunk(own, par) : dec_qkn_chunk(par, own);
+  }
+  const float half = (cs[0] + cs[1]) + (cs[2] + cs[3]);
+  const float r = rsqrtf((half + __shfl_xor(half, 16)) / 128.f + eps);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    float own[8], par[8];
+    dec_qkn_swap(qf[ks], own, par);
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float on = dec_qkn_norm(own[e], r, (float)pq.w[ks][e]);
+      const float pn = dec_qkn_norm(par[e], r, (float)pq.wp[ks][e]);
+      o[e] = dec_qkn_rope(on, pn, pq.c[2 * ks + (e >> 2)][e & 3], pq.s[2 * ks + (e >> 2)][e & 3], lo);
+    }
+    qf[ks] = o;
+  }
+}
+
+// One staged piece of the new k row: lane (tid % 16) = pc holds d = 8 pc + e and
+// the 16 lanes of the row are one DPP row, so the partner piece pc ^ 8 is a
+// rotation by 8 and the chunk sums combine by quad permutations (xor 1, 2) and a
+// rotation by 4 (lanes pc and pc ^ 8 hold the same chunk sum).  Every lane of the
+// wave runs it; only the lanes of the new row use the result.
+__device__ __forceinline__ uint4 dec_qkn_k(uint4 x, const DecQknK& pk, float eps, int pc) {
+  const bool lo = pc < 8;
+  const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+  float own[8], par[8];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t pw = (uint32_t)__builtin_amdgcn_mov_dpp((int)u[t], 0x128, 0xf, 0xf, false);   // row_ror:8
+    own[2 * t] = dec_bf_lo(u[t]);
+    own[2 * t + 1] = dec_bf_hi(u[t]);
+    par[2 * t] = dec_bf_lo(pw);
+    par[2 * t + 1] = dec_bf_hi(pw);
+  }
+  float ss = lo ? dec_qkn_chunk(own, par) : dec_qkn_chunk(par, own);
+  ss += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(ss), 0xb1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+  ss += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(ss), 0x4e, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+  ss += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(ss), 0x124, 0xf, 0xf, false));  // row_ror:4
+  const float r = rsqrtf(ss / 128.f + eps);
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float on = dec_qkn_norm(own[e], r, (float)pk.w[e]);
+    const float pn = dec_qkn_norm(par[e], r, (float)pk.wp[e]);
+    o[e] = dec_qkn_rope(on, pn, pk.c[e >> 2][e & 3], pk.s[e >> 2][e & 3], lo);
+  }
+  return __builtin_bit_cast(uint4, o);
+}
+
 __device__ __forceinline__ uint4 keep_if(bool c, uint4 x) {
   return make_uint4(c ? x.x : 0u, c ? x.y : 0u, c ? x.z : 0u, c ? x.w : 0u);
 }
@@ -801,8 +955,10 @@ __device__ __forceinline__ void dec_pool32(const DecodeArgs& a, const DecState32
 // `state` and `q` lead the argument list: the hardware preloads leading pointer
 // arguments into SGPRs (the library is built with a kernarg preload count), so
 // the counter read needs no kernel-argument load first.
-template <int D, bool kStep>
-__global__ void __launch_bounds__(256, D <= 128 ? 3 : 1)
+// kQkn: the fused q/k norm + RoPE (d = 128, bfly_decode_step_qk_norm); a separate
+// instance with room for its registers, for the batch-1 decoder steps it serves.
+template <int D, bool kStep, bool kQkn = false>
+__global__ void __launch_bounds__(256, kQkn ? 1 : (D <= 128 ? 3 : 1))
 decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) {
   StepArgs sa = sa_in;
   sa.state = state;
@@ -875,7 +1031,9 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   constexpr int SK = (SKN + 255) / 256;
   const DecState32 st =
       kStep ? dec_advance32(cnt[kStOffset], cnt[kStTail], cnt[kStCount], cnt[kStSumOff], a, sa) : dec_state32<false>(a, sa, bh);
-  if (kStep && st.err) {
+  // with the fused q/k norm, a position past the RoPE table is an error of the step
+  constexpr bool qkn = kQkn && D == 128;
+  if (kStep && (st.err || (qkn && st.kv_len - 1 >= a.rope_rows))) {
     if (tid == 0) sa.state[kStError] = 1;
     return;
   }
@@ -889,6 +1047,12 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
     for (int it = 0; it < SK; ++it) rsel[it] = rl[min(tid + it * 256, SKN - 1) / PIECES];
   }
   const int p = st.kv_len - 1;
+  DecQknQ qkn_q{};
+  DecQknK qkn_k{};
+  if constexpr (qkn) {
+    qkn_q = dec_qkn_q_load(a, p, lg);
+    qkn_k = dec_qkn_k_load(a, p, tid % PIECES);
+  }
   const int lo = max(max(p - a.W + 1, st.tail_start), 0);
   const int nw = p - lo + 1;
   const int ring = (int)a.ring;
@@ -963,7 +1127,7 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
     }
     // append the new token to its ring slot; requested after every staging load so
     // that its wait coincides with theirs (the staging reads it from k_new/v_new)
-    if (knew != nullptr && tid < 2 * PIECES) {
+    if (knew != nullptr && tid < 2 * PIECES && !(qkn && tid < PIECES)) {   // normed k: appended below
       const int pc = tid % PIECES;
       const T* src = tid < PIECES ? knew : vnew;
       T* dst = tid < PIECES ? rk : rv;
@@ -972,11 +1136,28 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
     auto put_v = [&](int r, int pc, uint4 x) {
       *reinterpret_cast<uint4*>(Vs + r * D + (pc ^ vrow_swizzle<D>(r)) * VEC) = x;
     };
+    if constexpr (D == 128) {
+      if constexpr (qkn) dec_qkn_q(qf, qkn_q, a.qk_eps, lg);
+    }
 #pragma unroll
     for (int it = 0; it < WK; ++it) {
       const int i = tid + it * 256;
       const int r = i / PIECES, pc = i % PIECES;
-      *reinterpret_cast<uint4*>(Ks + r * KP + pc * VEC) = keep_if(r < nw, kx[it]);
+      uint4 kv = kx[it];
+      if constexpr (D == 128) {
+        // the wave's four rows of this iteration hold the new one: norm + RoPE it
+        // (wave-uniform branch) and append the result to its ring slot
+        const int row0 = it * (256 / PIECES) + wave * (64 / PIECES);
+        if (qkn && knew != nullptr && nw - 1 >= row0 && nw - 1 < row0 + 64 / PIECES) {
+          // every lane runs the transform (DPP); only the new row's lanes keep it
+          const uint4 kn = dec_qkn_k(kv, qkn_k, a.qk_eps, pc);
+          if (r == nw - 1) {
+            kv = kn;
+            *reinterpret_cast<uint4*>(rk + ring_off(nw - 1) + pc * VEC) = kv;
+          }
+        }
+      }
+      *reinterpret_cast<uint4*>(Ks + r * KP + pc * VEC) = keep_if(r < nw, kv);
       put_v(r, pc, keep_if(r < nw, vx[it]));
     }
 #pragma unroll
@@ -993,7 +1174,12 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
 
   const float sl2 = a.scale * 1.4426950408889634f;   // host guarantees scale > 0 on this path
   for (int hg = 0; 16 * hg < gsz; ++hg) {
-    if (hg > 0) load_q(hg);
+    if (hg > 0) {
+      load_q(hg);
+      if constexpr (D == 128) {
+        if constexpr (qkn) dec_qkn_q(qf, qkn_q, a.qk_eps, lg);
+      }
+    }
     // S^T: lane (lg, lq) holds keys 16t + 4lg + i of head 16hg + lq
     f32x4 sc[NT];
 #pragma unroll
@@ -1079,16 +1265,22 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   }
 }
 
+// bf16 with a positive scale (folded into exp2) runs on MFMA when its 32-bit
+// positions and offsets suffice
+static bool decode_on_mfma(const DecodeArgs& a, int d, bool step) {
+  const int64_t lim = kDecPosLimit;
+  const bool fits = a.kv_rows * d < lim && a.pool_rows * d < lim && a.ring < lim &&
+                    (step ? (a.pool_rows + 2) * a.bs + a.ring + a.W < lim
+                          : a.kv_len < lim && a.nblocks < lim && a.nsum < lim);
+  return a.scale > 0.f && fits;
+}
+
 template <typename T, bool kStep>
 static void launch_decode(const DecodeArgs& a, const StepArgs& sa, int d, int64_t grid, hipStream_t stream) {
   // bf16 with a positive scale (folded into exp2) runs on MFMA when its 32-bit
   // positions and offsets suffice; fp32 and larger caches on the lane-per-key kernel
   if constexpr (sizeof(T) == 2) {
-    const int64_t lim = kDecPosLimit;
-    const bool fits = a.kv_rows * d < lim && a.pool_rows * d < lim && a.ring < lim &&
-                      (kStep ? (a.pool_rows + 2) * a.bs + a.ring + a.W < lim
-                             : a.kv_len < lim && a.nblocks < lim && a.nsum < lim);
-    if (a.scale > 0.f && fits) {
+    if (decode_on_mfma(a, d, kStep)) {
       DecodeArgs m = a;
       m.bs_div = FastDiv::make((uint32_t)a.bs);
       m.ring_div = FastDiv::make(a.ring > 0 ? (uint32_t)a.ring : 1u);
@@ -1101,8 +1293,12 @@ static void launch_decode(const DecodeArgs& a, const StepArgs& sa, int d, int64_
                              m.q, m, sa);
           return;
         case 128:
-          hipLaunchKernelGGL((decode_mfma_kernel<128, kStep>), dim3((unsigned)mgrid), dim3(256), 0, stream, sa.state,
-                             m.q, m, sa);
+          if (kStep && a.qn_w != nullptr)
+            hipLaunchKernelGGL((decode_mfma_kernel<128, kStep, true>), dim3((unsigned)mgrid), dim3(256), 0, stream,
+                               sa.state, m.q, m, sa);
+          else
+            hipLaunchKernelGGL((decode_mfma_kernel<128, kStep>), dim3((unsigned)mgrid), dim3(256), 0, stream, sa.state,
+                               m.q, m, sa);
           return;
         default:
           hipLaunchKernelGGL((decode_mfma_kernel<256, kStep>), dim3((unsigned)mgrid), dim3(256), 0, stream, sa.state,
@@ -1181,12 +1377,11 @@ extern "C" int64_t bfly_decode_state_words(int64_t batch, int hkv) {
   return kStHeader + kStSlot * (batch * hkv + kRouteGroups);
 }
 
-extern "C" int bfly_decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,
-                                const void* k_new, const void* v_new, void* ring_k, void* ring_v,
-                                int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity,
-                                int64_t* state, int64_t layer_idx, int partner_rule, int local_window_blocks,
-                                int sink_count, int partner_count, int block_size, int window, float scale,
-                                void* out, hipStream_t stream) {
+static int decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim, const void* k_new,
+                       const void* v_new, void* ring_k, void* ring_v, int64_t ring_capacity, void* pool_k,
+                       void* pool_v, int64_t pool_capacity, int64_t* state, int64_t layer_idx, int partner_rule,
+                       int local_window_blocks, int sink_count, int partner_count, int block_size, int window,
+                       float scale, void* out, const DecodeArgs* qkn, hipStream_t stream) {
   BFLY_CHECK_ARG(dtype == BFLY_DTYPE_F32 || dtype == BFLY_DTYPE_BF16, "unsupported dtype %d", dtype);
   BFLY_CHECK_ARG(q && k_new && v_new && ring_k && ring_v && pool_k && pool_v && state && out, "null pointer");
   BFLY_CHECK_ARG(aligned16(q) && aligned16(out) && aligned16(ring_k) && aligned16(ring_v) && aligned16(pool_k) &&
@@ -1212,11 +1407,52 @@ extern "C" int bfly_decode_step(const void* q, int dtype, int64_t batch, int hq,
   a.ring_k = ring_k; a.ring_v = ring_v; a.pool_k = pool_k; a.pool_v = pool_v;
   a.ring = ring_capacity; a.kv_rows = ring_capacity; a.pool_rows = pool_capacity;
   a.hq = hq; a.hkv = hkv; a.bs = block_size; a.W = window; a.scale = scale;
+  if (qkn != nullptr) {
+    BFLY_CHECK_ARG(dtype == BFLY_DTYPE_BF16 && head_dim == 128 && decode_on_mfma(a, head_dim, true),
+                   "bfly_decode_step_qk_norm: bf16, head_dim 128 and a positive scale only");
+    a.qn_w = qkn->qn_w; a.kn_w = qkn->kn_w; a.rope_cos = qkn->rope_cos; a.rope_sin = qkn->rope_sin;
+    a.rope_rows = qkn->rope_rows; a.qk_eps = qkn->qk_eps;
+  }
   StepArgs sa{state, layer_idx, partner_rule, local_window_blocks, sink_count, partner_count};
   if (dtype == BFLY_DTYPE_F32)
     launch_decode<float, true>(a, sa, head_dim, batch * hkv, stream);
   else
     launch_decode<__bf16, true>(a, sa, head_dim, batch * hkv, stream);
-  BFLY_CHECK_LAUNCH("bfly_decode_step");
+  BFLY_CHECK_LAUNCH(qkn ? "bfly_decode_step_qk_norm" : "bfly_decode_step");
   return BFLY_OK;
+}
+
+extern "C" int bfly_decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,
+                                const void* k_new, const void* v_new, void* ring_k, void* ring_v,
+                                int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity,
+                                int64_t* state, int64_t layer_idx, int partner_rule, int local_window_blocks,
+                                int sink_count, int partner_count, int block_size, int window, float scale,
+                                void* out, hipStream_t stream) {
+  return decode_step(q, dtype, batch, hq, hkv, head_dim, k_new, v_new, ring_k, ring_v, ring_capacity, pool_k, pool_v,
+                     pool_capacity, state, layer_idx, partner_rule, local_window_blocks, sink_count, partner_count,
+                     block_size, window, scale, out, nullptr, stream);
+}
+
+extern "C" int bfly_decode_step_qk_norm(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,
+                                        const void* k_new, const void* v_new, void* ring_k, void* ring_v,
+                                        int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity,
+                                        int64_t* state, int64_t layer_idx, int partner_rule, int local_window_blocks,
+                                        int sink_count, int partner_count, int block_size, int window, float scale,
+                                        const void* q_norm_weight, const void* k_norm_weight, const float* rope_cos,
+                                        const float* rope_sin, int64_t rope_rows, float eps, void* out,
+                                        hipStream_t stream) {
+  BFLY_CHECK_ARG(q_norm_weight && k_norm_weight && rope_cos && rope_sin, "null pointer");
+  BFLY_CHECK_ARG(aligned16(q_norm_weight) && aligned16(k_norm_weight) && aligned16(rope_cos) && aligned16(rope_sin),
+                 "norm weights and RoPE tables must be 16-byte aligned");
+  BFLY_CHECK_ARG(rope_rows > 0 && eps >= 0.f, "bad rope_rows / eps");
+  DecodeArgs n{};
+  n.qn_w = static_cast<const __bf16*>(q_norm_weight);
+  n.kn_w = static_cast<const __bf16*>(k_norm_weight);
+  n.rope_cos = rope_cos;
+  n.rope_sin = rope_sin;
+  n.rope_rows = rope_rows;
+  n.qk_eps = eps;
+  return decode_step(q, dtype, batch, hq, hkv, head_dim, k_new, v_new, ring_k, ring_v, ring_capacity, pool_k, pool_v,
+                     pool_capacity, state, layer_idx, partner_rule, local_window_blocks, sink_count, partner_count,
+                     block_size, window, scale, out, &n, stream);
 }

@@ -241,6 +241,19 @@ def rope_cos_sin(positions: torch.Tensor, head_dim: int, theta: float):
     return emb.cos(), emb.sin()
 
 
+class RopeTable:
+    """RoPE for one decode step whose position lives on the device: the full cos/sin tables
+    [rows, d] (fp32) and the position tensor [1].  ``rows()`` gives the ``(cos, sin)`` rows a
+    projection needs; a swapped attention with a device-counter cache passes the tables to
+    the decode step instead, which reads the row of its own position."""
+
+    def __init__(self, cos_tab: torch.Tensor, sin_tab: torch.Tensor, pos: torch.Tensor):
+        self.cos_tab, self.sin_tab, self.pos = cos_tab, sin_tab, pos
+
+    def rows(self):
+        return self.cos_tab.index_select(0, self.pos), self.sin_tab.index_select(0, self.pos)
+
+
 def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
     """x [B, H, T, d]; rotate-half RoPE in fp32."""
     d = x.shape[-1]
@@ -273,6 +286,8 @@ class Attention(nn.Module):
         ``rope`` is an optional precomputed ``(cos, sin)`` for ``positions``."""
         b, t, _ = x.shape
         c = self.cfg
+        if isinstance(rope, RopeTable):
+            rope = rope.rows()
         if _hip(x) and c.head_dim in (128, 256):
             return self.heads(self.qkv(x), positions, rope)
         q = self.q_proj(x).view(b, t, c.num_heads, c.head_dim).transpose(1, 2)
@@ -287,6 +302,8 @@ class Attention(nn.Module):
         q [B, Hq, T, d], k/v [B, Hkv, T, d]: q/k RMSNorm and RoPE in one ``bfly_qk_norm_rope``."""
         b, t, _ = qkv.shape
         c = self.cfg
+        if isinstance(rope, RopeTable):
+            rope = rope.rows()
         nq, nkv = c.num_heads * c.head_dim, c.num_kv_heads * c.head_dim
         base, ld, es = qkv.data_ptr(), qkv.shape[-1], qkv.element_size()
         cos, sin = rope if rope is not None else rope_cos_sin(positions, c.head_dim, c.rope_theta)
@@ -343,8 +360,20 @@ class ButterflyAttention(nn.Module):
         return self.core.last_profile
 
     def forward(self, x: torch.Tensor, positions: torch.Tensor, cache=None, rope=None) -> torch.Tensor:
-        q, k, v = self.base.project(x, positions, rope)
-        return self.base.output(self.core(q, k, v, cache))
+        base, c = self.base, self.base.cfg
+        if (isinstance(rope, RopeTable) and _one_row(x)
+                and self.core.fuses_qk_norm(cache, 1, c.head_dim, x.dtype)):
+            # one decode step with device counters: the raw q|k|v row goes to the decode
+            # step, which applies q/k RMSNorm and RoPE at its own position (one launch fewer)
+            row = base.qkv(x).view(-1)
+            nq, nkv = c.num_heads * c.head_dim, c.num_kv_heads * c.head_dim
+            q = row[:nq].view(1, c.num_heads, 1, c.head_dim)
+            k = row[nq:nq + nkv].view(1, c.num_kv_heads, 1, c.head_dim)
+            v = row[nq + nkv:].view(1, c.num_kv_heads, 1, c.head_dim)
+            qk = (base.q_norm.weight, base.k_norm.weight, rope.cos_tab, rope.sin_tab, base.q_norm.eps)
+            return base.output(self.core(q, k, v, cache, qk_norm=qk))
+        q, k, v = base.project(x, positions, rope)
+        return base.output(self.core(q, k, v, cache))
 
 
 class MLP(nn.Module):
@@ -486,7 +515,7 @@ class Decoder(nn.Module):
 
         def one_step():
             x = F.embedding(tok, self.embed_tokens)
-            rope = (cos_tab.index_select(0, pos), sin_tab.index_select(0, pos))
+            rope = RopeTable(cos_tab, sin_tab, pos)
             lg = self._logits(self._last_hidden(x, pos, caches, rope))
             nxt = argmax_rows(lg) if _hip(lg) else lg.argmax(-1, keepdim=True)
             tok.copy_(nxt)

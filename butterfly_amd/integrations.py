@@ -151,8 +151,17 @@ class ButterflyAttentionCore:
             local_window_blocks=int(c.block_local_window_blocks), sink_count=int(c.block_sink_blocks),
             partner_count=int(c.block_partner_count), partner_rule=c.block_partner_rule, device=device)
 
+    def fuses_qk_norm(self, cache, q_len: int, head_dim: int, dtype) -> bool:
+        """Whether ``__call__`` takes ``qk_norm`` for this step: a device-counter decode step of
+        bf16 rows with head_dim 128 (``bfly_decode_step_qk_norm``)."""
+        return (isinstance(cache, CompressedKVCache) and cache.device_counters is not None and q_len == 1
+                and self.cfg.butterfly_decode_backend != "dense" and head_dim == 128 and dtype == torch.bfloat16)
+
     def __call__(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                 cache: Optional[CompressedKVCache] = None) -> torch.Tensor:
+                 cache: Optional[CompressedKVCache] = None, qk_norm=None) -> torch.Tensor:
+        """``qk_norm`` (see ``CompressedKVCache.decode_step``) hands raw q/k projection rows to
+        the decode step, which applies the q/k RMSNorm and RoPE itself; only where
+        ``fuses_qk_norm`` holds."""
         t0 = _now_ms()
         b, hq, q_len, d = q.shape
         hkv = int(k.shape[1])
@@ -161,13 +170,15 @@ class ButterflyAttentionCore:
         groups = hq // hkv
         w = int(self.cfg.compressed_local_window_tokens)
         c = self.cfg
+        if qk_norm is not None and not self.fuses_qk_norm(cache, q_len, d, q.dtype):
+            raise ValueError("qk_norm is taken only by device-counter decode steps of bf16, head_dim 128 rows")
         if (cache is not None and cache.device_counters is not None and q_len == 1
                 and c.butterfly_decode_backend != "dense"):
             # device counters: one fixed-argument launch, no host bookkeeping (graph-capturable)
             out = cache.decode_step(q, k, v, layer_idx=self.layer_idx, local_window_tokens=w,
                                     partner_rule=c.block_partner_rule, local_window_blocks=c.block_local_window_blocks,
                                     sink_count=c.block_sink_blocks, partner_count=c.block_partner_count,
-                                    scale=self.scale)
+                                    scale=self.scale, qk_norm=qk_norm)
             self._last = (t0, _now_ms(), None, "block_sparse_compressed_active", _DEVICE_STEP_NOTES, None)
             return out
         if cache is not None:

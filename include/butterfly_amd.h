@@ -311,6 +311,29 @@ int bfly_decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv, i
                      void* out, hipStream_t stream);
 
 /*
+ * Device: bfly_decode_step for a decoder whose attention applies per-head q/k
+ * RMSNorm and rotate-half RoPE after its projections: q and k_new are the raw
+ * projection rows (for batch 1 they may be views of one fused q|k|v output), and
+ * the kernel norms them (q_norm_weight / k_norm_weight [128] bf16, eps) and
+ * rotates them at position kv_len - 1 with row kv_len - 1 of rope_cos / rope_sin
+ * ([rope_rows][128] fp32), then appends the normed k and attends as
+ * bfly_decode_step does.  The q and k rows are bit-identical to
+ * bfly_qk_norm_rope's (include/butterfly_amd_decoder.h).  bf16, head_dim 128
+ * only (else BFLY_ERR_INVALID).  A position at or past rope_rows sets the step
+ * error flag, like a capacity overflow.  Replaces the projection tail of the
+ * swapped attention (bna/integrations/qwen_torch.py:550-562, qwen_mlx.py:288-357)
+ * and the step of bfly_decode_step (bna/mlx/compressed_cache.py:94-172,
+ * bna/mlx/attention.py:1816-1876) in one launch.
+ */
+int bfly_decode_step_qk_norm(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,
+                             const void* k_new, const void* v_new, void* ring_k, void* ring_v,
+                             int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity,
+                             int64_t* state, int64_t layer_idx, int partner_rule, int local_window_blocks,
+                             int sink_count, int partner_count, int block_size, int window, float scale,
+                             const void* q_norm_weight, const void* k_norm_weight, const float* rope_cos,
+                             const float* rope_sin, int64_t rope_rows, float eps, void* out, hipStream_t stream);
+
+/*
  * Device: append `step` new tokens at positions [offset, offset+step) of the
  * tail ring (slot = position mod ring_capacity).
  * Replaces the tail append of CompressedKVCache.update_and_fetch

@@ -136,12 +136,20 @@ def test_graph_replays_match_eager_steps():
     assert err <= 2e-2, err
 
 
-def test_decoder_graph_greedy_equals_eager_greedy():
-    cfg = DecoderConfig(vocab_size=2048, hidden_size=512, num_layers=3, num_heads=8, num_kv_heads=2, head_dim=64,
-                        intermediate_size=1024)
+@pytest.mark.parametrize("batch,head_dim", [(2, 64), (1, 128)])
+def test_decoder_graph_greedy_equals_eager_greedy(batch, head_dim):
+    """Batch 1 at head_dim 128: the graphed steps take the fused q/k norm + RoPE decode
+    step (bfly_decode_step_qk_norm), the eager ones the separate launches; the tokens
+    agree only if the fused rows are bit-identical."""
+    cfg = DecoderConfig(vocab_size=2048, hidden_size=512, num_layers=3, num_heads=512 // head_dim, num_kv_heads=2,
+                        head_dim=head_dim, intermediate_size=1024)
     model = Decoder(cfg, seed=11)
     bf.swap_qwen_attention_with_butterfly(model, cfg=bf.QwenButterflyConfig())
-    prompt = torch.randint(0, cfg.vocab_size, (2, 300), generator=torch.Generator().manual_seed(5)).cuda()
+    for layer in model.layers:   # non-trivial q/k norm weights
+        g = torch.Generator(device="cuda").manual_seed(len(layer.self_attn.base.q_norm.weight))
+        for norm in (layer.self_attn.base.q_norm, layer.self_attn.base.k_norm):
+            norm.weight.data = (1 + 0.3 * torch.randn(head_dim, generator=g, device="cuda")).bfloat16()
+    prompt = torch.randint(0, cfg.vocab_size, (batch, 300), generator=torch.Generator().manual_seed(5)).cuda()
 
     def caches():
         c = [None] * cfg.num_layers

@@ -110,3 +110,18 @@ def test_decode_state_words_match_the_host_layout():
     assert lib.bfly_decode_state_words(1, 1) == 8 + 9 * _DEV_SLOT     # one sequence + 8 route copies
     assert lib.bfly_decode_state_words(32, 2) == 8 + 72 * _DEV_SLOT
     assert lib.bfly_decode_state_words(0, 2) == 0
+
+
+def test_decode_step_qk_norm_validates_before_launch():
+    """Fake, never dereferenced addresses: missing norm weights, a misaligned table and a
+    head_dim other than 128 are refused before any launch."""
+    lib = _native.lib()
+    base = (256, _native.DTYPE_BF16, 1, 8, 2, 128, 512, 768, 1024, 1280, 256, 1536, 1792, 16, 2048, 0, 3, 1, 1, 1,
+            128, 64, 0.088)
+    tail = (64, 1e-6, 0x3000, None)                    # rope_rows, eps, out, stream
+    assert lib.bfly_decode_step_qk_norm(*base, None, 0x2100, 0x2200, 0x2300, *tail) == _native.ERR_INVALID
+    assert lib.bfly_decode_step_qk_norm(*base, 0x2000, 0x2100, 0x2208, 0x2300, *tail) == _native.ERR_INVALID
+    assert b"16-byte" in lib.bfly_last_error()
+    d64 = base[:5] + (64,) + base[6:]
+    assert lib.bfly_decode_step_qk_norm(*d64, 0x2000, 0x2100, 0x2200, 0x2300, *tail) == _native.ERR_INVALID
+    assert b"head_dim 128" in lib.bfly_last_error()

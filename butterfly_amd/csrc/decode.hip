@@ -806,9 +806,9 @@ __device__ __forceinline__ void dec_qkn_swap(const bf16x8& f, float* own, float*
     par[2 * t + 1] = dec_bf_hi(pw);
   }
 }
-// Norm weights and the RoPE row of one lane, requested as soon as the position is
-// known so that their latency overlaps the staging loads: q lanes d = 32 lg + 8 ks
-// + e (and the partners' weights), k lanes d = 8 pc + e.
+// Norm weights and the RoPE row of one lane: q lanes d = 32 lg + 8 ks + e (and the
+// partners' weights), requested after the staging loads (earlier costs registers
+// for no gain); k lanes d = 8 pc + e, requested as soon as the position is known.
 struct DecQknQ {
   bf16x8 w[4], wp[4];
   f32x4 c[8], s[8];
@@ -1047,12 +1047,8 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
     for (int it = 0; it < SK; ++it) rsel[it] = rl[min(tid + it * 256, SKN - 1) / PIECES];
   }
   const int p = st.kv_len - 1;
-  DecQknQ qkn_q{};
   DecQknK qkn_k{};
-  if constexpr (qkn) {
-    qkn_q = dec_qkn_q_load(a, p, lg);
-    qkn_k = dec_qkn_k_load(a, p, tid % PIECES);
-  }
+  if constexpr (qkn) qkn_k = dec_qkn_k_load(a, p, tid % PIECES);
   const int lo = max(max(p - a.W + 1, st.tail_start), 0);
   const int nw = p - lo + 1;
   const int ring = (int)a.ring;
@@ -1137,7 +1133,10 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
       *reinterpret_cast<uint4*>(Vs + r * D + (pc ^ vrow_swizzle<D>(r)) * VEC) = x;
     };
     if constexpr (D == 128) {
-      if constexpr (qkn) dec_qkn_q(qf, qkn_q, a.qk_eps, lg);
+      if constexpr (qkn) {
+        const DecQknQ qq = dec_qkn_q_load(a, p, lg);
+        dec_qkn_q(qf, qq, a.qk_eps, lg);
+      }
     }
 #pragma unroll
     for (int it = 0; it < WK; ++it) {
@@ -1177,7 +1176,10 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
     if (hg > 0) {
       load_q(hg);
       if constexpr (D == 128) {
-        if constexpr (qkn) dec_qkn_q(qf, qkn_q, a.qk_eps, lg);
+        if constexpr (qkn) {
+          const DecQknQ qq = dec_qkn_q_load(a, p, lg);
+          dec_qkn_q(qf, qq, a.qk_eps, lg);
+        }
       }
     }
     // S^T: lane (lg, lq) holds keys 16t + 4lg + i of head 16hg + lq

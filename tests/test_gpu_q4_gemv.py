@@ -41,9 +41,9 @@ def _x(in_f, seed):
 
 # (out_features, in_features, group): one lane piece (64, 2048), partial second and third
 # pieces per lane (2112, 4160), three and four pieces (6144, 8192), groups of 32 / 64 / 128,
-# two rows per wave (small outputs) and four (9000 rows), the lm_head's shape.
-CASES = [(1, 64, 64), (100, 96, 32), (7, 2048, 64), (3072, 2048, 64), (9000, 2048, 64), (5, 2112, 32),
-         (2048, 6144, 64), (5, 4160, 64), (33, 8192, 128), (151936, 2048, 64)]
+# two rows per wave (small outputs) and four (9000 rows; 8195 ends in a partial set), the lm_head's shape.
+CASES = [(1, 64, 64), (100, 96, 32), (7, 2048, 64), (3072, 2048, 64), (9000, 2048, 64), (8195, 2048, 64),
+         (5, 2112, 32), (2048, 6144, 64), (5, 4160, 64), (33, 8192, 128), (151936, 2048, 64)]
 
 
 @pytest.mark.parametrize("out_f,in_f,group", CASES)
@@ -62,7 +62,7 @@ def test_q4_gemv_matches_fp32_weight_product(out_f, in_f, group):
     assert same >= 0.97, same
 
 
-@pytest.mark.parametrize("f,in_f", [(6144, 2048), (100, 2048), (1, 64), (2048, 6144), (300, 8192)])
+@pytest.mark.parametrize("f,in_f", [(6144, 2048), (4097, 2048), (100, 2048), (1, 64), (2048, 6144), (300, 8192)])
 def test_q4_gemv_silu_equals_projections_then_silu_mul(f, in_f):
     gate_up = _layer(2 * f, in_f, 64, seed=f)
     x = _x(in_f, seed=f + 1).cuda()

@@ -807,8 +807,9 @@ __device__ __forceinline__ void dec_qkn_swap(const bf16x8& f, float* own, float*
   }
 }
 // Norm weights and the RoPE row of one lane: q lanes d = 32 lg + 8 ks + e (and the
-// partners' weights), requested after the staging loads (earlier costs registers
-// for no gain); k lanes d = 8 pc + e, requested as soon as the position is known.
+// partners' weights), requested once the staged rows are in LDS (the q transform
+// then runs with the staging registers free); k lanes d = 8 pc + e, requested as
+// soon as the position is known.
 struct DecQknQ {
   bf16x8 w[4], wp[4];
   f32x4 c[8], s[8];
@@ -1132,12 +1133,6 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
     auto put_v = [&](int r, int pc, uint4 x) {
       *reinterpret_cast<uint4*>(Vs + r * D + (pc ^ vrow_swizzle<D>(r)) * VEC) = x;
     };
-    if constexpr (D == 128) {
-      if constexpr (qkn) {
-        const DecQknQ qq = dec_qkn_q_load(a, p, lg);
-        dec_qkn_q(qf, qq, a.qk_eps, lg);
-      }
-    }
 #pragma unroll
     for (int it = 0; it < WK; ++it) {
       const int i = tid + it * 256;
@@ -1166,6 +1161,12 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
       if (i < SKN) {
         *reinterpret_cast<uint4*>(Ks + (kDecMaxWin + j) * KP + pc * VEC) = keep_if(j < ns, skx[it]);
         put_v(kDecMaxWin + j, pc, keep_if(j < ns, svx[it]));
+      }
+    }
+    if constexpr (D == 128) {
+      if constexpr (qkn) {
+        const DecQknQ qq = dec_qkn_q_load(a, p, lg);
+        dec_qkn_q(qf, qq, a.qk_eps, lg);
       }
     }
   }

@@ -71,3 +71,28 @@ def test_swapped_decoder_tracks_cpu_reference_teacher_forced(cfg_):
     assert checked >= steps // 2
     prof = model.layers[2].self_attn.last_profile
     assert prof.path == "block_sparse_compressed_active" and prof.notes["q_len"] == 1
+
+
+def test_fuse_rows_gives_views_and_the_same_products():
+    from butterfly_amd.decoder import QuantLinear
+
+    g = torch.Generator().manual_seed(1)
+    parts = [QuantLinear(128, n, generator=g, device="cpu") for n in (64, 32, 32)]
+    want_w = torch.cat([p.weight for p in parts])
+    fused = QuantLinear.fuse_rows(*parts)
+    assert torch.equal(fused.weight, want_w) and fused.out_features == 128 and fused.in_features == 128
+    # each part's tensors are views of its row range of the fused layer
+    assert parts[1].weight.data_ptr() == fused.weight[64:].data_ptr()
+    assert parts[2].packed.data_ptr() == fused.packed[96:].data_ptr()
+    # the interleaved (scale, bias) pairs the 4-bit kernel reads
+    assert torch.equal(fused.scale_bias[..., 0], fused.scale) and torch.equal(fused.scale_bias[..., 1], fused.bias)
+    x = torch.randn(3, 128, generator=g).bfloat16()
+    torch.testing.assert_close(fused(x).float(), torch.cat([p(x) for p in parts], -1).float(), atol=2e-2, rtol=1e-2)
+
+
+def test_rope_table_rows_select_the_position():
+    from butterfly_amd.decoder import RopeTable, rope_cos_sin
+
+    cos, sin = rope_cos_sin(torch.arange(10), 8, 1e4)
+    c, s = RopeTable(cos, sin, torch.tensor([3])).rows()
+    assert torch.equal(c, cos[3:4]) and torch.equal(s, sin[3:4])

@@ -70,9 +70,9 @@ SIGNATURES = {
                            _i64, _i64, C.POINTER(Topology), _i64, _int, _int, _f32, _vp, _vp]),
     "bfly_decode_state_words": (_i64, [_i64, _int]),
     "bfly_decode_step": (_int, [_vp, _int, _i64, _int, _int, _int, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp,
-                                _i64, _int, _int, _int, _int, _int, _int, _f32, _vp, _vp]),
+                                _i64, _int, _int, _int, _int, _int, _int, _int, _f32, _vp, _vp]),
     "bfly_decode_step_qk_norm": (_int, [_vp, _int, _i64, _int, _int, _int, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64,
-                                        _vp, _i64, _int, _int, _int, _int, _int, _int, _f32, _vp, _vp, _vp, _vp,
+                                        _vp, _i64, _int, _int, _int, _int, _int, _int, _int, _f32, _vp, _vp, _vp, _vp,
                                         _i64, _f32, _vp, _vp]),
     "bfly_cache_append": (_int, [_vp, _vp, _int, _i64, _int, _i64, _int, _vp, _vp, _i64, _i64, _vp]),
     "bfly_cache_compress": (_int, [_vp, _vp, _int, _i64, _int, _int, _i64, _i64, _i64, _int, _vp, _vp,

@@ -30,6 +30,11 @@ from .attention import _c, _dtype_code, _on, _stream
 # an 8-word header, then one copy per sequence and eight for the step's route
 # workgroups, so bfly_decode_state_words(1, 1) == 8 + 9 * _DEV_SLOT.
 _DEV_SLOT = 32
+# device error word (state[4]) of a failed step: 1 = tail or pool capacity, 2 = a
+# position past the RoPE tables of the fused q/k norm step
+_DEV_ERR_CAPACITY, _DEV_ERR_ROPE = 1, 2
+# the bf16 MFMA decode kernel works in 32-bit positions and offsets below this
+_POS_LIMIT = 1 << 30
 
 
 @dataclass(frozen=True)
@@ -104,6 +109,18 @@ class CompressedKVCache:
         self._dev_dirty = False
         self._push()
 
+    def step_on_mfma(self, head_dim: int, window: int, scale: float, dtype: torch.dtype) -> bool:
+        """Whether ``decode_step`` of this cache runs on the bf16 MFMA kernel: a positive
+        scale and every position, row and element offset of the ring and pool below 2^30
+        (the host-side mirror of decode.hip's ``decode_on_mfma``).  The fused q/k norm step
+        exists only there."""
+        if self._ring_k is None or dtype != torch.bfloat16 or not scale > 0.0:
+            return False
+        lim = _POS_LIMIT
+        ring, pool, bs = self.tail_capacity, self.summary_capacity, self.block_size
+        return (ring * head_dim < lim and pool * head_dim < lim and ring < lim
+                and (pool + 2) * bs + ring + max(int(window), self.local_window_tokens) < lim)
+
     @property
     def device_counters(self) -> Optional[torch.Tensor]:
         """The device counter array, or None: word 4 is the error flag; sequence g
@@ -114,20 +131,29 @@ class CompressedKVCache:
         return self._dev
 
     def sync(self) -> None:
-        """Read device counters back; raise the capacity error a device step recorded."""
+        """Read device counters back; raise the error a device step recorded.
+
+        A failing step and every step after it leave the counters as they were, so
+        the cache keeps the last good state (the counters read back here) and the
+        error word is cleared before raising.
+        """
         if self._dev is None or not self._dev_dirty:
             return
         head = self._dev[:12].tolist()
         err = int(head[4])
         off, ts, sc, so = (int(x) for x in head[8:12])
         self._dev_dirty = False
+        self.offset, self.tail_size, self.summary_count, self.summary_offset = off, ts, sc, so
         if err:
             self._push()
+            if err == _DEV_ERR_ROPE:
+                raise RuntimeError(
+                    f"decode step at position {off} is past the RoPE tables given to the fused q/k norm "
+                    f"step; pass cos/sin tables with more rows.")
             raise RuntimeError(
                 f"CompressedKVCache capacity exceeded in a device decode step at offset={off} "
                 f"(tail_capacity={self.tail_capacity}, summary_capacity={self.summary_capacity}); "
                 f"raise max_chunk_size / max_kv_size at construction time.")
-        self.offset, self.tail_size, self.summary_count, self.summary_offset = off, ts, sc, so
 
     def _push(self) -> None:
         """Write the host counters into every copy; the kernel's routed-row cache is cleared."""
@@ -147,7 +173,10 @@ class CompressedKVCache:
         with the layer's layout at the live kv_len computed on the device.
 
         q [B, Hq, 1, d]; keys/values [B, Hkv, 1, d].  One kernel launch, fixed
-        arguments; the host counters are stale until ``sync()``.  ``qk_norm`` =
+        arguments; the host counters are stale until ``sync()``.  The cache's own
+        ``local_window_tokens`` decides which blocks are summarised and how far the
+        tail is trimmed (compressed_cache.py:120-164); ``local_window_tokens`` here is
+        the attention window.  ``qk_norm`` =
         ``(q_norm_weight, k_norm_weight, rope_cos, rope_sin, eps)``: q and keys are raw
         projection rows, normed and rotated at position ``offset`` inside the launch
         (``bfly_decode_step_qk_norm``: bf16, d = 128; rope tables [rows, 128] fp32).
@@ -170,15 +199,19 @@ class CompressedKVCache:
             out = torch.empty_like(q)
         if qk_norm is not None:
             qw, kw, cos, sin, eps = qk_norm
-            if cos.dtype != torch.float32 or cos.shape != sin.shape or cos.shape[-1] != d or not cos.is_contiguous() \
-                    or not sin.is_contiguous():
-                raise ValueError("rope tables must be contiguous fp32 [rows, head_dim]")
+            if cos.dtype != torch.float32 or cos.shape != sin.shape or cos.dim() != 2 or cos.shape[-1] != d or \
+                    not cos.is_contiguous() or not sin.is_contiguous() or cos.device != q.device or \
+                    sin.device != q.device:
+                raise ValueError("rope tables must be contiguous fp32 [rows, head_dim] on q's device")
+            for w in (qw, kw):
+                if w.dtype != torch.bfloat16 or tuple(w.shape) != (d,) or not w.is_contiguous() or w.device != q.device:
+                    raise ValueError("q/k norm weights must be contiguous bf16 [head_dim] on q's device")
             _native.call("bfly_decode_step_qk_norm", q.data_ptr(), _dtype_code(q), b, hq, int(keys.shape[1]), d,
                          keys.data_ptr(), values.data_ptr(), self._ring_k.data_ptr(), self._ring_v.data_ptr(),
                          self.tail_capacity, self._pool_k.data_ptr(), self._pool_v.data_ptr(), self.summary_capacity,
                          self._dev.data_ptr(), int(layer_idx), rule, int(local_window_blocks), int(sink_count),
-                         int(partner_count), self.block_size, int(local_window_tokens), _scale(scale, d),
-                         qw.data_ptr(), kw.data_ptr(), cos.data_ptr(), sin.data_ptr(), int(cos.shape[0]), float(eps),
+                         int(partner_count), self.block_size, int(local_window_tokens), self.local_window_tokens,
+                         _scale(scale, d), qw.data_ptr(), kw.data_ptr(), cos.data_ptr(), sin.data_ptr(), int(cos.shape[0]), float(eps),
                          out.data_ptr(), _stream(q))
             self._dev_dirty = True
             return out
@@ -186,7 +219,8 @@ class CompressedKVCache:
                      values.data_ptr(), self._ring_k.data_ptr(), self._ring_v.data_ptr(), self.tail_capacity,
                      self._pool_k.data_ptr(), self._pool_v.data_ptr(), self.summary_capacity, self._dev.data_ptr(),
                      int(layer_idx), rule, int(local_window_blocks), int(sink_count), int(partner_count),
-                     self.block_size, int(local_window_tokens), _scale(scale, d), out.data_ptr(), _stream(q))
+                     self.block_size, int(local_window_tokens), self.local_window_tokens, _scale(scale, d),
+                     out.data_ptr(), _stream(q))
         self._dev_dirty = True
         return out
 

@@ -63,13 +63,15 @@ constexpr int kDecMaxNew = 2;   // blocks pooled in one step (one per 128 steps 
 // kv_len has parity b, written during the step before it: word 0 a key
 // (kv_len | ns << 32 | W << 40 | rule << 48 | 1 << 62), word 1 layer_idx,
 // word 2 block_size | ring << 32, word 3 pool_rows | lwb << 32 | sinks << 40 |
-// partners << 48, words 4..11 the ns pool rows as int32.  A step uses it only
+// partners << 38 | cache window << 43, words 4..11 the ns pool rows as int32.  A step uses it only
 // when every word matches its own kv_len and arguments (anything else, a zero
 // key included, falls back to computing the row).  A launch reads the buffer
 // of its own parity and writes only the other one, so no word is read and
 // written within one launch.
 enum { kStOffset = 0, kStTail = 1, kStCount = 2, kStSumOff = 3 };
 constexpr int kStError = 4;
+constexpr int64_t kErrCapacity = 1;   // state[kStError]: tail or pool capacity exceeded
+constexpr int64_t kErrRope = 2;       // state[kStError]: position past the RoPE tables (fused q/k norm)
 constexpr int kStHeader = 8;
 constexpr int kStSlot = 32;
 constexpr int kStRoute = 4;
@@ -158,6 +160,7 @@ struct DecodeArgs {
   int64_t nsum;
   int64_t nblocks;
   int hq, hkv, bs, W;
+  int CW;                 // step mode: the cache's own local window (summarise and trim rules)
   float scale;
   FastDiv bs_div, ring_div, hkv_div;   // MFMA path: block_size, ring capacity, Hkv
   int gsz;                             // MFMA path: hq / hkv
@@ -224,7 +227,7 @@ __device__ __forceinline__ DecState dec_state(const DecodeArgs& a, const StepArg
     bool err = s.ts1 > a.ring;                              // tail capacity (compressed_cache.py:105-110)
     s.sc1 = s.sc0;
     s.so1 = s.so0;
-    while (!err && s.so1 + a.bs <= off1 - a.W) {            // summarise (:120-149)
+    while (!err && s.so1 + a.bs <= off1 - a.CW) {           // summarise (:120-149)
       const int64_t bstart = s.so1 - (off1 - s.ts1);
       if (bstart < 0 || bstart + a.bs > s.ts1) break;
       if (s.sc1 >= a.pool_rows || s.n_new == kDecMaxNew) {  // pool capacity (:128-132)
@@ -235,7 +238,7 @@ __device__ __forceinline__ DecState dec_state(const DecodeArgs& a, const StepArg
       ++s.sc1;
       s.so1 += a.bs;
     }
-    while (s.ts1 - a.bs >= a.W) s.ts1 -= a.bs;              // trim: target max(W, step + W - 1) = W
+    while (s.ts1 - a.bs >= a.CW) s.ts1 -= a.bs;             // trim: target max(CW, step + CW - 1) = CW
     s.err = err;
     s.kv_len = off1;
     s.tail_start = off1 - s.ts1;
@@ -356,7 +359,7 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
   // ---- this step's counters: from the arguments, or (step mode) derived on the device
   const DecState st = dec_state<kStep>(a, sa);
   if (kStep && st.err) {
-    if (tid == 0) sa.state[kStError] = 1;                 // the host raises at its next synchronisation
+    if (tid == 0) sa.state[kStError] = kErrCapacity;      // the host raises at its next synchronisation
     return;                                               // uniform: every workgroup sees the same counters
   }
   const int64_t kv_len = st.kv_len, tail_start = st.tail_start;
@@ -571,11 +574,11 @@ __device__ __forceinline__ DecState32 dec_advance32(int64_t off0, int64_t ts0, i
   {
     const bool range = (uint64_t)off0 < (uint64_t)kDecPosLimit && (uint64_t)ts0 < (uint64_t)kDecPosLimit &&
                        (uint64_t)sc0 < (uint64_t)kDecPosLimit && (uint64_t)so0 < (uint64_t)kDecPosLimit;
-    const int ring = (int)a.ring, bs = a.bs, W = a.W, pool_rows = (int)a.pool_rows;
+    const int ring = (int)a.ring, bs = a.bs, CW = a.CW, pool_rows = (int)a.pool_rows;
     const int off1 = (int)off0 + 1;
     int ts1 = (int)ts0 + 1, sc1 = (int)sc0, so1 = (int)so0, n_new = 0;
     bool err = !range || ts1 > ring;                        // tail capacity (compressed_cache.py:105-110)
-    while (!err && so1 + bs <= off1 - W) {                  // summarise (:120-149)
+    while (!err && so1 + bs <= off1 - CW) {                 // summarise (:120-149)
       const int bstart = so1 - (off1 - ts1);
       if (bstart < 0 || bstart + bs > ts1) break;
       if (sc1 >= pool_rows || n_new == kDecMaxNew) {        // pool capacity (:128-132)
@@ -586,7 +589,7 @@ __device__ __forceinline__ DecState32 dec_advance32(int64_t off0, int64_t ts0, i
       ++sc1;
       so1 += bs;
     }
-    while (ts1 - bs >= W) ts1 -= bs;                        // trim: target max(W, step + W - 1) = W
+    while (ts1 - bs >= CW) ts1 -= bs;                       // trim: target max(CW, step + CW - 1) = CW
     s.err = err;
     s.sc0 = (int)sc0;
     s.so0 = (int)so0;
@@ -706,8 +709,9 @@ __device__ __forceinline__ RouteKey route_key(int kv_len, int ns, const DecodeAr
           (1ll << 62);
   r.layer = sa.layer_idx;
   r.geom = (int64_t)(uint32_t)a.bs | (a.ring << 32);
-  r.shape = (int64_t)(uint32_t)a.pool_rows | ((int64_t)sa.lwb << 32) | ((int64_t)sa.sinks << 40) |
-            ((int64_t)sa.partners << 48);
+  // pool_rows < 2^30 (MFMA path), lwb, sinks, partners <= 15, CW < 2^20 (host checks)
+  r.shape = (int64_t)(uint32_t)a.pool_rows | ((int64_t)sa.lwb << 30) | ((int64_t)sa.sinks << 34) |
+            ((int64_t)sa.partners << 38) | ((int64_t)a.CW << 43);
   return r;
 }
 
@@ -724,7 +728,8 @@ __device__ __forceinline__ void dec_route_workgroup(const DecodeArgs& a, const S
   __shared__ int64_t hdr[4];
   const int64_t g_count = (int64_t)gridDim.x - kRouteGroups, g0 = blockIdx.x;
   const DecState32 st = dec_state32<true>(a, sa, g_count + g0);
-  if (st.err) return;                          // uniform: the attending workgroups report it
+  // uniform: the attending workgroups report it (and, like them, leave the copy as it was)
+  if (st.err || (a.qn_w != nullptr && st.kv_len - 1 >= a.rope_rows)) return;
   const DecState32 nx = dec_advance32(st.kv_len, st.ts1, st.sc1, st.so1, a, sa);
   if (!nx.err) {                               // uniform; else the next step computes its own row
     if (tid < 64) {
@@ -1035,7 +1040,7 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   // with the fused q/k norm, a position past the RoPE table is an error of the step
   constexpr bool qkn = kQkn && D == 128;
   if (kStep && (st.err || (qkn && st.kv_len - 1 >= a.rope_rows))) {
-    if (tid == 0) sa.state[kStError] = 1;
+    if (tid == 0) sa.state[kStError] = st.err ? kErrCapacity : kErrRope;
     return;
   }
   // the row-list entries of this step's route buffer that this thread's summary
@@ -1273,7 +1278,7 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
 static bool decode_on_mfma(const DecodeArgs& a, int d, bool step) {
   const int64_t lim = kDecPosLimit;
   const bool fits = a.kv_rows * d < lim && a.pool_rows * d < lim && a.ring < lim &&
-                    (step ? (a.pool_rows + 2) * a.bs + a.ring + a.W < lim
+                    (step ? (a.pool_rows + 2) * a.bs + a.ring + (a.W > a.CW ? a.W : a.CW) < lim
                           : a.kv_len < lim && a.nblocks < lim && a.nsum < lim);
   return a.scale > 0.f && fits;
 }
@@ -1365,7 +1370,7 @@ extern "C" int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int 
   a.kv_rows = ring_capacity ? ring_capacity : kv_len - tail_start;
   a.tail_start = tail_start; a.kv_len = kv_len;
   a.pool_rows = pool_capacity; a.nsum = summary_count; a.nblocks = num_blocks;
-  a.hq = hq; a.hkv = hkv; a.bs = block_size; a.W = window; a.scale = scale;
+  a.hq = hq; a.hkv = hkv; a.bs = block_size; a.W = window; a.CW = window; a.scale = scale;
   const StepArgs none{};
   if (dtype == BFLY_DTYPE_F32)
     launch_decode<float, false>(a, none, head_dim, batch * hkv, stream);
@@ -1384,7 +1389,7 @@ static int decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv,
                        const void* v_new, void* ring_k, void* ring_v, int64_t ring_capacity, void* pool_k,
                        void* pool_v, int64_t pool_capacity, int64_t* state, int64_t layer_idx, int partner_rule,
                        int local_window_blocks, int sink_count, int partner_count, int block_size, int window,
-                       float scale, void* out, const DecodeArgs* qkn, hipStream_t stream) {
+                       int cache_window, float scale, void* out, const DecodeArgs* qkn, hipStream_t stream) {
   BFLY_CHECK_ARG(dtype == BFLY_DTYPE_F32 || dtype == BFLY_DTYPE_BF16, "unsupported dtype %d", dtype);
   BFLY_CHECK_ARG(q && k_new && v_new && ring_k && ring_v && pool_k && pool_v && state && out, "null pointer");
   BFLY_CHECK_ARG(aligned16(q) && aligned16(out) && aligned16(ring_k) && aligned16(ring_v) && aligned16(pool_k) &&
@@ -1403,13 +1408,15 @@ static int decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv,
                      partner_count <= BFLY_MAX_PARTNERS &&
                      1 + local_window_blocks + partner_count + sink_count <= kDecMaxSum,
                  "bfly_decode_step: the routed row must fit %d slots", kDecMaxSum);
-  BFLY_CHECK_ARG(block_size > 0 && ring_capacity >= window + block_size && pool_capacity > 0,
-                 "bfly_decode_step: ring must hold W + BS rows and the pool at least one");
+  BFLY_CHECK_ARG(cache_window > 0 && cache_window < (1 << 20),
+                 "bfly_decode_step: cache_window=%d must be in [1, 2^20)", cache_window);
+  BFLY_CHECK_ARG(block_size > 0 && ring_capacity >= cache_window + block_size && pool_capacity > 0,
+                 "bfly_decode_step: ring must hold cache_window + BS rows and the pool at least one");
   DecodeArgs a{};
   a.q = q; a.out = out; a.k_new = k_new; a.v_new = v_new;
   a.ring_k = ring_k; a.ring_v = ring_v; a.pool_k = pool_k; a.pool_v = pool_v;
   a.ring = ring_capacity; a.kv_rows = ring_capacity; a.pool_rows = pool_capacity;
-  a.hq = hq; a.hkv = hkv; a.bs = block_size; a.W = window; a.scale = scale;
+  a.hq = hq; a.hkv = hkv; a.bs = block_size; a.W = window; a.CW = cache_window; a.scale = scale;
   if (qkn != nullptr) {
     BFLY_CHECK_ARG(dtype == BFLY_DTYPE_BF16 && head_dim == 128 && decode_on_mfma(a, head_dim, true),
                    "bfly_decode_step_qk_norm: bf16, head_dim 128 and a positive scale only");
@@ -1429,19 +1436,19 @@ extern "C" int bfly_decode_step(const void* q, int dtype, int64_t batch, int hq,
                                 const void* k_new, const void* v_new, void* ring_k, void* ring_v,
                                 int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity,
                                 int64_t* state, int64_t layer_idx, int partner_rule, int local_window_blocks,
-                                int sink_count, int partner_count, int block_size, int window, float scale,
-                                void* out, hipStream_t stream) {
+                                int sink_count, int partner_count, int block_size, int window, int cache_window,
+                                float scale, void* out, hipStream_t stream) {
   return decode_step(q, dtype, batch, hq, hkv, head_dim, k_new, v_new, ring_k, ring_v, ring_capacity, pool_k, pool_v,
                      pool_capacity, state, layer_idx, partner_rule, local_window_blocks, sink_count, partner_count,
-                     block_size, window, scale, out, nullptr, stream);
+                     block_size, window, cache_window, scale, out, nullptr, stream);
 }
 
 extern "C" int bfly_decode_step_qk_norm(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,
                                         const void* k_new, const void* v_new, void* ring_k, void* ring_v,
                                         int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity,
                                         int64_t* state, int64_t layer_idx, int partner_rule, int local_window_blocks,
-                                        int sink_count, int partner_count, int block_size, int window, float scale,
-                                        const void* q_norm_weight, const void* k_norm_weight, const float* rope_cos,
+                                        int sink_count, int partner_count, int block_size, int window,
+                                        int cache_window, float scale, const void* q_norm_weight, const void* k_norm_weight, const float* rope_cos,
                                         const float* rope_sin, int64_t rope_rows, float eps, void* out,
                                         hipStream_t stream) {
   BFLY_CHECK_ARG(q_norm_weight && k_norm_weight && rope_cos && rope_sin, "null pointer");
@@ -1457,5 +1464,5 @@ extern "C" int bfly_decode_step_qk_norm(const void* q, int dtype, int64_t batch,
   n.qk_eps = eps;
   return decode_step(q, dtype, batch, hq, hkv, head_dim, k_new, v_new, ring_k, ring_v, ring_capacity, pool_k, pool_v,
                      pool_capacity, state, layer_idx, partner_rule, local_window_blocks, sink_count, partner_count,
-                     block_size, window, scale, out, &n, stream);
+                     block_size, window, cache_window, scale, out, &n, stream);
 }

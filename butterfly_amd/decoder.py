@@ -134,10 +134,20 @@ class QuantLinear(nn.Module):
             row += n
         return fused
 
+    @property
+    def gemv_from_codes(self) -> bool:
+        """Whether ``bfly_q4_gemv`` takes this layer's shape: groups of a multiple of 32 codes
+        and at most 8192 inputs (the kernel keeps a lane's inputs in registers)."""
+        return self.group % Q4_PIECE_CODES == 0 and self.in_features <= Q4_MAX_IN
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if _one_row(x):
+        if _one_row(x) and self.gemv_from_codes:
             return q4_gemv(x, self)
         return _linear(x, self.weight)
+
+
+# shape limits of bfly_q4_gemv / bfly_q4_gemv_silu (include/butterfly_amd_decoder.h)
+Q4_PIECE_CODES, Q4_MAX_IN = 32, 8192
 
 
 def _one_row(x: torch.Tensor) -> bool:
@@ -386,7 +396,7 @@ class MLP(nn.Module):
         self.gate_up = QuantLinear.fuse_rows(self.gate_proj, self.up_proj)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if _one_row(x):
+        if _one_row(x) and self.gate_up.gemv_from_codes:
             return self.down_proj(q4_gemv_silu(x, self.gate_up))
         if _hip(x):
             gu = self.gate_up(x)                           # [..., 2f]: gate columns, then up columns
@@ -446,7 +456,7 @@ class Decoder(nn.Module):
     def _logits(self, h: torch.Tensor) -> torch.Tensor:
         """Tied lm_head for a few rows [B, hidden]: one row on the GPU from the 4-bit codes,
         else embed @ h^T over the dequantized table."""
-        if _one_row(h):
+        if _one_row(h) and self.lm_head.gemv_from_codes:
             return q4_gemv(h, self.lm_head)
         return torch.matmul(self.embed_tokens, h.t()).t()
 

@@ -153,9 +153,14 @@ class ButterflyAttentionCore:
 
     def fuses_qk_norm(self, cache, q_len: int, head_dim: int, dtype) -> bool:
         """Whether ``__call__`` takes ``qk_norm`` for this step: a device-counter decode step of
-        bf16 rows with head_dim 128 (``bfly_decode_step_qk_norm``)."""
+        bf16 rows with head_dim 128 that runs on the MFMA kernel (``bfly_decode_step_qk_norm``:
+        positive scale, 32-bit positions and offsets)."""
+        from .attention import _scale
+
         return (isinstance(cache, CompressedKVCache) and cache.device_counters is not None and q_len == 1
-                and self.cfg.butterfly_decode_backend != "dense" and head_dim == 128 and dtype == torch.bfloat16)
+                and self.cfg.butterfly_decode_backend != "dense" and head_dim == 128 and dtype == torch.bfloat16
+                and cache.step_on_mfma(head_dim, int(self.cfg.compressed_local_window_tokens),
+                                       _scale(self.scale, head_dim), dtype))
 
     def __call__(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                  cache: Optional[CompressedKVCache] = None, qk_norm=None) -> torch.Tensor:

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define BFLY_ABI_VERSION 1
+#define BFLY_ABI_VERSION 2
 
 #define BFLY_OK 0
 #define BFLY_ERR_INVALID (-1)     /* bad shape / argument: ValueError in the reference */
@@ -287,10 +287,13 @@ int64_t bfly_decode_state_words(int64_t batch, int hkv);
  * Device: one decode step with the cache counters held on the device, so a
  * step has fixed arguments and can be captured in a HIP graph.  Same result as
  * CompressedKVCache.update_and_fetch of one token (bna/mlx/compressed_cache.py:94-172:
- * append, summarise every block with end + W <= offset, trim whole blocks while
- * tail_size - BS >= W) followed by compressed_butterfly_attention_from_cache for
- * that token (bna/mlx/attention.py:1816-1876), with the layout of the live
- * kv_len (stage = layer_idx mod stage_count at ceil(kv_len / BS) blocks).
+ * append, summarise every block with end + cache_window <= offset, trim whole
+ * blocks while tail_size - BS >= cache_window, where cache_window is the cache's
+ * own local_window_tokens) followed by compressed_butterfly_attention_from_cache
+ * for that token with the attention window `window` (bna/mlx/attention.py:1816-1876),
+ * with the layout of the live kv_len (stage = layer_idx mod stage_count at
+ * ceil(kv_len / BS) blocks).  cache_window in [1, 2^20); the ring must hold
+ * cache_window + BS rows.
  * state: device int64[bfly_decode_state_words(batch, hkv)]: state[4] is the
  * error word; copy g (32 words at state[8 + 32g ..], g = b*Hkv + kv head, and
  * g = batch*Hkv + 0..7 for the route workgroups) holds {offset, tail_size,
@@ -300,15 +303,16 @@ int64_t bfly_decode_state_words(int64_t batch, int hkv);
  * the kernel uses an entry only when it names the step's kv_len and
  * arguments).  On a capacity
  * overflow the step changes nothing and sets state[4] = 1 (the reference's
- * RuntimeError; read it back to raise).
+ * RuntimeError; read it back to raise); later steps then change nothing either
+ * until the host rewrites the counters.
  * Other arguments as bfly_decode; ring_k/ring_v is the ring (capacity > 0).
  */
 int bfly_decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,
                      const void* k_new, const void* v_new, void* ring_k, void* ring_v,
                      int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity,
                      int64_t* state, int64_t layer_idx, int partner_rule, int local_window_blocks,
-                     int sink_count, int partner_count, int block_size, int window, float scale,
-                     void* out, hipStream_t stream);
+                     int sink_count, int partner_count, int block_size, int window, int cache_window,
+                     float scale, void* out, hipStream_t stream);
 
 /*
  * Device: bfly_decode_step for a decoder whose attention applies per-head q/k
@@ -320,7 +324,7 @@ int bfly_decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv, i
  * bfly_decode_step does.  The q and k rows are bit-identical to
  * bfly_qk_norm_rope's (include/butterfly_amd_decoder.h).  bf16, head_dim 128
  * only (else BFLY_ERR_INVALID).  A position at or past rope_rows sets the step
- * error flag, like a capacity overflow.  Replaces the projection tail of the
+ * error word to 2 (state[4] = 2; a capacity overflow sets 1) and changes nothing.  Replaces the projection tail of the
  * swapped attention (bna/integrations/qwen_torch.py:550-562, qwen_mlx.py:288-357)
  * and the step of bfly_decode_step (bna/mlx/compressed_cache.py:94-172,
  * bna/mlx/attention.py:1816-1876) in one launch.
@@ -329,8 +333,8 @@ int bfly_decode_step_qk_norm(const void* q, int dtype, int64_t batch, int hq, in
                              const void* k_new, const void* v_new, void* ring_k, void* ring_v,
                              int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity,
                              int64_t* state, int64_t layer_idx, int partner_rule, int local_window_blocks,
-                             int sink_count, int partner_count, int block_size, int window, float scale,
-                             const void* q_norm_weight, const void* k_norm_weight, const float* rope_cos,
+                             int sink_count, int partner_count, int block_size, int window, int cache_window,
+                             float scale, const void* q_norm_weight, const void* k_norm_weight, const float* rope_cos,
                              const float* rope_sin, int64_t rope_rows, float eps, void* out, hipStream_t stream);
 
 /*

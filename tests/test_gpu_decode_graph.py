@@ -84,6 +84,63 @@ def test_device_counter_steps_follow_changing_arguments():
             dev._push()
 
 
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float32, 64)])
+def test_cache_window_differs_from_attention_window(dtype, d):
+    """The cache's own window (128, the reference's default) decides summarising and
+    trimming; the attention window (64) only the keys a query sees
+    (bna/mlx/compressed_cache.py:120-164).  Device step, host path and the oracle cache
+    must agree on counters, pools and outputs."""
+    from oracle.cache import OracleCompressedKVCache
+
+    b, hq, hkv, layer, prompt, steps, cw, w = 2, 8, 2, 3, 333, 300, 128, 64
+    total = prompt + steps
+    q = _rand(91, (b, hq, total, d), dtype)
+    k = _rand(92, (b, hkv, total, d), dtype)
+    v = _rand(93, (b, hkv, total, d), dtype)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    host = bf.CompressedKVCache(block_size=128, local_window_tokens=cw, max_kv_size=total)
+    dev = bf.CompressedKVCache(block_size=128, local_window_tokens=cw, max_kv_size=total)
+    ref = OracleCompressedKVCache(block_size=128, local_window_tokens=cw, max_kv_size=total)
+    host.update(kd[:, :, :prompt], vd[:, :, :prompt])
+    dev.update(kd[:, :, :prompt], vd[:, :, :prompt])
+    ref.update_and_fetch(k[:, :, :prompt], v[:, :, :prompt])
+    dev.use_device_counters()
+    grp = hq // hkv
+    rep = lambda x: x.repeat_interleave(grp, dim=1)
+    for p in range(prompt, total):
+        a = host.update_and_attend(qd[:, :, p:p + 1], kd[:, :, p:p + 1], vd[:, :, p:p + 1],
+                                   layout=_layout(p + 1, hkv, grp, layer), local_window_tokens=w)
+        c = dev.decode_step(qd[:, :, p:p + 1], kd[:, :, p:p + 1], vd[:, :, p:p + 1], layer_idx=layer,
+                            local_window_tokens=w)
+        assert torch.equal(a, c), p
+        ref.update_and_fetch(k[:, :, p:p + 1], v[:, :, p:p + 1])
+        assert (host.offset, host.tail_size, host.summary_count, host.summary_offset) == \
+               (ref.offset, ref.tail_size, ref.summary_count, ref.summary_offset), p
+        tk, tv, sk, sv, ts, kv_len = ref.get_compressed_state()
+        lay = tp.build_layout(seq_len=kv_len, block_size=128, num_key_value_heads=hkv, num_key_value_groups=grp,
+                              layer_idx=layer, local_window_blocks=1, sink_count=1, partner_count=1,
+                              partner_rule="causal_shift")
+        want = oa.from_cache(q[:, :, p:p + 1], rep(tk), rep(tv), rep(sk), rep(sv), layout=lay,
+                             query_positions=torch.tensor([p]), W=w, tail_start=ts, kv_len=kv_len)
+        got, want = c.float().cpu(), want.float()
+        err = (got - want).abs().max().item()
+        if dtype == torch.float32:
+            assert err <= 1e-5, (p, err)
+        else:
+            assert err <= 2e-2 and ((got - want).norm() / want.norm()).item() <= 1e-2, (p, err)
+    dev.sync()
+    assert (dev.offset, dev.tail_size, dev.summary_count, dev.summary_offset) == \
+           (ref.offset, ref.tail_size, ref.summary_count, ref.summary_offset)
+    assert ref.tail_size >= cw                       # the tail holds the cache window, not the attention's
+    assert torch.equal(dev.keys, host.keys) and torch.equal(dev.k_summary, host.k_summary)
+    assert torch.equal(dev.keys.cpu(), ref.keys)
+    # pooled rows: fp32 means in another summation order, within one rounding of the oracle's
+    tol = 1e-6 if dtype == torch.float32 else 2 ** -7
+    for got_pool, want_pool in ((dev.k_summary, ref.k_summary), (dev.v_summary, ref.v_summary)):
+        diff = (got_pool.float().cpu() - want_pool.float()).abs()
+        assert (diff <= tol * want_pool.float().abs().clamp_min(1.0)).all()
+
+
 def test_device_counter_overflow_raises_at_sync():
     cache = bf.CompressedKVCache(block_size=4, local_window_tokens=4, max_kv_size=12)   # 7 summary slots
     kv = torch.randn(1, 1, 8, 64, device="cuda").bfloat16()

@@ -19,44 +19,53 @@ CFG = DecoderConfig(vocab_size=256, hidden_size=512, num_layers=1, num_heads=4, 
                     intermediate_size=512)
 
 
-def _setup(prompt_len, rope_rows, seed=0):
+def _setup(prompt_len, rope_rows, seed=0, cfg=CFG, batch=1, cache_window=64):
     g = torch.Generator(device="cuda").manual_seed(seed)
-    attn = Attention(CFG, generator=g, device="cuda")
+    attn = Attention(cfg, generator=g, device="cuda")
     for norm in (attn.q_norm, attn.k_norm):
-        norm.weight.data = (1 + 0.3 * torch.randn(CFG.head_dim, generator=g, device="cuda")).bfloat16()
-    cos, sin = rope_cos_sin(torch.arange(rope_rows, device="cuda"), CFG.head_dim, CFG.rope_theta)
-    k = torch.randn(1, CFG.num_kv_heads, prompt_len, CFG.head_dim, generator=g, device="cuda").bfloat16()
-    v = torch.randn(1, CFG.num_kv_heads, prompt_len, CFG.head_dim, generator=g, device="cuda").bfloat16()
+        norm.weight.data = (1 + 0.3 * torch.randn(cfg.head_dim, generator=g, device="cuda")).bfloat16()
+    cos, sin = rope_cos_sin(torch.arange(rope_rows, device="cuda"), cfg.head_dim, cfg.rope_theta)
+    k = torch.randn(batch, cfg.num_kv_heads, prompt_len, cfg.head_dim, generator=g, device="cuda").bfloat16()
+    v = torch.randn(batch, cfg.num_kv_heads, prompt_len, cfg.head_dim, generator=g, device="cuda").bfloat16()
     caches = []
     for _ in range(2):
-        c = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=prompt_len + 400)
+        c = bf.CompressedKVCache(block_size=128, local_window_tokens=cache_window, max_kv_size=prompt_len + 400)
         c.update_and_fetch(k, v)
         c.use_device_counters()
         caches.append(c)
     return attn, cos.contiguous(), sin.contiguous(), caches, g
 
 
-def _raw(qkv):
-    row = qkv.view(-1)
-    nq, nkv = CFG.num_heads * CFG.head_dim, CFG.num_kv_heads * CFG.head_dim
-    return (row[:nq].view(1, CFG.num_heads, 1, CFG.head_dim), row[nq:nq + nkv].view(1, CFG.num_kv_heads, 1, CFG.head_dim),
-            row[nq + nkv:].view(1, CFG.num_kv_heads, 1, CFG.head_dim))
+def _raw(qkv, cfg=CFG):
+    """Raw q, k, v rows of a fused projection output [B, 1, (Hq + 2 Hkv) d]: views for batch 1."""
+    b = qkv.shape[0]
+    row = qkv.view(b, -1)
+    nq, nkv = cfg.num_heads * cfg.head_dim, cfg.num_kv_heads * cfg.head_dim
+    return (row[:, :nq].reshape(b, cfg.num_heads, 1, cfg.head_dim),
+            row[:, nq:nq + nkv].reshape(b, cfg.num_kv_heads, 1, cfg.head_dim),
+            row[:, nq + nkv:].reshape(b, cfg.num_kv_heads, 1, cfg.head_dim))
 
 
-@pytest.mark.parametrize("layer_idx", [0, 5])
-def test_fused_qk_norm_step_equals_separate_launches(layer_idx):
+# GQA groups of 20 heads (two 16-column MFMA passes, the q transform redone for the
+# second) and batch 3; the cache window of 128 differs from the attention window of 64
+@pytest.mark.parametrize("layer_idx,heads,batch,cache_window", [(0, (4, 2), 1, 64), (5, (4, 2), 1, 64),
+                                                                (2, (40, 2), 1, 64), (3, (8, 2), 3, 128)])
+def test_fused_qk_norm_step_equals_separate_launches(layer_idx, heads, batch, cache_window):
     prompt = 700
-    attn, cos, sin, (ca, cb), g = _setup(prompt, 1024, seed=layer_idx)
+    cfg = DecoderConfig(vocab_size=256, hidden_size=512, num_layers=1, num_heads=heads[0], num_kv_heads=heads[1],
+                        head_dim=128, intermediate_size=512)
+    attn, cos, sin, (ca, cb), g = _setup(prompt, 1024, seed=layer_idx, cfg=cfg, batch=batch,
+                                         cache_window=cache_window)
     core = bf.ButterflyAttentionCore(bf.QwenButterflyConfig(), layer_idx)
-    assert core.fuses_qk_norm(cb, 1, CFG.head_dim, torch.bfloat16)
+    assert core.fuses_qk_norm(cb, 1, cfg.head_dim, torch.bfloat16)
     qk = (attn.q_norm.weight, attn.k_norm.weight, cos, sin, attn.q_norm.eps)
     for step in range(150):            # crosses block ends: appends, trims and pooling
         pos = prompt + step
-        x = torch.randn(1, 1, CFG.hidden_size, generator=g, device="cuda").bfloat16()
+        x = torch.randn(batch, 1, cfg.hidden_size, generator=g, device="cuda").bfloat16()
         qkv = attn.qkv(x)
         q, k, v = attn.heads(qkv, None, rope=(cos[pos:pos + 1], sin[pos:pos + 1]))
         oa = core(q, k, v, ca)
-        ob = core(*_raw(qkv), cb, qk_norm=qk)
+        ob = core(*_raw(qkv, cfg), cb, qk_norm=qk)
         assert torch.equal(oa, ob), (step, (oa.float() - ob.float()).abs().max().item(), oa.float().abs().max().item())
     ca.sync()
     cb.sync()
@@ -76,8 +85,19 @@ def test_fused_step_past_the_rope_table_is_an_error_at_sync():
              qk_norm=qk)
     cb.sync()
     core(*_raw(attn.qkv(torch.randn(1, 1, CFG.hidden_size, generator=g, device="cuda").bfloat16())), cb, qk_norm=qk)
-    with pytest.raises(RuntimeError):
+    with pytest.raises(RuntimeError, match="RoPE"):
         cb.sync()
+    # the failed step changed nothing: the cache holds the last good state
+    assert cb.offset == prompt + 2
+
+
+def test_fused_step_refuses_bad_norm_weights():
+    attn, cos, sin, (_, cb), g = _setup(200, 512)
+    core = bf.ButterflyAttentionCore(bf.QwenButterflyConfig(), 0)
+    raw = _raw(attn.qkv(torch.randn(1, 1, CFG.hidden_size, generator=g, device="cuda").bfloat16()))
+    for qw in (attn.q_norm.weight.float(), attn.q_norm.weight[:64], attn.q_norm.weight.cpu()):
+        with pytest.raises(ValueError):
+            core(*raw, cb, qk_norm=(qw, attn.k_norm.weight, cos, sin, 1e-6))
 
 
 def test_qk_norm_is_refused_off_the_device_counter_path():

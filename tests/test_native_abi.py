@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
     for name in sorted(_declared_symbols()):
         assert hasattr(lib, name), name
     assert set(_native.SIGNATURES) == _declared_symbols()
-    assert lib.bfly_abi_version() == 1
+    assert lib.bfly_abi_version() == 2
 
 
 @pytest.mark.parametrize("rule", list(tp.RULES))
@@ -117,7 +117,7 @@ def test_decode_step_qk_norm_validates_before_launch():
     head_dim other than 128 are refused before any launch."""
     lib = _native.lib()
     base = (256, _native.DTYPE_BF16, 1, 8, 2, 128, 512, 768, 1024, 1280, 256, 1536, 1792, 16, 2048, 0, 3, 1, 1, 1,
-            128, 64, 0.088)
+            128, 64, 64, 0.088)
     tail = (64, 1e-6, 0x3000, None)                    # rope_rows, eps, out, stream
     assert lib.bfly_decode_step_qk_norm(*base, None, 0x2100, 0x2200, 0x2300, *tail) == _native.ERR_INVALID
     assert lib.bfly_decode_step_qk_norm(*base, 0x2000, 0x2100, 0x2208, 0x2300, *tail) == _native.ERR_INVALID
@@ -125,3 +125,13 @@ def test_decode_step_qk_norm_validates_before_launch():
     d64 = base[:5] + (64,) + base[6:]
     assert lib.bfly_decode_step_qk_norm(*d64, 0x2000, 0x2100, 0x2200, 0x2300, *tail) == _native.ERR_INVALID
     assert b"head_dim 128" in lib.bfly_last_error()
+
+
+def test_decode_step_checks_the_cache_window_before_launch():
+    """The cache's own window must be positive, below 2^20, and fit the ring with a block."""
+    lib = _native.lib()
+    head = (256, _native.DTYPE_BF16, 1, 8, 2, 128, 512, 768, 1024, 1280, 256, 1536, 1792, 16, 2048, 0, 3, 1, 1, 1,
+            128, 64)
+    for cw in (0, 200, 1 << 20):                      # 200 + 128 rows do not fit a ring of 256
+        assert lib.bfly_decode_step(*head, cw, 0.088, 0x3000, None) == _native.ERR_INVALID
+        assert b"cache_window" in lib.bfly_last_error()

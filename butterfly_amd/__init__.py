@@ -27,8 +27,14 @@ from .integrations import (
 from .layout import BlockButterflyLayout, build_block_butterfly_layout, clear_layout_cache
 from .streams import compressed_stream_attention, online_softmax_merge, swa_stream_attention
 from .topology import (
+    ROLE_ORDER,
     ButterflyLayoutMetadata,
+    NeighborSpec,
     block_neighbor_table,
+    build_butterfly_neighbor_role_row,
+    build_butterfly_role_map,
+    butterfly_partner_block,
+    ordered_roles,
     butterfly_layout_metadata,
     butterfly_partner_bits,
     butterfly_stage_count,
@@ -49,6 +55,12 @@ __all__ = [
     "swap_qwen_attention_with_butterfly",
     "BlockButterflyLayout",
     "ButterflyLayoutMetadata",
+    "NeighborSpec",
+    "ROLE_ORDER",
+    "build_butterfly_neighbor_role_row",
+    "build_butterfly_role_map",
+    "butterfly_partner_block",
+    "ordered_roles",
     "CompressedKVCache",
     "block_mean_summaries",
     "block_neighbor_table",

@@ -130,3 +130,93 @@ def block_neighbor_table(*, num_blocks: int, layer_idx: int, partner_rule: str, 
                                                 partner_count=partner_count, device=device)
     k = max(1, int(degree.max().item()))
     return table[:, :k].contiguous()
+
+
+# ----------------------------------------------------------------------------- role-annotated rows
+@dataclass(frozen=True)
+class NeighborSpec:
+    """One entry of a role-annotated neighbour row.  Reference: bna/topology/butterfly.py:20-23."""
+
+    neighbor: int
+    roles: tuple[str, ...]
+
+
+def butterfly_partner_block(*, block_idx: int, bit_idx: int, num_blocks: int, partner_rule: str,
+                            width: int | None = None) -> int | None:
+    """Partner of ``block_idx`` along ``bit_idx`` under the rule, or None when it falls outside
+    ``[0, min(block_idx, num_blocks - 1)]``.  Reference: bna/topology/butterfly.py:108-141 (the
+    same function the kernels evaluate in ``bfly_topology.h``)."""
+    rule = str(partner_rule)
+    _rule_code(rule)
+    b, bit = int(block_idx), int(bit_idx)
+    w = butterfly_width(num_blocks) if width is None else int(width)
+    if bit < 0 or bit >= max(1, w):
+        return None
+    if rule == "causal_shift":
+        p = b - (1 << bit)
+    elif rule in ("xor", "benes"):
+        p = b ^ (1 << bit)
+    elif rule == "fixed_stride":
+        p = b - 1
+    elif rule == "random":
+        if b <= 0:
+            return None
+        p = ((b * 2654435761 + bit * 374761393) & 0xFFFFFFFF) % b
+    else:                                                     # bit_reversal over w bits
+        rev = int(format(b, f"0{w}b")[::-1], 2) if w > 0 else 0
+        flipped = rev ^ (1 << bit)
+        p = int(format(flipped, f"0{w}b")[::-1], 2)
+    if p < 0 or p >= int(num_blocks) or p > b:
+        return None
+    return int(p)
+
+
+def build_butterfly_role_map(*, block_idx: int, num_blocks: int, local_window_blocks: int, sink_blocks,
+                             partner_bits, partner_rule: str, width: int | None = None) -> dict[int, set[str]]:
+    """Neighbour block -> the roles it plays for ``block_idx`` (self, local, partner, sink).
+    Reference: bna/topology/butterfly.py:183-216."""
+    roles: dict[int, set[str]] = {int(block_idx): {"self"}}
+    for off in range(1, int(local_window_blocks) + 1):
+        if int(block_idx) - off < 0:
+            break
+        roles.setdefault(int(block_idx) - off, set()).add("local")
+    for bit in partner_bits:
+        p = butterfly_partner_block(block_idx=block_idx, bit_idx=bit, num_blocks=num_blocks,
+                                    partner_rule=partner_rule, width=width)
+        if p is not None:
+            roles.setdefault(p, set()).add("partner")
+    for s in sink_blocks:
+        if 0 <= int(s) < int(num_blocks):
+            roles.setdefault(int(s), set()).add("sink")
+    return roles
+
+
+def ordered_roles(roles) -> tuple[str, ...]:
+    """Roles in ``ROLE_ORDER``.  Reference: bna/topology/butterfly.py:264-265."""
+    return tuple(r for r in ROLE_ORDER if r in roles)
+
+
+def build_butterfly_neighbor_role_row(*, block_idx: int, metadata: ButterflyLayoutMetadata) -> list[NeighborSpec]:
+    """The ordered unique row ``[b, b-1..b-lwb, partners, sinks]`` (entries in ``[0, N)``, first
+    occurrence kept) with each entry's roles.  The neighbour order is the row of the device
+    table ``bfly_block_neighbors``.  Reference: bna/topology/butterfly.py:219-262, 275-284."""
+    m = metadata
+    b = int(block_idx)
+    role_map = build_butterfly_role_map(block_idx=b, num_blocks=m.num_blocks,
+                                        local_window_blocks=m.local_window_blocks, sink_blocks=m.sink_blocks,
+                                        partner_bits=m.partner_bits, partner_rule=m.partner_rule, width=m.width)
+    cand = [b] + [b - off for off in range(1, m.local_window_blocks + 1)]
+    for bit in m.partner_bits:
+        p = butterfly_partner_block(block_idx=b, bit_idx=bit, num_blocks=m.num_blocks, partner_rule=m.partner_rule,
+                                    width=m.width)
+        if p is not None:
+            cand.append(p)
+    cand += [int(s) for s in m.sink_blocks]
+    seen: set[int] = set()
+    row: list[NeighborSpec] = []
+    for v in cand:
+        if v < 0 or v >= m.num_blocks or v in seen:
+            continue
+        seen.add(v)
+        row.append(NeighborSpec(neighbor=v, roles=ordered_roles(role_map.get(v, {"self"}))))
+    return row

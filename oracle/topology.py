@@ -146,3 +146,31 @@ def build_layout(*, seq_len: int, block_size: int, num_key_value_heads: int, num
         partner_rule=partner_rule, partner_count=partner_count,
         sink_blocks=tuple(range(min(sink_count, n))),
     )
+
+
+ROLE_BITS = {"self": 1, "local": 2, "partner": 4, "sink": 8}
+
+
+def role_row(block: int, num_blocks: int, layer_idx: int, rule: str, local_window_blocks: int, sink_count: int,
+             partner_count: int) -> list[tuple[int, int]]:
+    """``neighbor_row`` with each entry's role bits (self 1, local 2, partner 4, sink 8).
+
+    butterfly.py:183-262: a block's roles are every reason it enters the row (a
+    partner that is also the previous block is local and partner).
+    """
+    w = width(num_blocks)
+    s, count = stage_meta(num_blocks, layer_idx, rule)
+    bits = partner_bits(s, count, w, partner_count, rule)
+    roles = {block: ROLE_BITS["self"]}
+    for off in range(1, local_window_blocks + 1):
+        if block - off < 0:
+            break
+        roles[block - off] = roles.get(block - off, 0) | ROLE_BITS["local"]
+    for bit in bits:
+        p = partner_block(block, bit, num_blocks, rule, w)
+        if p is not None:
+            roles[p] = roles.get(p, 0) | ROLE_BITS["partner"]
+    for sk in range(min(sink_count, num_blocks)):
+        roles[sk] = roles.get(sk, 0) | ROLE_BITS["sink"]
+    return [(v, roles[v]) for v in neighbor_row(block, num_blocks, layer_idx, rule, local_window_blocks,
+                                                sink_count, partner_count)]

@@ -26,6 +26,27 @@ def test_neighbor_table_bit_exact(n, rule):
             assert torch.equal(got.cpu().long(), want), (n, rule, layer, lwb, sinks, partners)
 
 
+def test_neighbor_table_matches_reference_role_rows():
+    """Device tables of every rule (fixed_stride and random included) against the rows the
+    reference's topology module wrote (tests/golden/golden_roles.npz)."""
+    from pathlib import Path
+
+    import numpy as np
+
+    roles = np.load(Path(__file__).resolve().parent / "golden" / "golden_roles.npz")
+    checked = 0
+    for key in roles.files:
+        if key.endswith("/stage"):
+            continue
+        _, rule, n, layer, params = key.split("/")
+        lwb, sinks, partners = (int(x) for x in params.split("-"))
+        got = bf.block_neighbor_table(num_blocks=int(n[1:]), layer_idx=int(layer[1:]), partner_rule=rule,
+                                      local_window_blocks=lwb, sink_count=sinks, partner_count=partners)
+        assert torch.equal(got.cpu().long(), torch.from_numpy(roles[key][:, :, 0].astype(np.int64))), key
+        checked += 1
+    assert checked >= 1500
+
+
 def test_layout_metadata_and_heads():
     lay = bf.build_block_butterfly_layout(seq_len=65536, block_size=128, num_key_value_heads=2,
                                           num_key_value_groups=4, layer_idx=12, local_window_blocks=1,

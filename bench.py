@@ -412,7 +412,7 @@ def bench_stream(torch, bf, seed=0, T=262144, chunk=384, layer=5):
     for s in range(0, T, chunk):
         n = min(chunk, T - s)
         chunks.append(tuple(torch.randn(1, h, n, d, generator=g, device=dev).bfloat16() for h in (hq, hkv, hkv)))
-    cfg = bf.QwenButterflyConfig()
+    cfg = bf.compressed_butterfly_config()
 
     def run():
         cache = bf.CompressedKVCache(block_size=bs, local_window_tokens=W, max_kv_size=T, max_chunk_size=512)
@@ -457,7 +457,7 @@ def bench_decoder(torch, bf, seed=0, prompt_len=32768, new_tokens=32, agree_prom
     cfg = DecoderConfig()
     model = Decoder(cfg, seed=seed, device=dev)
     cpu_model = copy.deepcopy(model).to("cpu") if cpu_agreement else None
-    bcfg = bf.QwenButterflyConfig()
+    bcfg = bf.compressed_butterfly_config()
     bf.swap_qwen_attention_with_butterfly(model, cfg=bcfg)
     prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=torch.Generator().manual_seed(seed + 1))
     pd = prompt.to(dev)

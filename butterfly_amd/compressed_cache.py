@@ -191,6 +191,9 @@ class CompressedKVCache:
         if tuple(keys.shape[:2]) != tuple(self._ring_k.shape[:2]) or keys.shape[3] != self._ring_k.shape[3] or \
                 keys.dtype != self._ring_k.dtype or q.dtype != keys.dtype:
             raise ValueError("q/keys do not match the cache's batch/head/dim/dtype")
+        dev = self._ring_k.device
+        if q.device != dev or keys.device != dev or values.device != dev or (out is not None and out.device != dev):
+            raise ValueError(f"decode_step tensors must be on the cache's device {dev}")
         rule = _native.RULES.get(str(partner_rule))
         if rule is None:
             raise ValueError(f"Unsupported Butterfly partner rule: {partner_rule!r}")

@@ -20,10 +20,16 @@ forms written below, which are the model's definition and what a CPU copy of
 the model runs.
 
 ``swap_qwen_attention_with_butterfly(model, cfg=...)`` replaces every
-attention by :class:`ButterflyAttention`, which keeps the projections, norms
-and RoPE and routes the attention core through the HIP kernels
-(:class:`butterfly_amd.ButterflyAttentionCore`).  The stock attention that it
-replaces is plain causal GQA softmax attention (PyTorch SDPA).
+attention by :class:`ButterflyAttention` (registered for :class:`Attention`), a
+``QwenButterflyAttention`` that keeps the projections, norms and RoPE, routes
+the attention core through the HIP kernels
+(:class:`butterfly_amd.ButterflyAttentionCore`) and adds this model's fused
+projection paths.  The attention exposes the attribute set the generic swapped
+module reads (``n_heads``, ``n_kv_heads``, ``head_dim``, ``scale``, the
+projections and norms), so ``QwenButterflyAttention`` itself also wraps it.  The
+stock attention that it replaces is plain causal GQA softmax attention (PyTorch
+SDPA).  Attention modules take ``(x, mask=None, cache=None, *,
+position_embeddings=(cos, sin))``, the RoPE rows of the call's positions.
 """
 from __future__ import annotations
 
@@ -38,7 +44,7 @@ import torch.nn.functional as F
 
 from . import _native
 from ._device import on, stream_of
-from .integrations import ButterflyAttentionCore, QwenButterflyConfig
+from .integrations import QwenButterflyAttention, QwenButterflyConfig, register_butterfly_attention
 
 
 @dataclass
@@ -286,6 +292,8 @@ class Attention(nn.Module):
         self.o_proj = QuantLinear(cfg.num_heads * d, h, generator=generator, device=device, group=cfg.quant_group)
         self.q_norm = RMSNorm(d, cfg.rms_eps, device)
         self.k_norm = RMSNorm(d, cfg.rms_eps, device)
+        self.n_heads, self.n_kv_heads, self.head_dim = cfg.num_heads, cfg.num_kv_heads, d
+        self.scale = d ** -0.5
         # q, k and v weights as row ranges of one [Hq*d + 2*Hkv*d, hidden] layer: one product per
         # projection on the GPU path, whose kernels read q, k and v as column ranges of its output.
         self.qkv = QuantLinear.fuse_rows(self.q_proj, self.k_proj, self.v_proj)
@@ -332,8 +340,15 @@ class Attention(nn.Module):
         b, _, t, _ = o.shape
         return self.o_proj(o.transpose(1, 2).reshape(b, t, -1))
 
-    def forward(self, x: torch.Tensor, positions: torch.Tensor, cache=None, rope=None) -> torch.Tensor:
-        q, k, v = self.project(x, positions, rope)
+    def forward(self, x: torch.Tensor, mask=None, cache=None, *, position_embeddings=None) -> torch.Tensor:
+        """``cache``: a list ``[k, v]`` of the full history (empty before the first call);
+        ``position_embeddings``: ``(cos, sin)`` rows of the call's positions (or a ``RopeTable``),
+        else computed from the cache length."""
+        positions = None
+        if position_embeddings is None:
+            start = int(cache[0].shape[2]) if cache else 0
+            positions = torch.arange(start, start + x.shape[1], device=x.device)
+        q, k, v = self.project(x, positions, position_embeddings)
         if cache is not None:           # a list cache [k, v] of the full history
             if cache:
                 k = torch.cat([cache[0], k], 2)
@@ -347,30 +362,25 @@ class Attention(nn.Module):
         o = F.scaled_dot_product_attention(q, kk, vv, attn_mask=mask)
         return self.output(o)
 
-    def butterfly_module(self, cfg: QwenButterflyConfig, layer_idx: int) -> "ButterflyAttention":
-        return ButterflyAttention(self, cfg, layer_idx)
-
-
-class ButterflyAttention(nn.Module):
-    """The swapped attention: the base module's projections, norms and RoPE, with the
-    attention core run by the Butterfly kernels over a ``CompressedKVCache``.
+class ButterflyAttention(QwenButterflyAttention):
+    """The swapped attention of this decoder: ``QwenButterflyAttention`` over the base
+    module's fused projection (q, k and v read as column ranges of one product, q/k norm
+    and RoPE in one launch) and, for a graph-replayed decode step with device counters,
+    the decode step that applies the q/k norm and RoPE itself at its device position.
 
     Counterpart of ``QwenButterflyAttention`` (bna/integrations/qwen_mlx.py:1295-1792)
     and ``QwenCUDAButterflyAttention.forward`` (qwen_torch.py:1221-1622).
     """
 
-    def __init__(self, base: Attention, cfg: QwenButterflyConfig, layer_idx: int):
-        super().__init__()
+    def __init__(self, base: Attention, cfg: QwenButterflyConfig, *, layer_idx: Optional[int] = None):
+        super().__init__(base, cfg, layer_idx=layer_idx)
         self.base = base
-        self.layer_idx = int(layer_idx)
-        self.core = ButterflyAttentionCore(cfg, layer_idx)
 
-    @property
-    def last_profile(self):
-        return self.core.last_profile
-
-    def forward(self, x: torch.Tensor, positions: torch.Tensor, cache=None, rope=None) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, mask=None, cache=None, *, position_embeddings=None) -> torch.Tensor:
         base, c = self.base, self.base.cfg
+        rope = position_embeddings
+        if rope is None:
+            raise ValueError("the decoder passes the RoPE rows of the call's positions (position_embeddings)")
         if (isinstance(rope, RopeTable) and _one_row(x)
                 and self.core.fuses_qk_norm(cache, 1, c.head_dim, x.dtype)):
             # one decode step with device counters: the raw q|k|v row goes to the decode
@@ -382,8 +392,11 @@ class ButterflyAttention(nn.Module):
             v = row[nq + nkv:].view(1, c.num_kv_heads, 1, c.head_dim)
             qk = (base.q_norm.weight, base.k_norm.weight, rope.cos_tab, rope.sin_tab, base.q_norm.eps)
             return base.output(self.core(q, k, v, cache, qk_norm=qk))
-        q, k, v = base.project(x, positions, rope)
-        return base.output(self.core(q, k, v, cache))
+        q, k, v = base.project(x, None, rope)
+        return base.output(self.attend(q, k, v, cache))
+
+
+register_butterfly_attention(Attention, ButterflyAttention)
 
 
 class MLP(nn.Module):
@@ -419,10 +432,10 @@ class DecoderLayer(nn.Module):
 
     def forward(self, x: torch.Tensor, positions: torch.Tensor, cache=None, rope=None) -> torch.Tensor:
         if _hip(x) and x.shape[-1] % 256 == 0:
-            a = self.self_attn(self.input_layernorm(x), positions, cache, rope)
+            a = self.self_attn(self.input_layernorm(x), cache=cache, position_embeddings=rope)
             h, n = add_rms_norm(x, a, self.post_attention_layernorm.weight, self.post_attention_layernorm.eps)
             return h + self.mlp(n)
-        x = x + self.self_attn(self.input_layernorm(x), positions, cache, rope)
+        x = x + self.self_attn(self.input_layernorm(x), cache=cache, position_embeddings=rope)
         return x + self.mlp(self.post_attention_layernorm(x))
 
     def forward_split(self, x: torch.Tensor, pending: Optional[torch.Tensor], positions: torch.Tensor, cache=None,
@@ -432,7 +445,7 @@ class DecoderLayer(nn.Module):
         is added to ``x`` in the launch that computes the input RMSNorm, which rounds the sum to
         bf16 before normalising it, as the separate add would."""
         x, n = add_rms_norm(x, pending, self.input_layernorm.weight, self.input_layernorm.eps)
-        a = self.self_attn(n, positions, cache, rope)
+        a = self.self_attn(n, cache=cache, position_embeddings=rope)
         h, n = add_rms_norm(x, a, self.post_attention_layernorm.weight, self.post_attention_layernorm.eps)
         return h, self.mlp(n)
 

@@ -28,30 +28,71 @@ from __future__ import annotations
 
 import time
 from dataclasses import dataclass, field
-from typing import Any, Dict, List, Optional, Sequence
+from typing import Any, Dict, List, Optional, Sequence, Union
 
 import torch
+import torch.nn as nn
 
-from .attention import _attend, _c, _on, compressed_butterfly_attention
+from .attention import (_attend, _c, _on, _require_cuda, compressed_butterfly_attention,
+                        compressed_butterfly_attention_active)
 from .compressed_cache import CompressedKVCache
 from .layout import build_block_butterfly_layout
 
 _RULES = {"xor", "bit_reversal", "benes", "causal_shift", "fixed_stride", "random"}
+_STRATEGIES = {"random", "greedy", "online_insertion", "regular_partition"}
 
 
 @dataclass
 class QwenButterflyConfig:
-    """Reference: bna/integrations/qwen_mlx.py:84-165 (field names and checks)."""
+    """The layer-swap config: the reference's field set, defaults and checks
+    (bna/integrations/qwen_mlx.py:84-165).
 
-    path: str = "block_sparse"
+    Only ``path="block_sparse"`` with ``block_compression="mean"`` -- compressed
+    Butterfly attention -- runs here; the attention modules refuse other paths
+    with ``NotImplementedError``.  Fields that steer only those other paths
+    (``strategy``, ``window``, ``landmark_stride``, ``num_cycles``, the permute
+    chunking, retro-backfill, graph metrics, ...) are accepted, validated as the
+    reference does, and otherwise ignored.  ``query_chunk_size`` bounds the
+    reference's memory per query chunk; the kernels here stream keys in constant
+    LDS, so it does not change results and is not used.
+    ``compressed_butterfly_config()`` gives the compressed configuration.
+    """
+
+    path: str = "permute"
+    strategy: str = "random"
+    window: int = 64
+    landmark_stride: Optional[int] = 64
+    num_cycles: Union[int, str] = 1
+    edge_disjoint: bool = True
+    enforce_hamiltonian: bool = True
+    regular_num_clusters: int = 8
+    seed: int = 0
+    edge_bias: bool = True
+    window_drop: float = 0.0
+    compiled_graph_dir: Optional[str] = None
     block_size: int = 128
     block_local_window_blocks: int = 1
     block_partner_count: int = 1
     block_sink_blocks: int = 1
-    block_partner_rule: str = "causal_shift"
-    block_compression: str = "mean"
-    compressed_local_window_tokens: int = 64
-    query_chunk_size: int = 64
+    block_partner_rule: str = "xor"
+    block_compression: str = "none"
+    compressed_local_window_tokens: int = 128
+    permute_head_chunk_size: int = 8
+    query_chunk_size: int = 256
+    permute_stream_o_proj: bool = False
+    permute_log_chunks: bool = False
+    compute_edge_utilization_proxy: bool = True
+    compute_graph_metrics: bool = True
+    retro_backfill_enabled: bool = False
+    retro_backfill_alpha: float = 0.0
+    retro_backfill_training_only: bool = True
+    retro_backfill_causal_only: bool = True
+    circular: bool = False
+    multi_cycle_mode: str = "average"
+    verify_spectral_gap: bool = False
+    spectral_gap_threshold: float = 4.0
+    use_fused_dispatch: bool = True
+    active_dense_threshold: Optional[Union[int, str]] = None
     wayfinder_decode_backend: str = "active_permute"
 
     @property
@@ -62,9 +103,20 @@ class QwenButterflyConfig:
     def butterfly_decode_backend(self, value: str) -> None:
         self.wayfinder_decode_backend = value
 
+    @property
+    def is_compressed(self) -> bool:
+        """Whether this config selects compressed Butterfly attention (the path built here)."""
+        return self.path == "block_sparse" and self.block_compression == "mean"
+
     def __post_init__(self) -> None:
         if self.path not in {"sparse", "permute", "block_sparse"}:
             raise ValueError(f"Unsupported Butterfly path: {self.path!r}")
+        if self.strategy not in _STRATEGIES:
+            raise ValueError(f"Unsupported Butterfly strategy: {self.strategy!r}")
+        if int(self.window) < 0:
+            raise ValueError("window must be >= 0")
+        if self.num_cycles != "auto" and int(self.num_cycles) <= 0:
+            raise ValueError("num_cycles must be > 0 or 'auto'")
         if int(self.block_size) <= 0:
             raise ValueError("block_size must be > 0")
         if int(self.block_local_window_blocks) < 0:
@@ -79,8 +131,24 @@ class QwenButterflyConfig:
             raise ValueError(f"Unsupported block_compression: {self.block_compression!r}")
         if int(self.compressed_local_window_tokens) <= 0:
             raise ValueError("compressed_local_window_tokens must be > 0")
+        if self.path == "block_sparse" and self.strategy in {"greedy", "online_insertion"}:
+            raise ValueError("block_sparse supports only static strategies ('random', 'regular_partition')")
         if self.wayfinder_decode_backend not in {"active_permute", "dense"}:
             raise ValueError(f"Unsupported butterfly_decode_backend: {self.wayfinder_decode_backend!r}")
+
+
+QwenWayfinderConfig = QwenButterflyConfig
+
+
+def compressed_butterfly_config(**overrides) -> QwenButterflyConfig:
+    """The compressed Butterfly configuration of this build's benchmark shapes:
+    ``path="block_sparse"``, ``block_compression="mean"``, ``causal_shift`` partners,
+    a 64-token local window and 64-query chunks (one partner, one sink, one local
+    block).  Keyword arguments override any field."""
+    kw = dict(path="block_sparse", block_compression="mean", block_partner_rule="causal_shift",
+              compressed_local_window_tokens=64, query_chunk_size=64)
+    kw.update(overrides)
+    return QwenButterflyConfig(**kw)
 
 
 @dataclass
@@ -112,10 +180,11 @@ class ButterflyAttentionCore:
     """
 
     def __init__(self, cfg: QwenButterflyConfig, layer_idx: int, *, scale: Optional[float] = None) -> None:
-        if cfg.path != "block_sparse" or cfg.block_compression != "mean":
+        if not cfg.is_compressed:
             raise NotImplementedError(
                 "butterfly_amd implements the compressed Butterfly path "
-                "(path='block_sparse', block_compression='mean') only")
+                "(path='block_sparse', block_compression='mean') only; "
+                f"got path={cfg.path!r}, block_compression={cfg.block_compression!r}")
         self.cfg = cfg
         self.layer_idx = int(layer_idx)
         self.scale = scale
@@ -168,6 +237,7 @@ class ButterflyAttentionCore:
         the decode step, which applies the q/k RMSNorm and RoPE itself; only where
         ``fuses_qk_norm`` holds."""
         t0 = _now_ms()
+        _require_cuda(q, k, v)
         b, hq, q_len, d = q.shape
         hkv = int(k.shape[1])
         if hq % hkv != 0:
@@ -223,18 +293,267 @@ class ButterflyAttentionCore:
         self._last = (t0, _now_ms(), graph_ms, path, notes, lay)
         return out
 
+    def attend_full(self, q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor) -> torch.Tensor:
+        """This call's queries (the last ``q_len`` positions) over the full keys/values that a
+        non-compressed cache returned from ``update_and_fetch``.  Reference: the
+        ``block_sparse_active_mode`` branch without a ``CompressedKVCache``
+        (bna/integrations/qwen_mlx.py:1547-1572: summaries recomputed over the full keys,
+        then the active rows), the one-shot prefill when ``q_len == k_len`` (:1574-1583) and
+        the stock decode fallback (dense over every cached key, :1273-1293)."""
+        t0 = _now_ms()
+        _require_cuda(q, keys, values)
+        _, hq, q_len, d = q.shape
+        hkv, k_len = int(keys.shape[1]), int(keys.shape[2])
+        if hq % hkv != 0:
+            raise ValueError(f"query heads {hq} must be a multiple of kv heads {hkv}")
+        w = int(self.cfg.compressed_local_window_tokens)
+        lay = self.layout(k_len, hkv, hq // hkv, q.device)
+        notes: Dict[str, Any] = {"seq_len": k_len, "q_len": int(q_len)}
+        if q_len == k_len:
+            out, _ = compressed_butterfly_attention(q, keys, values, layout=lay, local_window_tokens=w,
+                                                    scale=self.scale)
+            path = "block_sparse_compressed"
+        elif q_len <= 2 and self.cfg.butterfly_decode_backend == "dense":
+            kc, vc = _c(keys), _c(values)
+            out = _attend(_c(q), kc, vc, kc, vc, layout=lay, q_pos0=k_len - q_len, qpos_dev=None, ring_capacity=0,
+                          tail_start=0, kv_len=k_len, summary_count=0, local_window_tokens=k_len, scale=self.scale)
+            notes["dense_fallback_reason"] = "butterfly_decode_stock"
+            path = "block_sparse_dense_fallback"
+        else:
+            qp = torch.arange(k_len - q_len, k_len)
+            out, _ = compressed_butterfly_attention_active(q, keys, values, layout=lay, query_positions=qp,
+                                                           local_window_tokens=w, scale=self.scale)
+            notes["block_sparse_active_mode"] = True
+            path = "block_sparse_compressed_active"
+        self._last = (t0, _now_ms(), None, path, notes, lay)
+        return out
+
+
+# ----------------------------------------------------------------------------- the swapped attention module
+def _attn_get_first(attn, names: Sequence[str]) -> Any:
+    for name in names:
+        value = getattr(attn, name, None)
+        if value is not None:
+            return value
+    return None
+
+
+def _attn_num_heads(attn) -> int:
+    value = _attn_get_first(attn, ("n_heads", "num_attention_heads", "num_heads"))
+    if value is None:
+        raise AttributeError("Unable to resolve attention query head count.")
+    return int(value)
+
+
+def _attn_num_kv_heads(attn) -> int:
+    value = _attn_get_first(attn, ("n_kv_heads", "num_key_value_heads", "num_kv_heads"))
+    if value is None:
+        raise AttributeError("Unable to resolve attention KV head count.")
+    return int(value)
+
+
+def _attn_scale(attn) -> float:
+    value = _attn_get_first(attn, ("scale", "scaling"))
+    if value is not None:
+        return float(value)
+    head_dim = getattr(attn, "head_dim", None)
+    if head_dim is not None:
+        return float(int(head_dim) ** -0.5)
+    raise AttributeError("Unable to resolve attention scaling factor.")
+
+
+def _attn_head_dim(attn, scale: float) -> int:
+    value = getattr(attn, "head_dim", None)
+    if value is not None:
+        return int(value)
+    return int(round(float(scale) ** -2))
+
+
+def _rotate_half_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x [B, H, L, d] with cos/sin [L, d] or [B, L, d] (rotate-half RoPE in fp32, cast back)."""
+    if cos.dim() == 3:
+        cos, sin = cos[:, None], sin[:, None]
+    d = x.shape[-1]
+    xf = x.float()
+    rot = torch.cat([-xf[..., d // 2:], xf[..., : d // 2]], dim=-1)
+    return (xf * cos.float() + rot * sin.float()).to(x.dtype)
+
+
+def _cache_offset(cache) -> int:
+    if isinstance(cache, CompressedKVCache):
+        cache.sync()
+    return int(getattr(cache, "offset", 0))
+
+
+class QwenButterflyAttention(nn.Module):
+    """A decoder attention module with its attention swapped to compressed Butterfly.
+
+    Reference: ``QwenButterflyAttention`` (bna/integrations/qwen_mlx.py:859-975,
+    1295-1792) over ``extract_qkv_from_qwen_attention`` (:288-357).  It takes the
+    base module's ``q_proj``/``k_proj``/``v_proj`` (or a fused ``qkv_proj``),
+    ``o_proj``, ``q_norm``/``k_norm`` and RoPE (``rope`` / ``rotary_emb``), and
+    resolves head counts, scale and head_dim from the same attribute names.  A query
+    projection twice the head width carries the output gate
+    (``y * sigmoid(gate)`` before ``o_proj``).
+
+    ``forward(x, mask=None, cache=None, *, position_embeddings=None)`` returns the
+    post-``o_proj`` hidden states [B, L, hidden].  ``position_embeddings`` =
+    ``(cos, sin)`` for the call's positions (the PyTorch convention of computing
+    RoPE tables once per model step) replaces the base module's RoPE module.  With a
+    ``CompressedKVCache`` the call appends to it and attends through
+    ``ButterflyAttentionCore``; another cache object with ``update_and_fetch``
+    returns the full keys/values and the call takes the reference's active path over
+    them (``compressed_butterfly_attention_active``, summaries recomputed).
+    ``mask`` is accepted and unused, as in the reference's compressed path.
+    """
+
+    def __init__(self, base_attn: nn.Module, cfg: QwenButterflyConfig, *, layer_idx: Optional[int] = None):
+        super().__init__()
+        self.n_heads = _attn_num_heads(base_attn)
+        self.n_kv_heads = _attn_num_kv_heads(base_attn)
+        self.scale = _attn_scale(base_attn)
+        self.head_dim = _attn_head_dim(base_attn, self.scale)
+        self.layer_idx = int(layer_idx) if layer_idx is not None else int(getattr(base_attn, "layer_idx", 0) or 0)
+        for name in ("q_proj", "k_proj", "v_proj", "qkv_proj"):
+            if hasattr(base_attn, name):
+                setattr(self, name, getattr(base_attn, name))
+        self.o_proj = base_attn.o_proj
+        self.q_norm = getattr(base_attn, "q_norm", None) or nn.Identity()
+        self.k_norm = getattr(base_attn, "k_norm", None) or nn.Identity()
+        self.rope = _attn_get_first(base_attn, ("rope", "rotary_emb"))
+        self.cfg = cfg
+        self.path = cfg.path
+        self.butterfly_decode_backend = str(cfg.butterfly_decode_backend)
+        self.query_chunk_size = int(max(1, cfg.query_chunk_size))
+        self.core = ButterflyAttentionCore(cfg, self.layer_idx, scale=self.scale)
+
+    @property
+    def last_profile(self) -> Optional[AttentionProfile]:
+        return self.core.last_profile
+
+    def project(self, x: torch.Tensor, cache=None, position_embeddings=None):
+        """(q [B, Hq, L, d], k, v [B, Hkv, L, d], gate [B, L, Hq*d] or None), RoPE applied.
+        Reference: bna/integrations/qwen_mlx.py:288-357 (without the cache update)."""
+        b, length, _ = x.shape
+        if hasattr(self, "qkv_proj") and not all(hasattr(self, n) for n in ("q_proj", "k_proj", "v_proj")):
+            qkv = self.qkv_proj(x)
+            kd = self.n_kv_heads * self.head_dim
+            qd = int(qkv.shape[-1]) - 2 * kd
+            if qd <= 0:
+                raise ValueError(f"Unable to split qkv projection with shape {tuple(qkv.shape)}.")
+            q = qkv[..., :qd].reshape(b, length, self.n_heads, -1)
+            k = qkv[..., qd:qd + kd].reshape(b, length, self.n_kv_heads, -1)
+            v = qkv[..., qd + kd:].reshape(b, length, self.n_kv_heads, -1)
+        else:
+            q = self.q_proj(x).reshape(b, length, self.n_heads, -1)
+            k = self.k_proj(x).reshape(b, length, self.n_kv_heads, -1)
+            v = self.v_proj(x).reshape(b, length, self.n_kv_heads, -1)
+        gate = None
+        norm_w = getattr(self.q_norm, "weight", None)
+        expected = int(norm_w.shape[0]) if norm_w is not None else self.head_dim
+        if int(q.shape[-1]) == 2 * expected:
+            q, g = q.chunk(2, dim=-1)
+            gate = g.reshape(b, length, -1)
+        q = self.q_norm(q).transpose(1, 2)
+        k = self.k_norm(k).transpose(1, 2)
+        v = v.transpose(1, 2)
+        if position_embeddings is not None:
+            cos, sin = position_embeddings
+            q, k = _rotate_half_rope(q, cos, sin), _rotate_half_rope(k, cos, sin)
+        else:
+            q, k = self._apply_rope(q, k, cache)
+        return q.contiguous(), k.contiguous(), v.contiguous(), gate
+
+    def _apply_rope(self, q, k, cache):
+        """The reference's RoPE call resolution (bna/integrations/qwen_mlx.py:260-285)."""
+        rope = self.rope
+        if rope is None:
+            raise AttributeError("Unable to resolve attention RoPE module.")
+        if cache is not None:
+            offset = _cache_offset(cache)
+            try:
+                return rope(q, offset=offset), rope(k, offset=offset)
+            except TypeError:
+                pass
+        else:
+            try:
+                return rope(q), rope(k)
+            except TypeError:
+                pass
+        start = _cache_offset(cache) if cache is not None else 0
+        positions = (torch.arange(int(q.shape[2]), device=q.device) + start)[None, :]
+        try:
+            return rope(positions, q, k)
+        except TypeError:
+            return rope(positions, q), rope(positions, k)
+
+    def attend(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cache=None) -> torch.Tensor:
+        """The attention core over this call's q/k/v: [B, Hq, L, d]."""
+        if cache is None or isinstance(cache, CompressedKVCache):
+            return self.core(q, k, v, cache)
+        if not hasattr(cache, "update_and_fetch"):
+            raise TypeError("cache must be a CompressedKVCache or provide update_and_fetch(keys, values)")
+        keys, values = cache.update_and_fetch(k, v)
+        return self.core.attend_full(q, keys, values)
+
+    def forward(self, x: torch.Tensor, mask=None, cache=None, *, position_embeddings=None) -> torch.Tensor:
+        b, length, _ = x.shape
+        q, k, v, gate = self.project(x, cache, position_embeddings)
+        y = self.attend(q, k, v, cache)
+        y = y.transpose(1, 2).reshape(b, length, -1)
+        if gate is not None:
+            y = y * torch.sigmoid(gate[:, -length:, :]).to(y.dtype)
+        return self.o_proj(y)
+
+
+QwenWayfinderAttention = QwenButterflyAttention
+
+# base attention class -> the QwenButterflyAttention subclass that swaps it (see
+# register_butterfly_attention); anything else gets QwenButterflyAttention itself
+_WRAPPERS: Dict[type, type] = {}
+
+
+def register_butterfly_attention(base_cls: type, wrapper_cls: type) -> None:
+    """Make ``swap_qwen_attention_with_butterfly`` wrap instances of ``base_cls`` (and its
+    subclasses) in ``wrapper_cls``, a ``QwenButterflyAttention`` subclass with the same
+    constructor -- for a model whose attention has a faster swapped form than the generic
+    module (``butterfly_amd.decoder`` registers its attention this way)."""
+    if not (isinstance(wrapper_cls, type) and issubclass(wrapper_cls, QwenButterflyAttention)):
+        raise TypeError("wrapper_cls must subclass QwenButterflyAttention")
+    _WRAPPERS[base_cls] = wrapper_cls
+
+
+def _wrapper_for(base_attn) -> type:
+    for cls in type(base_attn).__mro__:
+        if cls in _WRAPPERS:
+            return _WRAPPERS[cls]
+    return QwenButterflyAttention
+
+
+def get_qwen_full_attention_layer_indices(model) -> List[int]:
+    """Layers with full attention: ``is_linear`` False, or a ``self_attn`` module.
+    Reference: bna/integrations/qwen_mlx.py:1849-1859."""
+    if not hasattr(model, "layers"):
+        raise ValueError("Model has no .layers attribute; expected a Qwen-style model.")
+    out: List[int] = []
+    for idx, layer in enumerate(model.layers):
+        if getattr(layer, "is_linear", None) is False or getattr(layer, "self_attn", None) is not None:
+            out.append(int(idx))
+    return out
+
 
 def install_compressed_kv_caches(model, prompt_cache: List[Any], *, layer_indices: Optional[Sequence[int]] = None,
                                  block_size: int = 128, local_window_tokens: int = 128,
                                  max_kv_size: Optional[int] = None, max_chunk_size: int = 512) -> List[int]:
     """Put a ``CompressedKVCache`` in ``prompt_cache[i]`` for the selected layers.
 
-    Reference: bna/integrations/qwen_mlx.py:1795-1819.  ``layer_indices=None``
-    selects every layer of ``model.layers``.
+    Reference: bna/integrations/qwen_mlx.py:1795-1819.  ``layer_indices=None`` selects
+    the full-attention layers (``get_qwen_full_attention_layer_indices``).
     """
     if not hasattr(model, "layers"):
-        raise ValueError("Model has no .layers attribute")
-    selected = range(len(model.layers)) if layer_indices is None else [int(x) for x in layer_indices]
+        raise ValueError("Model has no .layers attribute; expected a Qwen-style model.")
+    selected = get_qwen_full_attention_layer_indices(model) if layer_indices is None else \
+        [int(x) for x in layer_indices]
     replaced: List[int] = []
     for idx in sorted(set(selected)):
         if idx < 0 or idx >= len(prompt_cache):
@@ -248,15 +567,12 @@ def install_compressed_kv_caches(model, prompt_cache: List[Any], *, layer_indice
 
 def swap_qwen_attention_with_butterfly(model, *, cfg: QwenButterflyConfig,
                                        layer_indices: Optional[Sequence[int]] = None) -> List[int]:
-    """Replace ``model.layers[i].self_attn`` by ``butterfly_module(self_attn, cfg, layer_idx=i)``.
-
-    Reference: bna/integrations/qwen_mlx.py:1822-1846.  The layer's attention
-    module must provide ``butterfly_module(cfg, layer_idx)`` returning its
-    Butterfly replacement (the decoder in ``butterfly_amd.decoder`` does), the
-    counterpart of ``QwenButterflyAttention(base_attn, cfg, layer_idx=i)``.
+    """Replace ``model.layers[i].self_attn`` by ``QwenButterflyAttention(self_attn, cfg, layer_idx=i)``
+    for every selected layer that has one (or by the subclass registered for the base module's
+    class).  Returns the replaced indices.  Reference: bna/integrations/qwen_mlx.py:1822-1846.
     """
     if not hasattr(model, "layers"):
-        raise ValueError("Model has no .layers attribute")
+        raise ValueError("Model has no .layers attribute; expected a Qwen-style model.")
     selected = None if layer_indices is None else {int(i) for i in layer_indices}
     replaced: List[int] = []
     for i, layer in enumerate(model.layers):
@@ -265,9 +581,25 @@ def swap_qwen_attention_with_butterfly(model, *, cfg: QwenButterflyConfig,
         base = getattr(layer, "self_attn", None)
         if base is None:
             continue
-        layer.self_attn = base.butterfly_module(cfg, layer_idx=i)
+        layer.self_attn = _wrapper_for(base)(base, cfg, layer_idx=i)
         replaced.append(i)
     return replaced
+
+
+swap_qwen_attention_with_wayfinder = swap_qwen_attention_with_butterfly
+
+
+def iter_qwen_butterfly_layers(model):
+    """The swapped attention modules of ``model``.  Reference: bna/integrations/qwen_mlx.py:1880-1886."""
+    if not hasattr(model, "layers"):
+        raise ValueError("Model has no .layers attribute; expected a Qwen-style model.")
+    for layer in model.layers:
+        attn = getattr(layer, "self_attn", None)
+        if isinstance(attn, QwenButterflyAttention):
+            yield attn
+
+
+iter_qwen_wayfinder_layers = iter_qwen_butterfly_layers
 
 
 def split_chunks(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, chunk_size: int):

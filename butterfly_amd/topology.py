@@ -111,6 +111,8 @@ def block_neighbor_table_padded(*, num_blocks: int, layer_idx: int, partner_rule
     if int(partner_count) < 0:
         raise ValueError("partner_count must be >= 0")
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    if dev.type != "cuda":
+        raise ValueError(f"the neighbour table is built on a HIP device, not {dev}")
     kcap = 1 + int(local_window_blocks) + int(partner_count) + int(sink_count)
     table = torch.empty((int(num_blocks), kcap), dtype=torch.int32, device=dev)
     degree = torch.empty((int(num_blocks),), dtype=torch.int32, device=dev)

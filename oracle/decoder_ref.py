@@ -29,8 +29,8 @@ class OracleButterflyAttention(nn.Module):
                        partner_count=partner_count, partner_rule=partner_rule)
         self.W = int(local_window_tokens)
 
-    def forward(self, x: torch.Tensor, positions: torch.Tensor, cache=None, rope=None) -> torch.Tensor:
-        q, k, v = self.base.project(x, positions, rope)
+    def forward(self, x: torch.Tensor, mask=None, cache=None, *, position_embeddings=None) -> torch.Tensor:
+        q, k, v = self.base.project(x, None, position_embeddings)
         if cache is not None and cache:
             k = torch.cat([cache[0], k], 2)
             v = torch.cat([cache[1], v], 2)

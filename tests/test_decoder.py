@@ -44,7 +44,7 @@ def test_swapped_decoder_tracks_cpu_reference_teacher_forced(cfg_):
     the argmax agrees wherever the reference's top-2 margin exceeds that noise."""
     model = Decoder(cfg_, seed=7)
     cpu_model = copy.deepcopy(model).to("cpu")
-    cfg = bf.QwenButterflyConfig()
+    cfg = bf.compressed_butterfly_config()
     assert bf.swap_qwen_attention_with_butterfly(model, cfg=cfg) == [0, 1, 2, 3]
     swap_to_oracle(cpu_model, cfg)
     prompt = torch.randint(0, cfg_.vocab_size, (1, 700), generator=torch.Generator().manual_seed(3))

@@ -201,7 +201,7 @@ def test_decoder_graph_greedy_equals_eager_greedy(batch, head_dim):
     cfg = DecoderConfig(vocab_size=2048, hidden_size=512, num_layers=3, num_heads=512 // head_dim, num_kv_heads=2,
                         head_dim=head_dim, intermediate_size=1024)
     model = Decoder(cfg, seed=11)
-    bf.swap_qwen_attention_with_butterfly(model, cfg=bf.QwenButterflyConfig())
+    bf.swap_qwen_attention_with_butterfly(model, cfg=bf.compressed_butterfly_config())
     for layer in model.layers:   # non-trivial q/k norm weights
         g = torch.Generator(device="cuda").manual_seed(len(layer.self_attn.base.q_norm.weight))
         for norm in (layer.self_attn.base.q_norm, layer.self_attn.base.k_norm):

@@ -56,7 +56,7 @@ def test_fused_qk_norm_step_equals_separate_launches(layer_idx, heads, batch, ca
                         head_dim=128, intermediate_size=512)
     attn, cos, sin, (ca, cb), g = _setup(prompt, 1024, seed=layer_idx, cfg=cfg, batch=batch,
                                          cache_window=cache_window)
-    core = bf.ButterflyAttentionCore(bf.QwenButterflyConfig(), layer_idx)
+    core = bf.ButterflyAttentionCore(bf.compressed_butterfly_config(), layer_idx)
     assert core.fuses_qk_norm(cb, 1, cfg.head_dim, torch.bfloat16)
     qk = (attn.q_norm.weight, attn.k_norm.weight, cos, sin, attn.q_norm.eps)
     for step in range(150):            # crosses block ends: appends, trims and pooling
@@ -78,7 +78,7 @@ def test_fused_qk_norm_step_equals_separate_launches(layer_idx, heads, batch, ca
 def test_fused_step_past_the_rope_table_is_an_error_at_sync():
     prompt = 300
     attn, cos, sin, (_, cb), g = _setup(prompt, prompt + 2)
-    core = bf.ButterflyAttentionCore(bf.QwenButterflyConfig(), 1)
+    core = bf.ButterflyAttentionCore(bf.compressed_butterfly_config(), 1)
     qk = (attn.q_norm.weight, attn.k_norm.weight, cos, sin, attn.q_norm.eps)
     for _ in range(2):                 # positions 300 and 301 are in the table
         core(*_raw(attn.qkv(torch.randn(1, 1, CFG.hidden_size, generator=g, device="cuda").bfloat16())), cb,
@@ -93,7 +93,7 @@ def test_fused_step_past_the_rope_table_is_an_error_at_sync():
 
 def test_fused_step_refuses_bad_norm_weights():
     attn, cos, sin, (_, cb), g = _setup(200, 512)
-    core = bf.ButterflyAttentionCore(bf.QwenButterflyConfig(), 0)
+    core = bf.ButterflyAttentionCore(bf.compressed_butterfly_config(), 0)
     raw = _raw(attn.qkv(torch.randn(1, 1, CFG.hidden_size, generator=g, device="cuda").bfloat16()))
     for qw in (attn.q_norm.weight.float(), attn.q_norm.weight[:64], attn.q_norm.weight.cpu()):
         with pytest.raises(ValueError):
@@ -103,7 +103,7 @@ def test_fused_step_refuses_bad_norm_weights():
 def test_qk_norm_is_refused_off_the_device_counter_path():
     attn, cos, sin, (ca, _), g = _setup(200, 512)
     ca.use_device_counters(False)
-    core = bf.ButterflyAttentionCore(bf.QwenButterflyConfig(), 0)
+    core = bf.ButterflyAttentionCore(bf.compressed_butterfly_config(), 0)
     qkv = attn.qkv(torch.randn(1, 1, CFG.hidden_size, generator=g, device="cuda").bfloat16())
     with pytest.raises(ValueError):
         core(*_raw(qkv), ca, qk_norm=(attn.q_norm.weight, attn.k_norm.weight, cos, sin, 1e-6))

@@ -15,43 +15,141 @@ def test_config_validation_matches_reference_rules():
     for bad in [dict(path="dense"), dict(block_size=0), dict(block_local_window_blocks=-1),
                 dict(block_partner_count=-1), dict(block_sink_blocks=-1), dict(block_partner_rule="zigzag"),
                 dict(block_compression="max"), dict(compressed_local_window_tokens=0),
-                dict(wayfinder_decode_backend="flash")]:
+                dict(wayfinder_decode_backend="flash"), dict(strategy="spiral"), dict(window=-1),
+                dict(num_cycles=0), dict(path="block_sparse", strategy="greedy")]:
         with pytest.raises(ValueError):
             bf.QwenButterflyConfig(**bad)
-    cfg = bf.QwenButterflyConfig()
+    bf.QwenButterflyConfig(num_cycles="auto")
+    cfg = bf.compressed_butterfly_config()
     cfg.butterfly_decode_backend = "dense"
     assert cfg.wayfinder_decode_backend == "dense"
-    with pytest.raises(NotImplementedError):
-        bf.ButterflyAttentionCore(bf.QwenButterflyConfig(block_compression="none"), 0)
-    with pytest.raises(NotImplementedError):
-        bf.ButterflyAttentionCore(bf.QwenButterflyConfig(path="permute"), 0)
+    for bad_path in (bf.QwenButterflyConfig(), bf.QwenButterflyConfig(path="block_sparse"),
+                     bf.QwenButterflyConfig(path="permute", block_compression="mean")):
+        with pytest.raises(NotImplementedError):
+            bf.ButterflyAttentionCore(bad_path, 0)
+    bf.ButterflyAttentionCore(bf.compressed_butterfly_config(), 0)
 
 
-def test_install_and_swap_on_a_stub_model():
-    class Attn:
-        def __init__(self):
-            self.swapped = None
+def test_config_defaults_are_the_reference_defaults():
+    """bna/integrations/qwen_mlx.py:84-125: the dataclass defaults, field for field."""
+    c = bf.QwenButterflyConfig()
+    want = dict(path="permute", strategy="random", window=64, landmark_stride=64, num_cycles=1, edge_disjoint=True,
+                enforce_hamiltonian=True, regular_num_clusters=8, seed=0, edge_bias=True, window_drop=0.0,
+                compiled_graph_dir=None, block_size=128, block_local_window_blocks=1, block_partner_count=1,
+                block_sink_blocks=1, block_partner_rule="xor", block_compression="none",
+                compressed_local_window_tokens=128, permute_head_chunk_size=8, query_chunk_size=256,
+                permute_stream_o_proj=False, permute_log_chunks=False, compute_edge_utilization_proxy=True,
+                compute_graph_metrics=True, retro_backfill_enabled=False, retro_backfill_alpha=0.0,
+                retro_backfill_training_only=True, retro_backfill_causal_only=True, circular=False,
+                multi_cycle_mode="average", verify_spectral_gap=False, spectral_gap_threshold=4.0,
+                use_fused_dispatch=True, active_dense_threshold=None, wayfinder_decode_backend="active_permute")
+    import dataclasses
+    assert [f.name for f in dataclasses.fields(c)] == list(want)
+    assert {k: getattr(c, k) for k in want} == want
+    assert bf.QwenWayfinderConfig is bf.QwenButterflyConfig
 
-        def butterfly_module(self, cfg, layer_idx):
-            return ("butterfly", layer_idx)
 
-    class Layer:
-        def __init__(self):
-            self.self_attn = Attn()
+def test_harness_config_call_constructs():
+    """The keyword set of the reference harness's call (scripts/bench_qwen_consumer_mlx.py:1771-1800),
+    for its compressed_butterfly mode."""
+    cfg = bf.QwenButterflyConfig(
+        path="block_sparse", strategy="random", window=64, landmark_stride=None, num_cycles=1, edge_disjoint=True,
+        enforce_hamiltonian=True, seed=0, edge_bias=True, window_drop=0.0, permute_head_chunk_size=8,
+        query_chunk_size=64, compute_edge_utilization_proxy=False, compute_graph_metrics=False,
+        retro_backfill_enabled=False, retro_backfill_alpha=0.0, retro_backfill_training_only=True,
+        retro_backfill_causal_only=True, use_fused_dispatch=True, wayfinder_decode_backend="active_permute",
+        block_size=128, block_local_window_blocks=1, block_partner_count=1, block_sink_blocks=1,
+        block_partner_rule="causal_shift", block_compression="mean", compressed_local_window_tokens=64)
+    assert cfg.is_compressed
+    core = bf.ButterflyAttentionCore(cfg, 3)
+    assert core.cfg.compressed_local_window_tokens == 64
 
-    class Model:
-        layers = [Layer() for _ in range(5)]
 
-    m = Model()
+class _Linear(torch.nn.Linear):
+    pass
+
+
+class _Attn(torch.nn.Module):
+    """A module with the attribute set of mlx_lm / HF Qwen attention."""
+
+    def __init__(self, hidden=64, hq=4, hkv=2, d=16, gated=False):
+        super().__init__()
+        self.num_attention_heads, self.num_key_value_heads, self.head_dim = hq, hkv, d
+        self.scaling = d ** -0.5
+        self.q_proj = _Linear(hidden, hq * d * (2 if gated else 1), bias=False)
+        self.k_proj = _Linear(hidden, hkv * d, bias=False)
+        self.v_proj = _Linear(hidden, hkv * d, bias=False)
+        self.o_proj = _Linear(hq * d, hidden, bias=False)
+
+
+class _Layer:
+    def __init__(self, attn=True, is_linear=None):
+        if attn:
+            self.self_attn = _Attn()
+        else:
+            self.linear_attn = object()
+        if is_linear is not None:
+            self.is_linear = is_linear
+
+
+class _Model:
+    def __init__(self, layers):
+        self.layers = layers
+
+
+def test_full_attention_layers_and_install_default():
+    """Hybrid models: only layers with full attention get a cache or a swap by default
+    (bna/integrations/qwen_mlx.py:1795-1859)."""
+    m = _Model([_Layer(False, True), _Layer(False, True), _Layer(True, False), _Layer(False, True), _Layer(True)])
+    assert bf.get_qwen_full_attention_layer_indices(m) == [2, 4]
+    caches = [None] * 5
+    assert bf.install_compressed_kv_caches(m, caches) == [2, 4]
+    assert caches[0] is None and isinstance(caches[2], bf.CompressedKVCache)
+    assert caches[2].local_window_tokens == 128 and caches[2].max_chunk_size == 512
     caches = [None] * 5
     assert bf.install_compressed_kv_caches(m, caches, layer_indices=[1, 3, 9], block_size=128,
                                            local_window_tokens=64, max_kv_size=1000) == [1, 3]
-    assert isinstance(caches[1], bf.CompressedKVCache) and caches[0] is None
     assert caches[3].max_kv_size == 1000 and caches[3].local_window_tokens == 64
-    assert bf.swap_qwen_attention_with_butterfly(m, cfg=bf.QwenButterflyConfig(), layer_indices=[0, 4]) == [0, 4]
-    assert m.layers[4].self_attn == ("butterfly", 4)
     with pytest.raises(ValueError):
         bf.install_compressed_kv_caches(object(), caches)
+
+
+def test_swap_wraps_modules_with_the_attribute_set():
+    m = _Model([_Layer(False, True), _Layer(True, False), _Layer(True, False)])
+    cfg = bf.compressed_butterfly_config()
+    assert bf.swap_qwen_attention_with_butterfly(m, cfg=cfg) == [1, 2]
+    attn = m.layers[2].self_attn
+    assert isinstance(attn, bf.QwenButterflyAttention) and attn.layer_idx == 2
+    assert (attn.n_heads, attn.n_kv_heads, attn.head_dim) == (4, 2, 16) and attn.scale == 16 ** -0.5
+    assert [a.layer_idx for a in bf.iter_qwen_butterfly_layers(m)] == [1, 2]
+    m2 = _Model([_Layer(True, False) for _ in range(3)])
+    assert bf.swap_qwen_attention_with_butterfly(m2, cfg=cfg, layer_indices=[0, 2]) == [0, 2]
+    with pytest.raises(NotImplementedError):     # other Butterfly paths are not built here
+        bf.swap_qwen_attention_with_butterfly(_Model([_Layer(True, False)]), cfg=bf.QwenButterflyConfig())
+
+
+def test_swapped_module_projects_like_the_reference_on_cpu():
+    """Projection, q/k norm, gate split and RoPE of the swapped module (qwen_mlx.py:288-357); the
+    attention itself needs the GPU, and a CPU input is refused rather than computed another way."""
+    torch.manual_seed(0)
+    base = _Attn(gated=True)
+    base.q_norm = torch.nn.RMSNorm(16, eps=1e-6)
+    base.k_norm = torch.nn.RMSNorm(16, eps=1e-6)
+    attn = bf.QwenButterflyAttention(base, bf.compressed_butterfly_config(), layer_idx=1)
+    x = torch.randn(2, 5, 64)
+    pos = torch.arange(5).float()
+    inv = 1.0 / (1e4 ** (torch.arange(0, 16, 2).float() / 16))
+    ang = torch.cat([pos[:, None] * inv, pos[:, None] * inv], -1)
+    q, k, v, gate = attn.project(x, None, (ang.cos(), ang.sin()))
+    qr, gr = base.q_proj(x).view(2, 5, 4, 32).chunk(2, -1)
+    qr = base.q_norm(qr).transpose(1, 2)
+    rot = lambda t: torch.cat([-t[..., 8:], t[..., :8]], -1)
+    assert torch.allclose(q, qr * ang.cos() + rot(qr) * ang.sin(), atol=1e-5)
+    assert torch.allclose(gate, gr.reshape(2, 5, 64))
+    assert torch.allclose(v, base.v_proj(x).view(2, 5, 2, 16).transpose(1, 2))
+    assert k.shape == (2, 2, 5, 16)
+    with pytest.raises(ValueError):
+        attn(x, position_embeddings=(ang.cos(), ang.sin()))
 
 
 def _rand(seed, shape, dtype):
@@ -85,7 +183,7 @@ def test_chunked_prefill_then_decode_through_core(dtype):
     q = _rand(41, (b, hq, total, d), dtype)
     k = _rand(42, (b, hkv, total, d), dtype)
     v = _rand(43, (b, hkv, total, d), dtype)
-    cfg = bf.QwenButterflyConfig()
+    cfg = bf.compressed_butterfly_config()
     core = bf.ButterflyAttentionCore(cfg, layer)
     cache = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=total, max_chunk_size=512)
     outs = bf.chunked_prefill(core, bf.split_chunks(q[:, :, :T].cuda(), k[:, :, :T].cuda(), v[:, :, :T].cuda(),
@@ -117,7 +215,7 @@ def test_stock_decode_fallback_is_dense_over_the_tail():
     q = _rand(51, (b, hq, T + 1, d), dtype)
     k = _rand(52, (b, hkv, T + 1, d), dtype)
     v = _rand(53, (b, hkv, T + 1, d), dtype)
-    cfg = bf.QwenButterflyConfig(wayfinder_decode_backend="dense")
+    cfg = bf.compressed_butterfly_config(wayfinder_decode_backend="dense")
     core = bf.ButterflyAttentionCore(cfg, 3)
     cache = bf.CompressedKVCache(block_size=128, local_window_tokens=64)
     core(q[:, :, :T].cuda(), k[:, :, :T].cuda(), v[:, :, :T].cuda(), cache)
@@ -144,7 +242,7 @@ def test_native_chunk_loop_equals_per_chunk_calls(b, hq, hkv, d):
     for n in lens:
         chunks.append(tuple(t[:, :, pos:pos + n].contiguous() for t in (q, k, v)))
         pos += n
-    cfg = bf.QwenButterflyConfig()
+    cfg = bf.compressed_butterfly_config()
     runs = []
     for native in (True, False):
         core = bf.ButterflyAttentionCore(cfg, layer)
@@ -172,7 +270,7 @@ def test_native_chunk_loop_capacity_error_matches_per_chunk_calls():
     chunks = [tuple(t[:, :, i * 384:(i + 1) * 384].contiguous() for t in (q, k, v)) for i in range(6)]
     caches = []
     for native in (True, False):
-        core = bf.ButterflyAttentionCore(bf.QwenButterflyConfig(), layer)
+        core = bf.ButterflyAttentionCore(bf.compressed_butterfly_config(), layer)
         cache = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=1200, max_chunk_size=512)
         with pytest.raises(RuntimeError):
             if native:
@@ -202,7 +300,7 @@ def test_native_chunk_runs_mix_with_per_chunk_calls():
         pos += n
     runs = []
     for native in (True, False):
-        core = bf.ButterflyAttentionCore(bf.QwenButterflyConfig(), layer)
+        core = bf.ButterflyAttentionCore(bf.compressed_butterfly_config(), layer)
         cache = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=total, max_chunk_size=512)
         outs = bf.chunked_prefill(core, chunks, cache) if native else [core(*c, cache) for c in chunks]
         runs.append((cache, outs))

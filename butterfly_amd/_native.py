@@ -85,6 +85,7 @@ SIGNATURES = {
                                  _f32, _vp, _vp, _vp, _vp]),
     "bfly_silu_mul": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "bfly_argmax_rows": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "bfly_argmax_rows_noalloc": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),
     "bfly_q4_gemv": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _vp, _vp]),
     "bfly_q4_gemv_silu": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _i64, _vp, _vp]),
 }

@@ -10,6 +10,8 @@
 // after the residual add, after each norm, after RoPE, after SiLU and after the
 // product), so results differ from them only by the fp32 summation order of the
 // mean square and by the last bit of rsqrt/exp.
+#include <mutex>
+
 #include "bfly_common.h"
 #include "../../include/butterfly_amd_decoder.h"
 
@@ -503,11 +505,9 @@ __global__ void __launch_bounds__(256) argmax_final_kernel(const float* __restri
 
 }  // namespace bfly
 
-extern "C" int bfly_argmax_rows(const void* x, int64_t rows, int64_t n, int64_t row_stride, int64_t col_stride,
-                                void* workspace, int64_t workspace_bytes, void* out, hipStream_t stream) {
-  BFLY_CHECK_ARG(x && out, "null pointer");
-  BFLY_CHECK_ARG(rows > 0 && rows <= 65535 && n > 0 && col_stride > 0 && row_stride >= 0, "bad shape");
-  BFLY_CHECK_ARG(workspace_bytes >= 0 && (workspace != nullptr || workspace_bytes == 0), "bad workspace");
+// The two passes of bfly_argmax_rows over a workspace the caller checked.
+static int argmax_launch(const void* x, int64_t rows, int64_t n, int64_t row_stride, int64_t col_stride,
+                         void* workspace, int64_t workspace_bytes, void* out, hipStream_t stream, const char* what) {
   if (rows == 1) row_stride = 0;  // a single row: its stride is never used (a [1, n] view may carry any)
   const bool vec = col_stride == 1 && row_stride % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
   // about 4096 elements per workgroup, at most 256 parts, as many as the workspace holds
@@ -527,6 +527,77 @@ extern "C" int bfly_argmax_rows(const void* x, int64_t rows, int64_t n, int64_t 
   if (parts > 1)
     hipLaunchKernelGGL(bfly::argmax_final_kernel, dim3((unsigned)rows), dim3(256), 0, stream, part_v, part_i,
                        (int)parts, static_cast<int64_t*>(out));
-  BFLY_CHECK_LAUNCH("bfly_argmax_rows");
+  BFLY_CHECK_LAUNCH(what);
   return BFLY_OK;
+}
+
+extern "C" int bfly_argmax_rows(const void* x, int64_t rows, int64_t n, int64_t row_stride, int64_t col_stride,
+                                void* workspace, int64_t workspace_bytes, void* out, hipStream_t stream) {
+  BFLY_CHECK_ARG(x && out, "null pointer");
+  BFLY_CHECK_ARG(rows > 0 && rows <= 65535 && n > 0 && col_stride > 0 && row_stride >= 0, "bad shape");
+  BFLY_CHECK_ARG(workspace_bytes >= 0 && (workspace != nullptr || workspace_bytes == 0), "bad workspace");
+  return argmax_launch(x, rows, n, row_stride, col_stride, workspace, workspace_bytes, out, stream,
+                       "bfly_argmax_rows");
+}
+
+// ---------------------------------------------------------------------------------------------
+// bfly_argmax_rows_noalloc: the same passes with the per-workgroup candidates in a
+// file-scope device array instead of a caller workspace, for callers that cannot
+// allocate.  Every GPU the library runs on holds its own copy of `scratch` until the
+// process ends; calls on one GPU share it, so calls that overlap on one GPU (another
+// stream, another thread) race.  Pass 1 writes every candidate slot that pass 2 reads,
+// so nothing needs clearing between calls.
+constexpr int64_t kNoAllocMaxRows = 64;
+// rows * 256 parts * (float + int64) + 8 bytes of alignment padding
+constexpr int64_t kNoAllocScratchBytes = kNoAllocMaxRows * 256 * 12 + 8;
+constexpr int kNoAllocMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kNoAllocMaxDevices] = {};   // device address of `scratch`, per device
+
+// The device address of the current device's copy of `scratch`, looked up once per device
+// (host code never passes the array's own name to a kernel: that is a host-side stand-in).
+int scratch_address(void** ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    ::bfly::set_error("bfly_argmax_rows_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return BFLY_ERR_HIP;
+  }
+  if (dev < 0 || dev >= kNoAllocMaxDevices) {
+    ::bfly::set_error("bfly_argmax_rows_noalloc: device %d outside the %d it tracks", dev, kNoAllocMaxDevices);
+    return BFLY_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      ::bfly::set_error("bfly_argmax_rows_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+      return BFLY_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return BFLY_OK;
+}
+
+}  // namespace
+
+extern "C" int bfly_argmax_rows_noalloc(const void* x, int64_t rows, int64_t n, int64_t row_stride,
+                                        int64_t col_stride, void* out, hipStream_t stream) {
+  BFLY_CHECK_ARG(x && out, "null pointer");
+  BFLY_CHECK_ARG(rows > 0 && n > 0 && col_stride > 0 && row_stride >= 0, "bad shape");
+  BFLY_CHECK_ARG(rows <= kNoAllocMaxRows,
+                 "bfly_argmax_rows_noalloc: rows=%lld above the %lld its static workspace holds; "
+                 "use bfly_argmax_rows with a workspace", (long long)rows, (long long)kNoAllocMaxRows);
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != BFLY_OK) return rc;
+  return argmax_launch(x, rows, n, row_stride, col_stride, ws, kNoAllocScratchBytes, out, stream,
+                       "bfly_argmax_rows_noalloc");
 }

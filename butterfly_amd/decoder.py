@@ -236,6 +236,18 @@ def argmax_rows(x: torch.Tensor, parallel: bool = True) -> torch.Tensor:
     return out
 
 
+def argmax_rows_noalloc(x: torch.Tensor) -> torch.Tensor:
+    """``argmax_rows`` for at most 64 rows through ``bfly_argmax_rows_noalloc``: no workspace and
+    no allocation besides the output (the library's static device workspace holds the
+    per-workgroup candidates; calls that overlap on one GPU race)."""
+    rows, n = x.shape
+    out = torch.empty(rows, 1, dtype=torch.long, device=x.device)
+    with on(x.device):
+        _native.call("bfly_argmax_rows_noalloc", x.data_ptr(), rows, n, x.stride(0), x.stride(1), out.data_ptr(),
+                     stream_of(x))
+    return out
+
+
 class RMSNorm(nn.Module):
     def __init__(self, dim: int, eps: float, device):
         super().__init__()
@@ -540,7 +552,10 @@ class Decoder(nn.Module):
             x = F.embedding(tok, self.embed_tokens)
             rope = RopeTable(cos_tab, sin_tab, pos)
             lg = self._logits(self._last_hidden(x, pos, caches, rope))
-            nxt = argmax_rows(lg) if _hip(lg) else lg.argmax(-1, keepdim=True)
+            if _hip(lg):
+                nxt = argmax_rows_noalloc(lg) if lg.shape[0] <= 64 else argmax_rows(lg)
+            else:
+                nxt = lg.argmax(-1, keepdim=True)
             tok.copy_(nxt)
             out.index_copy_(1, step, nxt)
             pos.add_(1)

@@ -68,6 +68,20 @@ int bfly_argmax_rows(const void* x, int64_t rows, int64_t n, int64_t row_stride,
                      void* workspace, int64_t workspace_bytes, void* out, hipStream_t stream);
 
 /*
+ * Device: bfly_argmax_rows that allocates nothing and takes no workspace: the
+ * per-workgroup candidates live in a static device array of the library
+ * (64 * 3 KiB + 8 bytes per GPU, held until the process ends), so rows is at
+ * most 64 (larger counts return BFLY_ERR_INVALID).  Same result as
+ * bfly_argmax_rows.  Calls on one GPU share that array: calls that overlap on
+ * one GPU (other streams or threads) race.  The first call on a device looks
+ * up that device's copy of the array (make it outside graph capture).  No
+ * counterpart in the reference: for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ */
+int bfly_argmax_rows_noalloc(const void* x, int64_t rows, int64_t n, int64_t row_stride, int64_t col_stride,
+                             void* out, hipStream_t stream);
+
+/*
  * Device: out[n] (bf16) = sum_i x_i * (code_ni * scale_ng + bias_ng) for one row x
  * (in_features bf16, 16-byte aligned): a quantized linear layer's product at
  * batch 1, read from the 4-bit codes.  packed: [out_features][in_features / 2]

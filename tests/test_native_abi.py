@@ -135,3 +135,12 @@ def test_decode_step_checks_the_cache_window_before_launch():
     for cw in (0, 200, 1 << 20):                      # 200 + 128 rows do not fit a ring of 256
         assert lib.bfly_decode_step(*head, cw, 0.088, 0x3000, None) == _native.ERR_INVALID
         assert b"cache_window" in lib.bfly_last_error()
+
+
+def test_noalloc_argmax_refuses_before_any_device_call():
+    """Row counts beyond the static workspace and bad shapes fail before any HIP call (fake addresses)."""
+    lib = _native.lib()
+    assert lib.bfly_argmax_rows_noalloc(0x1000, 65, 16, 16, 1, 0x2000, None) == _native.ERR_INVALID
+    assert b"64" in lib.bfly_last_error()
+    assert lib.bfly_argmax_rows_noalloc(0x1000, 0, 16, 16, 1, 0x2000, None) == _native.ERR_INVALID
+    assert lib.bfly_argmax_rows_noalloc(None, 2, 16, 16, 1, 0x2000, None) == _native.ERR_INVALID

@@ -41,6 +41,19 @@ def measured_traffic():
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
+def _host_threads() -> int:
+    """Host threads for the CPU legs: the job's share (OMP_NUM_THREADS, as the GPU boxes set it)
+    rather than every core the machine reports."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return int(env) if env.isdigit() and int(env) > 0 else (os.cpu_count() or 1)
+
+
+def _log(msg: str) -> None:
+    """A progress line on stderr (stdout carries only the JSON result line): names the leg that
+    is running, so a failed run can be attributed to it."""
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -219,7 +232,7 @@ def bench_prefill(args, torch, bf, tp):
 
 
 def prefill_launches(args, torch, bf):
-    """cfg2 (stage 3): the compressor once, then ``--prefill-launches`` back-to-back prefill launches."""
+    """cfg2 (stage 3): ``--prefill-launches`` times the compressor (K and V) then one prefill launch."""
     T, hq, hkv, d, bs, W = 65536, 8, 2, 128, 128, 64
     dev = torch.device("cuda:0")
     q, k, v = (x.to(dev) for x in prefill_workload(args.seed, T, hq, hkv, d))
@@ -233,11 +246,36 @@ def prefill_launches(args, torch, bf):
     from butterfly_amd.attention import _dtype_code
     lib, nb, sh = _native.lib(), lay.neighbors, torch.cuda.current_stream(dev).cuda_stream
     for _ in range(args.prefill_launches):
+        _native.check(lib.bfly_block_mean(k.data_ptr(), ks.data_ptr(), v.data_ptr(), vs.data_ptr(), _dtype_code(k), hkv,
+                                          T, d, bs, n, sh), "bfly_block_mean")
         _native.check(lib.bfly_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), ks.data_ptr(), vs.data_ptr(),
                                        _dtype_code(q), 1, hq, hkv, T, d, nb.data_ptr(), n, nb.shape[1], bs, W,
                                        1.0 / d ** 0.5, out.data_ptr(), sh), "bfly_prefill")
     torch.cuda.synchronize()
     print(json.dumps({"prefill_launches": args.prefill_launches}), flush=True)
+
+
+def decode_steps_only(args, torch, bf, steps=64):
+    """cfg3 shapes at batch ``--decode-steps``: a restored 131072-token cache, then ``steps``
+    eager device-counter decode steps (one ``bfly_decode_step`` launch each), for counter
+    collection."""
+    hq, hkv, d, bs, W, ctx, B = 8, 2, 128, 128, 64, 131072, args.decode_steps
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    c = bf.CompressedKVCache(block_size=bs, local_window_tokens=W, max_kv_size=131328, max_chunk_size=512)
+    c.state = tuple(torch.randn(B, hkv, n, d, generator=g, device=dev).bfloat16() for n in (256, 256, 1023, 1023))
+    c.meta_state = (str(bs), str(W), str(ctx), str(1023 * bs))
+    c.ring_state()
+    c.use_device_counters()
+    qn = torch.randn(steps, B, hq, 1, d, generator=g, device=dev).bfloat16()
+    kn = torch.randn(steps, B, hkv, 1, d, generator=g, device=dev).bfloat16()
+    vn = torch.randn(steps, B, hkv, 1, d, generator=g, device=dev).bfloat16()
+    out = torch.empty(B, hq, 1, d, dtype=torch.bfloat16, device=dev)
+    for s in range(steps):
+        c.decode_step(qn[s], kn[s], vn[s], layer_idx=3, local_window_tokens=W, out=out)
+    torch.cuda.synchronize()
+    c.sync()
+    print(json.dumps({"decode_steps": steps, "batch": B, "summaries": c.summary_count}), flush=True)
 
 
 def _replay_steady(torch, graph, counters, reps=6):
@@ -500,8 +538,7 @@ def bench_decoder(torch, bf, seed=0, prompt_len=32768, new_tokens=32, agree_prom
            "peak_hbm_bytes": int(torch.cuda.max_memory_allocated())}
     if cpu_agreement:
         swap_to_oracle(cpu_model, bcfg)
-        threads = os.cpu_count() or 1
-        torch.set_num_threads(threads)
+        torch.set_num_threads(_host_threads())
         gp = model.greedy(pd[:, :agree_prompt], agree_tokens, fresh(agree_prompt + agree_tokens)).cpu()
         # teacher-forced: both paths fed the reference's greedy tokens, logits compared per step
         gcache, ccache = fresh(agree_prompt + agree_tokens), [[] for _ in range(cfg.num_layers)]
@@ -542,8 +579,7 @@ def cpu_baseline(q, k, v, ref_lays, repeats=3, max_seconds=30.0):
 
     from oracle import attention as oa
 
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
+    torch.set_num_threads(_host_threads())
     lay = ref_lays[3]
     T = q.shape[2]
     times = []
@@ -559,6 +595,128 @@ def cpu_baseline(q, k, v, ref_lays, repeats=3, max_seconds=30.0):
     return {"value": T / med, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"full cfg2 layer (T={T}, bf16, stage 3), 1 warmup + median of {len(times)}; "
                       f"{_cpu_model()}"}
+
+
+def _timed(fn, repeats):
+    fn()                                         # warmup
+    ts = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), len(ts)
+
+
+def cpu_baseline_cfg1(seed=0):
+    """cfg1: fp32 prefill, T=4096, Hq8/Hkv2, d128, layers 0..4 (the CPU oracle, host cores)."""
+    import torch
+
+    from oracle import attention as oa, topology as tp
+
+    g = torch.Generator().manual_seed(seed)
+    T, hq, hkv, d = 4096, 8, 2, 128
+    q, k, v = (torch.randn(1, h, T, d, generator=g) for h in (hq, hkv, hkv))
+    per_layer = []
+    for layer in range(5):
+        lay = tp.build_layout(seq_len=T, block_size=128, num_key_value_heads=hkv, num_key_value_groups=hq // hkv,
+                              layer_idx=layer, local_window_blocks=1, sink_count=1, partner_count=1,
+                              partner_rule="causal_shift")
+        per_layer.append(_timed(lambda: oa.prefill(q, k, v, layout=lay, W=64), 3)[0])
+    med = statistics.median(per_layer)
+    return {"value": T / med, "unit": "tok/s", "ms_per_layer": med * 1e3, "cores": torch.get_num_threads(),
+            "kind": "port", "sample": "full cfg1: fp32 T=4096 prefill, layers 0..4, 1 warmup + median of 3 each"}
+
+
+def cpu_baseline_cfg3(torch_gpu, batches=(1, 8, 32), seed=0):
+    """cfg3: one decode row per sequence at position 131072 through the CPU oracle's active rows,
+    which recompute the block summaries over the full context every call as the reference's Torch
+    active path does (bna/torch/attention_wayfinder_permute.py:1125-1197).  K/V are drawn on the
+    GPU and copied to the host (drawing 10^9 normals on one host core would take longer than the
+    measurement)."""
+    import torch
+
+    from oracle import attention as oa, topology as tp
+
+    hq, hkv, d, ctx = 8, 2, 128, 131073
+    lay = tp.build_layout(seq_len=ctx, block_size=128, num_key_value_heads=hkv, num_key_value_groups=hq // hkv,
+                          layer_idx=3, local_window_blocks=1, sink_count=1, partner_count=1, partner_rule="causal_shift")
+    g = torch_gpu.Generator(device="cuda:0").manual_seed(seed)
+    out = {}
+    for B in batches:
+        k = torch_gpu.randn(B, hkv, ctx, d, generator=g, device="cuda:0").bfloat16().cpu()
+        v = torch_gpu.randn(B, hkv, ctx, d, generator=g, device="cuda:0").bfloat16().cpu()
+        q = torch_gpu.randn(B, hq, 1, d, generator=g, device="cuda:0").bfloat16().cpu()
+        reps = 3 if B == 1 else 2 if B == 8 else 1
+        med, n = _timed(lambda: oa.active(q, k, v, layout=lay, query_positions=torch.tensor([ctx - 1]), W=64), reps)
+        out[str(B)] = {"ms_per_step": med * 1e3, "tok_s": B / med, "steps_timed": n}
+        del k, v
+    return {"value": out["32"]["tok_s"] if "32" in out else None, "unit": "tok/s (B=32)", "per_batch": out,
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": "one decode step per batch size at context 131072 (1 warmup + median of 3/2/1 for B=1/8/32); "
+                      "summaries recomputed over the full context each step, as the reference's Torch active path"}
+
+
+def cpu_baseline_cfg4(torch_gpu, seed=0, T=262144, chunk=384, samples=(1, 171, 341, 511, 682)):
+    """cfg4: the reference's Torch chunked path on the CPU oracle -- chunk 0 one-shot, every later
+    chunk the active rows over the full prefix (summaries recomputed per call, the Torch layer
+    swap's cached branch, bna/integrations/qwen_torch.py:1400-1427).  A labelled sample: the
+    listed chunks are timed once each and the per-chunk time, linear in the prefix length, is
+    fitted and summed over all 683 chunks."""
+    import torch
+
+    from oracle import attention as oa, topology as tp
+
+    hq, hkv, d = 16, 4, 256
+    g = torch_gpu.Generator(device="cuda:0").manual_seed(seed)
+    k = torch_gpu.randn(1, hkv, T, d, generator=g, device="cuda:0").bfloat16().cpu()
+    v = torch_gpu.randn(1, hkv, T, d, generator=g, device="cuda:0").bfloat16().cpu()
+    kw = dict(block_size=128, num_key_value_heads=hkv, num_key_value_groups=hq // hkv, layer_idx=5,
+              local_window_blocks=1, sink_count=1, partner_count=1, partner_rule="causal_shift")
+    q0 = torch_gpu.randn(1, hq, chunk, d, generator=g, device="cuda:0").bfloat16().cpu()
+    lay0 = tp.build_layout(seq_len=chunk, **kw)
+    t_first, _ = _timed(lambda: oa.prefill(q0, k[:, :, :chunk], v[:, :, :chunk], layout=lay0, W=64), 1)
+    pts = []
+    for c in samples:
+        s0, e = c * chunk, min(T, (c + 1) * chunk)
+        lay = tp.build_layout(seq_len=e, **kw)
+        qc = torch_gpu.randn(1, hq, e - s0, d, generator=g, device="cuda:0").bfloat16().cpu()
+        t0 = time.perf_counter()
+        oa.active(qc, k[:, :, :e], v[:, :, :e], layout=lay, query_positions=torch.arange(s0, e), W=64)
+        pts.append((e, time.perf_counter() - t0))
+    n = len(pts)
+    mx = sum(e for e, _ in pts) / n
+    my = sum(t for _, t in pts) / n
+    slope = sum((e - mx) * (t - my) for e, t in pts) / max(1e-9, sum((e - mx) ** 2 for e, _ in pts))
+    icpt = my - slope * mx
+    total = t_first + sum(icpt + slope * min(T, (c + 1) * chunk) for c in range(1, -(-T // chunk)))
+    return {"value": T / total, "unit": "tok/s", "e2e_s_extrapolated": total, "first_chunk_s": t_first,
+            "sampled_chunks": {str(c): round(t, 4) for c, (_, t) in zip(samples, pts)},
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"chunks {list(samples)} timed once each (plus the one-shot first chunk); per-chunk time "
+                      "fitted linearly in the prefix length and summed over all 683 chunks (extrapolated)"}
+
+
+def gpu_cfg1(torch, bf, seed=0, reps=20):
+    """cfg1 on the GPU: the fp32 prefill (T=4096, layers 0..4), summaries + attention per layer."""
+    g = torch.Generator(device="cuda:0").manual_seed(seed)
+    T, hq, hkv, d = 4096, 8, 2, 128
+    q, k, v = (torch.randn(1, h, T, d, generator=g, device="cuda:0") for h in (hq, hkv, hkv))
+    lays = [bf.build_block_butterfly_layout(seq_len=T, block_size=128, num_key_value_heads=hkv,
+                                            num_key_value_groups=hq // hkv, layer_idx=layer, local_window_blocks=1,
+                                            sink_count=1, partner_count=1, partner_rule="causal_shift")
+            for layer in range(5)]
+    for lay in lays:
+        bf.compressed_butterfly_attention(q, k, v, layout=lay, local_window_tokens=64)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(reps):
+        bf.compressed_butterfly_attention(q, k, v, layout=lays[i % 5], local_window_tokens=64)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    return {"ms_per_layer": ms, "tok_s": T / (ms / 1e3), "dtype": "f32",
+            "mode": "eager calls (compressor + fp32 attention kernel), events around 20 calls"}
 
 
 def hbm_ceiling(torch, nbytes: int = 1 << 30, reps: int = 10) -> dict:
@@ -602,6 +760,8 @@ def main():
                     help="only run a plain 256 MiB device copy (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--hbm-ceiling", action="store_true",
                     help="only time torch's streaming kernels (read-only reductions, fill, copy) on 1 GiB tensors")
+    ap.add_argument("--decode-steps", type=int, default=0,
+                    help="only run 64 eager device-counter decode steps at this batch size (counter collection)")
     ap.add_argument("--prefill-launches", type=int, default=0,
                     help="only run the cfg2 compressor once and this many prefill launches (counter collection)")
     args = ap.parse_args()
@@ -632,13 +792,32 @@ def main():
     if args.prefill_launches:
         prefill_launches(args, torch, bf)
         return
+    if args.decode_steps:
+        decode_steps_only(args, torch, bf)
+        return
+    _log("cfg2 prefill leg")
     pre = bench_prefill(args, torch, bf, tp)
     q, k, v, ref_lays = pre.pop("inputs")
-    decode = None if args.no_decode else bench_decode(torch, bf)
-    decode_sweep = None if args.no_decode else bench_decode_sweep(torch, bf)
-    stream = None if args.no_stream else bench_stream(torch, bf)
-    model = None if args.no_model else bench_decoder(torch, bf, cpu_agreement=not args.no_cpu_baseline)
-    cpu = None if args.no_cpu_baseline else cpu_baseline(q, k, v, ref_lays)
+    _log("cfg1 fp32 leg")
+    cfg1 = gpu_cfg1(torch, bf)
+    decode = decode_sweep = stream = model = cpu = None
+    if not args.no_decode:
+        _log("cfg3 decode leg")
+        decode = bench_decode(torch, bf)
+        _log("cfg3 batch sweep leg")
+        decode_sweep = bench_decode_sweep(torch, bf)
+    if not args.no_stream:
+        _log("cfg4 streaming leg")
+        stream = bench_stream(torch, bf)
+    if not args.no_model:
+        _log("cfg5 decoder leg")
+        model = bench_decoder(torch, bf, cpu_agreement=not args.no_cpu_baseline)
+    if not args.no_cpu_baseline:
+        _log("CPU baselines (cfg2, cfg1, cfg3, cfg4)")
+        cpu = cpu_baseline(q, k, v, ref_lays)
+        cpu["other_configs"] = {"cfg1": cpu_baseline_cfg1(), "cfg3": cpu_baseline_cfg3(torch),
+                                "cfg4": cpu_baseline_cfg4(torch)}
+    _log("done")
     line = {
         "metric": "prefill tok/s @64k (1 layer, bf16, 9-stage sweep)",
         "value": pre["tok_s"],
@@ -669,7 +848,7 @@ def main():
                   "eager_ms_per_step": pre["eager_ms_per_step"],
                   "prefill_event_ms_in_step_avg": pre["prefill_event_ms_in_step_avg"],
                   "prefill_event_ms_in_step_min": pre["prefill_event_ms_in_step_min"],
-                  "compress_alg_bytes": pre["compress_bytes"], "decode_cfg3": decode,
+                  "compress_alg_bytes": pre["compress_bytes"], "prefill_cfg1_f32": cfg1, "decode_cfg3": decode,
                   "decode_batch_sweep": decode_sweep,
                   "stream_cfg4": stream, "model_cfg5": model},
     }

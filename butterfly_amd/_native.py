@@ -9,7 +9,9 @@ import ctypes as C
 import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libbutterfly_amd.so"
+# BFLY_LIB names another build of the same library (a variant under test); the default is the
+# in-tree build that butterfly_amd.build writes.
+LIB_PATH = Path(os.environ.get("BFLY_LIB") or Path(__file__).resolve().parent / "_lib" / "libbutterfly_amd.so")
 
 OK = 0
 ERR_INVALID = -1

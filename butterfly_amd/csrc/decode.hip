@@ -65,9 +65,11 @@ constexpr int kDecMaxNew = 2;   // blocks pooled in one step (one per 128 steps 
 // word 2 block_size | ring << 32, word 3 pool_rows | lwb << 32 | sinks << 40 |
 // partners << 38 | cache window << 43, words 4..11 the ns pool rows as int32.  A step uses it only
 // when every word matches its own kv_len and arguments (anything else, a zero
-// key included, falls back to computing the row).  A launch reads the buffer
-// of its own parity and writes only the other one, so no word is read and
-// written within one launch.
+// key included, falls back to computing the row).  A launch uses the buffer
+// of its own parity and writes only the other one.  The attending workgroups
+// request the row entries of both buffers together with the counters (one
+// round trip instead of two) and keep those of their own parity, so no word
+// written within a launch is used by it.
 enum { kStOffset = 0, kStTail = 1, kStCount = 2, kStSumOff = 3 };
 constexpr int kStError = 4;
 constexpr int64_t kErrCapacity = 1;   // state[kStError]: tail or pool capacity exceeded
@@ -164,6 +166,7 @@ struct DecodeArgs {
   float scale;
   FastDiv bs_div, ring_div, hkv_div;   // MFMA path: block_size, ring capacity, Hkv
   int gsz;                             // MFMA path: hq / hkv
+  int nseq;                            // MFMA step path: batch * hkv (attending sequences)
   // MFMA step path, d = 128: when qn_w is set, q and k_new are the raw projection
   // rows and the kernel applies the per-head q/k RMSNorm and rotate-half RoPE at
   // position kv_len - 1 itself (rope_cos / rope_sin: [rope_rows][128] fp32)
@@ -716,18 +719,18 @@ __device__ __forceinline__ RouteKey route_key(int kv_len, int ns, const DecodeAr
 }
 
 // Route workgroup r of a step launch (blockIdx.x = r < kRouteGroups, 256
-// threads; its counter copy is g_count + r): it advances its own counter copy
+// threads; its counter copy is nseq + r): it advances its own counter copy
 // like every other workgroup, computes the routed row of the NEXT step (whose
 // counters are the ones this step writes back) with the same functions and
 // inputs as that step's own dec_state32 + dec_select32, and writes it into the
-// route buffer of that step's kv_len parity in the copies of the attending
-// workgroups g with g mod 8 = r (attending workgroup g is blockIdx g + 8, so it
-// runs on the same XCD).  It touches no q, cache row or output.
-__device__ __forceinline__ void dec_route_workgroup(const DecodeArgs& a, const StepArgs& sa, int tid) {
-  __shared__ int sel[kDecMaxSum];
-  __shared__ int64_t hdr[4];
-  const int64_t g_count = (int64_t)gridDim.x - kRouteGroups, g0 = blockIdx.x;
-  const DecState32 st = dec_state32<true>(a, sa, g_count + g0);
+// route buffer of that step's kv_len parity in the copies of the sequences of
+// the attending workgroups j with j mod 8 = r (attending workgroup j is blockIdx
+// j + 8 and holds sequences spw*j .. spw*j + spw - 1, so it runs on the same
+// XCD).  It touches no q, cache row or output.  sel / hdr: the caller's LDS.
+__device__ __forceinline__ void dec_route_workgroup(const DecodeArgs& a, const StepArgs& sa, int tid, int64_t nseq,
+                                                    int spw, int* sel, int64_t* hdr) {
+  const int64_t g0 = blockIdx.x;
+  const DecState32 st = dec_state32<true>(a, sa, nseq + g0);
   // uniform: the attending workgroups report it (and, like them, leave the copy as it was)
   if (st.err || (a.qn_w != nullptr && st.kv_len - 1 >= a.rope_rows)) return;
   const DecState32 nx = dec_advance32(st.kv_len, st.ts1, st.sc1, st.so1, a, sa);
@@ -747,18 +750,22 @@ __device__ __forceinline__ void dec_route_workgroup(const DecodeArgs& a, const S
     }
     __syncthreads();
     const int rb = nx.kv_len & 1;
-    const int64_t mine = g_count > g0 ? (g_count - g0 + 7) / 8 : 0;    // attending workgroups g0, g0 + 8, ...
-    for (int64_t e = tid; e < mine * kRouteWords; e += 256) {
-      const int64_t m = e / kRouteWords;
-      const int64_t g = g0 + 8 * m;
-      const int w = (int)(e - m * kRouteWords);
+    const int64_t nwg = (nseq + spw - 1) / spw;
+    const int64_t mine = nwg > g0 ? (nwg - g0 + 7) / 8 : 0;    // attending workgroups g0, g0 + 8, ...
+    const int per = spw * kRouteWords;
+    for (int64_t e = tid; e < mine * per; e += 256) {
+      const int64_t m = e / per;
+      const int rem = (int)(e - m * per);
+      const int64_t g = (g0 + 8 * m) * spw + rem / kRouteWords;
+      const int w = rem % kRouteWords;
+      if (g >= nseq) continue;
       const int64_t val =
           w < 4 ? hdr[w] : (int64_t)(uint32_t)sel[2 * (w - 4)] | ((int64_t)sel[2 * (w - 4) + 1] << 32);
       sa.state[kStHeader + kStSlot * g + kStRoute + kRouteWords * rb + w] = val;
     }
   }
   if (tid == 0) {
-    int64_t* slot = dec_slot(sa.state, g_count + g0);
+    int64_t* slot = dec_slot(sa.state, nseq + g0);
     slot[kStOffset] = st.kv_len;
     slot[kStTail] = st.ts1;
     slot[kStCount] = st.sc1;
@@ -987,6 +994,7 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   T* Ks = reinterpret_cast<T*>(stage_lds);
   T* Vs = reinterpret_cast<T*>(stage_lds + KS_BYTES);   // [80][D], pieces swizzled by row
   __shared__ int selw[4][kDecMaxSum];
+  __shared__ int64_t route_hdr[4];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
@@ -994,7 +1002,7 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   // them apart), attending workgroup bh is blockIdx bh + kRouteGroups
   if constexpr (kStep) {
     if (blockIdx.x < kRouteGroups) {
-      dec_route_workgroup(a, sa, tid);
+      dec_route_workgroup(a, sa, tid, (int64_t)gridDim.x - kRouteGroups, 1, selw[0], route_hdr);
       return;
     }
   }
@@ -1002,7 +1010,14 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   // step mode: this workgroup's counter copy and both route buffers' headers,
   // requested first (the state pointer needs no argument load); the kv_len
   // parity picks a route buffer below
+  // The row-list entries this thread's summary pieces need are requested from both
+  // buffers in the same round trip (the slot is one 256-byte line): waiting for
+  // them then adds no round trip after the counters.
+  constexpr int SKN = kDecMaxSum * PIECES;                         // summary K pieces
+  constexpr int SK = (SKN + 255) / 256;
   int64_t cnt[4] = {}, rh[2][4] = {};
+  uint64_t rsel2[SK] = {};                       // entry of buffer b in bits 32 b (shifted, not indexed:
+                                                 // a parity-indexed array would live in LDS)
   if constexpr (kStep) {
     const int64_t* slot = dec_slot(sa.state, bh);
 #pragma unroll
@@ -1011,6 +1026,13 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int w = 0; w < 4; ++w) rh[b][w] = slot[kStRoute + kRouteWords * b + w];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int* rl = reinterpret_cast<const int*>(slot + kStRoute + kRouteWords * b + 4);
+#pragma unroll
+      for (int it = 0; it < SK; ++it)
+        rsel2[it] |= (uint64_t)(uint32_t)rl[min(tid + it * 256, SKN - 1) / PIECES] << (32 * b);
+    }
     // keep these loads ahead of the first use of an argument: both round trips
     // then overlap instead of following each other
     __builtin_amdgcn_sched_barrier(0);
@@ -1033,8 +1055,6 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   };
   load_q(0);
 
-  constexpr int SKN = kDecMaxSum * PIECES;                         // summary K pieces
-  constexpr int SK = (SKN + 255) / 256;
   const DecState32 st =
       kStep ? dec_advance32(cnt[kStOffset], cnt[kStTail], cnt[kStCount], cnt[kStSumOff], a, sa) : dec_state32<false>(a, sa, bh);
   // with the fused q/k norm, a position past the RoPE table is an error of the step
@@ -1043,15 +1063,10 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
     if (tid == 0) sa.state[kStError] = st.err ? kErrCapacity : kErrRope;
     return;
   }
-  // the row-list entries of this step's route buffer that this thread's summary
-  // pieces need, requested before the window loads so that waiting for them
-  // does not wait for those
-  int rsel[SK] = {};
-  if constexpr (kStep) {
-    const int* rl = reinterpret_cast<const int*>(dec_slot(sa.state, bh) + kStRoute + kRouteWords * (st.kv_len & 1) + 4);
+  // the row-list entries of this step's route buffer (kv_len parity)
+  int rsel[SK];
 #pragma unroll
-    for (int it = 0; it < SK; ++it) rsel[it] = rl[min(tid + it * 256, SKN - 1) / PIECES];
-  }
+  for (int it = 0; it < SK; ++it) rsel[it] = (int)(uint32_t)(rsel2[it] >> (32 * (st.kv_len & 1)));
   const int p = st.kv_len - 1;
   DecQknK qkn_k{};
   if constexpr (qkn) qkn_k = dec_qkn_k_load(a, p, tid % PIECES);
@@ -1273,6 +1288,268 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Step-mode decode with the key tiles split over the waves (bf16, d = 128, GQA groups of at
+// most 16), for batches that fill the chip.  One workgroup per sequence as above, but:
+//   - K is not staged: wave w loads the MFMA A fragments of key tile w (window keys 16w ..
+//     16w + 15; wave 0 also the summary tile) straight from the ring / pool into registers and
+//     computes only that tile's scores (the workgroup kernel computes every tile in every wave);
+//   - V goes to LDS by DMA (global_load_lds_dwordx4: lane l of an instruction writes bytes
+//     16 l of its 1 KiB, so the row swizzle is chosen through the source addresses) -- no
+//     register staging and no LDS writes by the waves;
+//   - the waves exchange per-head tile maxima and the fp32 exponentials through LDS (two
+//     barriers); every wave then sums the exponentials in the workgroup kernel's order and
+//     forms the same P fragments, and computes O^T = V^T P^T for its output tile.
+// LDS is 26 KiB instead of 42, so more sequences are resident per CU, each with fewer memory
+// instructions in flight per lane.  Masks, exponentials, summation order and MFMA sequence
+// are the workgroup kernel's, so the results are bit-identical to it.
+constexpr int kSplitVBytes = kDecMfmaKeys * 128 * 2;
+
+__global__ void __launch_bounds__(256, 4)
+decode_split_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) {
+  StepArgs sa = sa_in;
+  sa.state = state;
+  using T = __bf16;
+  constexpr int D = 128, VEC = 8, KSTEPS = D / 32, NT = kDecMfmaKeys / 16, NPR = (NT + 1) / 2;
+  static_assert(NT == 5 && D / 32 == 4, "one key tile and one output tile per wave, tile 4 on wave 0");
+  __shared__ __attribute__((aligned(16))) unsigned char vlds[kSplitVBytes];
+  __shared__ __attribute__((aligned(16))) float ex[NT][64][4];   // exponentials, per tile and lane
+  __shared__ float tmax[NT][16];                                 // per-tile column maxima
+  __shared__ int selw[4][kDecMaxSum];
+  __shared__ int64_t route_hdr[4];
+  T* Vs = reinterpret_cast<T*>(vlds);            // [80][128], pieces swizzled by row
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lg = lane >> 4, lq = lane & 15;
+  if (blockIdx.x < kRouteGroups) {
+    dec_route_workgroup(a, sa, tid, (int64_t)gridDim.x - kRouteGroups, 1, selw[0], route_hdr);
+    return;
+  }
+  const int bh = (int)blockIdx.x - kRouteGroups;
+  const int64_t* slot = dec_slot(sa.state, bh);
+  int64_t cnt[4], rh[2][4];
+  // row-list entries lq and 4 wave + lg of both buffers, buffer b in bits 32 b (shifted, not
+  // indexed: a parity-indexed array would live in LDS)
+  uint64_t rk2 = 0, rv2 = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) cnt[w] = slot[w];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) rh[b][w] = slot[kStRoute + kRouteWords * b + w];
+    const int* rl = reinterpret_cast<const int*>(slot + kStRoute + kRouteWords * b + 4);
+    rk2 |= (uint64_t)(uint32_t)rl[lq] << (32 * b);
+    rv2 |= (uint64_t)(uint32_t)rl[4 * wave + lg] << (32 * b);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int bi = (int)a.hkv_div.div((uint32_t)bh);
+  const int kvh = bh - bi * a.hkv;
+  const int gsz = a.gsz;
+  const T* qhead = reinterpret_cast<const T*>(q) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz) * D;
+  bf16x8 qf[KSTEPS];
+  {
+    const T* qrow = qhead + (uint32_t)min(lq, gsz - 1) * D + lg * (D / 4);
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 8 * ks);
+  }
+  const DecState32 st = dec_advance32(cnt[kStOffset], cnt[kStTail], cnt[kStCount], cnt[kStSumOff], a, sa);
+  if (st.err) {                                  // uniform: every workgroup sees the same counters
+    if (tid == 0) sa.state[kStError] = kErrCapacity;
+    return;
+  }
+  // entries of this step's route buffer: lq (the summary K fragments of wave 0) and 4 wave + lg
+  // (the summary V row this lane's DMA fills); used when the buffer's key matches
+  const int rsel_k = (int)(uint32_t)(rk2 >> (32 * (st.kv_len & 1)));
+  const int rsel_v = (int)(uint32_t)(rv2 >> (32 * (st.kv_len & 1)));
+  const int p = st.kv_len - 1;
+  const int lo = max(max(p - a.W + 1, st.tail_start), 0);
+  const int nw = p - lo + 1;
+  const int ring = (int)a.ring;
+  const T* knew = reinterpret_cast<const T*>(a.k_new) + (int64_t)bh * D;
+  const T* vnew = reinterpret_cast<const T*>(a.v_new) + (int64_t)bh * D;
+  T* rk = reinterpret_cast<T*>(a.ring_k) + (int64_t)bh * a.kv_rows * D;
+  T* rv = reinterpret_cast<T*>(a.ring_v) + (int64_t)bh * a.kv_rows * D;
+  T* pk = reinterpret_cast<T*>(const_cast<void*>(a.pool_k)) + (int64_t)bh * a.pool_rows * D;
+  T* pv = reinterpret_cast<T*>(const_cast<void*>(a.pool_v)) + (int64_t)bh * a.pool_rows * D;
+  // blocks that became due: pooled (LDS scratch = the V block, free until the DMA below),
+  // written to the pool and read back after the barrier that ends dec_pool32
+  if (st.n_new > 0) dec_pool32<D>(a, st, rk, rv, pk, pv, reinterpret_cast<float*>(vlds), tid);
+  const int slot_lo = (int)a.ring_div.mod((uint32_t)lo);
+  const int r_new = nw - 1;                      // position p: read from k_new / v_new
+  auto ring_off = [&](int r) -> uint32_t {
+    int row = slot_lo + r;
+    if (row >= ring) row -= ring;
+    return (uint32_t)row * D;
+  };
+  // window row r clamped to the last one (finite data; masked keys get P = 0)
+  auto win_row = [&](int r, bool vside) -> const T* {
+    r = min(r, nw - 1);
+    if (r == r_new) return vside ? vnew : knew;
+    return (vside ? rv : rk) + ring_off(r);
+  };
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  // this wave's key tile: K fragments to registers, its 16 V rows by DMA
+  bf16x8 kf[KSTEPS];
+  {
+    const T* src = win_row(16 * wave + lq, false) + lg * (D / 4);
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) kf[ks] = *reinterpret_cast<const bf16x8*>(src + 8 * ks);
+  }
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) {
+    const int i = 4 * wave + ii;
+    const int r = 4 * i + lg;
+    const int pc = lq ^ vrow_swizzle<D>(r);
+    __builtin_amdgcn_global_load_lds(win_row(r, true) + pc * VEC, (lds_ptr)(Vs + 4 * i * D), 16, 0, 0);
+  }
+  // routed selection: left by the previous step's route workgroups, or computed by each wave
+  int ns;
+  bool pre;
+  {
+    const int rb = st.kv_len & 1;
+    const RouteKey want = route_key(st.kv_len, 0, a, sa);
+    const int64_t k0 = rb ? rh[1][0] : rh[0][0];
+    pre = (k0 & ~(0x1fll << 32)) == want.key && (rb ? rh[1][1] : rh[0][1]) == want.layer &&
+          (rb ? rh[1][2] : rh[0][2]) == want.geom && (rb ? rh[1][3] : rh[0][3]) == want.shape;
+    if (pre) {
+      ns = min((int)((k0 >> 32) & 0x1f), kDecMaxSum);
+    } else {
+      const int blk = min((int)a.bs_div.div((uint32_t)p), st.nblocks - 1);
+      ns = dec_select32<true>(p, blk, a, sa, st, lane, selw[wave]);
+    }
+  }
+  auto entry = [&](int j, int rs) -> int {       // pool row of summary j (row 0 when j >= ns)
+    if (j >= ns) return 0;
+    return pre ? min(max(rs, 0), (int)a.pool_rows - 1) : selw[wave][j];
+  };
+  {
+    // summary V rows 64 + 4 wave .. 64 + 4 wave + 3 (entries 4 wave + lg)
+    const int j = 4 * wave + lg;
+    const int r = kDecMaxWin + j;
+    const int pc = lq ^ vrow_swizzle<D>(r);
+    __builtin_amdgcn_global_load_lds(pv + (uint32_t)entry(j, rsel_v) * D + pc * VEC,
+                                     (lds_ptr)(Vs + (kDecMaxWin + 4 * wave) * D), 16, 0, 0);
+  }
+  bf16x8 kf4[KSTEPS];
+  if (wave == 0) {
+    const T* src = pk + (uint32_t)entry(lq, rsel_k) * D + lg * (D / 4);
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) kf4[ks] = *reinterpret_cast<const bf16x8*>(src + 8 * ks);
+  }
+  // append the new token to its ring slot (the staging read it from k_new / v_new)
+  if (wave == 1 && lane < 32) {
+    const int pc = lane & 15;
+    const T* src = lane < 16 ? knew : vnew;
+    T* dst = lane < 16 ? rk : rv;
+    *reinterpret_cast<uint4*>(dst + ring_off(nw - 1) + pc * VEC) = *reinterpret_cast<const uint4*>(src + pc * VEC);
+  }
+  // scores of this wave's tile (and of the summary tile on wave 0), column maxima
+  const float sl2 = a.scale * 1.4426950408889634f;
+  auto tile_scores = [&](const bf16x8 (&k)[KSTEPS], int t) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k[ks], qf[ks], acc, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = 16 * t + 4 * lg + i;
+      acc[i] = key < nw || (key >= kDecMaxWin && key < kDecMaxWin + ns) ? acc[i] : -INFINITY;
+    }
+    return acc;
+  };
+  const f32x4 sc = tile_scores(kf, wave);
+  f32x4 sc4 = {};
+  {
+    float m = col_max4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+    if (lg == 0) tmax[wave][lq] = m;
+    if (wave == 0) {
+      sc4 = tile_scores(kf4, NT - 1);
+      m = col_max4(fmaxf(fmaxf(sc4[0], sc4[1]), fmaxf(sc4[2], sc4[3])));
+      if (lg == 0) tmax[NT - 1][lq] = m;
+    }
+  }
+  __syncthreads();
+  float mx = tmax[0][lq];
+#pragma unroll
+  for (int t = 1; t < NT; ++t) mx = fmaxf(mx, tmax[t][lq]);
+  const float nm = -mx * sl2;                    // nw >= 1: every column has a finite max
+  {
+    f32x4 e;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(fmaf(sc[i], sl2, nm));
+    *reinterpret_cast<f32x4*>(&ex[wave][lane][0]) = e;
+    if (wave == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(fmaf(sc4[i], sl2, nm));
+      *reinterpret_cast<f32x4*>(&ex[NT - 1][lane][0]) = e;
+    }
+  }
+  // this wave's V rows have landed (the DMA counts as outstanding vector memory); after the
+  // barrier every wave's have
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  float lsum = 0.f;
+  bf16x8 pf[NPR];
+  pf[NPR - 1] = bf16x8{};
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const f32x4 e = *reinterpret_cast<const f32x4*>(&ex[t][lane][0]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lsum += e[i];
+      pf[t / 2][(t % 2) * 4 + i] = (__bf16)e[i];
+    }
+  }
+  lsum = col_sum4(lsum);
+  const float inv = __builtin_amdgcn_rcpf(fmaxf(lsum, 1e-30f));
+  // O^T = V^T P^T for output tile mt = wave (as the workgroup kernel)
+  const int mt = wave;
+  f32x4 o[2];
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const int unit = mt * 8 + (lq & 3) * 2 + half;
+    auto vfrag = [&](int t) {
+      const int r = 16 * t + 4 * lg + (lq >> 2);
+      return read_tr(Vs + r * D + (unit ^ (2 * vrow_swizzle<D>(r))) * 4);
+    };
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int pr = 0; pr < NPR; ++pr) {
+      const bf16x4 va = vfrag(2 * pr);
+      const bf16x4 vb = 2 * pr + 1 < NT ? vfrag(2 * pr + 1) : bf16x4{};
+      const bf16x8 vf = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[pr], acc, 0, 0, 0);
+    }
+    o[half] = acc;
+  }
+  if (lq < gsz) {
+    __bf16* orow = reinterpret_cast<__bf16*>(a.out) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz + lq) * D;
+    bf16x8 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = (__bf16)(o[0][i] * inv);
+      w[4 + i] = (__bf16)(o[1][i] * inv);
+    }
+    *reinterpret_cast<bf16x8*>(orow + mt * 32 + lg * 8) = w;
+  }
+  if (tid == 0) {
+    int64_t* ws = dec_slot(sa.state, bh);
+    ws[kStOffset] = st.kv_len;
+    ws[kStTail] = st.ts1;
+    ws[kStCount] = st.sc1;
+    ws[kStSumOff] = st.so1;
+  }
+}
+
+// Sequences (batch x kv heads) from which the step runs decode_split_kernel: measured on
+// MI355X at d = 128, the workgroup kernel is 0.1-0.2 us faster up to 256 sequences and the
+// split kernel 16-19 % faster from 1024 (BFLY_DECODE_SPLIT_MIN overrides; 0 disables it).
+static int64_t decode_split_min() {
+  static const int64_t v = [] {
+    const char* e = getenv("BFLY_DECODE_SPLIT_MIN");
+    return e && *e ? (int64_t)atoll(e) : (int64_t)512;
+  }();
+  return v;
+}
+
 // bf16 with a positive scale (folded into exp2) runs on MFMA when its 32-bit
 // positions and offsets suffice
 static bool decode_on_mfma(const DecodeArgs& a, int d, bool step) {
@@ -1294,7 +1571,15 @@ static void launch_decode(const DecodeArgs& a, const StepArgs& sa, int d, int64_
       m.ring_div = FastDiv::make(a.ring > 0 ? (uint32_t)a.ring : 1u);
       m.hkv_div = FastDiv::make((uint32_t)a.hkv);
       m.gsz = a.hq / a.hkv;
+      m.nseq = (int)grid;
       const int64_t mgrid = kStep ? grid + kRouteGroups : grid;   // step mode: plus the route workgroups
+      if constexpr (kStep) {
+        const int64_t smin = decode_split_min();
+        if (d == 128 && a.qn_w == nullptr && m.gsz <= 16 && smin > 0 && grid >= smin) {
+          hipLaunchKernelGGL(decode_split_kernel, dim3((unsigned)mgrid), dim3(256), 0, stream, sa.state, m.q, m, sa);
+          return;
+        }
+      }
       switch (d) {
         case 64:
           hipLaunchKernelGGL((decode_mfma_kernel<64, kStep>), dim3((unsigned)mgrid), dim3(256), 0, stream, sa.state,

@@ -84,6 +84,46 @@ def test_device_counter_steps_follow_changing_arguments():
             dev._push()
 
 
+# From 512 sequences (batch x kv heads) the step runs decode_split_kernel (d = 128, groups
+# <= 16; the host path runs the workgroup kernel), so equality pins the split kernel to it
+# bit for bit.  520 sequences: a count that is no multiple of the route workgroups; GQA
+# groups of 4 and 16; a cache window of 128 beside the attention window of 64.
+@pytest.mark.parametrize("b,hq,hkv,cw", [(256, 8, 2, 64), (260, 32, 2, 64), (128, 8, 4, 128)])
+def test_split_kernel_steps_equal_host_steps(b, hq, hkv, cw):
+    d, layer, prompt, steps = 128, 5, 333, 200
+    total = prompt + steps
+    g = torch.Generator(device="cuda").manual_seed(b + hq)
+    q = torch.randn(b, hq, total, d, generator=g, device="cuda").bfloat16()
+    k = torch.randn(b, hkv, total, d, generator=g, device="cuda").bfloat16()
+    v = torch.randn(b, hkv, total, d, generator=g, device="cuda").bfloat16()
+    host = bf.CompressedKVCache(block_size=128, local_window_tokens=cw, max_kv_size=total)
+    dev = bf.CompressedKVCache(block_size=128, local_window_tokens=cw, max_kv_size=total)
+    host.update(k[:, :, :prompt], v[:, :, :prompt])
+    dev.update(k[:, :, :prompt], v[:, :, :prompt])
+    dev.use_device_counters()
+    for p in range(prompt, total):
+        a = host.update_and_attend(q[:, :, p:p + 1], k[:, :, p:p + 1], v[:, :, p:p + 1],
+                                   layout=_layout(p + 1, hkv, hq // hkv, layer), local_window_tokens=64)
+        c = dev.decode_step(q[:, :, p:p + 1], k[:, :, p:p + 1], v[:, :, p:p + 1], layer_idx=layer,
+                            local_window_tokens=64)
+        assert torch.equal(a, c), p
+    dev.sync()
+    assert (dev.offset, dev.tail_size, dev.summary_count, dev.summary_offset) == \
+           (host.offset, host.tail_size, host.summary_count, host.summary_offset)
+    assert torch.equal(dev.k_summary, host.k_summary) and torch.equal(dev.v_summary, host.v_summary)
+    assert torch.equal(dev.keys, host.keys) and torch.equal(dev.values, host.values)
+    # and the last row is the reference's active row
+    lay = tp.build_layout(seq_len=total, block_size=128, num_key_value_heads=hkv, num_key_value_groups=hq // hkv,
+                          layer_idx=layer, local_window_blocks=1, sink_count=1, partner_count=1,
+                          partner_rule="causal_shift")
+    sel = slice(0, 4)
+    ref = oa.active(q[sel, :, total - 1:].cpu(), k[sel].cpu(), v[sel].cpu(), layout=lay,
+                    query_positions=torch.tensor([total - 1]), W=64)
+    if cw == 64:
+        err = (c[sel].float().cpu() - ref.float()).abs().max().item()
+        assert err <= 2e-2, err
+
+
 @pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float32, 64)])
 def test_cache_window_differs_from_attention_window(dtype, d):
     """The cache's own window (128, the reference's default) decides summarising and
@@ -153,8 +193,9 @@ def test_device_counter_overflow_raises_at_sync():
             cache.sync()
 
 
-def test_graph_replays_match_eager_steps():
-    b, hq, hkv, d, layer, prompt, steps = 4, 8, 2, 128, 3, 1000, 150
+@pytest.mark.parametrize("b", [4, 256])            # 512 sequences: the split kernel
+def test_graph_replays_match_eager_steps(b):
+    hq, hkv, d, layer, prompt, steps = 8, 2, 128, 3, 1000, 150
     total = prompt + steps
     q = _rand(71, (b, hq, total, d), torch.bfloat16).cuda()
     k = _rand(72, (b, hkv, total, d), torch.bfloat16).cuda()

@@ -728,7 +728,7 @@ __device__ __forceinline__ RouteKey route_key(int kv_len, int ns, const DecodeAr
 // j + 8 and holds sequences spw*j .. spw*j + spw - 1, so it runs on the same
 // XCD).  It touches no q, cache row or output.  sel / hdr: the caller's LDS.
 __device__ __forceinline__ void dec_route_workgroup(const DecodeArgs& a, const StepArgs& sa, int tid, int64_t nseq,
-                                                    int spw, int* sel, int64_t* hdr) {
+                                                    int spw, int* sel, int64_t* hdr, int nthreads = 256) {
   const int64_t g0 = blockIdx.x;
   const DecState32 st = dec_state32<true>(a, sa, nseq + g0);
   // uniform: the attending workgroups report it (and, like them, leave the copy as it was)
@@ -753,7 +753,7 @@ __device__ __forceinline__ void dec_route_workgroup(const DecodeArgs& a, const S
     const int64_t nwg = (nseq + spw - 1) / spw;
     const int64_t mine = nwg > g0 ? (nwg - g0 + 7) / 8 : 0;    // attending workgroups g0, g0 + 8, ...
     const int per = spw * kRouteWords;
-    for (int64_t e = tid; e < mine * per; e += 256) {
+    for (int64_t e = tid; e < mine * per; e += nthreads) {
       const int64_t m = e / per;
       const int rem = (int)(e - m * per);
       const int64_t g = (g0 + 8 * m) * spw + rem / kRouteWords;
@@ -1291,45 +1291,74 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
 // ---------------------------------------------------------------------------------------------
 // Step-mode decode with the key tiles split over the waves (bf16, d = 128, GQA groups of at
 // most 16), for batches that fill the chip.  One workgroup per sequence as above, but:
-//   - K is not staged: wave w loads the MFMA A fragments of key tile w (window keys 16w ..
-//     16w + 15; wave 0 also the summary tile) straight from the ring / pool into registers and
-//     computes only that tile's scores (the workgroup kernel computes every tile in every wave);
+//   - window K is not staged: wave w loads the MFMA A fragments of key tile w (window keys
+//     16w .. 16w + 15) straight from the ring into registers and computes only that tile's
+//     scores (the workgroup kernel computes every tile in every wave); wave 0 also computes
+//     the summary tile, whose 16 rows it stages in LDS by DMA (so no wave holds two tiles of
+//     K fragments in registers);
 //   - V goes to LDS by DMA (global_load_lds_dwordx4: lane l of an instruction writes bytes
-//     16 l of its 1 KiB, so the row swizzle is chosen through the source addresses) -- no
+//     16 l of its 1 KiB, so the row swizzles are chosen through the source addresses) -- no
 //     register staging and no LDS writes by the waves;
+//   - the routed summaries' V enters the last PV k-step as register fragments: lane (lq, lg)
+//     loads the 2-byte elements that the transposing LDS read would give it, so only the 64
+//     window rows of V are staged;
 //   - the waves exchange per-head tile maxima and the fp32 exponentials through LDS (two
-//     barriers); every wave then sums the exponentials in the workgroup kernel's order and
-//     forms the same P fragments, and computes O^T = V^T P^T for its output tile.
-// LDS is 26 KiB instead of 42, so more sequences are resident per CU, each with fewer memory
-// instructions in flight per lane.  Masks, exponentials, summation order and MFMA sequence
-// are the workgroup kernel's, so the results are bit-identical to it.
-constexpr int kSplitVBytes = kDecMfmaKeys * 128 * 2;
+//     barriers; the exponentials of tiles 0..3 reuse the summary K rows); every wave then sums
+//     the exponentials in the workgroup kernel's order, forms the same P fragments, and
+//     computes O^T = V^T P^T for its output tile.
+// 22 KiB of LDS and at most 72 VGPRs, so 7 sequences are resident per CU.  Masks,
+// exponentials, summation order and MFMA inputs are the workgroup kernel's, so the results
+// are bit-identical to it.
+constexpr int kSplitOffSK = kDecMaxWin * 128 * 2;                  // V window rows [64][128]
+constexpr int kSplitOffEx4 = kSplitOffSK + kDecMaxSum * 128 * 2;   // summary K [16][128] / ex tiles 0..3
+constexpr int kSplitOffTmax = kSplitOffEx4 + 64 * 4 * 4;           // ex tile 4 [64][4]
+constexpr int kSplitOffSel = kSplitOffTmax + 5 * 16 * 4;           // tmax [5][16]
+constexpr int kSplitLds = kSplitOffSel + 4 * kDecMaxSum * 4;       // selw [4][16]
+static_assert(kDecMaxSum * 128 * 2 == 4 * 64 * 4 * 4, "ex tiles 0..3 fill the summary K rows");
 
-__global__ void __launch_bounds__(256, 4)
+// piece pc of summary K row r sits at pc ^ (r & 15): the fragment reads of 16 rows hit 16
+// distinct 16-byte positions
+__device__ __forceinline__ constexpr int krow_swizzle(int row) { return row & 15; }
+
+// global_load_lds_dwordx4: lane l's 16 bytes at g go to LDS bytes lds + 16 l (lds wave-uniform).
+// Issued as assembly so that the compiler's wait counting sees only loads into registers:
+// with an LDS DMA in its count it cannot rely on return order and waits for everything before
+// any register use.  Loads still return in order among themselves, so its waits stay
+// sufficient; whoever reads the LDS waits for the DMA itself (s_waitcnt vmcnt(0)).
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory", "m0");
+}
+
+__global__ void __launch_bounds__(256, 7)   // 7 waves per SIMD: 7 sequences per CU (LDS)
 decode_split_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) {
   StepArgs sa = sa_in;
   sa.state = state;
   using T = __bf16;
   constexpr int D = 128, VEC = 8, KSTEPS = D / 32, NT = kDecMfmaKeys / 16, NPR = (NT + 1) / 2;
   static_assert(NT == 5 && D / 32 == 4, "one key tile and one output tile per wave, tile 4 on wave 0");
-  __shared__ __attribute__((aligned(16))) unsigned char vlds[kSplitVBytes];
-  __shared__ __attribute__((aligned(16))) float ex[NT][64][4];   // exponentials, per tile and lane
-  __shared__ float tmax[NT][16];                                 // per-tile column maxima
-  __shared__ int selw[4][kDecMaxSum];
-  __shared__ int64_t route_hdr[4];
-  T* Vs = reinterpret_cast<T*>(vlds);            // [80][128], pieces swizzled by row
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kSplitLds];
+  T* Vs = reinterpret_cast<T*>(lds);                                 // pieces swizzled by row
+  T* SKs = reinterpret_cast<T*>(lds + kSplitOffSK);                  // until the first barrier
+  auto ex = [&](int t) -> float* {                                   // [64][4] per tile, after it
+    return reinterpret_cast<float*>(lds + (t < 4 ? kSplitOffSK + t * 1024 : kSplitOffEx4));
+  };
+  float(*tmax)[16] = reinterpret_cast<float(*)[16]>(lds + kSplitOffTmax);
+  int(*selw)[kDecMaxSum] = reinterpret_cast<int(*)[kDecMaxSum]>(lds + kSplitOffSel);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
   if (blockIdx.x < kRouteGroups) {
-    dec_route_workgroup(a, sa, tid, (int64_t)gridDim.x - kRouteGroups, 1, selw[0], route_hdr);
+    dec_route_workgroup(a, sa, tid, a.nseq, 1, selw[0], reinterpret_cast<int64_t*>(lds));
     return;
   }
   const int bh = (int)blockIdx.x - kRouteGroups;
   const int64_t* slot = dec_slot(sa.state, bh);
   int64_t cnt[4], rh[2][4];
-  // row-list entries lq and 4 wave + lg of both buffers, buffer b in bits 32 b (shifted, not
-  // indexed: a parity-indexed array would live in LDS)
-  uint64_t rk2 = 0, rv2 = 0;
+  // row-list entry lq of both buffers, buffer b in bits 32 b (shifted, not indexed: a
+  // parity-indexed array would live in LDS)
+  uint64_t rk2 = 0;
 #pragma unroll
   for (int w = 0; w < 4; ++w) cnt[w] = slot[w];
 #pragma unroll
@@ -1338,7 +1367,6 @@ decode_split_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in)
     for (int w = 0; w < 4; ++w) rh[b][w] = slot[kStRoute + kRouteWords * b + w];
     const int* rl = reinterpret_cast<const int*>(slot + kStRoute + kRouteWords * b + 4);
     rk2 |= (uint64_t)(uint32_t)rl[lq] << (32 * b);
-    rv2 |= (uint64_t)(uint32_t)rl[4 * wave + lg] << (32 * b);
   }
   __builtin_amdgcn_sched_barrier(0);
   const int bi = (int)a.hkv_div.div((uint32_t)bh);
@@ -1356,10 +1384,9 @@ decode_split_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in)
     if (tid == 0) sa.state[kStError] = kErrCapacity;
     return;
   }
-  // entries of this step's route buffer: lq (the summary K fragments of wave 0) and 4 wave + lg
-  // (the summary V row this lane's DMA fills); used when the buffer's key matches
+  // entry lq of this step's route buffer (used when the buffer's key matches); lane
+  // 16 g + j holds entry j for every g
   const int rsel_k = (int)(uint32_t)(rk2 >> (32 * (st.kv_len & 1)));
-  const int rsel_v = (int)(uint32_t)(rv2 >> (32 * (st.kv_len & 1)));
   const int p = st.kv_len - 1;
   const int lo = max(max(p - a.W + 1, st.tail_start), 0);
   const int nw = p - lo + 1;
@@ -1370,9 +1397,9 @@ decode_split_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in)
   T* rv = reinterpret_cast<T*>(a.ring_v) + (int64_t)bh * a.kv_rows * D;
   T* pk = reinterpret_cast<T*>(const_cast<void*>(a.pool_k)) + (int64_t)bh * a.pool_rows * D;
   T* pv = reinterpret_cast<T*>(const_cast<void*>(a.pool_v)) + (int64_t)bh * a.pool_rows * D;
-  // blocks that became due: pooled (LDS scratch = the V block, free until the DMA below),
+  // blocks that became due: pooled (LDS scratch = the V rows, free until the DMA below),
   // written to the pool and read back after the barrier that ends dec_pool32
-  if (st.n_new > 0) dec_pool32<D>(a, st, rk, rv, pk, pv, reinterpret_cast<float*>(vlds), tid);
+  if (st.n_new > 0) dec_pool32<D>(a, st, rk, rv, pk, pv, reinterpret_cast<float*>(lds), tid);
   const int slot_lo = (int)a.ring_div.mod((uint32_t)lo);
   const int r_new = nw - 1;                      // position p: read from k_new / v_new
   auto ring_off = [&](int r) -> uint32_t {
@@ -1387,19 +1414,14 @@ decode_split_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in)
     return (vside ? rv : rk) + ring_off(r);
   };
   typedef __attribute__((address_space(3))) void* lds_ptr;
-  // this wave's key tile: K fragments to registers, its 16 V rows by DMA
+  // Requests in the order of their use: this wave's K fragments (window tile `wave`), the
+  // summary K rows (wave 0, DMA), then the V rows (DMA) and the summary V fragments, which are
+  // needed only after the first barrier.
   bf16x8 kf[KSTEPS];
   {
     const T* src = win_row(16 * wave + lq, false) + lg * (D / 4);
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) kf[ks] = *reinterpret_cast<const bf16x8*>(src + 8 * ks);
-  }
-#pragma unroll
-  for (int ii = 0; ii < 4; ++ii) {
-    const int i = 4 * wave + ii;
-    const int r = 4 * i + lg;
-    const int pc = lq ^ vrow_swizzle<D>(r);
-    __builtin_amdgcn_global_load_lds(win_row(r, true) + pc * VEC, (lds_ptr)(Vs + 4 * i * D), 16, 0, 0);
   }
   // routed selection: left by the previous step's route workgroups, or computed by each wave
   int ns;
@@ -1417,30 +1439,53 @@ decode_split_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in)
       ns = dec_select32<true>(p, blk, a, sa, st, lane, selw[wave]);
     }
   }
-  auto entry = [&](int j, int rs) -> int {       // pool row of summary j (row 0 when j >= ns)
-    if (j >= ns) return 0;
-    return pre ? min(max(rs, 0), (int)a.pool_rows - 1) : selw[wave][j];
+  // pool row of summary j < 16 (row 0 when j >= ns); rs = entry j of the route buffer.
+  // Branch-free: selw is read either way (unused when the route buffer is)
+  auto entry = [&](int j, int rs) -> int {
+    const int e = pre ? min(max(rs, 0), (int)a.pool_rows - 1) : selw[wave][j];
+    return j < ns ? e : 0;
   };
-  {
-    // summary V rows 64 + 4 wave .. 64 + 4 wave + 3 (entries 4 wave + lg)
-    const int j = 4 * wave + lg;
-    const int r = kDecMaxWin + j;
-    const int pc = lq ^ vrow_swizzle<D>(r);
-    __builtin_amdgcn_global_load_lds(pv + (uint32_t)entry(j, rsel_v) * D + pc * VEC,
-                                     (lds_ptr)(Vs + (kDecMaxWin + 4 * wave) * D), 16, 0, 0);
-  }
-  bf16x8 kf4[KSTEPS];
-  if (wave == 0) {
-    const T* src = pk + (uint32_t)entry(lq, rsel_k) * D + lg * (D / 4);
+  // route-buffer entries of summaries 4 lg + jj (summary V fragments) and 4 jj + lg (summary K
+  // rows), fetched together from the lanes that hold them (lane j holds entry j)
+  int ev[4], ek[4];
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) kf4[ks] = *reinterpret_cast<const bf16x8*>(src + 8 * ks);
+  for (int jj = 0; jj < 4; ++jj) {
+    ev[jj] = __builtin_amdgcn_ds_bpermute(4 * (4 * lg + jj), rsel_k);
+    ek[jj] = __builtin_amdgcn_ds_bpermute(4 * (4 * jj + lg), rsel_k);
   }
-  // append the new token to its ring slot (the staging read it from k_new / v_new)
-  if (wave == 1 && lane < 32) {
-    const int pc = lane & 15;
-    const T* src = lane < 16 ? knew : vnew;
-    T* dst = lane < 16 ? rk : rv;
-    *reinterpret_cast<uint4*>(dst + ring_off(nw - 1) + pc * VEC) = *reinterpret_cast<const uint4*>(src + pc * VEC);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr)lds;
+  if (wave == 0) {
+    // summary K rows 4 i + lg (instruction i), pieces swizzled by row
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * i + lg;
+      const int pc = lq ^ krow_swizzle(r);
+      lds_dma16(pk + (uint32_t)entry(r, ek[i]) * D + pc * VEC, lds0 + kSplitOffSK + 1024 * i);
+    }
+  }
+  // this wave's 16 V rows by DMA (rows 4 i + lg of instruction i, pieces swizzled by row)
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) {
+    const int i = 4 * wave + ii;
+    const int r = 4 * i + lg;
+    const int pc = lq ^ vrow_swizzle<D>(r);
+    lds_dma16(win_row(r, true) + pc * VEC, lds0 + 1024 * i);
+  }
+  // summary V fragments of output tile mt = wave: element jj of half h is summary 4 lg + jj at
+  // d = 32 wave + 8 (lq >> 2) + 4 h + (lq & 3) -- what read_tr would return for staged row
+  // 64 + 4 lg + jj.  Summaries past ns read pool row 0 and are zeroed at their use, as the
+  // workgroup kernel zeroes its staged rows.  16-bit vector lanes, so that the loads fill
+  // register halves in place (no packing that would wait for them here).
+  typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+  u16x4 svraw[2] = {u16x4{}, u16x4{}};
+  {
+    const unsigned short* col = reinterpret_cast<const unsigned short*>(pv) + wave * 32 + 8 * (lq >> 2) + (lq & 3);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const unsigned short* src = col + (uint32_t)entry(4 * lg + jj, ev[jj]) * D;
+      svraw[0][jj] = src[0];
+      svraw[1][jj] = src[4];
+    }
   }
   // scores of this wave's tile (and of the summary tile on wave 0), column maxima
   const float sl2 = a.scale * 1.4426950408889634f;
@@ -1456,11 +1501,26 @@ decode_split_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in)
     return acc;
   };
   const f32x4 sc = tile_scores(kf, wave);
+  // append the new token's K to its ring slot: window row nw - 1 was read from k_new, and the
+  // lanes of row 16 wave + lq = nw - 1 hold it (d = 32 lg + 8 ks + 0..7)
+  if (16 * wave + lq == nw - 1) {
+    T* dst = rk + ring_off(nw - 1) + lg * (D / 4);
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) *reinterpret_cast<bf16x8*>(dst + 8 * ks) = kf[ks];
+  }
   f32x4 sc4 = {};
   {
     float m = col_max4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
     if (lg == 0) tmax[wave][lq] = m;
     if (wave == 0) {
+      // the summary rows (this wave's DMA) have landed: a full wait, since LDS-DMA and loads
+      // returning to registers are not guaranteed to complete in issue order (the compiler
+      // waits for everything before the first score MFMA for the same reason)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      bf16x8 kf4[KSTEPS];
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks)
+        kf4[ks] = *reinterpret_cast<const bf16x8*>(SKs + lq * D + ((4 * lg + ks) ^ krow_swizzle(lq)) * VEC);
       sc4 = tile_scores(kf4, NT - 1);
       m = col_max4(fmaxf(fmaxf(sc4[0], sc4[1]), fmaxf(sc4[2], sc4[3])));
       if (lg == 0) tmax[NT - 1][lq] = m;
@@ -1475,23 +1535,29 @@ decode_split_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in)
     f32x4 e;
 #pragma unroll
     for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(fmaf(sc[i], sl2, nm));
-    *reinterpret_cast<f32x4*>(&ex[wave][lane][0]) = e;
+    *reinterpret_cast<f32x4*>(ex(wave) + lane * 4) = e;
     if (wave == 0) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(fmaf(sc4[i], sl2, nm));
-      *reinterpret_cast<f32x4*>(&ex[NT - 1][lane][0]) = e;
+      *reinterpret_cast<f32x4*>(ex(NT - 1) + lane * 4) = e;
     }
   }
   // this wave's V rows have landed (the DMA counts as outstanding vector memory); after the
   // barrier every wave's have
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  // append the new token's V (staged row nw - 1, read from v_new)
+  if (wave == 1 && lane < 16) {
+    const int r = nw - 1;
+    *reinterpret_cast<uint4*>(rv + ring_off(r) + lane * VEC) =
+        *reinterpret_cast<const uint4*>(Vs + r * D + (lane ^ vrow_swizzle<D>(r)) * VEC);
+  }
   float lsum = 0.f;
   bf16x8 pf[NPR];
   pf[NPR - 1] = bf16x8{};
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    const f32x4 e = *reinterpret_cast<const f32x4*>(&ex[t][lane][0]);
+    const f32x4 e = *reinterpret_cast<const f32x4*>(ex(t) + lane * 4);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       lsum += e[i];
@@ -1500,7 +1566,15 @@ decode_split_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in)
   }
   lsum = col_sum4(lsum);
   const float inv = __builtin_amdgcn_rcpf(fmaxf(lsum, 1e-30f));
-  // O^T = V^T P^T for output tile mt = wave (as the workgroup kernel)
+  bf16x4 svf[2];
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const bool live = 4 * lg + jj < ns;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) svf[h][jj] = __builtin_bit_cast(T, (unsigned short)(live ? svraw[h][jj] : 0));
+  }
+  // O^T = V^T P^T for output tile mt = wave (as the workgroup kernel); the summary tile's V
+  // fragments come from registers
   const int mt = wave;
   f32x4 o[2];
 #pragma unroll
@@ -1513,7 +1587,7 @@ decode_split_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in)
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int pr = 0; pr < NPR; ++pr) {
-      const bf16x4 va = vfrag(2 * pr);
+      const bf16x4 va = 2 * pr == NT - 1 ? svf[half] : vfrag(2 * pr);
       const bf16x4 vb = 2 * pr + 1 < NT ? vfrag(2 * pr + 1) : bf16x4{};
       const bf16x8 vf = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[pr], acc, 0, 0, 0);

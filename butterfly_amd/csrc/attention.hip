@@ -20,6 +20,8 @@
 //    (batch, kv head, query); lanes over keys for scores and over d for output.
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "bfly_topology.h"
 #include "cache_update.h"
 
@@ -235,6 +237,22 @@ struct MfmaArgs {
   int64_t upd_wgs;
 };
 
+// A batched streaming launch: the attention of up to kMaxUpdateParts consecutive chunks whose
+// cache updates are all done, one grid row band per chunk.  Each chunk keeps the arguments of
+// its own cache state (the counters right after its update), so its results are those of a
+// launch of its own.
+struct ChunkArgs {
+  const void* q;
+  void* out;
+  int tq, qlo, qhi, key_lo, kv_len, nsum, nblocks, c_first, nchunks;
+  bfly_topology_t topo;
+};
+struct ChunkBatch {
+  int rows_per_chunk;     // grid rows of one chunk (batch x kv heads x head parts)
+  ChunkArgs c[kMaxUpdateParts];
+};
+struct NoBatch {};
+
 // Work unit = (batch, kv head, segment of seg_chunks 64-position chunks).
 // Software pipeline per chunk c (even segments walk chunks upwards, odd ones
 // downwards; see `dir`):
@@ -251,9 +269,13 @@ struct MfmaArgs {
 // workgroups that run the NEXT chunk's cache update (append + pooling) while
 // the attention workgroups run this chunk; the host fuses only when the update
 // writes no ring slot or pool row that this chunk's attention reads.
-template <int D, bool kUpd = false>
+template <int D, bool kUpd = false, bool kBatch = false>
 __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1)
-attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunks, int hper) {
+attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, int nchunks_in, int hper,
+                 std::conditional_t<kBatch, ChunkBatch, NoBatch> cb) {
+  AttnArgs a = a_in;
+  MfmaArgs m = m_in;
+  int c_first = c_first_in, nchunks = nchunks_in;
   using C = MfmaCfg<D>;
   __shared__ __attribute__((aligned(16))) unsigned char smem[C::LDS];
   __shared__ int cand_n[kSumSlots], cand_b[kSumSlots];
@@ -262,16 +284,39 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
   __bf16* Vs = reinterpret_cast<__bf16*>(smem + C::K_BYTES);    // [kSlots][D], pieces swizzled by row
   static_assert(C::LDS >= 256 * 8 * 4, "pooling scratch aliases the staging tiles");
   if constexpr (kUpd) {
-    if ((int)blockIdx.y >= m.attn_y) {
-      const int64_t lin = (int64_t)(blockIdx.y - m.attn_y) * gridDim.x + blockIdx.x;
-      if (lin >= m.upd_wgs) return;
-      const int64_t per_kv = (int64_t)m.upd_x * m.upd_rows;
+    // (the kernel argument itself, not the local copy: the job's part arrays are indexed at
+    // run time, which would put a modified copy in scratch memory)
+    const MfmaArgs& mu = m_in;
+    if ((int)blockIdx.y >= mu.attn_y) {
+      const int64_t lin = (int64_t)(blockIdx.y - mu.attn_y) * gridDim.x + blockIdx.x;
+      if (lin >= mu.upd_wgs) return;
+      const int64_t per_kv = (int64_t)mu.upd_x * mu.upd_rows;
       const int kv = (int)(lin / per_kv);
       const int64_t r = lin - kv * per_kv;
-      const int64_t row = r / m.upd_x;
-      cache_update_body<__bf16, 8>(m.upd, r - row * m.upd_x, row, kv, reinterpret_cast<float*>(smem));
+      const int64_t row = r / mu.upd_x;
+      cache_update_body<__bf16, 8>(mu.upd, r - row * mu.upd_x, row, kv, reinterpret_cast<float*>(smem));
       return;
     }
+  }
+
+  int yrow = (int)blockIdx.y;
+  if constexpr (kBatch) {
+    // this workgroup's chunk: its queries, output and cache state
+    const int zc = yrow / cb.rows_per_chunk;
+    yrow -= zc * cb.rows_per_chunk;
+    const ChunkArgs& ck = cb.c[zc];
+    a.q = ck.q;
+    a.out = ck.out;
+    a.tq = ck.tq;
+    a.topo = ck.topo;
+    m.qlo = ck.qlo;
+    m.qhi = ck.qhi;
+    m.key_lo = ck.key_lo;
+    m.kv_len = ck.kv_len;
+    m.nsum = ck.nsum;
+    m.nblocks = ck.nblocks;
+    c_first = ck.c_first;
+    nchunks = ck.nchunks;
   }
 
   const int tid = threadIdx.x;
@@ -281,13 +326,16 @@ attn_mfma_kernel(AttnArgs a, MfmaArgs m, int seg_chunks, int c_first, int nchunk
   // small grids split a GQA group's heads over workgroups of hper heads each
   const int gsz = a.hq / a.hkv;
   const int nparts = (gsz + hper - 1) / hper;
-  const int bh = blockIdx.y / nparts, hpart = blockIdx.y - bh * nparts;
+  const int bh = yrow / nparts, hpart = yrow - bh * nparts;
   const int bi = bh / a.hkv;
   const int kvh = bh - bi * a.hkv;
   const int hlo = hpart * hper;
   const int hhi = min(gsz, hlo + hper);
   const int cbeg = c_first + seg * seg_chunks;
   const int cend = min(cbeg + seg_chunks, c_first + nchunks);
+  if constexpr (kBatch) {
+    if (cbeg >= cend) return;   // the grid's segments cover the batch's longest chunk
+  }
 
   const int64_t kv_off = ((int64_t)bi * a.hkv + kvh) * a.kv_rows * D;
   const int64_t pool_off = ((int64_t)bi * a.hkv + kvh) * a.pool_rows * D;
@@ -758,15 +806,15 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
       BFLY_CHECK_ARG(ux <= INT32_MAX && upd_rows <= 65535 && grid.y + extra <= 65535, "%s: grid too large", what);
       grid.y += (unsigned)extra;
       switch (a.d) {
-        case 64: hipLaunchKernelGGL((attn_mfma_kernel<64, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
-        case 128: hipLaunchKernelGGL((attn_mfma_kernel<128, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
-        default: hipLaunchKernelGGL((attn_mfma_kernel<256, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
+        case 64: hipLaunchKernelGGL((attn_mfma_kernel<64, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
+        case 128: hipLaunchKernelGGL((attn_mfma_kernel<128, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
+        default: hipLaunchKernelGGL((attn_mfma_kernel<256, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
       }
     } else {
       switch (a.d) {
-        case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
-        case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
-        default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper); break;
+        case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
+        case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
+        default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
       }
     }
   } else {
@@ -779,6 +827,84 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
       hipLaunchKernelGGL(attn_generic_kernel<float>, grid, dim3(64), 0, stream, a);
     else
       hipLaunchKernelGGL(attn_generic_kernel<__bf16>, grid, dim3(64), 0, stream, a);
+  }
+  BFLY_CHECK_LAUNCH(what);
+  return BFLY_OK;
+}
+
+// The attention of n (<= kMaxUpdateParts) consecutive streaming chunks in one launch (MFMA
+// path, neighbour rows from each chunk's topology): ch[j] holds chunk j's arguments as
+// bfly_stream_chunks builds them for a launch of its own; they differ only in the query range,
+// q / out and the cache state.  Optionally with a cache update on extra grid rows.  The grid
+// shape follows launch_attention's rules for the whole batch.
+static int launch_attention_batch(const AttnArgs* ch, int n, hipStream_t stream, const char* what,
+                                  const UpdateJob* upd = nullptr, int64_t upd_rows = 0) {
+  BFLY_CHECK_ARG(n >= 1 && n <= kMaxUpdateParts, "%s: batch of %d chunks", what, n);
+  const AttnArgs& a = ch[0];
+  ChunkBatch cb{};
+  int64_t nch_max = 0;
+  for (int j = 0; j < n; ++j) {
+    const AttnArgs& c = ch[j];
+    BFLY_CHECK_ARG(aligned16(c.q) && aligned16(c.out), "%s: tensor pointers must be 16-byte aligned", what);
+    BFLY_CHECK_ARG(c.tq > 0 && c.nbr == nullptr && c.qpos == nullptr, "%s: chunk %d arguments", what, j);
+    const int64_t cf = floordiv(c.q_pos0, kPage);
+    const int64_t nc = floordiv(c.q_pos0 + c.tq - 1, kPage) - cf + 1;
+    nch_max = nc > nch_max ? nc : nch_max;
+    ChunkArgs& k = cb.c[j];
+    k.q = c.q;
+    k.out = c.out;
+    k.tq = (int)c.tq;
+    k.qlo = (int)c.q_pos0;
+    k.qhi = (int)(c.q_pos0 + c.tq);
+    k.key_lo = (int)c.key_lo;
+    k.kv_len = (int)c.kv_len;
+    k.nsum = (int)(c.nsum < c.nblocks ? c.nsum : c.nblocks);
+    k.nblocks = (int)c.nblocks;
+    k.c_first = (int)cf;
+    k.nchunks = (int)nc;
+    k.topo = c.topo;
+  }
+  const int64_t groups = a.batch * a.hkv;
+  int seg = 1;
+  while (seg < kMaxSegChunks && (nch_max + 2 * seg - 1) / (2 * seg) * groups * n >= 512) seg *= 2;
+  const int64_t nseg = (nch_max + seg - 1) / seg;
+  const int64_t capacity = a.d <= 128 ? 512 : 256;
+  const int gsz = a.hq / a.hkv;
+  int hsplit = 1;
+  while (hsplit < gsz && nseg * groups * n * hsplit * 2 <= capacity) hsplit *= 2;
+  const int hq_per = (gsz + hsplit - 1) / hsplit;
+  const int hper = hq_per >= 2 ? (hq_per + 1) & ~1 : 1;
+  const int nparts = (gsz + hper - 1) / hper;
+  cb.rows_per_chunk = (int)(groups * nparts);
+  BFLY_CHECK_ARG(nseg <= INT32_MAX && groups * nparts * n <= 65535, "%s: grid too large", what);
+  MfmaArgs m{};
+  m.ring = (int)a.ring;
+  m.kcap = a.kcap;
+  m.bs = a.bs;
+  m.W = a.W;
+  m.token_cutoff = a.token_cutoff;
+  dim3 grid((unsigned)nseg, (unsigned)(groups * nparts * n));
+  if (upd != nullptr) {
+    const int64_t ux = update_x(upd->n_blocks, upd->step, upd->d, 8);
+    m.upd = *upd;
+    m.attn_y = (int)grid.y;
+    m.upd_x = (int)ux;
+    m.upd_rows = (int)upd_rows;
+    m.upd_wgs = ux * upd_rows * 2;
+    const int64_t extra = (m.upd_wgs + nseg - 1) / nseg;
+    BFLY_CHECK_ARG(ux <= INT32_MAX && upd_rows <= 65535 && grid.y + extra <= 65535, "%s: grid too large", what);
+    grid.y += (unsigned)extra;
+    switch (a.d) {
+      case 64: hipLaunchKernelGGL((attn_mfma_kernel<64, true, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
+      case 128: hipLaunchKernelGGL((attn_mfma_kernel<128, true, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
+      default: hipLaunchKernelGGL((attn_mfma_kernel<256, true, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
+    }
+  } else {
+    switch (a.d) {
+      case 64: hipLaunchKernelGGL((attn_mfma_kernel<64, false, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
+      case 128: hipLaunchKernelGGL((attn_mfma_kernel<128, false, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
+      default: hipLaunchKernelGGL((attn_mfma_kernel<256, false, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
+    }
   }
   BFLY_CHECK_LAUNCH(what);
   return BFLY_OK;
@@ -960,73 +1086,118 @@ extern "C" int bfly_stream_chunks(int64_t n_chunks, const void* const* q, const 
     return BFLY_ERR_UNSUPPORTED;
   }
   const int64_t rows = batch * hkv;
-  auto publish = [&]() {
-    counters[0] = s.offset;
-    counters[1] = s.tail;
-    counters[2] = s.count;
-    counters[3] = s.sum_off;
+  auto publish = [&](const StreamCounters& st) {
+    counters[0] = st.offset;
+    counters[1] = st.tail;
+    counters[2] = st.count;
+    counters[3] = st.sum_off;
   };
-  auto launch_update = [&](const PlannedUpdate& u) -> int {
-    const UpdateJob& j = u.job;
-    return bfly_cache_update(j.k_new, j.v_new, dtype, batch, hkv, j.step, head_dim, ring_k, ring_v, ring_capacity,
-                             j.offset, j.first_pos, j.n_blocks, block_size, pool_k, pool_v, pool_capacity,
-                             j.first_slot, stream);
+  // Chunks go in batches: one attention launch per batch, each chunk with the arguments of
+  // its own cache state (so its output is that of a launch of its own), and one update job per
+  // batch that appends all its chunks and pools every block that becomes due over them (the
+  // per-chunk counter steps run on the host; the pooled blocks are consecutive).  A batch's
+  // update rides with the previous batch's attention when the two touch disjoint ring slots.
+  // Batch tokens are capped at (ring - 2*64) / 2 so that consecutive batches can share a
+  // launch; with a ring of a few chunks that is one chunk per batch, the per-chunk schedule.
+  struct Batch {
+    int64_t first = 0, count = 0, total = 0;
+    AttnArgs args[kMaxUpdateParts];
+    UpdateJob job{};
+    StreamCounters end{};
+    bool overflow = false;   // the last chunk exhausted the pool: its update runs, its attention not
+    int stop_rc = BFLY_OK;   // the chunk after the batch does not fit (its error)
   };
+  const int64_t budget = (ring_capacity - 2 * kPage) / 2;
+  auto plan_batch = [&](const StreamCounters& s0, int64_t from, Batch& bt) -> int {
+    bt = Batch{};
+    bt.first = from;
+    bt.end = s0;
+    StreamCounters st = s0;
+    int64_t blocks = 0;
+    for (int64_t c = from; c < n_chunks && bt.count < kMaxUpdateParts; ++c) {
+      const int64_t len = chunk_len[c];
+      if (bt.count > 0 && (bt.total + len > budget || s0.tail + bt.total + len > ring_capacity)) break;
+      StreamCounters nx = st;
+      PlannedUpdate pu{};
+      const int prc = plan_update(nx, len, k[c], v[c], ring_k, ring_v, ring_capacity, pool_k, pool_v, pool_capacity,
+                                  block_size, cache_window, head_dim, &pu);
+      if (prc) {                      // does not fit: the batch ends before it, the error is its
+        bt.stop_rc = prc;
+        break;
+      }
+      if (pu.overflow && bt.count > 0) break;   // it starts the next batch, alone
+      const int frc = finish_update(nx, pu, len, pool_capacity, block_size, cache_window);
+      if (bt.count == 0) bt.job = pu.job;      // offset, first pooled block and slot of the batch
+      bt.job.k_part[bt.count] = k[c];
+      bt.job.v_part[bt.count] = v[c];
+      bt.job.part_end[bt.count] = bt.total + len;
+      blocks += pu.n_new;
+      bt.total += len;
+      const int64_t nblocks = (nx.offset + block_size - 1) / block_size;
+      AttnArgs& a = bt.args[bt.count];
+      a = AttnArgs{};
+      const int trc = bfly_topology_init(nblocks, layer_idx, partner_rule, local_window_blocks, sink_count,
+                                         partner_count, &a.topo);
+      if (trc) return trc;
+      a.q = q[c]; a.out = out[c]; a.k = ring_k; a.v = ring_v; a.ks = pool_k; a.vs = pool_v;
+      a.nbr = nullptr; a.qpos = nullptr;
+      a.batch = batch; a.hq = hq; a.hkv = hkv; a.tq = len; a.d = head_dim;
+      a.q_pos0 = nx.offset - len; a.kv_rows = ring_capacity; a.ring = ring_capacity;
+      a.key_lo = nx.offset - nx.tail; a.kv_len = nx.offset;
+      a.pool_rows = pool_capacity; a.nsum = nx.count; a.nblocks = nblocks;
+      a.kcap = kcap; a.bs = block_size; a.W = window; a.scale = scale; a.token_cutoff = 1;
+      ++bt.count;
+      st = nx;
+      if (pu.overflow) {              // finish_update reported it
+        bt.overflow = true;
+        (void)frc;
+        break;
+      }
+    }
+    bt.end = st;
+    bt.job.step = bt.total;
+    bt.job.n_blocks = (int)blocks;
+    bt.job.nparts = (int)bt.count;
+    return BFLY_OK;
+  };
+  auto launch_update = [&](const UpdateJob& j) -> int { return launch_update_job(j, rows, stream); };
   if (n_chunks == 0) return BFLY_OK;
-  // the first chunk's update runs alone; every later one rides with the previous attention
-  PlannedUpdate cur{};
-  int rc = plan_update(s, chunk_len[0], k[0], v[0], ring_k, ring_v, ring_capacity, pool_k, pool_v, pool_capacity,
-                       block_size, cache_window, head_dim, &cur);
+  // the first batch's update runs alone; every later one rides with the previous attention
+  // when their ring slots are disjoint
+  Batch cur{}, nxt{};
+  int rc = plan_batch(s, 0, cur);
   if (rc) return rc;
-  rc = launch_update(cur);
+  if (cur.count == 0) return cur.stop_rc;
+  rc = launch_update(cur.job);
   if (rc) return rc;
-  rc = finish_update(s, cur, chunk_len[0], pool_capacity, block_size, cache_window);
-  publish();
-  if (rc) return rc;
-  for (int64_t c = 0; c < n_chunks; ++c) {
-    const int64_t step = chunk_len[c];
-    const int64_t nblocks = (s.offset + block_size - 1) / block_size;
-    AttnArgs a{};
-    rc = bfly_topology_init(nblocks, layer_idx, partner_rule, local_window_blocks, sink_count, partner_count, &a.topo);
-    if (rc) return rc;
-    a.q = q[c]; a.out = out[c]; a.k = ring_k; a.v = ring_v; a.ks = pool_k; a.vs = pool_v;
-    a.nbr = nullptr; a.qpos = nullptr;
-    a.batch = batch; a.hq = hq; a.hkv = hkv; a.tq = step; a.d = head_dim;
-    a.q_pos0 = s.offset - step; a.kv_rows = ring_capacity; a.ring = ring_capacity;
-    a.key_lo = s.offset - s.tail; a.kv_len = s.offset;
-    a.pool_rows = pool_capacity; a.nsum = s.count; a.nblocks = nblocks;
-    a.kcap = kcap; a.bs = block_size; a.W = window; a.scale = scale; a.token_cutoff = 1;
-    if (c + 1 == n_chunks) {
-      rc = launch_attention(a, dtype, stream, "bfly_stream_chunks");
-      if (rc) return rc;
-      *chunks_done = c + 1;
-      break;
-    }
-    const int64_t next = chunk_len[c + 1];
-    PlannedUpdate nu{};
-    StreamCounters s_next = s;
-    const int prc = plan_update(s_next, next, k[c + 1], v[c + 1], ring_k, ring_v, ring_capacity, pool_k, pool_v,
-                                pool_capacity, block_size, cache_window, head_dim, &nu);
-    if (prc) {   // chunk c+1 does not fit: chunk c completes, the error is chunk c+1's
-      rc = launch_attention(a, dtype, stream, "bfly_stream_chunks");
-      if (rc) return rc;
-      *chunks_done = c + 1;
-      return prc;
-    }
-    if (step + next + 2 * kPage <= ring_capacity) {
-      rc = launch_attention(a, dtype, stream, "bfly_stream_chunks", &nu.job, rows);
+  s = cur.end;
+  publish(s);
+  if (cur.overflow) return BFLY_ERR_CAPACITY;   // the message was set when it was planned
+  for (;;) {
+    const int64_t next_from = cur.first + cur.count;
+    if (cur.stop_rc == BFLY_OK && next_from < n_chunks) {
+      rc = plan_batch(s, next_from, nxt);
       if (rc) return rc;
     } else {
-      rc = launch_attention(a, dtype, stream, "bfly_stream_chunks");
-      if (rc) return rc;
-      rc = launch_update(nu);
-      if (rc) return rc;
+      nxt = Batch{};
+      nxt.stop_rc = cur.stop_rc;
     }
-    *chunks_done = c + 1;
-    s = s_next;
-    rc = finish_update(s, nu, next, pool_capacity, block_size, cache_window);
-    publish();
-    if (rc) return rc;
+    if (nxt.count > 0 && cur.total + nxt.total + 2 * kPage <= ring_capacity) {
+      rc = launch_attention_batch(cur.args, (int)cur.count, stream, "bfly_stream_chunks", &nxt.job, rows);
+      if (rc) return rc;
+    } else {
+      rc = launch_attention_batch(cur.args, (int)cur.count, stream, "bfly_stream_chunks");
+      if (rc) return rc;
+      if (nxt.count > 0) {
+        rc = launch_update(nxt.job);
+        if (rc) return rc;
+      }
+    }
+    *chunks_done = next_from;
+    if (nxt.count == 0) return nxt.stop_rc;
+    s = nxt.end;
+    publish(s);
+    if (nxt.overflow) return BFLY_ERR_CAPACITY;
+    cur = nxt;
   }
-  return BFLY_OK;
 }

@@ -30,16 +30,19 @@ __device__ __forceinline__ void pool_rows(TokPtr tok_ptr, int64_t cnt, T* dst, i
   for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
   if (s < rs) {
     if constexpr (VEC * sizeof(T) == 16) {
-      // eight loads in flight per thread, then the adds in token order
-      for (int64_t base = s; base < cnt; base += 8 * (int64_t)rs) {
-        uint4 raw[8];
+      // sixteen loads in flight per thread (a 128-token block at d = 256 in one round trip),
+      // then the adds in token order
+      for (int64_t base = s; base < cnt; base += 16 * (int64_t)rs) {
+        uint4 raw[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < 16; ++u) {
+          // unconditional (past the block's end: its last token again, not added): a
+          // conditional load would be a branch that waits for each load in turn
           const int64_t tok = base + (int64_t)u * rs;
-          raw[u] = tok < cnt ? *reinterpret_cast<const uint4*>(tok_ptr(tok) + c * VEC) : make_uint4(0, 0, 0, 0);
+          raw[u] = *reinterpret_cast<const uint4*>(tok_ptr(tok < cnt ? tok : cnt - 1) + c * VEC);
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < 16; ++u) {
           if (base + (int64_t)u * rs >= cnt) continue;
           const T* v = reinterpret_cast<const T*>(&raw[u]);
 #pragma unroll
@@ -74,6 +77,11 @@ __device__ __forceinline__ void pool_rows(TokPtr tok_ptr, int64_t cnt, T* dst, i
 // independent: the pooled blocks and the new tokens all lie in the post-append
 // tail, which holds at most C positions, so their ring slots are distinct.
 // Work: x in [0, n_blocks + append workgroups), rows, K|V.
+// Chunks whose appends one update job may carry (the streaming loop's batches).
+constexpr int kMaxUpdateParts = 8;
+// Rounds of 16-byte pieces per thread in an update's append workgroups.
+constexpr int kAppendRounds = 8;
+
 struct UpdateJob {
   const void* k_new;
   const void* v_new;     // [rows, step, d]
@@ -83,22 +91,64 @@ struct UpdateJob {
   void* pool_v;          // [rows, pool_rows, d]
   int64_t step, ring, pool_rows, offset, first_pos, first_slot;
   int n_blocks, bs, d;
+  // nparts > 0: the step's new tokens come from nparts consecutive chunks instead of
+  // k_new / v_new: tokens [part_end[j-1], part_end[j]) are chunk j's, laid out
+  // [rows, chunk length, d] at k_part[j] / v_part[j] (part_end[nparts-1] == step)
+  int nparts;
+  const void* k_part[kMaxUpdateParts];
+  const void* v_part[kMaxUpdateParts];
+  int64_t part_end[kMaxUpdateParts];
 };
+
+// Row of new token t (< step) of batch row `row` in an update's input.  The part is found by
+// selects over every part slot (constant indices: the job's words stay scalar loads; a lane-
+// dependent index would turn each into a dependent vector load).
+// Branch-free (a branch between the rounds of loads would make each wait for the last).
+template <typename T>
+__device__ __forceinline__ const T* update_fresh_row(const UpdateJob& u, int kv, int64_t row, int64_t t) {
+  const bool single = u.nparts == 0;
+  const void* base = single ? (kv ? u.v_new : u.k_new) : (kv ? u.v_part[0] : u.k_part[0]);
+  int64_t t0 = 0, len = single ? u.step : u.part_end[0];
+#pragma unroll
+  for (int j = 1; j < kMaxUpdateParts; ++j) {
+    const bool in = j < u.nparts && t >= u.part_end[j - 1];   // part_end increases: the last such j
+    base = in ? (kv ? u.v_part[j] : u.k_part[j]) : base;
+    len = in ? u.part_end[j] - u.part_end[j - 1] : len;
+    t0 = in ? u.part_end[j - 1] : t0;
+  }
+  return reinterpret_cast<const T*>(base) + (row * len + (t - t0)) * u.d;
+}
 
 // Work item (bx, row, kv) of an update: workgroup-uniform, 256 threads.
 template <typename T, int VEC>
 __device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx, int64_t row, int kv, float* part) {
   const int d = u.d;
-  const T* fresh = reinterpret_cast<const T*>(kv ? u.v_new : u.k_new) + row * u.step * d;
   T* ring = reinterpret_cast<T*>(kv ? u.ring_v : u.ring_k) + row * u.ring * d;
   if (bx >= u.n_blocks) {
-    // append: 256 / (d / VEC) tokens per workgroup, one 16-byte piece per thread
+    // append: kAppendRounds x 256 / (d / VEC) tokens per workgroup, one 16-byte piece per
+    // thread and round; every round's load is issued before the first store
     const int lpr = d / VEC, tpw = 256 / lpr;
     const int t = threadIdx.x, c = t % lpr;
-    const int64_t tok = (bx - u.n_blocks) * tpw + t / lpr;
-    if (t / lpr >= tpw || tok >= u.step) return;
-    const int64_t slot = posmod(u.offset + tok, u.ring);
-    *reinterpret_cast<uint4*>(ring + slot * d + c * VEC) = *reinterpret_cast<const uint4*>(fresh + tok * d + c * VEC);
+    if (t / lpr >= tpw) return;
+    const int64_t tok0 = (bx - u.n_blocks) * tpw * kAppendRounds + t / lpr;
+    if (tok0 >= u.step) return;
+    // loads unconditional (past the last token: the last token again), stores kept in range
+    // (a native vector type: arrays of HIP's uint4 struct are copied by memcpy and stay in
+    // scratch memory)
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 x[kAppendRounds];
+#pragma unroll
+    for (int i = 0; i < kAppendRounds; ++i) {
+      const int64_t tok = min(tok0 + (int64_t)i * tpw, u.step - 1);
+      x[i] = *reinterpret_cast<const u32x4*>(update_fresh_row<T>(u, kv, row, tok) + c * VEC);
+    }
+    int64_t slot = posmod(u.offset + tok0, u.ring);   // then + tpw per round (tpw < ring: one wrap)
+#pragma unroll
+    for (int i = 0; i < kAppendRounds; ++i) {
+      if (tok0 + (int64_t)i * tpw < u.step) *reinterpret_cast<u32x4*>(ring + slot * d + c * VEC) = x[i];
+      slot += tpw;
+      if (slot >= u.ring) slot -= u.ring;
+    }
     return;
   }
   const int64_t n = bx;
@@ -106,7 +156,7 @@ __device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx
   const int64_t r0 = posmod(p0, u.ring);   // tokens < bs <= ring: one wrap at most
   auto tok_ptr = [&](int64_t tok) -> const T* {
     const int64_t p = p0 + tok;
-    if (p >= u.offset) return fresh + (p - u.offset) * d;
+    if (p >= u.offset) return update_fresh_row<T>(u, kv, row, p - u.offset);
     int64_t r = r0 + tok;
     if (r >= u.ring) r -= u.ring;
     return ring + r * d;
@@ -115,10 +165,13 @@ __device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx
   pool_rows<T, VEC>(tok_ptr, (int64_t)u.bs, dst, d, part);
 }
 
+// One bf16 update job in one launch (compress.hip); rows = batch x kv heads.
+int launch_update_job(const UpdateJob& u, int64_t rows, hipStream_t stream);
+
 // Workgroups along x of an update with a 16-byte row split (VEC elements per
 // 16 bytes): the due blocks, then the append workgroups.
 inline int64_t update_x(int64_t n_blocks, int64_t step, int head_dim, int vec) {
-  const int tpw = 256 / (head_dim / vec);
+  const int tpw = 256 / (head_dim / vec) * kAppendRounds;
   return n_blocks + (step + tpw - 1) / tpw;
 }
 

@@ -56,6 +56,22 @@ __global__ void __launch_bounds__(256) cache_update_kernel(UpdateJob u) {
   cache_update_body<T, VEC>(u, blockIdx.x, blockIdx.y, blockIdx.z, part);
 }
 
+// One update job (bf16, 16-byte row split: d in {64, 128, 256}) in one launch; the streaming
+// loop's batches, whose new tokens may come from several chunk buffers.
+int launch_update_job(const UpdateJob& u, int64_t rows, hipStream_t stream) {
+  BFLY_CHECK_ARG((u.d == 64 || u.d == 128 || u.d == 256) && rows > 0 && rows <= 65535, "update job shape");
+  // the due blocks lie inside the post-append tail: [offset + step - ring, offset + step)
+  BFLY_CHECK_ARG(u.n_blocks == 0 || (u.first_pos >= u.offset + u.step - u.ring &&
+                                     u.first_pos + (int64_t)u.n_blocks * u.bs <= u.offset + u.step),
+                 "update job: due blocks outside the tail after the append");
+  if (u.step == 0 && u.n_blocks == 0) return BFLY_OK;
+  const int64_t ux = update_x(u.n_blocks, u.step, u.d, 8);
+  BFLY_CHECK_ARG(ux <= INT32_MAX, "update job: grid too large");
+  hipLaunchKernelGGL((cache_update_kernel<__bf16, 8>), dim3((unsigned)ux, (unsigned)rows, 2), dim3(256), 0, stream, u);
+  BFLY_CHECK_LAUNCH("cache update job");
+  return BFLY_OK;
+}
+
 template <typename T>
 static int launch_pool(const PoolJob& a, const PoolJob* b, int64_t rows, int d, int bs,
                        int64_t nblocks, hipStream_t stream) {

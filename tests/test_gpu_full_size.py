@@ -47,7 +47,8 @@ def _width(n):
 
 
 @pytest.mark.timeout(600)
-def test_cfg4_full_stream_matches_oracle_at_stage_changes():
+@pytest.mark.parametrize("max_chunk", [512, 2048])   # 2048: five chunks per launch (the bench's ring)
+def test_cfg4_full_stream_matches_oracle_at_stage_changes(max_chunk):
     hq, hkv, d, bs, W, T, chunk, layer = 16, 4, 256, 128, 64, 262144, 384, 10
     dev = torch.device("cuda")
     g = torch.Generator(device=dev).manual_seed(41)
@@ -55,7 +56,7 @@ def test_cfg4_full_stream_matches_oracle_at_stage_changes():
     k = torch.randn(1, hkv, T, d, generator=g, device=dev).bfloat16()
     v = torch.randn(1, hkv, T, d, generator=g, device=dev).bfloat16()
     chunks = bf.split_chunks(q, k, v, chunk)
-    cache = bf.CompressedKVCache(block_size=bs, local_window_tokens=W, max_kv_size=T, max_chunk_size=512)
+    cache = bf.CompressedKVCache(block_size=bs, local_window_tokens=W, max_kv_size=T, max_chunk_size=max_chunk)
     core = bf.ButterflyAttentionCore(bf.compressed_butterfly_config(), layer)
     outs = bf.chunked_prefill(core, chunks, cache)
     torch.cuda.synchronize()

@@ -90,6 +90,9 @@ SIGNATURES = {
     "bfly_argmax_rows_noalloc": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),
     "bfly_q4_gemv": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _vp, _vp]),
     "bfly_q4_gemv_silu": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _i64, _vp, _vp]),
+    "bfly_add_rms_norm_q4_gemv": (_int, [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _i64, _i64, _int, _vp, _vp]),
+    "bfly_add_rms_norm_q4_gemv_silu": (_int, [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _i64, _i64, _int, _i64, _vp,
+                                              _vp]),
 }
 
 _lib = None

@@ -13,18 +13,13 @@
 #include <mutex>
 
 #include "bfly_common.h"
+#include "rmsnorm_row.h"
 #include "../../include/butterfly_amd_decoder.h"
 
 // products and sums are rounded one by one, as the PyTorch forms do
 #pragma clang fp contract(off)
 
 namespace bfly {
-
-__device__ __forceinline__ float dec_wave_sum64(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
 
 // Any dim that is a multiple of 256: the sum of squares from global memory,
 // then the row is read again (it is in cache) for the output.
@@ -64,66 +59,10 @@ template <int PER, bool kVec>
 __global__ void __launch_bounds__(256) add_rmsnorm_kernel(const __bf16* __restrict__ x, const __bf16* __restrict__ y,
                                                           const __bf16* __restrict__ w, __bf16* __restrict__ h_out,
                                                           __bf16* __restrict__ n_out, int dim, float eps) {
-  const int64_t row = blockIdx.x;
-  const int t = threadIdx.x;
-  const int64_t base = row * dim + (int64_t)t * PER;
-  float h[PER];
-  if constexpr (kVec) {
-#pragma unroll
-    for (int c = 0; c < PER / 8; ++c) {
-      const bf16x8 xv = *reinterpret_cast<const bf16x8*>(x + base + 8 * c);
-      bf16x8 yv{};
-      if (y != nullptr) yv = *reinterpret_cast<const bf16x8*>(y + base + 8 * c);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float v = (float)xv[e];
-        if (y != nullptr) v = (float)(__bf16)(v + (float)yv[e]);   // residual stream in bf16
-        h[8 * c + e] = v;
-      }
-    }
-    if (y != nullptr && h_out != nullptr) {
-#pragma unroll
-      for (int c = 0; c < PER / 8; ++c) {
-        bf16x8 hv;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) hv[e] = (__bf16)h[8 * c + e];
-        *reinterpret_cast<bf16x8*>(h_out + base + 8 * c) = hv;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      float v = (float)x[base + e];
-      if (y != nullptr) v = (float)(__bf16)(v + (float)y[base + e]);   // residual stream in bf16
-      h[e] = v;
-    }
-    if (y != nullptr && h_out != nullptr) {
-#pragma unroll
-      for (int e = 0; e < PER; ++e) h_out[base + e] = (__bf16)h[e];
-    }
-  }
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < PER; ++e) ss = fmaf(h[e], h[e], ss);
-  ss = dec_wave_sum64(ss);
+  const int64_t row = (int64_t)blockIdx.x * dim;
   __shared__ float part[4];
-  if ((t & 63) == 0) part[t >> 6] = ss;
-  __syncthreads();
-  const float tot = (part[0] + part[1]) + (part[2] + part[3]);
-  const float r = rsqrtf(tot / (float)dim + eps);
-  if constexpr (kVec) {
-#pragma unroll
-    for (int c = 0; c < PER / 8; ++c) {
-      const bf16x8 wv = *reinterpret_cast<const bf16x8*>(w + t * PER + 8 * c);
-      bf16x8 nv;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) nv[e] = (__bf16)(h[8 * c + e] * r * (float)wv[e]);
-      *reinterpret_cast<bf16x8*>(n_out + base + 8 * c) = nv;
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < PER; ++e) n_out[base + e] = (__bf16)(h[e] * r * (float)w[t * PER + e]);
-  }
+  add_rmsnorm_row<PER, kVec>(x + row, y != nullptr ? y + row : nullptr, w, h_out != nullptr ? h_out + row : nullptr,
+                             n_out + row, dim, eps, (int)threadIdx.x, true, part);
 }
 
 // One wave per (row of B*T, head): q/k heads are normed over d with their weight,

@@ -13,6 +13,7 @@
 // fp32 throughout; y is rounded once to bf16.  The results equal the product
 // with the fp32 weights code * scale + bias up to the fp32 summation order.
 #include "bfly_common.h"
+#include "rmsnorm_row.h"
 #include "../../include/butterfly_amd_decoder.h"
 
 namespace bfly {
@@ -66,9 +67,12 @@ struct Q4Args {
   int pieces, groups, pieces_per_group;
 };
 
-template <int NP, int R, bool kSilu>
-__global__ void __launch_bounds__(64) q4_gemv_kernel(Q4Args a) {
-  const int lane = threadIdx.x;
+// The sets of one wave: set0, set0 + stride, ... < n_sets.  form_x() runs after the first
+// set's weights are requested and before x (xsrc, bf16) is read: the fused form computes x
+// there.
+template <int NP, int R, bool kSilu, class XPtr, class FormX>
+__device__ __forceinline__ void q4_sets(const Q4Args& a, int lane, int64_t set0, int64_t stride, XPtr xsrc,
+                                        FormX&& form_x) {
   const int pieces = a.pieces, groups = a.groups;
   const u32x4* __restrict__ w = a.w;
   const uint32_t* __restrict__ sb = a.sb;
@@ -100,15 +104,16 @@ __global__ void __launch_bounds__(64) q4_gemv_kernel(Q4Args a) {
       }
     }
   };
-  load_set(blockIdx.x);   // the grid never exceeds the number of sets
+  if (set0 < a.n_sets) load_set(set0);
+  form_x();
+  if (set0 >= a.n_sets) return;
 
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
     const bool valid = lane + 64 * j < pieces;
-    const bf16x8* xp = reinterpret_cast<const bf16x8*>(a.x) + (int64_t)pc[j] * 4;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const bf16x8 v = xp[c];
+      const bf16x8 v = xsrc[(int64_t)pc[j] * 4 + c];
 #pragma unroll
       for (int e = 0; e < 8; ++e) xq[j][8 * c + e] = valid ? (float)v[e] : 0.f;
     }
@@ -124,7 +129,7 @@ __global__ void __launch_bounds__(64) q4_gemv_kernel(Q4Args a) {
     xs[j] = s;
   }
 
-  for (int64_t set = blockIdx.x; set < a.n_sets; set += gridDim.x) {
+  for (int64_t set = set0; set < a.n_sets; set += stride) {
     const int64_t o0 = set * OUTS;
     float tot[R];
 #pragma unroll
@@ -152,7 +157,7 @@ __global__ void __launch_bounds__(64) q4_gemv_kernel(Q4Args a) {
       }
       tot[r] = acc;
     }
-    if (set + gridDim.x < a.n_sets) load_set(set + gridDim.x);
+    if (set + stride < a.n_sets) load_set(set + stride);
 #pragma unroll
     for (int r = 0; r < R; ++r) tot[r] = q4_wave_sum(tot[r]);
     float mine = 0.f, mate = 0.f;
@@ -166,6 +171,37 @@ __global__ void __launch_bounds__(64) q4_gemv_kernel(Q4Args a) {
     const int64_t o = o0 + lane;
     if (lane < OUTS && o < n_out) a.y[o] = kSilu ? q4_silu_times(mine, mate) : (__bf16)mine;
   }
+}
+
+template <int NP, int R, bool kSilu>
+__global__ void __launch_bounds__(64) q4_gemv_kernel(Q4Args a) {
+  q4_sets<NP, R, kSilu>(a, (int)threadIdx.x, blockIdx.x, gridDim.x, reinterpret_cast<const bf16x8*>(a.x), [] {});
+}
+
+// The residual add + RMSNorm of the input row inside the product: 512 threads; threads
+// 0..255 form h = x + residual and its normed row exactly as bfly_add_rms_norm does (into
+// LDS; workgroup 0 also writes h), then each of the 8 waves runs its sets on that row.
+// in_features = 256 PER.
+struct Q4NormArgs {
+  const __bf16* x;
+  const __bf16* residual;   // or null (then h_out is null: a plain RMSNorm)
+  const __bf16* weight;
+  __bf16* h_out;
+  float eps;
+};
+
+template <int NP, int R, bool kSilu, int PER>
+__global__ void __launch_bounds__(512) q4_norm_gemv_kernel(Q4Args a, Q4NormArgs nm) {
+  constexpr int DIM = 256 * PER;
+  __shared__ __attribute__((aligned(16))) __bf16 xn[DIM];
+  __shared__ float part[4];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t waves = (int64_t)gridDim.x * 8;
+  q4_sets<NP, R, kSilu>(a, lane, (int64_t)blockIdx.x * 8 + wave, waves, reinterpret_cast<const bf16x8*>(xn), [&] {
+    add_rmsnorm_row<PER, true>(nm.x, nm.residual, nm.weight, blockIdx.x == 0 ? nm.h_out : nullptr, xn, DIM, nm.eps,
+                               tid, tid < 256, part);
+    __syncthreads();   // the normed row is in LDS
+  });
 }
 
 template <int NP, int R, bool kSilu>
@@ -198,6 +234,46 @@ void q4_dispatch(Q4Args a, int64_t in_features, int group, hipStream_t stream) {
     case 3: q4_launch<3, 2, kSilu>(a, stream); break;
     default: q4_launch<4, 2, kSilu>(a, stream); break;
   }
+}
+
+template <int NP, int R, bool kSilu, int PER>
+void q4_norm_launch(Q4Args a, Q4NormArgs nm, hipStream_t stream) {
+  constexpr int OUTS = kSilu ? R / 2 : R;
+  a.n_sets = (a.n_out + OUTS - 1) / OUTS;
+  const int64_t iters = (a.n_sets + kQ4MaxWaves - 1) / kQ4MaxWaves;
+  const int64_t waves = (a.n_sets + iters - 1) / iters;
+  hipLaunchKernelGGL((q4_norm_gemv_kernel<NP, R, kSilu, PER>), dim3((unsigned)((waves + 7) / 8)), dim3(512), 0, stream,
+                     a, nm);
+}
+
+// in_features = 256 PER with PER in {8, 16, 24} (one to three pieces per lane; a fourth would
+// not fit the registers of two waves per SIMD); rows per set as q4_dispatch chooses them
+template <bool kSilu>
+void q4_norm_dispatch(Q4Args a, Q4NormArgs nm, int64_t in_features, int group, hipStream_t stream) {
+  a.pieces = (int)(in_features / kQ4PieceCodes);
+  a.groups = (int)(in_features / group);
+  a.pieces_per_group = group / kQ4PieceCodes;
+  const int64_t sets4 = (a.n_out + (kSilu ? 1 : 3)) / (kSilu ? 2 : 4);
+  switch (in_features / 256) {
+    case 8:
+      if (sets4 >= 2048)
+        q4_norm_launch<1, 4, kSilu, 8>(a, nm, stream);
+      else
+        q4_norm_launch<1, 2, kSilu, 8>(a, nm, stream);
+      break;
+    case 16: q4_norm_launch<2, 2, kSilu, 16>(a, nm, stream); break;
+    default: q4_norm_launch<3, 2, kSilu, 24>(a, nm, stream); break;
+  }
+}
+
+int q4_norm_check(const void* x, const void* residual, const void* weight, void* h_out, int64_t in_features) {
+  BFLY_CHECK_ARG(weight != nullptr, "null norm weight");
+  BFLY_CHECK_ARG((residual == nullptr) == (h_out == nullptr), "residual and h_out must both be given or both NULL");
+  BFLY_CHECK_ARG(in_features % 2048 == 0 && in_features <= 6144,
+                 "in_features=%lld: the normed product takes 2048, 4096 or 6144", (long long)in_features);
+  BFLY_CHECK_ARG(aligned16(x) && aligned16(residual) && aligned16(weight) && aligned16(h_out),
+                 "x, residual, weight and h_out must be 16-byte aligned");
+  return BFLY_OK;
 }
 
 Q4Args q4_args(const void* x, const void* packed, const void* scale_bias, int64_t out_features, void* out) {
@@ -248,5 +324,39 @@ extern "C" int bfly_q4_gemv_silu(const void* x, const void* packed, const void* 
   a.up_off = up_row_offset;
   q4_dispatch<true>(a, in_features, group, stream);
   BFLY_CHECK_LAUNCH("bfly_q4_gemv_silu");
+  return BFLY_OK;
+}
+
+extern "C" int bfly_add_rms_norm_q4_gemv(const void* x, const void* residual, const void* norm_weight, float eps,
+                                         void* h_out, const void* packed, const void* scale_bias,
+                                         int64_t out_features, int64_t in_features, int group, void* out,
+                                         hipStream_t stream) {
+  int rc = q4_check(x, packed, scale_bias, out_features, in_features, group, out);
+  if (rc) return rc;
+  rc = q4_norm_check(x, residual, norm_weight, h_out, in_features);
+  if (rc) return rc;
+  const Q4NormArgs nm{static_cast<const __bf16*>(x), static_cast<const __bf16*>(residual),
+                      static_cast<const __bf16*>(norm_weight), static_cast<__bf16*>(h_out), eps};
+  q4_norm_dispatch<false>(q4_args(x, packed, scale_bias, out_features, out), nm, in_features, group, stream);
+  BFLY_CHECK_LAUNCH("bfly_add_rms_norm_q4_gemv");
+  return BFLY_OK;
+}
+
+extern "C" int bfly_add_rms_norm_q4_gemv_silu(const void* x, const void* residual, const void* norm_weight, float eps,
+                                              void* h_out, const void* packed, const void* scale_bias,
+                                              int64_t out_features, int64_t in_features, int group,
+                                              int64_t up_row_offset, void* out, hipStream_t stream) {
+  int rc = q4_check(x, packed, scale_bias, out_features, in_features, group, out);
+  if (rc) return rc;
+  rc = q4_norm_check(x, residual, norm_weight, h_out, in_features);
+  if (rc) return rc;
+  BFLY_CHECK_ARG(up_row_offset >= out_features, "up_row_offset=%lld overlaps the gate rows",
+                 (long long)up_row_offset);
+  const Q4NormArgs nm{static_cast<const __bf16*>(x), static_cast<const __bf16*>(residual),
+                      static_cast<const __bf16*>(norm_weight), static_cast<__bf16*>(h_out), eps};
+  Q4Args a = q4_args(x, packed, scale_bias, out_features, out);
+  a.up_off = up_row_offset;
+  q4_norm_dispatch<true>(a, nm, in_features, group, stream);
+  BFLY_CHECK_LAUNCH("bfly_add_rms_norm_q4_gemv_silu");
   return BFLY_OK;
 }

@@ -192,6 +192,49 @@ def q4_gemv_silu(x: torch.Tensor, gate_up: QuantLinear) -> torch.Tensor:
     return out
 
 
+NORM_Q4_DIMS = (2048, 4096, 6144)   # row lengths of bfly_add_rms_norm_q4_gemv(_silu)
+
+
+def norm_q4_fits(x: torch.Tensor, layer: QuantLinear) -> bool:
+    """Whether one row ``x`` takes the fused residual add + RMSNorm + 4-bit product."""
+    return _one_row(x) and layer.gemv_from_codes and layer.in_features in NORM_Q4_DIMS \
+        and int(x.shape[-1]) == layer.in_features
+
+
+def add_rms_norm_q4_gemv(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torch.Tensor, eps: float,
+                         layer: QuantLinear):
+    """``(h, layer(n))`` with ``h, n = add_rms_norm(x, residual, weight, eps)`` for one bf16 row, in
+    one launch of ``bfly_add_rms_norm_q4_gemv`` (bit-identical to the two launches; ``h`` is
+    computed even when the caller drops it)."""
+    xr = _row16(x)
+    rr = _row16(residual) if residual is not None else None
+    h = torch.empty_like(xr)
+    out = torch.empty(*x.shape[:-1], layer.out_features, dtype=torch.bfloat16, device=x.device)
+    with on(x.device):
+        _native.call("bfly_add_rms_norm_q4_gemv", xr.data_ptr(), rr.data_ptr() if rr is not None else None,
+                     weight.data_ptr(), float(eps), h.data_ptr() if rr is not None else None,
+                     layer.packed.data_ptr(), layer.scale_bias.data_ptr(), layer.out_features, layer.in_features,
+                     layer.group, out.data_ptr(), stream_of(x))
+    return (h.view(x.shape) if rr is not None else x), out
+
+
+def add_rms_norm_q4_gemv_silu(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torch.Tensor, eps: float,
+                              gate_up: QuantLinear):
+    """``(h, SiLU(gate(n)) * up(n))`` with ``h, n = add_rms_norm(...)`` for one bf16 row, in one
+    launch of ``bfly_add_rms_norm_q4_gemv_silu`` (bit-identical to the two launches)."""
+    xr = _row16(x)
+    rr = _row16(residual) if residual is not None else None
+    h = torch.empty_like(xr)
+    f = gate_up.out_features // 2
+    out = torch.empty(*x.shape[:-1], f, dtype=torch.bfloat16, device=x.device)
+    with on(x.device):
+        _native.call("bfly_add_rms_norm_q4_gemv_silu", xr.data_ptr(), rr.data_ptr() if rr is not None else None,
+                     weight.data_ptr(), float(eps), h.data_ptr() if rr is not None else None,
+                     gate_up.packed.data_ptr(), gate_up.scale_bias.data_ptr(), f, gate_up.in_features,
+                     gate_up.group, f, out.data_ptr(), stream_of(x))
+    return (h.view(x.shape) if rr is not None else x), out
+
+
 def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """``x @ w^T``.  One row of activations on the GPU (a decode step at batch 1) runs as
     ``w @ x^T``, which PyTorch-ROCm hands to a GEMV kernel that streams the weight at close
@@ -393,19 +436,30 @@ class ButterflyAttention(QwenButterflyAttention):
         rope = position_embeddings
         if rope is None:
             raise ValueError("the decoder passes the RoPE rows of the call's positions (position_embeddings)")
-        if (isinstance(rope, RopeTable) and _one_row(x)
-                and self.core.fuses_qk_norm(cache, 1, c.head_dim, x.dtype)):
+        if self.takes_qkv_row(x, cache, rope):
             # one decode step with device counters: the raw q|k|v row goes to the decode
             # step, which applies q/k RMSNorm and RoPE at its own position (one launch fewer)
-            row = base.qkv(x).view(-1)
-            nq, nkv = c.num_heads * c.head_dim, c.num_kv_heads * c.head_dim
-            q = row[:nq].view(1, c.num_heads, 1, c.head_dim)
-            k = row[nq:nq + nkv].view(1, c.num_kv_heads, 1, c.head_dim)
-            v = row[nq + nkv:].view(1, c.num_kv_heads, 1, c.head_dim)
-            qk = (base.q_norm.weight, base.k_norm.weight, rope.cos_tab, rope.sin_tab, base.q_norm.eps)
-            return base.output(self.core(q, k, v, cache, qk_norm=qk))
+            return self.forward_qkv_row(base.qkv(x), cache, rope)
         q, k, v = base.project(x, None, rope)
         return base.output(self.attend(q, k, v, cache))
+
+    def takes_qkv_row(self, x: torch.Tensor, cache, rope) -> bool:
+        """Whether this call is a device-counter decode step fed with the raw q|k|v row."""
+        c = self.base.cfg
+        return (isinstance(rope, RopeTable) and _one_row(x)
+                and self.core.fuses_qk_norm(cache, 1, c.head_dim, x.dtype))
+
+    def forward_qkv_row(self, qkv: torch.Tensor, cache, rope) -> torch.Tensor:
+        """The decode step from the fused projection's raw output row (``base.qkv`` of the
+        normed input; ``takes_qkv_row`` held), through the output projection."""
+        base, c = self.base, self.base.cfg
+        row = qkv.view(-1)
+        nq, nkv = c.num_heads * c.head_dim, c.num_kv_heads * c.head_dim
+        q = row[:nq].view(1, c.num_heads, 1, c.head_dim)
+        k = row[nq:nq + nkv].view(1, c.num_kv_heads, 1, c.head_dim)
+        v = row[nq + nkv:].view(1, c.num_kv_heads, 1, c.head_dim)
+        qk = (base.q_norm.weight, base.k_norm.weight, rope.cos_tab, rope.sin_tab, base.q_norm.eps)
+        return base.output(self.core(q, k, v, cache, qk_norm=qk))
 
 
 register_butterfly_attention(Attention, ButterflyAttention)
@@ -456,10 +510,21 @@ class DecoderLayer(nn.Module):
         whose sum is the layer's output.  ``pending`` is the previous layer's ``m`` (or None); it
         is added to ``x`` in the launch that computes the input RMSNorm, which rounds the sum to
         bf16 before normalising it, as the separate add would."""
-        x, n = add_rms_norm(x, pending, self.input_layernorm.weight, self.input_layernorm.eps)
-        a = self.self_attn(n, cache=cache, position_embeddings=rope)
-        h, n = add_rms_norm(x, a, self.post_attention_layernorm.weight, self.post_attention_layernorm.eps)
-        return h, self.mlp(n)
+        attn, mlp = self.self_attn, self.mlp
+        ln, post = self.input_layernorm, self.post_attention_layernorm
+        if (isinstance(attn, ButterflyAttention) and attn.takes_qkv_row(x, cache, rope)
+                and norm_q4_fits(x, attn.base.qkv)):
+            # a decode step: each norm rides in the launch of the product that consumes it
+            x, qkv = add_rms_norm_q4_gemv(x, pending, ln.weight, ln.eps, attn.base.qkv)
+            a = attn.forward_qkv_row(qkv, cache, rope)
+        else:
+            x, n = add_rms_norm(x, pending, ln.weight, ln.eps)
+            a = attn(n, cache=cache, position_embeddings=rope)
+        if norm_q4_fits(x, mlp.gate_up) and mlp.down_proj.gemv_from_codes:
+            h, s = add_rms_norm_q4_gemv_silu(x, a, post.weight, post.eps, mlp.gate_up)
+            return h, mlp.down_proj(s)
+        h, n = add_rms_norm(x, a, post.weight, post.eps)
+        return h, mlp(n)
 
 
 class Decoder(nn.Module):
@@ -495,18 +560,22 @@ class Decoder(nn.Module):
             self._rope_tab = tab
         return tab[0][start:need], tab[1][start:need]
 
-    def _last_hidden(self, x: torch.Tensor, positions: torch.Tensor, caches: List, rope) -> torch.Tensor:
-        """Run every layer over the embedded ``x`` [B, T, hidden]; returns the final RMSNorm of
-        the last position, [B, hidden].  On the HIP path each layer's closing residual add is
-        folded into the next layer's (or the final) RMSNorm launch."""
+    def _last_logits(self, x: torch.Tensor, positions: torch.Tensor, caches: List, rope) -> torch.Tensor:
+        """Run every layer over the embedded ``x`` [B, T, hidden]; returns the logits of the last
+        position (final RMSNorm, tied lm_head).  On the HIP path each layer's closing residual
+        add is folded into the next layer's (or the final) RMSNorm launch, and for one row the
+        final norm rides in the lm_head product's launch."""
         if _hip(x) and x.shape[-1] % 256 == 0:
             m = None
             for layer, cache in zip(self.layers, caches):
                 x, m = layer.forward_split(x, m, positions, cache, rope)
-            return add_rms_norm(x[:, -1], m[:, -1] if m is not None else None, self.norm.weight, self.norm.eps)[1]
+            xl, ml = x[:, -1], (m[:, -1] if m is not None else None)
+            if norm_q4_fits(xl, self.lm_head):
+                return add_rms_norm_q4_gemv(xl, ml, self.norm.weight, self.norm.eps, self.lm_head)[1]
+            return self._logits(add_rms_norm(xl, ml, self.norm.weight, self.norm.eps)[1])
         for layer, cache in zip(self.layers, caches):
             x = layer(x, positions, cache, rope)
-        return self.norm(x[:, -1])
+        return self._logits(self.norm(x[:, -1]))
 
     @torch.no_grad()
     def forward(self, tokens: torch.Tensor, caches: List, start: int) -> torch.Tensor:
@@ -514,7 +583,7 @@ class Decoder(nn.Module):
         x = F.embedding(tokens, self.embed_tokens)
         positions = torch.arange(start, start + tokens.shape[1], device=tokens.device)
         rope = self._rope(start, tokens.shape[1], tokens.device)
-        return self._logits(self._last_hidden(x, positions, caches, rope)).float()
+        return self._last_logits(x, positions, caches, rope).float()
 
     @torch.no_grad()
     def greedy_graph(self, prompt: torch.Tensor, new_tokens: int, caches: List) -> torch.Tensor:
@@ -551,7 +620,7 @@ class Decoder(nn.Module):
         def one_step():
             x = F.embedding(tok, self.embed_tokens)
             rope = RopeTable(cos_tab, sin_tab, pos)
-            lg = self._logits(self._last_hidden(x, pos, caches, rope))
+            lg = self._last_logits(x, pos, caches, rope)
             if _hip(lg):
                 nxt = argmax_rows_noalloc(lg) if lg.shape[0] <= 64 else argmax_rows(lg)
             else:

@@ -106,6 +106,31 @@ int bfly_q4_gemv(const void* x, const void* packed, const void* scale_bias, int6
 int bfly_q4_gemv_silu(const void* x, const void* packed, const void* scale_bias, int64_t out_features,
                       int64_t in_features, int group, int64_t up_row_offset, void* out, hipStream_t stream);
 
+/*
+ * Device: bfly_add_rms_norm of one row followed by bfly_q4_gemv of the normed row, in
+ * one launch: h_out = x + residual (bf16; skipped when residual and h_out are NULL),
+ * out = W RMSNorm(h) * norm_weight, with the rounding points and summation order of
+ * the two separate calls (bit-identical outputs).  in_features (the row's length)
+ * 2048, 4096 or 6144; x, residual, norm_weight and h_out 16-byte aligned;
+ * weight layout and other limits as bfly_q4_gemv.  The decoder's input and final
+ * norms with the product that consumes them; no counterpart in the reference's
+ * own code.
+ */
+int bfly_add_rms_norm_q4_gemv(const void* x, const void* residual, const void* norm_weight, float eps,
+                              void* h_out, const void* packed, const void* scale_bias, int64_t out_features,
+                              int64_t in_features, int group, void* out, hipStream_t stream);
+
+/*
+ * Device: bfly_add_rms_norm of one row followed by bfly_q4_gemv_silu of the normed
+ * row, in one launch (the post-attention norm with the MLP's gate|up product);
+ * bit-identical to the two calls.  Limits as bfly_add_rms_norm_q4_gemv and
+ * bfly_q4_gemv_silu.  No counterpart in the reference's own code.
+ */
+int bfly_add_rms_norm_q4_gemv_silu(const void* x, const void* residual, const void* norm_weight, float eps,
+                                   void* h_out, const void* packed, const void* scale_bias,
+                                   int64_t out_features, int64_t in_features, int group,
+                                   int64_t up_row_offset, void* out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -96,3 +96,36 @@ def test_q4_gemv_unaligned_row_is_copied():
     y = q4_gemv(x, layer)
     assert torch.equal(y, q4_gemv(x.clone(), layer))
 
+
+
+@pytest.mark.parametrize("out_f,in_f,residual", [(3072, 2048, True), (9000, 2048, True), (151936, 2048, True),
+                                                 (100, 2048, False), (2048, 4096, True), (33, 6144, True)])
+def test_add_rms_norm_q4_gemv_equals_two_launches(out_f, in_f, residual):
+    """The residual add + RMSNorm inside the product's launch gives the same h and the same
+    outputs, bit for bit, as bfly_add_rms_norm followed by bfly_q4_gemv."""
+    from butterfly_amd.decoder import add_rms_norm, add_rms_norm_q4_gemv
+
+    layer = _layer(out_f, in_f, 64, seed=out_f)
+    g = torch.Generator().manual_seed(in_f + out_f)
+    x = (torch.randn(1, in_f, generator=g) * 3).bfloat16().cuda()
+    r = torch.randn(1, in_f, generator=g).bfloat16().cuda() if residual else None
+    w = (1 + 0.5 * torch.randn(in_f, generator=g)).bfloat16().cuda()
+    h, y = add_rms_norm_q4_gemv(x, r, w, 1e-6, layer)
+    h2, n = add_rms_norm(x, r, w, 1e-6)
+    assert torch.equal(h, h2)
+    assert torch.equal(y, q4_gemv(n, layer))
+
+
+@pytest.mark.parametrize("f,in_f", [(6144, 2048), (4097, 2048), (100, 4096), (300, 6144)])
+def test_add_rms_norm_q4_gemv_silu_equals_two_launches(f, in_f):
+    from butterfly_amd.decoder import add_rms_norm, add_rms_norm_q4_gemv_silu
+
+    gate_up = _layer(2 * f, in_f, 64, seed=f)
+    g = torch.Generator().manual_seed(f)
+    x = torch.randn(1, in_f, generator=g).bfloat16().cuda()
+    r = torch.randn(1, in_f, generator=g).bfloat16().cuda()
+    w = (1 + 0.5 * torch.randn(in_f, generator=g)).bfloat16().cuda()
+    h, s = add_rms_norm_q4_gemv_silu(x, r, w, 1e-6, gate_up)
+    h2, n = add_rms_norm(x, r, w, 1e-6)
+    assert torch.equal(h, h2)
+    assert torch.equal(s, q4_gemv_silu(n, gate_up))

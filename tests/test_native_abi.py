@@ -144,3 +144,20 @@ def test_noalloc_argmax_refuses_before_any_device_call():
     assert b"64" in lib.bfly_last_error()
     assert lib.bfly_argmax_rows_noalloc(0x1000, 0, 16, 16, 1, 0x2000, None) == _native.ERR_INVALID
     assert lib.bfly_argmax_rows_noalloc(None, 2, 16, 16, 1, 0x2000, None) == _native.ERR_INVALID
+
+
+@pytest.mark.parametrize("args,msg", [
+    ((256, 512, 768, 1e-6, 1024, 1280, 1536, 8, 8192, 64, 2048, None), b"2048, 4096 or 6144"),
+    ((256, 512, 768, 1e-6, 1024, 1280, 1536, 8, 3072, 64, 2048, None), b"2048, 4096 or 6144"),
+    ((256, 520, 768, 1e-6, 1024, 1280, 1536, 8, 2048, 64, 2048, None), b"16-byte"),   # residual misaligned
+    ((256, 512, 768, 1e-6, None, 1280, 1536, 8, 2048, 64, 2048, None), b"both"),      # residual without h_out
+    ((256, 512, None, 1e-6, 1024, 1280, 1536, 8, 2048, 64, 2048, None), b"norm weight"),
+])
+def test_add_rms_norm_q4_gemv_validates_before_launch(args, msg):
+    """Fake, never dereferenced addresses: every case fails its checks before a launch."""
+    lib = _native.lib()
+    assert lib.bfly_add_rms_norm_q4_gemv(*args) == _native.ERR_INVALID
+    assert msg in lib.bfly_last_error()
+    *head, out, st = args
+    assert lib.bfly_add_rms_norm_q4_gemv_silu(*head, head[7], out, st) == _native.ERR_INVALID
+    assert msg in lib.bfly_last_error()

@@ -18,8 +18,11 @@
 namespace bfly {
 
 // Mean of `cnt` token rows into dst (one workgroup, 256 threads); tok_ptr(tok)
-// is the row of token tok; `part` is 256 * 8 floats of LDS scratch.
-template <typename T, int VEC, class TokPtr>
+// is the row of token tok; `part` is 256 * 8 floats of LDS scratch.  INFLIGHT
+// 16-byte loads per thread are requested before their adds (8 keeps the
+// compressor's registers low; the update job's pooling takes 16, a whole block
+// at d = 256 in one round trip).
+template <typename T, int VEC, int INFLIGHT = 8, class TokPtr>
 __device__ __forceinline__ void pool_rows(TokPtr tok_ptr, int64_t cnt, T* dst, int d, float* part) {
   const int lpr = d / VEC;               // lanes per token row
   const int rs = 256 / lpr;              // token slots
@@ -30,19 +33,18 @@ __device__ __forceinline__ void pool_rows(TokPtr tok_ptr, int64_t cnt, T* dst, i
   for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
   if (s < rs) {
     if constexpr (VEC * sizeof(T) == 16) {
-      // sixteen loads in flight per thread (a 128-token block at d = 256 in one round trip),
-      // then the adds in token order
-      for (int64_t base = s; base < cnt; base += 16 * (int64_t)rs) {
-        uint4 raw[16];
+      // INFLIGHT loads per thread, then the adds in token order
+      for (int64_t base = s; base < cnt; base += INFLIGHT * (int64_t)rs) {
+        uint4 raw[INFLIGHT];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
+        for (int u = 0; u < INFLIGHT; ++u) {
           // unconditional (past the block's end: its last token again, not added): a
           // conditional load would be a branch that waits for each load in turn
           const int64_t tok = base + (int64_t)u * rs;
           raw[u] = *reinterpret_cast<const uint4*>(tok_ptr(tok < cnt ? tok : cnt - 1) + c * VEC);
         }
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
+        for (int u = 0; u < INFLIGHT; ++u) {
           if (base + (int64_t)u * rs >= cnt) continue;
           const T* v = reinterpret_cast<const T*>(&raw[u]);
 #pragma unroll
@@ -162,7 +164,7 @@ __device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx
     return ring + r * d;
   };
   T* dst = reinterpret_cast<T*>(kv ? u.pool_v : u.pool_k) + (row * u.pool_rows + u.first_slot + n) * d;
-  pool_rows<T, VEC>(tok_ptr, (int64_t)u.bs, dst, d, part);
+  pool_rows<T, VEC, 16>(tok_ptr, (int64_t)u.bs, dst, d, part);
 }
 
 // One bf16 update job in one launch (compress.hip); rows = batch x kv heads.

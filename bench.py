@@ -386,7 +386,7 @@ def bench_decode(torch, bf, batches=(1, 8, 32), steps=64, seed=0):
     return out
 
 
-def bench_decode_sweep(torch, bf, batches=(128, 512, 1024), steps=64, seed=1):
+def bench_decode_sweep(torch, bf, batches=(128, 512, 1024, 2048), steps=64, seed=1):
     """cfg3 shapes at batch sizes beyond the config (labelled as such): the same
     device-counter decode step, 64 steps in one HIP graph, to show where the
     per-step latency floor gives way to HBM bandwidth."""

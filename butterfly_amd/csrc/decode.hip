@@ -798,59 +798,19 @@ __device__ __forceinline__ __bf16 dec_qkn_rope(float own, float par, float c, fl
 }
 __device__ __forceinline__ float dec_bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float dec_bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
-typedef unsigned int dec_u32x4 __attribute__((ext_vector_type(4)));
 
-// q fragments of one head group: lane (lg, lq) holds d = 32 lg + 8 ks + e of its
-// head, so the partner d ^ 64 sits in lane ^ 32 (v_permlane32_swap), and lanes
-// lg and lg ^ 2 together hold chunks 4 (lg & 1) .. 4 (lg & 1) + 3; the other four
-// chunks' sum is in lane ^ 16.
-__device__ __forceinline__ void dec_qkn_swap(const bf16x8& f, float* own, float* par) {
-  const dec_u32x4 u = __builtin_bit_cast(dec_u32x4, f);
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    // one of the two results is this lane's own word, the other lane ^ 32's (when
-    // both equal the own word, so does the partner's)
-    const auto sw = __builtin_amdgcn_permlane32_swap(u[t], u[t], false, false);
-    const uint32_t pw = sw[0] == u[t] ? sw[1] : sw[0];
-    own[2 * t] = dec_bf_lo(u[t]);
-    own[2 * t + 1] = dec_bf_hi(u[t]);
-    par[2 * t] = dec_bf_lo(pw);
-    par[2 * t + 1] = dec_bf_hi(pw);
-  }
-}
-// Norm weights and the RoPE row of one lane: q lanes d = 32 lg + 8 ks + e (and the
-// partners' weights), requested once the staged rows are in LDS (the q transform
-// then runs with the staging registers free); k lanes d = 8 pc + e, requested as
-// soon as the position is known.
-struct DecQknQ {
-  bf16x8 w[4], wp[4];
-  f32x4 c[8], s[8];
-};
+// Norm weights and the RoPE row of one lane's piece d = 8 pc + e (and the partner
+// piece's weights), requested as soon as the position is known.  q and k share the
+// RoPE row and differ in the norm weights.
 struct DecQknK {
   bf16x8 w, wp;
   f32x4 c[2], s[2];
 };
-__device__ __forceinline__ DecQknQ dec_qkn_q_load(const DecodeArgs& a, int p, int lg) {
-  DecQknQ o;
-  const float* cr = a.rope_cos + (int64_t)p * 128;
-  const float* sr = a.rope_sin + (int64_t)p * 128;
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int d0 = 32 * lg + 8 * ks;
-    o.w[ks] = *reinterpret_cast<const bf16x8*>(a.qn_w + d0);
-    o.wp[ks] = *reinterpret_cast<const bf16x8*>(a.qn_w + (d0 ^ 64));
-    o.c[2 * ks] = *reinterpret_cast<const f32x4*>(cr + d0);
-    o.c[2 * ks + 1] = *reinterpret_cast<const f32x4*>(cr + d0 + 4);
-    o.s[2 * ks] = *reinterpret_cast<const f32x4*>(sr + d0);
-    o.s[2 * ks + 1] = *reinterpret_cast<const f32x4*>(sr + d0 + 4);
-  }
-  return o;
-}
-__device__ __forceinline__ DecQknK dec_qkn_k_load(const DecodeArgs& a, int p, int pc) {
+__device__ __forceinline__ DecQknK dec_qkn_load(const __bf16* nw, const DecodeArgs& a, int p, int pc) {
   DecQknK o;
   const int d0 = 8 * pc;
-  o.w = *reinterpret_cast<const bf16x8*>(a.kn_w + d0);
-  o.wp = *reinterpret_cast<const bf16x8*>(a.kn_w + (d0 ^ 64));
+  o.w = *reinterpret_cast<const bf16x8*>(nw + d0);
+  o.wp = *reinterpret_cast<const bf16x8*>(nw + (d0 ^ 64));
   const float* cr = a.rope_cos + (int64_t)p * 128 + d0;
   const float* sr = a.rope_sin + (int64_t)p * 128 + d0;
   o.c[0] = *reinterpret_cast<const f32x4*>(cr);
@@ -860,39 +820,11 @@ __device__ __forceinline__ DecQknK dec_qkn_k_load(const DecodeArgs& a, int p, in
   return o;
 }
 
-// Two passes over the fragments (the partner values are swapped in again for the
-// second), so that no more than one fragment's values are live at a time.
-__device__ __forceinline__ void dec_qkn_q(bf16x8 (&qf)[4], const DecQknQ& pq, float eps, int lg) {
-  const bool lo = lg < 2;   // lanes 0..31 hold d < 64
-  float cs[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    float own[8], par[8];
-    dec_qkn_swap(qf[ks], own, par);
-    cs[ks] = lo ? dec_qkn_chunk(own, par) : dec_qkn_chunk(par, own);
-  }
-  const float half = (cs[0] + cs[1]) + (cs[2] + cs[3]);
-  const float r = rsqrtf((half + __shfl_xor(half, 16)) / 128.f + eps);
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    float own[8], par[8];
-    dec_qkn_swap(qf[ks], own, par);
-    bf16x8 o;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float on = dec_qkn_norm(own[e], r, (float)pq.w[ks][e]);
-      const float pn = dec_qkn_norm(par[e], r, (float)pq.wp[ks][e]);
-      o[e] = dec_qkn_rope(on, pn, pq.c[2 * ks + (e >> 2)][e & 3], pq.s[2 * ks + (e >> 2)][e & 3], lo);
-    }
-    qf[ks] = o;
-  }
-}
-
-// One staged piece of the new k row: lane (tid % 16) = pc holds d = 8 pc + e and
+// One 16-byte piece of a q or k row: lane (tid % 16) = pc holds d = 8 pc + e and
 // the 16 lanes of the row are one DPP row, so the partner piece pc ^ 8 is a
 // rotation by 8 and the chunk sums combine by quad permutations (xor 1, 2) and a
 // rotation by 4 (lanes pc and pc ^ 8 hold the same chunk sum).  Every lane of the
-// wave runs it; only the lanes of the new row use the result.
+// wave runs it (DPP); lanes whose row is not wanted ignore the result.
 __device__ __forceinline__ uint4 dec_qkn_k(uint4 x, const DecQknK& pk, float eps, int pc) {
   const bool lo = pc < 8;
   const uint32_t u[4] = {x.x, x.y, x.z, x.w};
@@ -995,6 +927,11 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   T* Vs = reinterpret_cast<T*>(stage_lds + KS_BYTES);   // [80][D], pieces swizzled by row
   __shared__ int selw[4][kDecMaxSum];
   __shared__ int64_t route_hdr[4];
+  // kQkn: the 16 normed + rotated q rows of a head group (row pitch 136: the fragment
+  // reads of 16 rows at one column hit distinct banks)
+  constexpr bool qkn = kQkn && D == 128;
+  constexpr int QP = 136;
+  __shared__ __attribute__((aligned(16))) T q_lds[qkn ? 16 * QP : 8];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
@@ -1053,12 +990,20 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 8 * ks);
   };
-  load_q(0);
+  // kQkn: thread tid holds piece tid % 16 of raw q row 16 hg + tid / 16 (the group's
+  // last head past gsz); the 256 threads transform the 16 rows of a head group into
+  // q_lds, from which every wave reads its fragments
+  uint4 q_raw{};
+  auto load_q_raw = [&](int hg) {
+    const int head = min(16 * hg + (tid >> 4), gsz - 1);
+    q_raw = *reinterpret_cast<const uint4*>(qhead + (uint32_t)head * D + (tid & 15) * VEC);
+  };
+  if constexpr (qkn) load_q_raw(0);
+  else load_q(0);
 
   const DecState32 st =
       kStep ? dec_advance32(cnt[kStOffset], cnt[kStTail], cnt[kStCount], cnt[kStSumOff], a, sa) : dec_state32<false>(a, sa, bh);
   // with the fused q/k norm, a position past the RoPE table is an error of the step
-  constexpr bool qkn = kQkn && D == 128;
   if (kStep && (st.err || (qkn && st.kv_len - 1 >= a.rope_rows))) {
     if (tid == 0) sa.state[kStError] = st.err ? kErrCapacity : kErrRope;
     return;
@@ -1069,7 +1014,21 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   for (int it = 0; it < SK; ++it) rsel[it] = (int)(uint32_t)(rsel2[it] >> (32 * (st.kv_len & 1)));
   const int p = st.kv_len - 1;
   DecQknK qkn_k{};
-  if constexpr (qkn) qkn_k = dec_qkn_k_load(a, p, tid % PIECES);
+  bf16x8 qn_w{}, qn_wp{};   // q's norm weights of this thread's piece (RoPE row: qkn_k's)
+  if constexpr (qkn) {
+    qkn_k = dec_qkn_load(a.kn_w, a, p, tid % PIECES);
+    qn_w = *reinterpret_cast<const bf16x8*>(a.qn_w + 8 * (tid % PIECES));
+    qn_wp = *reinterpret_cast<const bf16x8*>(a.qn_w + ((8 * (tid % PIECES)) ^ 64));
+  }
+  // norm + RoPE of this thread's q piece into q_lds
+  auto put_q = [&]() {
+    const DecQknK pq{qn_w, qn_wp, {qkn_k.c[0], qkn_k.c[1]}, {qkn_k.s[0], qkn_k.s[1]}};
+    *reinterpret_cast<uint4*>(q_lds + (tid >> 4) * QP + (tid & 15) * VEC) = dec_qkn_k(q_raw, pq, a.qk_eps, tid & 15);
+  };
+  auto read_q = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(q_lds + lq * QP + lg * (D / 4) + 8 * ks);
+  };
   const int lo = max(max(p - a.W + 1, st.tail_start), 0);
   const int nw = p - lo + 1;
   const int ring = (int)a.ring;
@@ -1183,24 +1142,22 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
         put_v(kDecMaxWin + j, pc, keep_if(j < ns, svx[it]));
       }
     }
-    if constexpr (D == 128) {
-      if constexpr (qkn) {
-        const DecQknQ qq = dec_qkn_q_load(a, p, lg);
-        dec_qkn_q(qf, qq, a.qk_eps, lg);
-      }
-    }
+    if constexpr (qkn) put_q();
   }
   __syncthreads();
+  if constexpr (qkn) read_q();
 
   const float sl2 = a.scale * 1.4426950408889634f;   // host guarantees scale > 0 on this path
   for (int hg = 0; 16 * hg < gsz; ++hg) {
     if (hg > 0) {
-      load_q(hg);
-      if constexpr (D == 128) {
-        if constexpr (qkn) {
-          const DecQknQ qq = dec_qkn_q_load(a, p, lg);
-          dec_qkn_q(qf, qq, a.qk_eps, lg);
-        }
+      if constexpr (qkn) {
+        load_q_raw(hg);
+        __syncthreads();                 // every wave has read the previous group's rows
+        put_q();
+        __syncthreads();
+        read_q();
+      } else {
+        load_q(hg);
       }
     }
     // S^T: lane (lg, lq) holds keys 16t + 4lg + i of head 16hg + lq

@@ -87,10 +87,12 @@ def test_device_counter_steps_follow_changing_arguments():
 # From 512 sequences (batch x kv heads) the step runs decode_split_kernel (d = 128, groups
 # <= 16; the host path runs the workgroup kernel), so equality pins the split kernel to it
 # bit for bit.  520 and 513 sequences (3 kv heads): counts that are no multiple of the route
-# workgroups; GQA groups of 4 and 16; a cache window of 128 beside the attention window of 64.
-@pytest.mark.parametrize("b,hq,hkv,cw", [(256, 8, 2, 64), (260, 32, 2, 64), (171, 12, 3, 128)])
-def test_split_kernel_steps_equal_host_steps(b, hq, hkv, cw):
-    d, layer, prompt, steps = 128, 5, 333, 200
+# workgroups; GQA groups of 4 and 16; a cache window of 128 beside the attention window of 64;
+# 2048 and 4096 sequences: the batch sweep's sizes, more workgroups than the chip holds at once.
+@pytest.mark.parametrize("b,hq,hkv,cw,steps", [(256, 8, 2, 64, 200), (260, 32, 2, 64, 200), (171, 12, 3, 128, 200),
+                                               (1024, 8, 2, 64, 60), (2048, 8, 2, 64, 60)])
+def test_split_kernel_steps_equal_host_steps(b, hq, hkv, cw, steps):
+    d, layer, prompt = 128, 5, 333
     total = prompt + steps
     g = torch.Generator(device="cuda").manual_seed(b + hq)
     q = torch.randn(b, hq, total, d, generator=g, device="cuda").bfloat16()

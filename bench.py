@@ -435,7 +435,7 @@ def bench_decode_sweep(torch, bf, batches=(128, 512, 1024, 2048), steps=64, seed
     return out
 
 
-def bench_stream(torch, bf, seed=0, T=262144, chunk=384, layer=5):
+def bench_stream(torch, bf, seed=0, T=262144, chunk=384, layer=5, max_chunk=4096):
     """cfg4: streaming chunked prefill, Hq=16, Hkv=4, d=256, bf16, 384-token chunks.
 
     Per chunk (the harness schedule): cache update (append + compress due
@@ -453,9 +453,9 @@ def bench_stream(torch, bf, seed=0, T=262144, chunk=384, layer=5):
     cfg = bf.compressed_butterfly_config()
 
     def run():
-        # a ring of 4416 rows (about 11 chunks): the native loop then runs five chunks per attention
-        # launch and per update job (the outputs and the cache equal the one-chunk schedule's)
-        cache = bf.CompressedKVCache(block_size=bs, local_window_tokens=W, max_kv_size=T, max_chunk_size=2048)
+        # a ring of 8512 rows (about 22 chunks): the native loop then runs eight chunks (its cap) per
+        # attention launch and per update job (the outputs and the cache equal the one-chunk schedule's)
+        cache = bf.CompressedKVCache(block_size=bs, local_window_tokens=W, max_kv_size=T, max_chunk_size=max_chunk)
         core = bf.ButterflyAttentionCore(cfg, layer)
         outs = bf.chunked_prefill(core, chunks, cache)
         return cache, outs

@@ -669,10 +669,11 @@ def _stream_chunks(core: ButterflyAttentionCore, chunks, start: int, run: int,
     b, hq, _, d = (int(x) for x in q0.shape)
     hkv = int(k0.shape[1])
     qs, ks, vs = [], [], []
+    bf16 = torch.bfloat16
     for qc, kc, vc in chunks[start:start + run]:
-        n = int(qc.shape[2])
-        if (n <= 2 or tuple(qc.shape) != (b, hq, n, d) or tuple(kc.shape) != (b, hkv, n, d) or kc.shape != vc.shape
-                or not (qc.dtype == kc.dtype == vc.dtype == torch.bfloat16) or not qc.is_cuda):
+        n = qc.shape[2]
+        if (n <= 2 or qc.shape != (b, hq, n, d) or kc.shape != (b, hkv, n, d) or vc.shape != kc.shape
+                or qc.dtype != bf16 or kc.dtype != bf16 or vc.dtype != bf16 or not qc.is_cuda):
             break
         qs.append(_c(qc))
         ks.append(_c(kc))
@@ -684,15 +685,20 @@ def _stream_chunks(core: ButterflyAttentionCore, chunks, start: int, run: int,
     ring_k, ring_v, pool_k, pool_v = cache._ring_k, cache._ring_v, cache._pool_k, cache._pool_v
     if tuple(ring_k.shape[:2]) != (b, hkv) or ring_k.shape[3] != d or ring_k.dtype != torch.bfloat16:
         raise ValueError("keys do not match the cache's batch/head/dim/dtype")
-    # outputs: consecutive 16-byte aligned ranges of one allocation
-    sizes = [q.numel() for q in qs]
-    starts, off = [], 0
-    for n in sizes:
-        starts.append(off)
-        off += (n + 7) // 8 * 8
-    flat = torch.empty(off, dtype=torch.bfloat16, device=q0.device)
-    outs = [flat[s:s + n].view(q.shape) for s, n, q in zip(starts, sizes, qs)]
+    # outputs: consecutive 16-byte aligned ranges of one allocation (chunks of one length: one
+    # [m, b, hq, n, d] tensor unbound into its rows, which costs the host far less per chunk)
     m = len(qs)
+    n0 = int(qs[0].shape[2])
+    if all(int(q.shape[2]) == n0 for q in qs):
+        outs = list(torch.empty((m, b, hq, n0, d), dtype=torch.bfloat16, device=q0.device).unbind(0))
+    else:
+        sizes = [q.numel() for q in qs]
+        starts, off = [], 0
+        for n in sizes:
+            starts.append(off)
+            off += (n + 7) // 8 * 8
+        flat = torch.empty(off, dtype=torch.bfloat16, device=q0.device)
+        outs = [flat[s:s + n].view(q.shape) for s, n, q in zip(starts, sizes, qs)]
     ptrs = lambda ts: (C.c_void_p * m)(*[t.data_ptr() for t in ts])
     lens = (C.c_int64 * m)(*[int(q.shape[2]) for q in qs])
     counters = (C.c_int64 * 4)(cache.offset, cache.tail_size, cache.summary_count, cache.summary_offset)

@@ -47,7 +47,7 @@ def _width(n):
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("max_chunk", [512, 2048])   # 2048: five chunks per launch (the bench's ring)
+@pytest.mark.parametrize("max_chunk", [512, 2048, 4096])   # 2048: five chunks per launch; 4096: eight (the bench's ring)
 def test_cfg4_full_stream_matches_oracle_at_stage_changes(max_chunk):
     hq, hkv, d, bs, W, T, chunk, layer = 16, 4, 256, 128, 64, 262144, 384, 10
     dev = torch.device("cuda")

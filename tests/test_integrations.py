@@ -230,7 +230,7 @@ def test_stock_decode_fallback_is_dense_over_the_tail():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("b,hq,hkv,d,max_chunk", [(1, 16, 4, 256, 512), (2, 8, 2, 128, 512), (1, 16, 4, 256, 2048),
-                                                   (2, 8, 2, 128, 1024)])
+                                                   (2, 8, 2, 128, 1024), (1, 16, 4, 256, 4096)])
 def test_native_chunk_loop_equals_per_chunk_calls(b, hq, hkv, d, max_chunk):
     """chunked_prefill runs chunks 2.. through bfly_stream_chunks: outputs, counters,
     ring and pool must equal those of one ButterflyAttentionCore call per chunk.  A ring of

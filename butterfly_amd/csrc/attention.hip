@@ -187,13 +187,18 @@ constexpr int kQPipe = 2;              // query heads whose Q fragments are held
 
 template <int D>
 struct MfmaCfg {
+  // d = 256: 512 threads, one query head per wave (waves w and w + 4 share query rows 16 (w & 3)..
+  // and take the two heads of a pair), so a wave holds one head's Q, S and O and two waves fit
+  // per SIMD; smaller d: 256 threads, each wave runs a head pair over its 16 query rows
+  static constexpr bool kWaveHead = D == 256;
+  static constexpr int NTHR = kWaveHead ? 512 : 256;
   static constexpr int KP = D + 8;                 // bf16 per K row (pad 16 B)
   static constexpr int KSTEPS = D / 32;            // MFMA k-steps over head_dim
   static constexpr int DTILES = D / 16;            // output d tiles
   static constexpr int PIECES = D / 8;             // 16-byte pieces per row
-  static constexpr int KLD = kPage * PIECES / 256;         // K (and V) pieces per thread per page
+  static constexpr int KLD = kPage * PIECES / NTHR;        // K (and V) pieces per thread per page
   static constexpr int SITEMS = kSumSlots * PIECES;        // summary pieces per chunk
-  static constexpr int SLD = (SITEMS + 255) / 256;
+  static constexpr int SLD = (SITEMS + NTHR - 1) / NTHR;
   static constexpr int K_BYTES = kSlots * KP * 2;
   static constexpr int V_BYTES = kSlots * D * 2;           // V row-major, unpadded, swizzled
   static constexpr int LDS = K_BYTES + V_BYTES;
@@ -270,7 +275,7 @@ struct NoBatch {};
 // the attention workgroups run this chunk; the host fuses only when the update
 // writes no ring slot or pool row that this chunk's attention reads.
 template <int D, bool kUpd = false, bool kBatch = false>
-__global__ void __launch_bounds__(256, D <= 128 ? 2 : 1)
+__global__ void __launch_bounds__(MfmaCfg<D>::NTHR, D <= 128 || MfmaCfg<D>::kWaveHead ? 2 : 1)
 attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, int nchunks_in, int hper,
                  std::conditional_t<kBatch, ChunkBatch, NoBatch> cb) {
   AttnArgs a = a_in;
@@ -319,9 +324,15 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
     nchunks = ck.nchunks;
   }
 
+  constexpr int NTHR = C::NTHR, NWAVES = NTHR / 64;
+  constexpr bool kWaveHead = C::kWaveHead;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
+  // query rows 16 qwave .. 16 qwave + 15 of each 64-position chunk; with kWaveHead, head
+  // parity hpar (the wave takes heads hlo + hpar, hlo + hpar + 2, ...)
+  const int qwave = kWaveHead ? (wave & 3) : wave;
+  const int hpar = kWaveHead ? (wave >> 2) : 0;
   const int seg = xcd_remap(blockIdx.x, gridDim.x);
   // small grids split a GQA group's heads over workgroups of hper heads each
   const int gsz = a.hq / a.hkv;
@@ -357,7 +368,7 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
   chunk_blocks(cend - 1, tmp, b_hi);
   if (a.nbr != nullptr) {
     const int cnt = (b_hi - b_lo + 1) * m.kcap;
-    for (int i = tid; i < cnt; i += 256) s_nbr[i] = a.nbr[(int64_t)b_lo * m.kcap + i];
+    for (int i = tid; i < cnt; i += NTHR) s_nbr[i] = a.nbr[(int64_t)b_lo * m.kcap + i];
   } else {
     // the table builder's row (neighbor_row, bfly_block_neighbors), one wave per
     // block and one lane per row entry: lane j holds the j-th candidate of
@@ -372,7 +383,7 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
     int bit = 0;
 #pragma unroll
     for (int jj = 0; jj < BFLY_MAX_PARTNERS; ++jj) bit = jj == jp ? t.partner_bits[jj] : bit;
-    for (int bb = b_lo + wave; bb <= b_hi; bb += 4) {
+    for (int bb = b_lo + wave; bb <= b_hi; bb += NWAVES) {
       int cand = -1;
       if (lane == 0) {
         cand = bb;
@@ -424,12 +435,12 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
     };
 #pragma unroll
     for (int it = 0; it < C::KLD; ++it) {
-      const int i = tid + it * 256;
+      const int i = tid + it * NTHR;
       kst[it] = ld(kbase, i / C::PIECES, i % C::PIECES);
     }
 #pragma unroll
     for (int it = 0; it < C::KLD; ++it) {
-      const int i = tid + it * 256;
+      const int i = tid + it * NTHR;
       vst[it] = ld(vbase, i / C::PIECES, i % C::PIECES);
     }
   };
@@ -437,13 +448,13 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
     const int sbase = (pg & 1) * kPage;
 #pragma unroll
     for (int it = 0; it < C::KLD; ++it) {
-      const int i = tid + it * 256;
+      const int i = tid + it * NTHR;
       const int r = i / C::PIECES, pc = i % C::PIECES;
       *reinterpret_cast<uint4*>(Ks + (sbase + r) * C::KP + pc * 8) = kst[it];
     }
 #pragma unroll
     for (int it = 0; it < C::KLD; ++it) {
-      const int i = tid + it * 256;
+      const int i = tid + it * NTHR;
       const int r = sbase + i / C::PIECES, pc = i % C::PIECES;
       *reinterpret_cast<uint4*>(Vs + r * D + (pc ^ C::vswz(r)) * 8) = vst[it];
     }
@@ -458,7 +469,7 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
     chunk_blocks(c, bA, bB);
 #pragma unroll
     for (int it = 0; it < C::SLD; ++it) {
-      const int i = tid + it * 256;
+      const int i = tid + it * NTHR;
       const int s = i / C::PIECES, pc = i % C::PIECES;
       int cn = -1, cb = -1;
       if (i < C::SITEMS) {
@@ -488,7 +499,7 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
   auto store_sum = [&]() {
 #pragma unroll
     for (int it = 0; it < C::SLD; ++it) {
-      const int i = tid + it * 256;
+      const int i = tid + it * NTHR;
       if (i >= C::SITEMS) continue;
       const int s = i / C::PIECES, pc = i % C::PIECES;
       *reinterpret_cast<uint4*>(Ks + (kRing + s) * C::KP + pc * 8) = skst[it];
@@ -503,14 +514,15 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
   // ---- register-resident Q fragments: lane holds query (chunk row wave*16+lq),
   // d in [lg*D/4, (lg+1)*D/4); k-step ks takes d = lg*D/4 + 8*ks + [0, 8)
   // (the K fragments use the same map, so the k permutation cancels).
-  bf16x8 qbuf[kQPipe][C::KSTEPS];
+  constexpr int QSLOTS = kWaveHead ? 1 : kQPipe;   // a wave-per-head wave holds one head's Q
+  bf16x8 qbuf[QSLOTS][C::KSTEPS];
 #pragma unroll
-  for (int u = 0; u < kQPipe; ++u)
+  for (int u = 0; u < QSLOTS; ++u)
 #pragma unroll
     for (int ks = 0; ks < C::KSTEPS; ++ks) qbuf[u][ks] = bf16x8{};
   const __bf16* qhead0 = reinterpret_cast<const __bf16*>(a.q) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz) * a.tq * D;
   auto load_q = [&](int u, int c, int hh) {
-    const int qp = c * kPage + wave * 16 + lq;
+    const int qp = c * kPage + qwave * 16 + lq;
     const bool ok = qp >= m.qlo && qp < m.qhi;
     // Rows outside the query range read row 0 instead: their scores are masked
     // and their outputs are never stored.
@@ -530,17 +542,31 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
   const int cstop = dir > 0 ? cend : cbeg - 1;
   auto new_page = [&](int c) { return dir > 0 ? c : c - 1; };
   auto refill_q = [&](int u, int c, int hh) {
-    int nh = hh + kQPipe, nc = c;
-    if (nh >= hhi) {
-      nh = hlo + u;
-      nc = c + dir;
+    if constexpr (kWaveHead) {
+      // this wave's next head: two on, or the first of its parity in the next chunk
+      int nh = hh + 2, nc = c;
+      if (nh >= hhi) {
+        nh = hlo + hpar;
+        nc = c + dir;
+      }
+      if (nc != cstop && nh < hhi) load_q(0, nc, nh);
+    } else {
+      int nh = hh + kQPipe, nc = c;
+      if (nh >= hhi) {
+        nh = hlo + u;
+        nc = c + dir;
+      }
+      if (nc != cstop) load_q(u, nc, nh);
     }
-    if (nc != cstop) load_q(u, nc, nh);
   };
 
+  if constexpr (kWaveHead) {
+    if (hlo + hpar < hhi) load_q(0, cfirst, hlo + hpar);
+  } else {
 #pragma unroll
-  for (int u = 0; u < kQPipe; ++u)
-    if (hlo + u < hhi) load_q(u, cfirst, hlo + u);
+    for (int u = 0; u < kQPipe; ++u)
+      if (hlo + u < hhi) load_q(u, cfirst, hlo + u);
+  }
   fetch_page(dir > 0 ? cbeg - 1 : cend - 1);
   store_page(dir > 0 ? cbeg - 1 : cend - 1);
   fetch_page(new_page(cfirst));
@@ -559,7 +585,7 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
     }
 
     // ---------------- per-lane state shared by every head: wave owns positions [pw, pw+16)
-    const int pw = c * kPage + wave * 16;
+    const int pw = c * kPage + qwave * 16;
     const int qp = pw + lq;                          // this lane's query position
     const bool wave_active = (pw + 15 >= m.qlo) && (pw < m.qhi);
     const bool row_ok = qp >= m.qlo && qp < m.qhi;
@@ -609,10 +635,11 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
     for (int hb = hlo; hb < hhi; hb += kQPipe) {
 #pragma unroll
       for (int pp = 0; pp < kQPipe / 2; ++pp) {
-        const int h0 = hb + 2 * pp;
+        // kWaveHead: this wave's head of the pair alone, in Q slot 0
+        const int h0 = kWaveHead ? hb + hpar : hb + 2 * pp;
         if (h0 >= hhi) break;
-        const bool two = h0 + 1 < hhi;
-        const int u0 = 2 * pp, u1 = 2 * pp + 1;
+        const bool two = !kWaveHead && h0 + 1 < hhi;
+        const int u0 = kWaveHead ? 0 : 2 * pp, u1 = kWaveHead ? 0 : 2 * pp + 1;
         if (!wave_active) {
           refill_q(u0, c, h0);
           if (two) refill_q(u1, c, h0 + 1);
@@ -720,11 +747,8 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
             }
           }
         };
-        if constexpr (D == 256) {
-          if (two)
-            pair_body(std::true_type{});
-          else
-            pair_body(std::false_type{});
+        if constexpr (kWaveHead) {
+          pair_body(std::false_type{});
         } else {
           pair_body(std::true_type{});
         }
@@ -808,13 +832,13 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
       switch (a.d) {
         case 64: hipLaunchKernelGGL((attn_mfma_kernel<64, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
         case 128: hipLaunchKernelGGL((attn_mfma_kernel<128, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
-        default: hipLaunchKernelGGL((attn_mfma_kernel<256, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
+        default: hipLaunchKernelGGL((attn_mfma_kernel<256, true>), grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
       }
     } else {
       switch (a.d) {
         case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
         case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
-        default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
+        default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
       }
     }
   } else {
@@ -897,13 +921,13 @@ static int launch_attention_batch(const AttnArgs* ch, int n, hipStream_t stream,
     switch (a.d) {
       case 64: hipLaunchKernelGGL((attn_mfma_kernel<64, true, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
       case 128: hipLaunchKernelGGL((attn_mfma_kernel<128, true, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
-      default: hipLaunchKernelGGL((attn_mfma_kernel<256, true, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
+      default: hipLaunchKernelGGL((attn_mfma_kernel<256, true, true>), grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, 0, 0, hper, cb); break;
     }
   } else {
     switch (a.d) {
       case 64: hipLaunchKernelGGL((attn_mfma_kernel<64, false, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
       case 128: hipLaunchKernelGGL((attn_mfma_kernel<128, false, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
-      default: hipLaunchKernelGGL((attn_mfma_kernel<256, false, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
+      default: hipLaunchKernelGGL((attn_mfma_kernel<256, false, true>), grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, 0, 0, hper, cb); break;
     }
   }
   BFLY_CHECK_LAUNCH(what);

@@ -362,10 +362,12 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
     bB = blk_of(min((c + 1) * kPage, m.qhi) - 1);
   };
 
-  // ---- neighbour rows of every query block of the segment, once, into LDS
+  // ---- neighbour rows of every query block of the segment, once, into LDS (see the
+  // prologue below for when)
   int b_lo, b_hi, tmp;
   chunk_blocks(cbeg, b_lo, tmp);
   chunk_blocks(cend - 1, tmp, b_hi);
+  auto build_rows = [&]() {
   if (a.nbr != nullptr) {
     const int cnt = (b_hi - b_lo + 1) * m.kcap;
     for (int i = tid; i < cnt; i += NTHR) s_nbr[i] = a.nbr[(int64_t)b_lo * m.kcap + i];
@@ -407,6 +409,7 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
       if (lane >= __popcll(mask) && lane < m.kcap) row[lane] = -1;
     }
   }
+  };
 
   // ---- register staging of one page (K rows and V row pairs) and of the routed summaries
   uint4 kst[C::KLD], vst[C::KLD];
@@ -567,7 +570,11 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
     for (int u = 0; u < kQPipe; ++u)
       if (hlo + u < hhi) load_q(u, cfirst, hlo + u);
   }
+  // d <= 128: the rows are built while the first page is in flight; at d = 256 the rows'
+  // registers would join the page's (spills), so they come first
+  if constexpr (kWaveHead) build_rows();
   fetch_page(dir > 0 ? cbeg - 1 : cend - 1);
+  if constexpr (!kWaveHead) build_rows();
   store_page(dir > 0 ? cbeg - 1 : cend - 1);
   fetch_page(new_page(cfirst));
   __syncthreads();   // s_nbr visible

@@ -78,9 +78,30 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // --------------------------------------------------------------------------------------------
-// Generic kernel: grid (tq, batch*hkv), block 64 (one wave).
+// Generic kernel: grid (tq, batch*hkv), block 64 (one wave).  Up to kGenericHeads query heads of
+// the GQA group at a time share every K and V row read (scores: one lane per key, the row read in
+// 4-element pieces; output: one lane per d); each head's score and output sums keep the order
+// of a plain loop over d and over keys.
 constexpr int kGenericMaxKeys = 2048;
 constexpr int kGenericMaxD = 512;
+constexpr int kGenericHeads = 4;
+
+// dynamic LDS of attn_generic_kernel: q rows and scores of kGenericHeads heads
+inline size_t generic_lds_bytes(int d, int W, int kcap) {
+  return (size_t)kGenericHeads * (size_t)(d + W + kcap) * sizeof(float);
+}
+
+// 4 consecutive elements of a row as fp32 (16 bytes for fp32, 8 for bf16; d % 4 == 0 keeps
+// every row start aligned to the piece)
+__device__ __forceinline__ void load4_f32(const float* p, float (&x)[4]) {
+  const float4 v = *reinterpret_cast<const float4*>(p);
+  x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+}
+__device__ __forceinline__ void load4_f32(const __bf16* p, float (&x)[4]) {
+  const uint2 v = *reinterpret_cast<const uint2*>(p);
+  x[0] = __uint_as_float(v.x << 16); x[1] = __uint_as_float(v.x & 0xFFFF0000u);
+  x[2] = __uint_as_float(v.y << 16); x[3] = __uint_as_float(v.y & 0xFFFF0000u);
+}
 
 template <typename T>
 __global__ void __launch_bounds__(64) attn_generic_kernel(AttnArgs a) {
@@ -92,9 +113,13 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(AttnArgs a) {
   const int g = a.hq / a.hkv;
   const int d = a.d;
   const int64_t p = a.qpos ? (int64_t)a.qpos[r] : a.q_pos0 + r;
+  constexpr int GH = kGenericHeads;
 
-  __shared__ float qs[kGenericMaxD];
-  __shared__ float ps[kGenericMaxKeys];
+  // dynamic LDS: q rows [GH][d], then scores [GH][W + kcap] (generic_lds_bytes)
+  extern __shared__ float gen_lds[];
+  const int kmax = a.W + a.kcap;
+  auto qs = [&](int hh, int c) -> float& { return gen_lds[hh * d + c]; };
+  auto ps = [&](int hh, int idx) -> float& { return gen_lds[GH * d + hh * kmax + idx]; };
   __shared__ int sel[64];
   __shared__ int nsel;
 
@@ -139,37 +164,73 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(AttnArgs a) {
     }
     return vsb + (int64_t)sel[idx - nw] * d;
   };
+  const bool vec = (d & 3) == 0;
 
-  for (int hh = 0; hh < g; ++hh) {
-    const int h = kvh * g + hh;
-    const T* qrow = reinterpret_cast<const T*>(a.q) + ((bi * a.hq + h) * a.tq + r) * d;
-    T* orow = reinterpret_cast<T*>(a.out) + ((bi * a.hq + h) * a.tq + r) * d;
+  for (int h0 = 0; h0 < g; h0 += GH) {
+    const int nh = g - h0 < GH ? g - h0 : GH;
+    const T* qhead = reinterpret_cast<const T*>(a.q) + ((bi * a.hq + kvh * g + h0) * a.tq + r) * d;
     __syncthreads();
-    for (int c = lane; c < d; c += 64) qs[c] = to_f32(qrow[c]);
+    for (int i = lane; i < GH * d; i += 64) {
+      const int hh = i / d, c = i - hh * d;
+      // heads past the group repeat its last one (computed, never stored)
+      qs(hh, c) = to_f32(qhead[(int64_t)(hh < nh ? hh : nh - 1) * a.tq * d + c]);
+    }
     __syncthreads();
-    float mloc = -INFINITY;
+    float mloc[GH];
+#pragma unroll
+    for (int hh = 0; hh < GH; ++hh) mloc[hh] = -INFINITY;
     for (int idx = lane; idx < nk; idx += 64) {
       const T* kr = krow(idx);
-      float s = 0.f;
-      for (int c = 0; c < d; ++c) s = fmaf(qs[c], to_f32(kr[c]), s);
-      s *= a.scale;
-      ps[idx] = s;
-      mloc = fmaxf(mloc, s);
+      float s[GH];
+#pragma unroll
+      for (int hh = 0; hh < GH; ++hh) s[hh] = 0.f;
+      if (vec) {
+        for (int c = 0; c < d; c += 4) {
+          float kx[4];
+          load4_f32(kr + c, kx);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int hh = 0; hh < GH; ++hh) s[hh] = fmaf(qs(hh, c + e), kx[e], s[hh]);
+        }
+      } else {
+        for (int c = 0; c < d; ++c) {
+          const float kx = to_f32(kr[c]);
+#pragma unroll
+          for (int hh = 0; hh < GH; ++hh) s[hh] = fmaf(qs(hh, c), kx, s[hh]);
+        }
+      }
+#pragma unroll
+      for (int hh = 0; hh < GH; ++hh) {
+        s[hh] *= a.scale;
+        ps(hh, idx) = s[hh];
+        mloc[hh] = fmaxf(mloc[hh], s[hh]);
+      }
     }
-    const float m = wave_max(mloc);
-    float lloc = 0.f;
-    for (int idx = lane; idx < nk; idx += 64) {
-      float e = nk > 0 ? expf(ps[idx] - m) : 0.f;
-      ps[idx] = e;
-      lloc += e;
+    float inv[GH];
+#pragma unroll
+    for (int hh = 0; hh < GH; ++hh) {
+      const float m = wave_max(mloc[hh]);
+      float lloc = 0.f;
+      for (int idx = lane; idx < nk; idx += 64) {
+        const float e = expf(ps(hh, idx) - m);
+        ps(hh, idx) = e;
+        lloc += e;
+      }
+      inv[hh] = 1.f / fmaxf(wave_sum(lloc), 1e-9f);
     }
-    const float l = wave_sum(lloc);
     __syncthreads();
-    const float inv = 1.f / fmaxf(l, 1e-9f);
     for (int c = lane; c < d; c += 64) {
-      float acc = 0.f;
-      for (int idx = 0; idx < nk; ++idx) acc = fmaf(ps[idx], to_f32(vrow(idx)[c]), acc);
-      orow[c] = from_f32<T>(acc * inv);
+      float acc[GH];
+#pragma unroll
+      for (int hh = 0; hh < GH; ++hh) acc[hh] = 0.f;
+      for (int idx = 0; idx < nk; ++idx) {
+        const float vx = to_f32(vrow(idx)[c]);
+#pragma unroll
+        for (int hh = 0; hh < GH; ++hh) acc[hh] = fmaf(ps(hh, idx), vx, acc[hh]);
+      }
+      for (int hh = 0; hh < nh; ++hh)
+        reinterpret_cast<T*>(a.out)[((bi * a.hq + kvh * g + h0 + hh) * a.tq + r) * d + c] = from_f32<T>(acc[hh] * inv[hh]);
     }
   }
 }
@@ -854,10 +915,11 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
     BFLY_CHECK_ARG(a.kcap <= 64, "%s: kcap > 64", what);
     BFLY_CHECK_ARG(a.tq <= INT32_MAX && a.batch * a.hkv <= 65535, "%s: grid too large", what);
     dim3 grid((unsigned)a.tq, (unsigned)(a.batch * a.hkv));
+    const size_t lds = generic_lds_bytes(a.d, a.W, a.kcap);
     if (dtype == BFLY_DTYPE_F32)
-      hipLaunchKernelGGL(attn_generic_kernel<float>, grid, dim3(64), 0, stream, a);
+      hipLaunchKernelGGL(attn_generic_kernel<float>, grid, dim3(64), lds, stream, a);
     else
-      hipLaunchKernelGGL(attn_generic_kernel<__bf16>, grid, dim3(64), 0, stream, a);
+      hipLaunchKernelGGL(attn_generic_kernel<__bf16>, grid, dim3(64), lds, stream, a);
   }
   BFLY_CHECK_LAUNCH(what);
   return BFLY_OK;

@@ -104,7 +104,10 @@ __device__ __forceinline__ void q4_sets(const Q4Args& a, int lane, int64_t set0,
       }
     }
   };
-  if (set0 < a.n_sets) load_set(set0);
+  // issued on every path (a wave past the sets loads set 0 and drops it): behind a branch, the
+  // wait in form_x() for loads issued before these would count as on the path without them
+  // and wait for these too
+  load_set(set0 < a.n_sets ? set0 : 0);
   form_x();
   if (set0 >= a.n_sets) return;
 
@@ -197,9 +200,12 @@ __global__ void __launch_bounds__(512) q4_norm_gemv_kernel(Q4Args a, Q4NormArgs 
   __shared__ float part[4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t waves = (int64_t)gridDim.x * 8;
+  // the norm's inputs are requested before the weights, so that forming the row waits for them
+  // alone and runs while the weights are in flight
+  const RmsRowIn<PER> in = rms_row_load<PER>(nm.x, nm.residual, nm.weight, tid, tid < 256);
   q4_sets<NP, R, kSilu>(a, lane, (int64_t)blockIdx.x * 8 + wave, waves, reinterpret_cast<const bf16x8*>(xn), [&] {
-    add_rmsnorm_row<PER, true>(nm.x, nm.residual, nm.weight, blockIdx.x == 0 ? nm.h_out : nullptr, xn, DIM, nm.eps,
-                               tid, tid < 256, part);
+    add_rmsnorm_row_from<PER>(in, nm.residual != nullptr, blockIdx.x == 0 ? nm.h_out : nullptr, xn, DIM, nm.eps, tid,
+                              tid < 256, part);
     __syncthreads();   // the normed row is in LDS
   });
 }

@@ -17,53 +17,59 @@ __device__ __forceinline__ float dec_wave_sum64(float v) {
   return v;
 }
 
+// The row's inputs of one thread in 16-byte pieces: x, y (zero when null) and the norm weight.
+template <int PER>
+struct RmsRowIn {
+  bf16x8 x[PER / 8], y[PER / 8], w[PER / 8];
+};
+
 // Thread t < 256 of the participating threads holds elements [t PER, t PER + PER)
-// of the row (dim = 256 PER).  x, y (may be null), h_out (null when y is), n_out:
-// the row's first element; w: the norm weight.  Every thread of the workgroup calls
-// it (the barrier is the workgroup's); threads with `active` false only take the
-// barrier.  part: 4 floats of LDS.  kVec: 16-byte pieces (PER a multiple of 8 and
-// every pointer 16-byte aligned).
-template <int PER, bool kVec>
-__device__ __forceinline__ void add_rmsnorm_row(const __bf16* __restrict__ x, const __bf16* __restrict__ y,
-                                                const __bf16* __restrict__ w, __bf16* __restrict__ h_out,
-                                                __bf16* __restrict__ n_out, int dim, float eps, int t, bool active,
-                                                float* part) {
+// of the row (dim = 256 PER), 16-byte pieces (PER a multiple of 8, every pointer 16-byte
+// aligned).  Requested apart from the arithmetic, so that a caller can issue them ahead of
+// other loads and not wait for those.
+template <int PER>
+__device__ __forceinline__ RmsRowIn<PER> rms_row_load(const __bf16* __restrict__ x, const __bf16* __restrict__ y,
+                                                      const __bf16* __restrict__ w, int t, bool active) {
+  RmsRowIn<PER> in{};
+  if (active) {
+    const int64_t base = (int64_t)t * PER;
+#pragma unroll
+    for (int c = 0; c < PER / 8; ++c) {
+      in.x[c] = *reinterpret_cast<const bf16x8*>(x + base + 8 * c);
+      if (y != nullptr) in.y[c] = *reinterpret_cast<const bf16x8*>(y + base + 8 * c);
+      in.w[c] = *reinterpret_cast<const bf16x8*>(w + base + 8 * c);
+    }
+  }
+  return in;
+}
+
+// The residual add + RMSNorm of rms_row_load's pieces: h_out (null when y is) and n_out get
+// the row's elements [t PER, t PER + PER).  Every thread of the workgroup calls it (the
+// barrier is the workgroup's); threads with `active` false only take the barrier.  part: 4
+// floats of LDS.
+template <int PER>
+__device__ __forceinline__ void add_rmsnorm_row_from(const RmsRowIn<PER>& in, bool has_y, __bf16* __restrict__ h_out,
+                                                     __bf16* __restrict__ n_out, int dim, float eps, int t,
+                                                     bool active, float* part) {
 #pragma clang fp contract(off)
   const int64_t base = (int64_t)t * PER;
   float h[PER];
   if (active) {
-    if constexpr (kVec) {
+#pragma unroll
+    for (int c = 0; c < PER / 8; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float v = (float)in.x[c][e];
+        if (has_y) v = (float)(__bf16)(v + (float)in.y[c][e]);   // residual stream in bf16
+        h[8 * c + e] = v;
+      }
+    if (has_y && h_out != nullptr) {
 #pragma unroll
       for (int c = 0; c < PER / 8; ++c) {
-        const bf16x8 xv = *reinterpret_cast<const bf16x8*>(x + base + 8 * c);
-        bf16x8 yv{};
-        if (y != nullptr) yv = *reinterpret_cast<const bf16x8*>(y + base + 8 * c);
+        bf16x8 hv;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float v = (float)xv[e];
-          if (y != nullptr) v = (float)(__bf16)(v + (float)yv[e]);   // residual stream in bf16
-          h[8 * c + e] = v;
-        }
-      }
-      if (y != nullptr && h_out != nullptr) {
-#pragma unroll
-        for (int c = 0; c < PER / 8; ++c) {
-          bf16x8 hv;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) hv[e] = (__bf16)h[8 * c + e];
-          *reinterpret_cast<bf16x8*>(h_out + base + 8 * c) = hv;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        float v = (float)x[base + e];
-        if (y != nullptr) v = (float)(__bf16)(v + (float)y[base + e]);   // residual stream in bf16
-        h[e] = v;
-      }
-      if (y != nullptr && h_out != nullptr) {
-#pragma unroll
-        for (int e = 0; e < PER; ++e) h_out[base + e] = (__bf16)h[e];
+        for (int e = 0; e < 8; ++e) hv[e] = (__bf16)h[8 * c + e];
+        *reinterpret_cast<bf16x8*>(h_out + base + 8 * c) = hv;
       }
     }
     float ss = 0.f;
@@ -76,16 +82,49 @@ __device__ __forceinline__ void add_rmsnorm_row(const __bf16* __restrict__ x, co
   if (!active) return;
   const float tot = (part[0] + part[1]) + (part[2] + part[3]);
   const float r = rsqrtf(tot / (float)dim + eps);
+#pragma unroll
+  for (int c = 0; c < PER / 8; ++c) {
+    bf16x8 nv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) nv[e] = (__bf16)(h[8 * c + e] * r * (float)in.w[c][e]);
+    *reinterpret_cast<bf16x8*>(n_out + base + 8 * c) = nv;
+  }
+}
+
+// Both steps at once; kVec false: element loads (any alignment), the same arithmetic.
+template <int PER, bool kVec>
+__device__ __forceinline__ void add_rmsnorm_row(const __bf16* __restrict__ x, const __bf16* __restrict__ y,
+                                                const __bf16* __restrict__ w, __bf16* __restrict__ h_out,
+                                                __bf16* __restrict__ n_out, int dim, float eps, int t, bool active,
+                                                float* part) {
+#pragma clang fp contract(off)
   if constexpr (kVec) {
-#pragma unroll
-    for (int c = 0; c < PER / 8; ++c) {
-      const bf16x8 wv = *reinterpret_cast<const bf16x8*>(w + t * PER + 8 * c);
-      bf16x8 nv;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) nv[e] = (__bf16)(h[8 * c + e] * r * (float)wv[e]);
-      *reinterpret_cast<bf16x8*>(n_out + base + 8 * c) = nv;
-    }
+    const RmsRowIn<PER> in = rms_row_load<PER>(x, y, w, t, active);
+    add_rmsnorm_row_from<PER>(in, y != nullptr, h_out, n_out, dim, eps, t, active, part);
   } else {
+    const int64_t base = (int64_t)t * PER;
+    float h[PER];
+    if (active) {
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        float v = (float)x[base + e];
+        if (y != nullptr) v = (float)(__bf16)(v + (float)y[base + e]);   // residual stream in bf16
+        h[e] = v;
+      }
+      if (y != nullptr && h_out != nullptr) {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) h_out[base + e] = (__bf16)h[e];
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) ss = fmaf(h[e], h[e], ss);
+      ss = dec_wave_sum64(ss);
+      if ((t & 63) == 0) part[t >> 6] = ss;
+    }
+    __syncthreads();
+    if (!active) return;
+    const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float r = rsqrtf(tot / (float)dim + eps);
 #pragma unroll
     for (int e = 0; e < PER; ++e) n_out[base + e] = (__bf16)(h[e] * r * (float)w[t * PER + e]);
   }

@@ -69,8 +69,9 @@ struct Q4Args {
 
 // The sets of one wave: set0, set0 + stride, ... < n_sets.  form_x() runs after the first
 // set's weights are requested and before x (xsrc, bf16) is read: the fused form computes x
-// there.
-template <int NP, int R, bool kSilu, class XPtr, class FormX>
+// there.  kXFirst (x already in memory): x is requested before the weights, so that its
+// pre-sums wait for x alone.
+template <int NP, int R, bool kSilu, bool kXFirst, class XPtr, class FormX>
 __device__ __forceinline__ void q4_sets(const Q4Args& a, int lane, int64_t set0, int64_t stride, XPtr xsrc,
                                         FormX&& form_x) {
   const int pieces = a.pieces, groups = a.groups;
@@ -107,19 +108,37 @@ __device__ __forceinline__ void q4_sets(const Q4Args& a, int lane, int64_t set0,
   // issued on every path (a wave past the sets loads set 0 and drops it): behind a branch, the
   // wait in form_x() for loads issued before these would count as on the path without them
   // and wait for these too
+  bf16x8 xr[NP][4];
+  auto read_x = [&] {
+#pragma unroll
+    for (int j = 0; j < NP; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xr[j][c] = xsrc[(int64_t)pc[j] * 4 + c];
+  };
+  if constexpr (kXFirst) {
+    // returned from before any load: the weights, used after a later return, would be sunk
+    // behind it and x's pre-sums
+    if (set0 >= a.n_sets) return;
+    read_x();
+    __builtin_amdgcn_sched_barrier(0);
+  }
   load_set(set0 < a.n_sets ? set0 : 0);
+  // the scheduler keeps the order: x's requests, the weights', then x's pre-sums (it would
+  // hoist the pre-sums above the weights, which then were requested only after x arrived)
+  if constexpr (kXFirst) __builtin_amdgcn_sched_barrier(0);
   form_x();
-  if (set0 >= a.n_sets) return;
+  if constexpr (!kXFirst) {
+    if (set0 >= a.n_sets) return;
+    read_x();
+  }
 
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
     const bool valid = lane + 64 * j < pieces;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const bf16x8 v = xsrc[(int64_t)pc[j] * 4 + c];
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) xq[j][8 * c + e] = valid ? (float)v[e] : 0.f;
-    }
+      for (int e = 0; e < 8; ++e) xq[j][8 * c + e] = valid ? (float)xr[j][c][e] : 0.f;
   }
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
@@ -178,7 +197,8 @@ __device__ __forceinline__ void q4_sets(const Q4Args& a, int lane, int64_t set0,
 
 template <int NP, int R, bool kSilu>
 __global__ void __launch_bounds__(64) q4_gemv_kernel(Q4Args a) {
-  q4_sets<NP, R, kSilu>(a, (int)threadIdx.x, blockIdx.x, gridDim.x, reinterpret_cast<const bf16x8*>(a.x), [] {});
+  q4_sets<NP, R, kSilu, true>(a, (int)threadIdx.x, blockIdx.x, gridDim.x, reinterpret_cast<const bf16x8*>(a.x),
+                              [] {});
 }
 
 // The residual add + RMSNorm of the input row inside the product: 512 threads; threads
@@ -203,7 +223,7 @@ __global__ void __launch_bounds__(512) q4_norm_gemv_kernel(Q4Args a, Q4NormArgs 
   // the norm's inputs are requested before the weights, so that forming the row waits for them
   // alone and runs while the weights are in flight
   const RmsRowIn<PER> in = rms_row_load<PER>(nm.x, nm.residual, nm.weight, tid, tid < 256);
-  q4_sets<NP, R, kSilu>(a, lane, (int64_t)blockIdx.x * 8 + wave, waves, reinterpret_cast<const bf16x8*>(xn), [&] {
+  q4_sets<NP, R, kSilu, false>(a, lane, (int64_t)blockIdx.x * 8 + wave, waves, reinterpret_cast<const bf16x8*>(xn), [&] {
     add_rmsnorm_row_from<PER>(in, nm.residual != nullptr, blockIdx.x == 0 ? nm.h_out : nullptr, xn, DIM, nm.eps, tid,
                               tid < 256, part);
     __syncthreads();   // the normed row is in LDS

@@ -453,7 +453,7 @@ def bench_stream(torch, bf, seed=0, T=262144, chunk=384, layer=5, max_chunk=4096
     cfg = bf.compressed_butterfly_config()
 
     def run():
-        # a ring of 8512 rows (about 22 chunks): the native loop then runs eight chunks (its cap) per
+        # a ring of 8512 rows (about 22 chunks): the native loop then runs ten chunks (its cap) per
         # attention launch and per update job (the outputs and the cache equal the one-chunk schedule's)
         cache = bf.CompressedKVCache(block_size=bs, local_window_tokens=W, max_kv_size=T, max_chunk_size=max_chunk)
         core = bf.ButterflyAttentionCore(cfg, layer)

@@ -43,12 +43,17 @@ __device__ __forceinline__ void pool_rows(TokPtr tok_ptr, int64_t cnt, T* dst, i
           const int64_t tok = base + (int64_t)u * rs;
           raw[u] = *reinterpret_cast<const uint4*>(tok_ptr(tok < cnt ? tok : cnt - 1) + c * VEC);
         }
+        // every load is issued before the first add (the scheduler hoisted adds between them,
+        // each add's wait then also waiting for the loads before it); a row past the end adds +0
+        // (acc is never -0, so acc + 0 is acc): no branch, into which the compiler would sink
+        // that row's load and wait for it alone
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < INFLIGHT; ++u) {
-          if (base + (int64_t)u * rs >= cnt) continue;
+          const bool in = base + (int64_t)u * rs < cnt;
           const T* v = reinterpret_cast<const T*>(&raw[u]);
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) acc[e] += to_f32(v[e]);
+          for (int e = 0; e < VEC; ++e) acc[e] += in ? to_f32(v[e]) : 0.f;
         }
       }
     } else {
@@ -80,7 +85,7 @@ __device__ __forceinline__ void pool_rows(TokPtr tok_ptr, int64_t cnt, T* dst, i
 // tail, which holds at most C positions, so their ring slots are distinct.
 // Work: x in [0, n_blocks + append workgroups), rows, K|V.
 // Chunks whose appends one update job may carry (the streaming loop's batches).
-constexpr int kMaxUpdateParts = 8;
+constexpr int kMaxUpdateParts = 10;
 // Rounds of 16-byte pieces per thread in an update's append workgroups.
 constexpr int kAppendRounds = 8;
 
@@ -102,26 +107,46 @@ struct UpdateJob {
   int64_t part_end[kMaxUpdateParts];
 };
 
-// Row of new token t (< step) of batch row `row` in an update's input.  The part is found by
-// selects over every part slot (constant indices: the job's words stay scalar loads; a lane-
-// dependent index would turn each into a dependent vector load).
-// Branch-free (a branch between the rounds of loads would make each wait for the last).
-template <typename T>
-__device__ __forceinline__ const T* update_fresh_row(const UpdateJob& u, int kv, int64_t row, int64_t t) {
+// The part of an update's input that holds new token t (< step): its buffer (K or V), first
+// token and length, found by selects over every part slot (constant indices).  With a
+// workgroup-uniform t this is scalar work; with a lane-dependent t the compiler makes the
+// pointer selection a vector load from a selected address, whose wait also waits for every
+// row load issued before it (loads complete in order), so the rows' lookups go first.
+struct FreshPart {
+  const void* base;
+  int64_t t0, len;
+};
+__device__ __forceinline__ FreshPart update_part_of(const UpdateJob& u, int kv, int64_t t) {
   const bool single = u.nparts == 0;
-  const void* base = single ? (kv ? u.v_new : u.k_new) : (kv ? u.v_part[0] : u.k_part[0]);
-  int64_t t0 = 0, len = single ? u.step : u.part_end[0];
+  FreshPart f{single ? (kv ? u.v_new : u.k_new) : (kv ? u.v_part[0] : u.k_part[0]), 0,
+              single ? u.step : u.part_end[0]};
 #pragma unroll
   for (int j = 1; j < kMaxUpdateParts; ++j) {
+    const void* pj = kv ? u.v_part[j] : u.k_part[j];
     const bool in = j < u.nparts && t >= u.part_end[j - 1];   // part_end increases: the last such j
-    base = in ? (kv ? u.v_part[j] : u.k_part[j]) : base;
-    len = in ? u.part_end[j] - u.part_end[j - 1] : len;
-    t0 = in ? u.part_end[j - 1] : t0;
+    f.base = in ? pj : f.base;
+    f.len = in ? u.part_end[j] - u.part_end[j - 1] : f.len;
+    f.t0 = in ? u.part_end[j - 1] : f.t0;
   }
-  return reinterpret_cast<const T*>(base) + (row * len + (t - t0)) * u.d;
+  return f;
 }
 
-// Work item (bx, row, kv) of an update: workgroup-uniform, 256 threads.
+// Row of new token t of batch row `row` in part f (t0 <= t < t0 + len).
+template <typename T>
+__device__ __forceinline__ const T* update_part_row(const FreshPart& f, int64_t row, int64_t t, int d) {
+  return reinterpret_cast<const T*>(f.base) + (row * f.len + (t - f.t0)) * d;
+}
+
+// Row of new token t (< step) of batch row `row` in an update's input, any t.
+template <typename T>
+__device__ __forceinline__ const T* update_fresh_row(const UpdateJob& u, int kv, int64_t row, int64_t t) {
+  return update_part_row<T>(update_part_of(u, kv, t), row, t, u.d);
+}
+
+// Work item (bx, row, kv) of an update: workgroup-uniform, 256 threads.  A workgroup's new
+// tokens normally lie in one part (the parts are whole chunks): its part is then looked up once,
+// from workgroup-uniform values (scalar work), and every row follows by adding; a workgroup
+// whose tokens straddle parts looks each row up.
 template <typename T, int VEC>
 __device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx, int64_t row, int kv, float* part) {
   const int d = u.d;
@@ -132,17 +157,29 @@ __device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx
     const int lpr = d / VEC, tpw = 256 / lpr;
     const int t = threadIdx.x, c = t % lpr;
     if (t / lpr >= tpw) return;
-    const int64_t tok0 = (bx - u.n_blocks) * tpw * kAppendRounds + t / lpr;
+    const int64_t wg_tok0 = (bx - u.n_blocks) * tpw * kAppendRounds;
+    const int64_t tok0 = wg_tok0 + t / lpr;
     if (tok0 >= u.step) return;
+    const int64_t wg_last = min(wg_tok0 + (int64_t)tpw * kAppendRounds, u.step) - 1;
+    const FreshPart f = update_part_of(u, kv, wg_tok0);
+    const bool one_part = wg_last < f.t0 + f.len;
     // loads unconditional (past the last token: the last token again), stores kept in range
     // (a native vector type: arrays of HIP's uint4 struct are copied by memcpy and stay in
     // scratch memory)
+    // (each branch issues its own loads: pointers merged from the two would be flat pointers,
+    // whose loads the scalar-load waits also count)
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     u32x4 x[kAppendRounds];
+    if (one_part) {
 #pragma unroll
-    for (int i = 0; i < kAppendRounds; ++i) {
-      const int64_t tok = min(tok0 + (int64_t)i * tpw, u.step - 1);
-      x[i] = *reinterpret_cast<const u32x4*>(update_fresh_row<T>(u, kv, row, tok) + c * VEC);
+      for (int i = 0; i < kAppendRounds; ++i)
+        x[i] = *reinterpret_cast<const u32x4*>(
+            update_part_row<T>(f, row, min(tok0 + (int64_t)i * tpw, u.step - 1), d) + c * VEC);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kAppendRounds; ++i)
+        x[i] = *reinterpret_cast<const u32x4*>(
+            update_fresh_row<T>(u, kv, row, min(tok0 + (int64_t)i * tpw, u.step - 1)) + c * VEC);
     }
     int64_t slot = posmod(u.offset + tok0, u.ring);   // then + tpw per round (tpw < ring: one wrap)
 #pragma unroll
@@ -156,14 +193,30 @@ __device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx
   const int64_t n = bx;
   const int64_t p0 = u.first_pos + n * u.bs;
   const int64_t r0 = posmod(p0, u.ring);   // tokens < bs <= ring: one wrap at most
-  auto tok_ptr = [&](int64_t tok) -> const T* {
-    const int64_t p = p0 + tok;
-    if (p >= u.offset) return update_fresh_row<T>(u, kv, row, p - u.offset);
+  T* dst = reinterpret_cast<T*>(kv ? u.pool_v : u.pool_k) + (row * u.pool_rows + u.first_slot + n) * d;
+  auto ring_row = [&](int64_t tok) -> const T* {
     int64_t r = r0 + tok;
     if (r >= u.ring) r -= u.ring;
     return ring + r * d;
   };
-  T* dst = reinterpret_cast<T*>(kv ? u.pool_v : u.pool_k) + (row * u.pool_rows + u.first_slot + n) * d;
+  if (p0 + u.bs <= u.offset) {   // the whole block was appended before: ring rows
+    pool_rows<T, VEC, 16>(ring_row, (int64_t)u.bs, dst, d, part);
+    return;
+  }
+  if (p0 >= u.offset) {          // the whole block is new
+    const FreshPart f = update_part_of(u, kv, p0 - u.offset);
+    if (p0 + u.bs - 1 - u.offset < f.t0 + f.len) {
+      const int64_t f0 = p0 - u.offset;
+      pool_rows<T, VEC, 16>([&](int64_t tok) { return update_part_row<T>(f, row, f0 + tok, d); }, (int64_t)u.bs, dst,
+                            d, part);
+      return;
+    }
+  }
+  auto tok_ptr = [&](int64_t tok) -> const T* {
+    const int64_t p = p0 + tok;
+    if (p >= u.offset) return update_fresh_row<T>(u, kv, row, p - u.offset);
+    return ring_row(tok);
+  };
   pool_rows<T, VEC, 16>(tok_ptr, (int64_t)u.bs, dst, d, part);
 }
 

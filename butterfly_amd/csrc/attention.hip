@@ -297,7 +297,7 @@ struct MfmaArgs {
   int nblocks, nsum, kcap, bs, W;
   int token_cutoff;
   // fused launch (kUpd): grid rows >= attn_y run a cache update instead
-  // (cache_update_body over upd_x x upd_rows x K|V work items, upd_wgs in all)
+  // (cache_update_body over upd_x x upd_rows x K|V work items, upd_wgs in all; NTHR / 256 per workgroup)
   UpdateJob upd;
   int attn_y, upd_x, upd_rows;
   int64_t upd_wgs;
@@ -348,19 +348,25 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
   __shared__ int s_nbr[kMaxSegBlocks * kMaxKcap];
   __bf16* Ks = reinterpret_cast<__bf16*>(smem);                 // [kSlots][KP]
   __bf16* Vs = reinterpret_cast<__bf16*>(smem + C::K_BYTES);    // [kSlots][D], pieces swizzled by row
-  static_assert(C::LDS >= 256 * 8 * 4, "pooling scratch aliases the staging tiles");
+  static_assert(C::LDS >= C::NTHR / 256 * 256 * 8 * 4, "pooling scratch aliases the staging tiles");
   if constexpr (kUpd) {
     // (the kernel argument itself, not the local copy: the job's part arrays are indexed at
     // run time, which would put a modified copy in scratch memory)
+    // Each 256 threads of an update workgroup run one work item (kUpdPerWg per workgroup), with
+    // their own pooling scratch; a group whose item is past the end exits (an exited wave no
+    // longer counts at a barrier).
     const MfmaArgs& mu = m_in;
     if ((int)blockIdx.y >= mu.attn_y) {
-      const int64_t lin = (int64_t)(blockIdx.y - mu.attn_y) * gridDim.x + blockIdx.x;
+      constexpr int kUpdPerWg = MfmaCfg<D>::NTHR / 256;
+      const int grp = (int)threadIdx.x >> 8;
+      const int64_t lin = ((int64_t)(blockIdx.y - mu.attn_y) * gridDim.x + blockIdx.x) * kUpdPerWg + grp;
       if (lin >= mu.upd_wgs) return;
       const int64_t per_kv = (int64_t)mu.upd_x * mu.upd_rows;
       const int kv = (int)(lin / per_kv);
       const int64_t r = lin - kv * per_kv;
       const int64_t row = r / mu.upd_x;
-      cache_update_body<__bf16, 8>(mu.upd, r - row * mu.upd_x, row, kv, reinterpret_cast<float*>(smem));
+      cache_update_body<__bf16, 8>(mu.upd, r - row * mu.upd_x, row, kv, reinterpret_cast<float*>(smem) + grp * 256 * 8,
+                                   (int)threadIdx.x & 255);
       return;
     }
   }
@@ -893,8 +899,9 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
       m.attn_y = (int)grid.y;
       m.upd_x = (int)ux;
       m.upd_rows = (int)upd_rows;
-      m.upd_wgs = ux * upd_rows * 2;
-      const int64_t extra = (m.upd_wgs + nseg - 1) / nseg;
+      m.upd_wgs = ux * upd_rows * 2;   // work items; a d = 256 workgroup (512 threads) runs two
+      const int64_t per_wg = a.d == 256 ? MfmaCfg<256>::NTHR / 256 : 1;
+      const int64_t extra = ((m.upd_wgs + per_wg - 1) / per_wg + nseg - 1) / nseg;
       BFLY_CHECK_ARG(ux <= INT32_MAX && upd_rows <= 65535 && grid.y + extra <= 65535, "%s: grid too large", what);
       grid.y += (unsigned)extra;
       switch (a.d) {
@@ -983,8 +990,9 @@ static int launch_attention_batch(const AttnArgs* ch, int n, hipStream_t stream,
     m.attn_y = (int)grid.y;
     m.upd_x = (int)ux;
     m.upd_rows = (int)upd_rows;
-    m.upd_wgs = ux * upd_rows * 2;
-    const int64_t extra = (m.upd_wgs + nseg - 1) / nseg;
+    m.upd_wgs = ux * upd_rows * 2;   // work items; a d = 256 workgroup (512 threads) runs two
+    const int64_t per_wg = a.d == 256 ? MfmaCfg<256>::NTHR / 256 : 1;
+    const int64_t extra = ((m.upd_wgs + per_wg - 1) / per_wg + nseg - 1) / nseg;
     BFLY_CHECK_ARG(ux <= INT32_MAX && upd_rows <= 65535 && grid.y + extra <= 65535, "%s: grid too large", what);
     grid.y += (unsigned)extra;
     switch (a.d) {

@@ -17,16 +17,16 @@
 
 namespace bfly {
 
-// Mean of `cnt` token rows into dst (one workgroup, 256 threads); tok_ptr(tok)
-// is the row of token tok; `part` is 256 * 8 floats of LDS scratch.  INFLIGHT
+// Mean of `cnt` token rows into dst (256 threads: t = 0..255 of the group that runs it; the
+// workgroup barrier is taken once); tok_ptr(tok) is the row of token tok; `part` is 256 * 8
+// floats of LDS scratch.  INFLIGHT
 // 16-byte loads per thread are requested before their adds (8 keeps the
 // compressor's registers low; the update job's pooling takes 16, a whole block
 // at d = 256 in one round trip).
 template <typename T, int VEC, int INFLIGHT = 8, class TokPtr>
-__device__ __forceinline__ void pool_rows(TokPtr tok_ptr, int64_t cnt, T* dst, int d, float* part) {
+__device__ __forceinline__ void pool_rows(TokPtr tok_ptr, int64_t cnt, T* dst, int d, float* part, int t) {
   const int lpr = d / VEC;               // lanes per token row
   const int rs = 256 / lpr;              // token slots
-  const int t = threadIdx.x;
   const int c = t % lpr, s = t / lpr;
   float acc[VEC];
 #pragma unroll
@@ -143,19 +143,21 @@ __device__ __forceinline__ const T* update_fresh_row(const UpdateJob& u, int kv,
   return update_part_row<T>(update_part_of(u, kv, t), row, t, u.d);
 }
 
-// Work item (bx, row, kv) of an update: workgroup-uniform, 256 threads.  A workgroup's new
+// Work item (bx, row, kv) of an update, run by 256 threads (t = 0..255; the pooling items take the
+// workgroup barrier once, the append items none).  A workgroup's new
 // tokens normally lie in one part (the parts are whole chunks): its part is then looked up once,
 // from workgroup-uniform values (scalar work), and every row follows by adding; a workgroup
 // whose tokens straddle parts looks each row up.
 template <typename T, int VEC>
-__device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx, int64_t row, int kv, float* part) {
+__device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx, int64_t row, int kv, float* part,
+                                                  int t) {
   const int d = u.d;
   T* ring = reinterpret_cast<T*>(kv ? u.ring_v : u.ring_k) + row * u.ring * d;
   if (bx >= u.n_blocks) {
     // append: kAppendRounds x 256 / (d / VEC) tokens per workgroup, one 16-byte piece per
     // thread and round; every round's load is issued before the first store
     const int lpr = d / VEC, tpw = 256 / lpr;
-    const int t = threadIdx.x, c = t % lpr;
+    const int c = t % lpr;
     if (t / lpr >= tpw) return;
     const int64_t wg_tok0 = (bx - u.n_blocks) * tpw * kAppendRounds;
     const int64_t tok0 = wg_tok0 + t / lpr;
@@ -200,7 +202,7 @@ __device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx
     return ring + r * d;
   };
   if (p0 + u.bs <= u.offset) {   // the whole block was appended before: ring rows
-    pool_rows<T, VEC, 16>(ring_row, (int64_t)u.bs, dst, d, part);
+    pool_rows<T, VEC, 16>(ring_row, (int64_t)u.bs, dst, d, part, t);
     return;
   }
   if (p0 >= u.offset) {          // the whole block is new
@@ -208,7 +210,7 @@ __device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx
     if (p0 + u.bs - 1 - u.offset < f.t0 + f.len) {
       const int64_t f0 = p0 - u.offset;
       pool_rows<T, VEC, 16>([&](int64_t tok) { return update_part_row<T>(f, row, f0 + tok, d); }, (int64_t)u.bs, dst,
-                            d, part);
+                            d, part, t);
       return;
     }
   }
@@ -217,7 +219,7 @@ __device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx
     if (p >= u.offset) return update_fresh_row<T>(u, kv, row, p - u.offset);
     return ring_row(tok);
   };
-  pool_rows<T, VEC, 16>(tok_ptr, (int64_t)u.bs, dst, d, part);
+  pool_rows<T, VEC, 16>(tok_ptr, (int64_t)u.bs, dst, d, part, t);
 }
 
 // One bf16 update job in one launch (compress.hip); rows = batch x kv heads.

@@ -45,7 +45,7 @@ __global__ void __launch_bounds__(256) block_mean_kernel(PoolJob j0, PoolJob j1,
   };
   T* dst = reinterpret_cast<T*>(job.dst) + (row * job.dst_rows + job.dst_slot0 + n) * d;
   __shared__ float part[256 * 8];
-  pool_rows<T, VEC>(tok_ptr, cnt, dst, d, part);
+  pool_rows<T, VEC>(tok_ptr, cnt, dst, d, part, (int)threadIdx.x);
 }
 
 // One chunk's cache update in one launch: cache_update_body over the grid
@@ -53,7 +53,7 @@ __global__ void __launch_bounds__(256) block_mean_kernel(PoolJob j0, PoolJob j1,
 template <typename T, int VEC>
 __global__ void __launch_bounds__(256) cache_update_kernel(UpdateJob u) {
   __shared__ float part[256 * 8];
-  cache_update_body<T, VEC>(u, blockIdx.x, blockIdx.y, blockIdx.z, part);
+  cache_update_body<T, VEC>(u, blockIdx.x, blockIdx.y, blockIdx.z, part, (int)threadIdx.x);
 }
 
 // One update job (bf16, 16-byte row split: d in {64, 128, 256}) in one launch; the streaming

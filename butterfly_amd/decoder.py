@@ -279,12 +279,16 @@ def argmax_rows(x: torch.Tensor, parallel: bool = True) -> torch.Tensor:
     return out
 
 
-def argmax_rows_noalloc(x: torch.Tensor) -> torch.Tensor:
+def argmax_rows_noalloc(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``argmax_rows`` for at most 64 rows through ``bfly_argmax_rows_noalloc``: no workspace and
     no allocation besides the output (the library's static device workspace holds the
-    per-workgroup candidates; calls that overlap on one GPU race)."""
+    per-workgroup candidates; calls that overlap on one GPU race).  ``out``: a contiguous int64
+    [rows, 1] tensor to write instead of a new one."""
     rows, n = x.shape
-    out = torch.empty(rows, 1, dtype=torch.long, device=x.device)
+    if out is None:
+        out = torch.empty(rows, 1, dtype=torch.long, device=x.device)
+    elif out.shape != (rows, 1) or out.dtype != torch.long or not out.is_contiguous() or out.device != x.device:
+        raise ValueError("out must be a contiguous int64 [rows, 1] tensor on the input's device")
     with on(x.device):
         _native.call("bfly_argmax_rows_noalloc", x.data_ptr(), rows, n, x.stride(0), x.stride(1), out.data_ptr(),
                      stream_of(x))
@@ -613,22 +617,21 @@ class Decoder(nn.Module):
         tok = logits.argmax(-1, keepdim=True)
         out = torch.empty(b, new_tokens, dtype=torch.long, device=dev)
         out[:, :1] = tok
-        pos = torch.full((1,), t, dtype=torch.long, device=dev)
-        step = torch.ones(1, dtype=torch.long, device=dev)
+        ctr = torch.tensor([t, 1], dtype=torch.long, device=dev)   # position, output column: one add per step
+        pos, step = ctr[0:1], ctr[1:2]
         cos_tab, sin_tab = self._rope_tab
 
         def one_step():
             x = F.embedding(tok, self.embed_tokens)
             rope = RopeTable(cos_tab, sin_tab, pos)
             lg = self._last_logits(x, pos, caches, rope)
-            if _hip(lg):
-                nxt = argmax_rows_noalloc(lg) if lg.shape[0] <= 64 else argmax_rows(lg)
+            if _hip(lg) and lg.shape[0] <= 64:
+                nxt = argmax_rows_noalloc(lg, out=tok)    # the next step's token, written in place
             else:
-                nxt = lg.argmax(-1, keepdim=True)
-            tok.copy_(nxt)
+                nxt = argmax_rows(lg) if _hip(lg) else lg.argmax(-1, keepdim=True)
+                tok.copy_(nxt)
             out.index_copy_(1, step, nxt)
-            pos.add_(1)
-            step.add_(1)
+            ctr.add_(1)
 
         if new_tokens > 1:
             one_step()           # eager first step: every op meets its decode shapes before capture

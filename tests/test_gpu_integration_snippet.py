@@ -1,7 +1,8 @@
-"""GPU: the reference-side dispatch snippet of INTEGRATION.md, executed as written.
+"""GPU: the reference-side dispatch snippet of the repository's integration notes, executed
+as written.
 
-The fenced Python block under "The reference-side binding a maintainer would add" is
-read from INTEGRATION.md and run against a layout object with the fields of the
+The fenced Python block under "The reference-side binding a maintainer would add" is read
+from the notes (``_NOTES`` below) and run against a layout object with the fields of the
 reference's Torch ``BlockHamiltonianLayout`` (bna/torch/attention_wayfinder_permute.py:382-405);
 its output must match the CPU oracle of ``butterfly_compressed_attention``.
 """
@@ -38,8 +39,11 @@ class ReferenceShapedLayout:
     partner_count: int = 0
 
 
+_NOTES = Path(__file__).resolve().parents[1] / "INTEGRATION.md"
+
+
 def _snippet():
-    text = (Path(__file__).resolve().parents[1] / "INTEGRATION.md").read_text()
+    text = _NOTES.read_text()
     section = text[text.index("## 2. The reference-side binding"):]
     return re.search(r"```python\n(.*?)```", section, re.S).group(1)
 
@@ -47,7 +51,7 @@ def _snippet():
 @pytest.mark.parametrize("layer", [3, 13])
 def test_integration_snippet_runs_and_matches_the_oracle(layer):
     ns = {"torch": torch}
-    exec(compile(_snippet(), "INTEGRATION.md", "exec"), ns)
+    exec(compile(_snippet(), _NOTES.name, "exec"), ns)
     t, hq, hkv, d = 1000, 8, 2, 128
     g = torch.Generator().manual_seed(layer)
     q = torch.randn(1, hq, t, d, generator=g).bfloat16()

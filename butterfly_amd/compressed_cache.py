@@ -35,6 +35,9 @@ _DEV_SLOT = 32
 _DEV_ERR_CAPACITY, _DEV_ERR_ROPE = 1, 2
 # the bf16 MFMA decode kernel works in 32-bit positions and offsets below this
 _POS_LIMIT = 1 << 30
+# what bfly_decode_step takes (decode.hip kDecMaxWin, kDecMaxSum): an attention window of
+# at most 64 tokens and a routed row (self, local blocks, partners, sinks) of at most 16
+_DEC_MAX_WIN, _DEC_MAX_ROW = 64, 16
 
 
 @dataclass(frozen=True)
@@ -108,6 +111,16 @@ class CompressedKVCache:
         self._dev = torch.zeros(words, dtype=torch.int64, device=self._ring_k.device)
         self._dev_dirty = False
         self._push()
+
+    def device_step_supported(self, head_dim: int, window: int, dtype: torch.dtype, row_slots: int) -> bool:
+        """Whether ``decode_step`` takes a step of this cache: ``window`` (the attention window)
+        in [1, 64], head_dim 64 or 128 (256 for bf16), a routed row of at most 16 slots
+        (1 + local blocks + partners + sinks) and the cache's own window below 2^20.  Other
+        steps run on the host-counter path (``update_and_attend``), which cannot be captured."""
+        return (self._ring_k is not None and 0 < int(window) <= _DEC_MAX_WIN
+                and (head_dim in (64, 128) or (head_dim == 256 and dtype == torch.bfloat16))
+                and dtype in (torch.bfloat16, torch.float32) and 0 < int(row_slots) <= _DEC_MAX_ROW
+                and 0 < self.local_window_tokens < (1 << 20))
 
     def step_on_mfma(self, head_dim: int, window: int, scale: float, dtype: torch.dtype) -> bool:
         """Whether ``decode_step`` of this cache runs on the bf16 MFMA kernel: a positive

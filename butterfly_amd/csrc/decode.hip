@@ -62,8 +62,10 @@ constexpr int kDecMaxNew = 2;   // blocks pooled in one step (one per 128 steps 
 // Route buffer b (12 words) holds the routed row of the step whose post-update
 // kv_len has parity b, written during the step before it: word 0 a key
 // (kv_len | ns << 32 | W << 40 | rule << 48 | 1 << 62), word 1 layer_idx,
-// word 2 block_size | ring << 32, word 3 pool_rows | lwb << 32 | sinks << 40 |
-// partners << 38 | cache window << 43, words 4..11 the ns pool rows as int32.  A step uses it only
+// word 2 block_size | ring << 32, word 3 pool_rows | lwb << 30 | sinks << 34 |
+// partners << 38 | cache window << 43 (pool_rows < 2^30, lwb, sinks and partners
+// 4 bits each, cache window < 2^20; route_key below), words 4..11 the ns pool
+// rows as int32.  A step uses it only
 // when every word matches its own kv_len and arguments (anything else, a zero
 // key included, falls back to computing the row).  A launch uses the buffer
 // of its own parity and writes only the other one.  The attending workgroups

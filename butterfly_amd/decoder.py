@@ -44,6 +44,7 @@ import torch.nn.functional as F
 
 from . import _native
 from ._device import on, stream_of
+from .compressed_cache import CompressedKVCache
 from .integrations import QwenButterflyAttention, QwenButterflyConfig, register_butterfly_attention
 
 
@@ -611,6 +612,15 @@ class Decoder(nn.Module):
         their wall time is kept in ``self.last_graph_decode_s``."""
         dev = logits.device
         b = logits.shape[0]
+        for i, (layer, c) in enumerate(zip(self.layers, caches)):
+            attn = layer.self_attn
+            if not isinstance(c, CompressedKVCache) or not (
+                    isinstance(attn, ButterflyAttention)
+                    and attn.core.device_step_fits(c, self.cfg.head_dim, self.embed_tokens.dtype)):
+                raise ValueError(
+                    f"greedy_graph: layer {i} cannot run its decode step as one device launch (it needs a swapped "
+                    f"layer over a CompressedKVCache, an attention window of at most 64 tokens and a routed row "
+                    f"of at most 16 blocks); use greedy() for this configuration")
         for c in caches:
             c.use_device_counters()
         self._rope(0, t + new_tokens + 1, dev)               # table sized before capture

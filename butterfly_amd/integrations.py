@@ -220,14 +220,31 @@ class ButterflyAttentionCore:
             local_window_blocks=int(c.block_local_window_blocks), sink_count=int(c.block_sink_blocks),
             partner_count=int(c.block_partner_count), partner_rule=c.block_partner_rule, device=device)
 
+    def runs_device_step(self, cache, q_len: int, head_dim: int, dtype) -> bool:
+        """Whether ``__call__`` runs this step as one device-counter launch
+        (``CompressedKVCache.decode_step``, capturable in a HIP graph): one new token on a
+        cache with device counters, the compressed decode backend, and a step that
+        ``bfly_decode_step`` takes (attention window <= 64 tokens, routed row <= 16 slots).
+        Other steps with device counters read the counters back and run the host path."""
+        return (isinstance(cache, CompressedKVCache) and cache.device_counters is not None and q_len == 1
+                and self.device_step_fits(cache, head_dim, dtype))
+
+    def device_step_fits(self, cache, head_dim: int, dtype) -> bool:
+        """Whether this layer's one-token steps over ``cache`` can run as ``bfly_decode_step``
+        once device counters are on (``runs_device_step`` without the counter condition)."""
+        c = self.cfg
+        row = 1 + int(c.block_local_window_blocks) + int(c.block_partner_count) + int(c.block_sink_blocks)
+        return (isinstance(cache, CompressedKVCache) and c.butterfly_decode_backend != "dense"
+                and cache.device_step_supported(head_dim, int(c.compressed_local_window_tokens), dtype, row))
+
     def fuses_qk_norm(self, cache, q_len: int, head_dim: int, dtype) -> bool:
-        """Whether ``__call__`` takes ``qk_norm`` for this step: a device-counter decode step of
-        bf16 rows with head_dim 128 that runs on the MFMA kernel (``bfly_decode_step_qk_norm``:
-        positive scale, 32-bit positions and offsets)."""
+        """Whether ``__call__`` takes ``qk_norm`` for this step: a device step
+        (``runs_device_step``) of bf16 rows with head_dim 128 that runs on the MFMA kernel
+        (``bfly_decode_step_qk_norm``: positive scale, 32-bit positions and offsets)."""
         from .attention import _scale
 
-        return (isinstance(cache, CompressedKVCache) and cache.device_counters is not None and q_len == 1
-                and self.cfg.butterfly_decode_backend != "dense" and head_dim == 128 and dtype == torch.bfloat16
+        return (self.runs_device_step(cache, q_len, head_dim, dtype) and head_dim == 128
+                and dtype == torch.bfloat16
                 and cache.step_on_mfma(head_dim, int(self.cfg.compressed_local_window_tokens),
                                        _scale(self.scale, head_dim), dtype))
 
@@ -247,8 +264,7 @@ class ButterflyAttentionCore:
         c = self.cfg
         if qk_norm is not None and not self.fuses_qk_norm(cache, q_len, d, q.dtype):
             raise ValueError("qk_norm is taken only by device-counter decode steps of bf16, head_dim 128 rows")
-        if (cache is not None and cache.device_counters is not None and q_len == 1
-                and c.butterfly_decode_backend != "dense"):
+        if self.runs_device_step(cache, q_len, d, q.dtype):
             # device counters: one fixed-argument launch, no host bookkeeping (graph-capturable)
             out = cache.decode_step(q, k, v, layer_idx=self.layer_idx, local_window_tokens=w,
                                     partner_rule=c.block_partner_rule, local_window_blocks=c.block_local_window_blocks,

@@ -143,6 +143,15 @@ class NeighborSpec:
     roles: tuple[str, ...]
 
 
+def _reverse_low_bits(value: int, width: int) -> int:
+    """The low ``width`` bits of ``value`` in reverse order (higher bits dropped; 0 for
+    width 0).  Reference: bna/topology/butterfly.py:45-49."""
+    out = 0
+    for i in range(max(0, int(width))):
+        out = (out << 1) | ((int(value) >> i) & 1)
+    return out
+
+
 def butterfly_partner_block(*, block_idx: int, bit_idx: int, num_blocks: int, partner_rule: str,
                             width: int | None = None) -> int | None:
     """Partner of ``block_idx`` along ``bit_idx`` under the rule, or None when it falls outside
@@ -164,10 +173,8 @@ def butterfly_partner_block(*, block_idx: int, bit_idx: int, num_blocks: int, pa
         if b <= 0:
             return None
         p = ((b * 2654435761 + bit * 374761393) & 0xFFFFFFFF) % b
-    else:                                                     # bit_reversal over w bits
-        rev = int(format(b, f"0{w}b")[::-1], 2) if w > 0 else 0
-        flipped = rev ^ (1 << bit)
-        p = int(format(flipped, f"0{w}b")[::-1], 2)
+    else:                                                     # bit_reversal over the low w bits
+        p = _reverse_low_bits(_reverse_low_bits(b, w) ^ (1 << bit), w)
     if p < 0 or p >= int(num_blocks) or p > b:
         return None
     return int(p)

@@ -90,7 +90,17 @@ def active_tables(layout, *, kv_len: int, query_positions, W: int):
 
 def active_tables_from_tail(layout, *, kv_len: int, tail_start: int, num_summary_blocks: int, tail_len: int,
                             query_positions, W: int):
-    """Tail-relative active routing.  bna/mlx/attention.py:1601-1666."""
+    """Tail-relative active routing.  bna/mlx/attention.py:1601-1666.
+
+    Pinned by tests/test_oracle_attention.py: reduces to ``active_tables`` (itself
+    pinned by the reference-written golden tables) for a tail holding the whole
+    context with every block pooled, and equals a per-query enumeration over all
+    tokens and blocks on tiny layouts; planted off-by-one variants fail both.
+    """
+    if int(kv_len) <= 0:
+        raise ValueError("kv_len must be positive")
+    if torch.as_tensor(query_positions).dim() != 1:
+        raise ValueError("query_positions must be 1D")
     qp = torch.as_tensor(query_positions).long().view(-1)
     bs, n = layout.block_size, layout.num_blocks
     k = layout.block_neighbors.shape[-1]

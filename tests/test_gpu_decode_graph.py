@@ -259,3 +259,50 @@ def test_decoder_graph_greedy_equals_eager_greedy(batch, head_dim):
     eager = model.greedy(prompt, 40, caches())
     graphed = model.greedy_graph(prompt, 40, caches())
     assert torch.equal(eager, graphed), (eager, graphed)
+
+
+def test_default_window_128_with_device_counters_takes_the_host_path():
+    """The reference's compressed defaults give a 128-token attention window, beyond the
+    device step's 64: with device counters on, a one-token call of the swapped layer's
+    attention reads the counters back and runs the host path; its rows match the oracle
+    cache's from-cache rows, and a graph-replayed decode of such a model is refused."""
+    from oracle.cache import OracleCompressedKVCache
+
+    b, hq, hkv, d, layer, prompt, steps, w = 1, 8, 2, 128, 3, 300, 80, 128
+    total = prompt + steps
+    q, k, v = (_rand(121 + i, (b, h, total, d), torch.bfloat16) for i, h in enumerate((hq, hkv, hkv)))
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    cfg = bf.QwenButterflyConfig(path="block_sparse", block_compression="mean", block_partner_rule="causal_shift")
+    assert cfg.compressed_local_window_tokens == w
+    core = bf.ButterflyAttentionCore(cfg, layer_idx=layer)
+    cache = bf.CompressedKVCache(block_size=128, local_window_tokens=w, max_kv_size=total)
+    ref = OracleCompressedKVCache(block_size=128, local_window_tokens=w, max_kv_size=total)
+    core(qd[:, :, :prompt], kd[:, :, :prompt], vd[:, :, :prompt], cache)
+    ref.update_and_fetch(k[:, :, :prompt], v[:, :, :prompt])
+    cache.use_device_counters()
+    grp = hq // hkv
+    rep = lambda x: x.repeat_interleave(grp, dim=1)
+    for p in range(prompt, total):
+        assert not core.runs_device_step(cache, 1, d, torch.bfloat16)
+        got = core(qd[:, :, p:p + 1], kd[:, :, p:p + 1], vd[:, :, p:p + 1], cache).float().cpu()
+        ref.update_and_fetch(k[:, :, p:p + 1], v[:, :, p:p + 1])
+        tk, tv, sk, sv, ts, kv_len = ref.get_compressed_state()
+        lay = tp.build_layout(seq_len=kv_len, block_size=128, num_key_value_heads=hkv, num_key_value_groups=grp,
+                              layer_idx=layer, local_window_blocks=1, sink_count=1, partner_count=1,
+                              partner_rule="causal_shift")
+        want = oa.from_cache(q[:, :, p:p + 1], rep(tk), rep(tv), rep(sk), rep(sv), layout=lay,
+                             query_positions=torch.tensor([p]), W=w, tail_start=ts, kv_len=kv_len).float()
+        err = (got - want).abs().max().item()
+        assert err <= 2e-2 and ((got - want).norm() / want.norm()).item() <= 1e-2, (p, err)
+    cache.sync()
+    assert (cache.offset, cache.tail_size, cache.summary_count) == (ref.offset, ref.tail_size, ref.summary_count)
+
+    dcfg = DecoderConfig(vocab_size=1024, hidden_size=256, num_layers=2, num_heads=2, num_kv_heads=1, head_dim=128,
+                         intermediate_size=512)
+    model = Decoder(dcfg, seed=3)
+    bf.swap_qwen_attention_with_butterfly(model, cfg=cfg)
+    caches = [None] * dcfg.num_layers
+    bf.install_compressed_kv_caches(model, caches, block_size=128, local_window_tokens=w, max_kv_size=512)
+    prompt_ids = torch.randint(0, dcfg.vocab_size, (1, 200), generator=torch.Generator().manual_seed(9)).cuda()
+    with pytest.raises(ValueError, match="at most 64 tokens"):
+        model.greedy_graph(prompt_ids, 8, caches)

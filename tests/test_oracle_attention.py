@@ -243,3 +243,146 @@ def test_swa_and_routed_streams_merge_to_one_shot_prefill():
     got = oa.merge(a, c)
     want = oa.prefill(q, k, v, layout=lay, W=W)
     assert torch.allclose(got, want, atol=2e-6)
+
+
+# ---- tail-relative active routing (bna/mlx/attention.py:1601-1666)
+# Three checks pin oracle.attention.active_tables_from_tail: (1) with a tail that
+# holds the whole context and every block pooled it reduces to the reference-written
+# active tables (tests/golden/golden.npz, bna/torch/attention_wayfinder_permute.py:969-1019);
+# (2) on tiny layouts it equals a per-query enumeration over every token and every
+# block (which positions the query sees, where in the tail they sit, which summary
+# rows exist and lie wholly before the window); (3) planted off-by-one variants of
+# the oracle fail (1) or (2).
+def _from_tail_golden_failures(fn):
+    from tests.golden.make_golden import ACTIVE_CASES
+    import pathlib
+    g = np.load(pathlib.Path(__file__).resolve().parent / "golden" / "golden.npz")
+    bad = []
+    for name, _dt, _b, hq, hkv, t, _d, bs, w, layers, pos in ACTIVE_CASES:
+        for layer in layers:
+            lay = _layout(t, bs, layer, hkv=hkv, groups=hq // hkv)
+            tabs = fn(lay, kv_len=t, tail_start=0, num_summary_blocks=lay.num_blocks, tail_len=t,
+                      query_positions=torch.tensor(pos), W=w)
+            for tn, got in zip(("raw_idx", "raw_mask", "summary_idx", "summary_mask"), tabs):
+                want = torch.from_numpy(g[f"{name}/L{layer}/{tn}"])
+                if not torch.equal(got.to(want.dtype), want):
+                    bad.append((name, layer, tn))
+    return bad
+
+
+def _from_tail_enumerated(lay, *, kv_len, tail_start, num_summary_blocks, tail_len, query_positions, W):
+    """Per-query enumeration from the definitions, over every token and block."""
+    bs, n = lay.block_size, lay.num_blocks
+    k = lay.block_neighbors.shape[-1]
+    row_of = lay.block_neighbors[0].tolist()
+    tail = list(range(tail_start, tail_start + tail_len))          # absolute position per tail slot
+    out = []
+    for p in query_positions:
+        blk = min(p // bs, n - 1)
+        first = max(0, p - W + 1)
+        # raw slot j stands for absolute position first + j; it is live when that token
+        # exists, is causal for p and is held in the tail
+        seen = {}
+        for j in range(W):
+            a = first + j
+            if a <= p and a < kv_len and a in tail:
+                seen[j] = tail.index(a)
+        ridx = [seen.get(j, min(max(first + j - tail_start, 0), max(0, tail_len - 1))) for j in range(W)]
+        rmask = [j in seen for j in range(W)]
+        # summary rows: entries of the block's neighbour row, in row order, that name a
+        # pooled block other than the query's own whose every token precedes the window
+        picks = []
+        for nb in row_of[blk]:
+            if nb < 0 or nb == blk or nb >= num_summary_blocks:
+                continue
+            if all(t < first for t in range(nb * bs, (nb + 1) * bs)) and len(picks) < k:
+                picks.append(nb)
+        out.append((ridx, rmask, picks + [0] * (k - len(picks)), [True] * len(picks) + [False] * (k - len(picks))))
+    return out
+
+
+_FROM_TAIL_TINY = [
+    # (T, bs, layer, W, kv_len, tail_start, tail_len, num_summary_blocks)
+    (64, 4, 2, 4, 64, 52, 12, 13), (64, 4, 3, 6, 61, 40, 21, 9), (64, 4, 1, 4, 64, 60, 4, 15),
+    (40, 8, 2, 5, 40, 24, 16, 3), (40, 8, 1, 10, 37, 16, 21, 2), (33, 4, 4, 3, 33, 28, 5, 7),
+    (96, 8, 3, 12, 90, 72, 18, 1), (96, 8, 2, 9, 96, 0, 96, 12), (24, 4, 0, 4, 24, 8, 16, 0),
+    (64, 4, 2, 6, 64, 40, 16, 10), (48, 8, 1, 7, 45, 20, 19, 2),     # tails that end before kv_len
+]
+
+
+def _from_tail_enumeration_failures(fn):
+    bad = []
+    for T, bs, layer, W, kv_len, ts, tl, ns in _FROM_TAIL_TINY:
+        lay = _layout(T, bs, layer)
+        qps = [p for p in range(max(0, ts - W), kv_len)]
+        got = fn(lay, kv_len=kv_len, tail_start=ts, num_summary_blocks=ns, tail_len=tl,
+                 query_positions=torch.tensor(qps), W=W)
+        want = _from_tail_enumerated(lay, kv_len=kv_len, tail_start=ts, num_summary_blocks=ns, tail_len=tl,
+                                     query_positions=qps, W=W)
+        for r, (ri, rm, si, sm) in enumerate(want):
+            if (got[0][r].tolist() != ri or got[1][r].tolist() != rm or got[2][r].tolist() != si
+                    or got[3][r].tolist() != sm):
+                bad.append((T, bs, layer, W, kv_len, ts, tl, ns, qps[r]))
+    return bad
+
+
+def test_from_tail_reduces_to_reference_active_tables():
+    assert _from_tail_golden_failures(oa.active_tables_from_tail) == []
+
+
+def test_from_tail_equals_per_query_enumeration():
+    # the cases cover tails that start mid-window, tails that end before kv_len, pools
+    # that stop short of the routed partner (and an empty pool), ragged kv_len and a
+    # tail holding everything
+    assert _from_tail_enumeration_failures(oa.active_tables_from_tail) == []
+
+
+def test_from_tail_tables_gather_the_from_cache_attention():
+    # the tables drive one softmax over tail rows and pool rows; it equals the
+    # from-cache entry, which the reference's from_cache == active test pins
+    rng = np.random.default_rng(71)
+    B, H, Tk, dh, bs, W = 1, 2, 40, 8, 4, 5
+    lay = _layout(Tk, bs, 3, hkv=H)
+    k = torch.from_numpy(rng.standard_normal((B, H, Tk, dh), dtype=np.float32))
+    v = torch.from_numpy(rng.standard_normal((B, H, Tk, dh), dtype=np.float32))
+    q = torch.from_numpy(rng.standard_normal((B, H, 6, dh), dtype=np.float32))
+    cache = OracleCompressedKVCache(block_size=bs, local_window_tokens=W)
+    for s in range(0, Tk, 3):
+        cache.update_and_fetch(k[:, :, s:s + 3], v[:, :, s:s + 3])
+    tk_, tv_, ks, vs, ts, off = cache.get_compressed_state()
+    qp = torch.arange(off - 6, off)
+    ri, rm, si, sm = oa.active_tables_from_tail(lay, kv_len=off, tail_start=ts, num_summary_blocks=ks.shape[2],
+                                                tail_len=tk_.shape[2], query_positions=qp, W=W)
+    want = oa.from_cache(q, tk_, tv_, ks, vs, layout=lay, query_positions=qp, W=W, tail_start=ts, kv_len=off)
+    for r in range(6):
+        keys = torch.cat([tk_[0, :, ri[r][rm[r]]], ks[0, :, si[r][sm[r]]]], 1)
+        vals = torch.cat([tv_[0, :, ri[r][rm[r]]], vs[0, :, si[r][sm[r]]]], 1)
+        for h in range(H):
+            o = oa.dense_union_attention(q[0, h, r], keys[h], vals[h], scale=dh ** -0.5)
+            assert torch.allclose(o.float(), want[0, h, r], atol=1e-5)
+
+
+@pytest.mark.parametrize("old,new", [
+    ("nb >= num_summary_blocks", "nb > num_summary_blocks"),          # one pool row too many
+    ("(rpos < tail_end)", "(rpos <= tail_end)"),                      # one tail slot too many
+    ("(rpos >= tail_start)", "(rpos > tail_start)"),                  # first tail slot dropped
+    ("(rpos - tail_start)", "(rpos - tail_start + 1)"),               # tail slot index off by one
+    ("(nb + 1) * bs > start", "nb * bs > start"),                     # partner inside the window
+    ("start = max(0, p - W + 1)", "start = max(0, p - W)"),           # window one token wide too many
+])
+def test_from_tail_checks_catch_planted_mistakes(old, new):
+    import inspect
+    import textwrap
+    src = textwrap.dedent(inspect.getsource(oa.active_tables_from_tail))
+    assert src.count(old) == 1, old
+    ns = dict(vars(oa))
+    exec(compile(src.replace(old, new), "<planted>", "exec"), ns)
+    planted = ns["active_tables_from_tail"]
+    assert _from_tail_golden_failures(planted) or _from_tail_enumeration_failures(planted)
+
+
+def test_from_tail_rejects_empty_context():
+    lay = _layout(16, 4, 1)
+    with pytest.raises(ValueError):
+        oa.active_tables_from_tail(lay, kv_len=0, tail_start=0, num_summary_blocks=0, tail_len=0,
+                                   query_positions=torch.tensor([0]), W=4)

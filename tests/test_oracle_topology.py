@@ -130,3 +130,24 @@ def test_causal_shift_needs_every_layer():
     n = 64
     reach = _reach(n, tp.width(n) - 1, "causal_shift")
     assert any(not reach[b] >= set(range(b + 1)) for b in range(n))
+
+
+def test_partner_block_with_explicit_widths():
+    """butterfly_partner_block with an explicit width: bit_reversal reverses exactly the low
+    ``width`` bits (bna/topology/butterfly.py:45-49, 137-138), dropping higher bits, and width
+    0 reverses nothing.  Known answers worked by hand from those lines: block 5 = 0b101 over
+    2 bits is 0b01 -> 0b10, flip bit 0 -> 0b11, reversed 0b11 = 3; block 3 over 0 bits is
+    0, flipped to 1, reversed over 0 bits is 0.  Every rule agrees with the oracle."""
+    from butterfly_amd.topology import butterfly_partner_block
+
+    assert butterfly_partner_block(block_idx=5, bit_idx=0, num_blocks=8, partner_rule="bit_reversal", width=2) == 3
+    assert butterfly_partner_block(block_idx=3, bit_idx=0, num_blocks=8, partner_rule="bit_reversal", width=0) == 0
+    assert tp.bit_reverse(0b1011, 3) == 0b110 and tp.bit_reverse(0b1011, 0) == 0
+    for rule in tp.RULES:
+        for n in (1, 5, 8, 33, 300):
+            for w in range(0, 11):
+                for b in range(n):
+                    for bit in range(-1, w + 1):
+                        got = butterfly_partner_block(block_idx=b, bit_idx=bit, num_blocks=n, partner_rule=rule,
+                                                      width=w)
+                        assert got == tp.partner_block(b, bit, n, rule, w), (rule, n, w, b, bit)

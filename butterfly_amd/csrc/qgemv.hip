@@ -201,9 +201,9 @@ __global__ void __launch_bounds__(64) q4_gemv_kernel(Q4Args a) {
                               [] {});
 }
 
-// The residual add + RMSNorm of the input row inside the product: 512 threads; threads
-// 0..255 form h = x + residual and its normed row exactly as bfly_add_rms_norm does (into
-// LDS; workgroup 0 also writes h), then each of the 8 waves runs its sets on that row.
+// The residual add + RMSNorm of the input row inside the product: NW waves (8 or 12);
+// threads 0..255 form h = x + residual and its normed row exactly as bfly_add_rms_norm does
+// (into LDS; workgroup 0 also writes h), then each of the NW waves runs its sets on that row.
 // in_features = 256 PER.
 struct Q4NormArgs {
   const __bf16* x;
@@ -213,17 +213,18 @@ struct Q4NormArgs {
   float eps;
 };
 
-template <int NP, int R, bool kSilu, int PER>
-__global__ void __launch_bounds__(512) q4_norm_gemv_kernel(Q4Args a, Q4NormArgs nm) {
+template <int NP, int R, bool kSilu, int PER, int NW>
+__global__ void __launch_bounds__(64 * NW) q4_norm_gemv_kernel(Q4Args a, Q4NormArgs nm) {
+  static_assert(NW >= 4, "the row is formed by the first 256 threads");
   constexpr int DIM = 256 * PER;
   __shared__ __attribute__((aligned(16))) __bf16 xn[DIM];
   __shared__ float part[4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int64_t waves = (int64_t)gridDim.x * 8;
+  const int64_t waves = (int64_t)gridDim.x * NW;
   // the norm's inputs are requested before the weights, so that forming the row waits for them
   // alone and runs while the weights are in flight
   const RmsRowIn<PER> in = rms_row_load<PER>(nm.x, nm.residual, nm.weight, tid, tid < 256);
-  q4_sets<NP, R, kSilu, false>(a, lane, (int64_t)blockIdx.x * 8 + wave, waves, reinterpret_cast<const bf16x8*>(xn), [&] {
+  q4_sets<NP, R, kSilu, false>(a, lane, (int64_t)blockIdx.x * NW + wave, waves, reinterpret_cast<const bf16x8*>(xn), [&] {
     add_rmsnorm_row_from<PER>(in, nm.residual != nullptr, blockIdx.x == 0 ? nm.h_out : nullptr, xn, DIM, nm.eps, tid,
                               tid < 256, part);
     __syncthreads();   // the normed row is in LDS
@@ -262,18 +263,21 @@ void q4_dispatch(Q4Args a, int64_t in_features, int group, hipStream_t stream) {
   }
 }
 
-template <int NP, int R, bool kSilu, int PER>
+template <int NP, int R, bool kSilu, int PER, int NW = 8>
 void q4_norm_launch(Q4Args a, Q4NormArgs nm, hipStream_t stream) {
   constexpr int OUTS = kSilu ? R / 2 : R;
   a.n_sets = (a.n_out + OUTS - 1) / OUTS;
   const int64_t iters = (a.n_sets + kQ4MaxWaves - 1) / kQ4MaxWaves;
   const int64_t waves = (a.n_sets + iters - 1) / iters;
-  hipLaunchKernelGGL((q4_norm_gemv_kernel<NP, R, kSilu, PER>), dim3((unsigned)((waves + 7) / 8)), dim3(512), 0, stream,
-                     a, nm);
+  hipLaunchKernelGGL((q4_norm_gemv_kernel<NP, R, kSilu, PER, NW>), dim3((unsigned)((waves + NW - 1) / NW)),
+                     dim3(64 * NW), 0, stream, a, nm);
 }
 
 // in_features = 256 PER with PER in {8, 16, 24} (one to three pieces per lane; a fourth would
-// not fit the registers of two waves per SIMD); rows per set as q4_dispatch chooses them
+// not fit the registers of two waves per SIMD); rows per set as q4_dispatch chooses them.  The
+// SiLU form at four rows per set runs 12 waves per workgroup: cfg5's gate|up (3072 sets) is then
+// 256 workgroups, one per CU, where 8 waves gave 384 and half the CUs ran two (7.26 -> 6.35 us,
+// graph-replayed over 24 weight sets; other shapes measured no faster).
 template <bool kSilu>
 void q4_norm_dispatch(Q4Args a, Q4NormArgs nm, int64_t in_features, int group, hipStream_t stream) {
   a.pieces = (int)(in_features / kQ4PieceCodes);
@@ -282,7 +286,9 @@ void q4_norm_dispatch(Q4Args a, Q4NormArgs nm, int64_t in_features, int group, h
   const int64_t sets4 = (a.n_out + (kSilu ? 1 : 3)) / (kSilu ? 2 : 4);
   switch (in_features / 256) {
     case 8:
-      if (sets4 >= 2048)
+      if (sets4 >= 2048 && kSilu)
+        q4_norm_launch<1, 4, kSilu, 8, 12>(a, nm, stream);
+      else if (sets4 >= 2048)
         q4_norm_launch<1, 4, kSilu, 8>(a, nm, stream);
       else
         q4_norm_launch<1, 2, kSilu, 8>(a, nm, stream);

@@ -458,6 +458,14 @@ class CompressedKVCache:
         return 2 * b * h * d * e * (self.tail_size + self.summary_count)
 
     @property
+    def allocated_bytes(self) -> int:
+        """Device bytes the cache holds: the K and V rings at their full capacity and the K and
+        V summary pools (this build's physical layout; ``nbytes`` counts the valid slices)."""
+        if self._ring_k is None:
+            return 0
+        return sum(t.numel() * t.element_size() for t in (self._ring_k, self._ring_v, self._pool_k, self._pool_v))
+
+    @property
     def state(self) -> tuple[Any, Any, Any, Any]:
         self.sync()
         return self.keys, self.values, self.k_summary, self.v_summary

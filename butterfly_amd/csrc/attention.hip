@@ -8,7 +8,7 @@
 // both streams in one register tile under one running max and one running sum
 // is the online log-sum-exp merge of the two streams evaluated in place.
 //
-// Two kernels:
+// Three kernels:
 //  * attn_mfma_kernel<D>: bf16, head_dim 64/128/256, W <= 64, BS >= 64.
 //    Work unit = (batch, kv head, segment of 64-position chunks).  Keys of the
 //    current and previous 64-position page live in an LDS ring (K row-major,
@@ -16,6 +16,9 @@
 //    16 query positions and loops over the GQA group's query heads:
 //      S^T = K Q^T  and  O^T = V^T P^T  on v_mfma_f32_16x16x32_bf16,
 //    fp32 softmax with wavefront shuffles between the 4 lane groups.
+//  * attn_f32_tile_kernel<D>: fp32, head_dim 64/128, W <= 64, GQA groups of at
+//    most 4, BS a multiple of 16; one workgroup per (batch, kv head, 16-query
+//    tile), keys staged in LDS, both products on v_mfma_f32_16x16x4_f32.
 //  * attn_generic_kernel<T>: fp32 or bf16, any shape; one wave per
 //    (batch, kv head, query); lanes over keys for scores and over d for output.
 #include <stdlib.h>
@@ -232,6 +235,199 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(AttnArgs a) {
       for (int hh = 0; hh < nh; ++hh)
         reinterpret_cast<T*>(a.out)[((bi * a.hq + kvh * g + h0 + hh) * a.tq + r) * d + c] = from_f32<T>(acc[hh] * inv[hh]);
     }
+  }
+}
+
+// --------------------------------------------------------------------------------------------
+// fp32 tile kernel: contiguous query ranges, W <= 64, d in {64, 128}, GQA groups of at most 4
+// heads, block_size % 16 == 0, neighbour rows from a table with kcap <= 16.  One 256-thread
+// workgroup per (batch, kv head, 16-query tile at positions 16k .. 16k + 15); wave w computes
+// query head w of the group.  The tile's key rows: the window [k0, k0 + 16 nwt) covering
+// [q0 - W + 1, q0 + 15], then one 16-row tile of the routed summary rows of the tile's block in
+// neighbour-row order (slot j = the row's j-th entry; the 16 queries share the block because
+// block_size % 16 == 0).  Each thread requests its share of the K and the V rows together; K goes
+// to LDS first, V stays in registers until the scores are done and then overwrites K in the same
+// LDS buffer (50 KB at d = 128: three workgroups per CU).
+//   * S^T = K Q^T on v_mfma_f32_16x16x4_f32, the key tiles' accumulation chains interleaved.
+//     Lane l: r = l % 16, lane group lg = l / 16.  In the i-th step the lane supplies
+//     K[tile row r][DG lg + i] and Q[q0 + r][DG lg + i] (DG = D / 4) and receives the score of
+//     tile row 4 lg + jj for query q0 + r.  Every tile is computed (no branch joins inside the
+//     unrolled loops, which would copy the accumulators); unused tiles hold copies of valid rows
+//     and are masked.
+//   * Masks: window keys [max(p - W + 1, key_lo, 0), min(p, kv_len - 1)]; summary slot j is used
+//     when its neighbour n satisfies 0 <= n < block, n < nsum and (n + 1) BS <= the cut-off
+//     (block-level for one-shot prefill, token-level for active rows).
+//   * Softmax in fp32 over the lane's scores and the four lane groups (xor shuffles 16, 32).
+//   * O^T = V^T P^T, one MFMA per (key tile, jj, d tile e): the lane supplies
+//     V[tile row 4 lg + jj][E r + e] (E = D / 16) and its own probability for that key, and
+//     receives O[q0 + r][DG lg + E jj' + e] (jj' = 0..3).
+// Positions are 32-bit (the host sends only caches below 2^30 rows here).
+constexpr int kF32MaxKcap = 16;
+constexpr int kF32WinTiles = 5;        // (64 - 1 + 15) / 16 + 1
+constexpr int kF32Tiles = kF32WinTiles + 1;
+constexpr int kF32Rows = 16 * kF32Tiles;
+
+template <int D>
+__global__ void __launch_bounds__(256, 3) attn_f32_tile_kernel(AttnArgs a, int tile0, int ntiles, int per_xcd) {
+  constexpr int DG = D / 4, E = D / 16, KP = D + 4;        // LDS rows padded by 16 bytes
+  constexpr int PER_ROW = D / 4;                            // 16-byte pieces per row
+  constexpr int WIN_PIECES = 16 * kF32WinTiles * PER_ROW;
+  constexpr int STAGE = (kF32Rows * PER_ROW + 255) / 256;   // pieces of K (and of V) per thread
+  static_assert(kF32Rows * PER_ROW % 256 == 0, "every thread stages the same number of pieces");
+  __shared__ __attribute__((aligned(16))) float kvl[kF32Rows * KP];   // K, then V
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // workgroups are dispatched to the 8 XCDs round-robin: XCD x = blockIdx % 8 takes the items
+  // x per_xcd .. x per_xcd + per_xcd - 1, consecutive tiles of one (batch, kv head), which share
+  // most of their window rows in that XCD's L2
+  const int item = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (item >= ntiles * (int)(a.batch * a.hkv)) return;   // the whole workgroup
+  const int tile = tile0 + item % ntiles;
+  const int bh = item / ntiles;
+  const int64_t bi = bh / a.hkv;
+  const int kvh = bh % a.hkv;
+  const int gsz = a.hq / a.hkv;
+  const int r = lane & 15, lg = lane >> 4;
+  const int q0 = tile * 16;
+  const int p = q0 + r;                                     // this lane's query (column r)
+  const int qlo = (int)a.q_pos0, qhi = (int)(a.q_pos0 + a.tq);
+  const bool qok = p >= qlo && p < qhi && w < gsz;
+  const int qrow = p >= qlo && p < qhi ? p - qlo : 0;
+  const int key_lo = (int)a.key_lo, kv_len = (int)a.kv_len, W = a.W, bs = a.bs;
+  // the workgroup's window: [q0 - W + 1, q0 + 15] clipped to the keys that exist
+  const int wlo = max(max(q0 - W + 1, key_lo), 0);
+  const int whi = min(q0 + 15, kv_len - 1);
+  const int nwt = (W - 1 + 15) / 16 + 1;                    // window tiles
+  const int kstart = q0 - 16 * (nwt - 1);
+  const int blk = (int)clamp_block(q0, a);
+  const int hq_i = kvh * gsz + (w < gsz ? w : 0);           // a wave past the group repeats head 0
+  const float* kb = reinterpret_cast<const float*>(a.k) + (bi * a.hkv + kvh) * a.kv_rows * D;
+  const float* vb = reinterpret_cast<const float*>(a.v) + (bi * a.hkv + kvh) * a.kv_rows * D;
+  const float* ksb = reinterpret_cast<const float*>(a.ks) + (bi * a.hkv + kvh) * a.pool_rows * D;
+  const float* vsb = reinterpret_cast<const float*>(a.vs) + (bi * a.hkv + kvh) * a.pool_rows * D;
+  // summary slot j's pool row, or -1
+  auto slot_row = [&](int j) -> int {
+    if (j >= a.kcap) return -1;
+    const int n = a.nbr[(int64_t)blk * a.kcap + j];
+    return n >= 0 && n < blk && n < a.nsum ? n : -1;
+  };
+  const float* qp = reinterpret_cast<const float*>(a.q) + ((bi * a.hq + hq_i) * a.tq + qrow) * D + DG * lg;
+  f32x4 qv[DG / 4];
+#pragma unroll
+  for (int c = 0; c < DG / 4; ++c) qv[c] = *reinterpret_cast<const f32x4*>(qp + 4 * c);
+  // pieces 0 .. WIN_STAGE - 1 of every thread are window rows, the rest summary rows
+  constexpr int WIN_STAGE = WIN_PIECES / 256;
+  static_assert(WIN_PIECES % 256 == 0, "window pieces split evenly over the threads");
+  f32x4 kx[STAGE], vx[STAGE];
+#pragma unroll
+  for (int u = 0; u < WIN_STAGE; ++u) {
+    const int idx = tid + 256 * u;
+    const int row = idx / PER_ROW, c4 = idx - row * PER_ROW;
+    const int pos = min(max(kstart + row, wlo), whi);     // rows past the window repeat its ends
+    const int64_t off = (a.ring ? posmod(pos, a.ring) : pos - key_lo) * D + 4 * c4;
+    kx[u] = *reinterpret_cast<const f32x4*>(kb + off);
+    vx[u] = *reinterpret_cast<const f32x4*>(vb + off);
+  }
+#pragma unroll
+  for (int u = WIN_STAGE; u < STAGE; ++u) {
+    const int idx = tid + 256 * u - WIN_PIECES;
+    const int row = idx / PER_ROW, c4 = idx - row * PER_ROW;
+    const int n = slot_row(row);
+    const int64_t off = (int64_t)(n < 0 ? 0 : n) * D + 4 * c4;   // unused slots read pool row 0
+    kx[u] = *reinterpret_cast<const f32x4*>(ksb + off);
+    vx[u] = *reinterpret_cast<const f32x4*>(vsb + off);
+  }
+#pragma unroll
+  for (int u = 0; u < STAGE; ++u) {
+    const int idx = tid + 256 * u;
+    const int row = idx / PER_ROW, c4 = idx - row * PER_ROW;
+    *reinterpret_cast<f32x4*>(kvl + row * KP + 4 * c4) = kx[u];
+  }
+  // this lane's summary slots 4 lg + jj
+  int sn[4];
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) sn[jj] = slot_row(4 * lg + jj);
+  const int cut = max(a.token_cutoff ? p - W + 1 : blk * bs - W + 1, 0);
+  const int klo = max(max(p - W + 1, key_lo), 0), khi = min(p, kv_len - 1);
+  __syncthreads();   // K rows in LDS
+
+  f32x4 c[kF32Tiles];
+#pragma unroll
+  for (int t = 0; t < kF32Tiles; ++t) c[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < DG; i += 4) {
+#pragma unroll
+    for (int t = 0; t < kF32Tiles; ++t) {
+      const f32x4 k4 = *reinterpret_cast<const f32x4*>(kvl + (16 * t + r) * KP + DG * lg + i);
+      const f32x4 q4 = qv[i / 4];
+#pragma unroll
+      for (int x = 0; x < 4; ++x) c[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[x], q4[x], c[t], 0, 0, 0);
+    }
+  }
+  float sc[kF32Tiles][4];
+  float m = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < kF32Tiles; ++t)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      bool ok;
+      if (t < kF32WinTiles) {
+        const int kpos = kstart + 16 * t + 4 * lg + jj;
+        ok = t < nwt && kpos >= klo && kpos <= khi;
+      } else {
+        ok = sn[jj] >= 0 && (sn[jj] + 1) * bs <= cut;
+      }
+      sc[t][jj] = ok ? c[t][jj] * a.scale : -INFINITY;
+      m = fmaxf(m, sc[t][jj]);
+    }
+  m = fmaxf(m, __shfl_xor(m, 16));
+  m = fmaxf(m, __shfl_xor(m, 32));
+  if (m == -INFINITY) m = 0.f;   // a column with nothing to attend (outside the query range)
+  float l = 0.f;
+#pragma unroll
+  for (int t = 0; t < kF32Tiles; ++t)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      sc[t][jj] = expf(sc[t][jj] - m);
+      l += sc[t][jj];
+    }
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+
+  __syncthreads();   // every wave is done with K
+#pragma unroll
+  for (int u = 0; u < STAGE; ++u) {
+    const int idx = tid + 256 * u;
+    const int row = idx / PER_ROW, c4 = idx - row * PER_ROW;
+    *reinterpret_cast<f32x4*>(kvl + row * KP + 4 * c4) = vx[u];
+  }
+  __syncthreads();   // V rows in LDS
+
+  f32x4 acc[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < kF32Tiles; ++t) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const float* vp = kvl + (16 * t + 4 * lg + jj) * KP + E * r;
+#pragma unroll
+      for (int e = 0; e < E; e += 4) {
+        const f32x4 v4 = *reinterpret_cast<const f32x4*>(vp + e);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) acc[e + x] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[x], sc[t][jj], acc[e + x], 0, 0, 0);
+      }
+    }
+  }
+  if (qok) {
+    // acc[e][jj'] is O[q0 + r][DG lg + E jj' + e]
+    const float inv = 1.f / fmaxf(l, 1e-9f);
+    float* op = reinterpret_cast<float*>(a.out) + ((bi * a.hq + hq_i) * a.tq + qrow) * D + DG * lg;
+#pragma unroll
+    for (int jp = 0; jp < 4; ++jp)
+#pragma unroll
+      for (int e = 0; e < E; e += 4)
+        *reinterpret_cast<f32x4*>(op + E * jp + e) =
+            f32x4{acc[e][jp] * inv, acc[e + 1][jp] * inv, acc[e + 2][jp] * inv, acc[e + 3][jp] * inv};
   }
 }
 
@@ -916,6 +1112,20 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
         default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
       }
     }
+  } else if (dtype == BFLY_DTYPE_F32 && contiguous && a.nbr != nullptr && a.W <= 64 && a.bs % 16 == 0 &&
+             a.hq / a.hkv <= 4 &&
+             (a.d == 64 || a.d == 128) && a.kcap <= kF32MaxKcap && a.kv_len + 2 * kF32Rows < (1 << 30) &&
+             a.nblocks * (int64_t)a.bs < (1 << 30) && a.q_pos0 + a.tq < (1 << 30) && a.pool_rows > 0) {
+    const int64_t tile0 = floordiv(a.q_pos0, 16);
+    const int64_t ntiles = floordiv(a.q_pos0 + a.tq - 1, 16) - tile0 + 1;
+    const int64_t items = ntiles * a.batch * a.hkv;
+    const int64_t per_xcd = (items + 7) / 8;
+    BFLY_CHECK_ARG(8 * per_xcd <= INT32_MAX, "%s: grid too large", what);
+    const dim3 grid((unsigned)(8 * per_xcd));
+    if (a.d == 64)
+      hipLaunchKernelGGL(attn_f32_tile_kernel<64>, grid, dim3(256), 0, stream, a, (int)tile0, (int)ntiles, (int)per_xcd);
+    else
+      hipLaunchKernelGGL(attn_f32_tile_kernel<128>, grid, dim3(256), 0, stream, a, (int)tile0, (int)ntiles, (int)per_xcd);
   } else {
     BFLY_CHECK_ARG(a.d <= kGenericMaxD, "%s: head_dim=%d > %d", what, a.d, kGenericMaxD);
     BFLY_CHECK_ARG(a.W + a.kcap <= kGenericMaxKeys, "%s: window + kcap > %d", what, kGenericMaxKeys);

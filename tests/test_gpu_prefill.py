@@ -134,3 +134,57 @@ def test_prefill_custom_scale_and_errors():
     lay3, _ = _layouts(511, 128, 2, 4, 1)
     with pytest.raises(ValueError):
         bf.compressed_butterfly_attention(q.cuda(), k.cuda(), v.cuda(), layout=lay3, local_window_tokens=64)
+
+
+# fp32 tile kernel (attn_f32_tile_kernel): W <= 64, d 64 / 128, GQA groups of at most 4, block size a
+# multiple of 16; ragged lengths, windows shorter than a tile, batch 2
+F32_TILE_CASES = [
+    # b, hq, hkv, t, d, bs, W, layer
+    (2, 6, 2, 333, 64, 16, 17, 3),
+    (1, 3, 3, 500, 128, 32, 1, 2),
+    (1, 4, 1, 777, 128, 64, 64, 5),
+    (2, 8, 2, 1000, 128, 128, 64, 2),
+    (1, 2, 2, 100, 64, 16, 64, 1),
+    (1, 8, 4, 4099, 128, 128, 48, 7),
+]
+
+
+@pytest.mark.parametrize("case", F32_TILE_CASES, ids=lambda c: "-".join(str(x) for x in c))
+def test_f32_tile_prefill_cases(case):
+    b, hq, hkv, t, d, bs, W, layer = case
+    q, k, v = _inputs(t + 11 * d, b, hq, hkv, t, d, torch.float32)
+    lay, ref_lay = _layouts(t, bs, hkv, hq // hkv, layer)
+    y, _ = bf.compressed_butterfly_attention(q.cuda(), k.cuda(), v.cuda(), layout=lay, local_window_tokens=W)
+    want = oa.prefill(q, k, v, layout=ref_lay, W=W)
+    assert (y.cpu() - want).abs().max().item() <= F32_MAX_ABS
+
+
+@pytest.mark.parametrize("d,W,bs,step,hq,hkv", [(128, 64, 128, 100, 8, 2), (64, 20, 16, 37, 4, 4),
+                                                (128, 64, 64, 384, 4, 1)])
+def test_f32_tile_ring_chunks_match_active(d, W, bs, step, hq, hkv):
+    """Chunks attended from the device ring (fp32 tile kernel, ring mode): chunk starts off the
+    16-position tiles, the ring wrapping, token-level summary cut-off; each chunk against the
+    oracle's active rows over the full keys."""
+    from butterfly_amd import CompressedKVCache
+
+    b, layer, total = 2, 6, 2000
+    q, k, v = _inputs(d + step, b, hq, hkv, total, d, torch.float32)
+    cache = CompressedKVCache(block_size=bs, local_window_tokens=W, max_kv_size=total, max_chunk_size=512)
+    pos = 0
+    while pos < total:
+        n = min(step, total - pos)
+        kc, vc, qc = k[:, :, pos:pos + n].cuda(), v[:, :, pos:pos + n].cuda(), q[:, :, pos:pos + n].cuda()
+        cache.update(kc, vc)
+        kv_len = pos + n
+        lay, ref_lay = _layouts(kv_len, bs, hkv, hq // hkv, layer)
+        if pos == 0:
+            got, _ = bf.compressed_butterfly_attention(qc, kc, vc, layout=lay, local_window_tokens=W)
+            want = oa.prefill(q[:, :, :n], k[:, :, :n], v[:, :, :n], layout=ref_lay, W=W)
+        else:
+            got = bf.compressed_butterfly_attention_cached(qc, cache, layout=lay, local_window_tokens=W)
+            want = oa.active(q[:, :, pos:kv_len], k[:, :, :kv_len], v[:, :, :kv_len], layout=ref_lay,
+                             query_positions=torch.arange(pos, kv_len), W=W)
+        err = (got.cpu() - want).abs().max().item()
+        assert err <= F32_MAX_ABS, (pos, err)
+        pos = kv_len
+    assert cache.tail_capacity < total          # the ring wrapped

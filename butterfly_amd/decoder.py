@@ -605,11 +605,13 @@ class Decoder(nn.Module):
 
     @torch.no_grad()
     def greedy_graph_from_logits(self, logits: torch.Tensor, t: int, new_tokens: int, caches: List,
-                                 timed: bool = False) -> torch.Tensor:
+                                 timed: bool = False, on_step: Optional[Callable[[int], None]] = None) -> torch.Tensor:
         """The decode part of ``greedy_graph`` after a prefill of ``t`` tokens that produced ``logits``.
 
         With ``timed`` the replays are bracketed by device synchronisations and
-        their wall time is kept in ``self.last_graph_decode_s``."""
+        their wall time is kept in ``self.last_graph_decode_s``.  ``on_step(i)`` is called after
+        replay ``i`` (the step at position ``t + 1 + i``) with the device synchronised, for
+        inspection of what the replay wrote."""
         dev = logits.device
         b = logits.shape[0]
         for i, (layer, c) in enumerate(zip(self.layers, caches)):
@@ -656,8 +658,11 @@ class Decoder(nn.Module):
             if timed:
                 torch.cuda.synchronize(dev)
             t0 = time.perf_counter()
-            for _ in range(new_tokens - 2):
+            for i in range(new_tokens - 2):
                 graph.replay()
+                if on_step is not None:
+                    torch.cuda.synchronize(dev)
+                    on_step(i)
             if timed:
                 torch.cuda.synchronize(dev)
             self.last_graph_decode_s = time.perf_counter() - t0

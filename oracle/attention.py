@@ -149,8 +149,11 @@ def block_mean(x: torch.Tensor, *, seq_len: int, block_size: int, num_blocks: in
 
 
 # --------------------------------------------------------------------------- one-shot prefill
-def prefill(q, k, v, *, layout, W: int, block_chunk_size: int = 0):
-    """One-shot compressed prefill.  attention_wayfinder_permute.py:1046-1122."""
+def prefill(q, k, v, *, layout, W: int, block_chunk_size: int = 0, k_summary=None, v_summary=None):
+    """One-shot compressed prefill.  attention_wayfinder_permute.py:1046-1122.
+
+    ``k_summary``/``v_summary`` optionally replace the block means computed from k/v (a
+    float32 evaluation over bf16 inputs then keeps the bf16 summaries that path pools)."""
     b, hq, t, d = q.shape
     hkv = k.shape[1]
     if k.shape[2] != t or v.shape[2] != t:
@@ -158,8 +161,8 @@ def prefill(q, k, v, *, layout, W: int, block_chunk_size: int = 0):
     bs, n = layout.block_size, layout.num_blocks
     raw_idx, raw_mask, sidx, smask = prefill_tables(layout, T=t, W=W)
     slots, ks = raw_idx.shape[-1], sidx.shape[-1]
-    ksum = block_mean(k, seq_len=t, block_size=bs, num_blocks=n)
-    vsum = block_mean(v, seq_len=t, block_size=bs, num_blocks=n)
+    ksum = block_mean(k, seq_len=t, block_size=bs, num_blocks=n) if k_summary is None else k_summary
+    vsum = block_mean(v, seq_len=t, block_size=bs, num_blocks=n) if v_summary is None else v_summary
     pad = n * bs - t
     qb = (F.pad(q, (0, 0, 0, pad)) if pad > 0 else q).view(b, hq, n, bs, d)
     c = n if block_chunk_size <= 0 else min(block_chunk_size, n)

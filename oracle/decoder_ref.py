@@ -59,3 +59,52 @@ def swap_to_oracle(model, cfg, layer_indices=None):
             partner_count=cfg.block_partner_count, partner_rule=cfg.block_partner_rule)
         out.append(i)
     return out
+
+
+# --------------------------------------------------------------------------- rounding points
+def q4_weight_fp32(layer) -> torch.Tensor:
+    """The layer's weights ``code * scale + bias`` in fp32, not rounded to bf16: what the GPU's
+    one-row product from the 4-bit codes multiplies by (its factorised sum is this product
+    up to fp32 summation order).  Cached on the layer."""
+    w = getattr(layer, "_oracle_w32", None)
+    if w is None:
+        out_f, group = layer.packed.shape[0], layer.group
+        q = torch.stack([layer.packed & 0xF, layer.packed >> 4], dim=-1).view(out_f, -1).float()
+        w = (q.view(out_f, -1, group) * layer.scale.float().unsqueeze(-1)
+             + layer.bias.float().unsqueeze(-1)).view(out_f, -1)
+        layer._oracle_w32 = w
+    return w
+
+
+def q4_row(x: torch.Tensor, layer) -> torch.Tensor:
+    """One activation row through a 4-bit layer with the GPU decode step's rounding points:
+    fp32 weights from the codes, fp32 accumulation, one rounding of each output to bf16
+    (``bfly_q4_gemv``).  Multi-row products on the GPU run over the bf16-dequantised weights, as
+    the layer's own forward does on the CPU."""
+    y = x.reshape(1, -1).float() @ q4_weight_fp32(layer).t()
+    return y.to(x.dtype).view(*x.shape[:-1], y.shape[-1])
+
+
+def match_gpu_rounding(model) -> None:
+    """Give a CPU copy of ``butterfly_amd.decoder.Decoder`` the GPU's rounding points: every
+    one-row product (a decode step's projections, the last position's lm_head) from the 4-bit
+    codes in fp32 (``q4_row``); prefill products stay on the bf16-dequantised weights."""
+    import types
+
+    from butterfly_amd.decoder import QuantLinear
+
+    def forward(self, x):
+        if x.numel() == x.shape[-1] and not x.is_cuda:
+            return q4_row(x, self)
+        return type(self).forward(self, x)
+
+    for m in model.modules():
+        if isinstance(m, QuantLinear):
+            m.forward = types.MethodType(forward, m)
+
+    def logits(self, h):
+        if h.numel() == h.shape[-1] and not h.is_cuda:
+            return q4_row(h, self.lm_head)
+        return type(self)._logits(self, h)
+
+    model._logits = types.MethodType(logits, model)

@@ -96,3 +96,34 @@ def test_rope_table_rows_select_the_position():
     cos, sin = rope_cos_sin(torch.arange(10), 8, 1e4)
     c, s = RopeTable(cos, sin, torch.tensor([3])).rows()
     assert torch.equal(c, cos[3:4]) and torch.equal(s, sin[3:4])
+
+
+def test_cpu_reference_one_row_products_take_the_gpu_rounding_points():
+    """oracle.decoder_ref.match_gpu_rounding: a one-row product runs over the fp32 weights
+    code * scale + bias (which round to the layer's bf16 weights), accumulates in fp32 and
+    rounds once, i.e. equals the float64 product rounded to bf16 up to fp32 summation order;
+    multi-row products and the layer's own forward are untouched."""
+    from butterfly_amd.decoder import QuantLinear
+    from oracle.decoder_ref import match_gpu_rounding, q4_row, q4_weight_fp32
+
+    g = torch.Generator().manual_seed(4)
+    layer = QuantLinear(2048, 96, generator=g)
+    w32 = q4_weight_fp32(layer)
+    assert torch.equal(w32.to(torch.bfloat16), layer.weight)          # the bf16 weights are its rounding
+    assert not torch.equal(w32, layer.weight.float())                # and it keeps bits they drop
+    x = torch.randn(1, 1, 2048, generator=g).bfloat16()
+    y = q4_row(x, layer)
+    exact = (x.double().view(1, -1) @ w32.double().t()).view(1, 1, -1)
+    assert torch.equal(y, exact.to(torch.bfloat16)) or \
+        ((y.double() - exact).abs() <= exact.abs() * 2 ** -8 + 1e-30).all()
+    model = Decoder(DecoderConfig(vocab_size=256, hidden_size=256, num_layers=1, num_heads=2, num_kv_heads=1,
+                                  head_dim=128, intermediate_size=512), seed=1, device="cpu")
+    rows = torch.randn(1, 3, 256, generator=g).bfloat16()
+    before = model.layers[0].mlp.gate_proj(rows)
+    match_gpu_rounding(model)
+    q = model.layers[0].self_attn.q_proj
+    one = rows[:, :1]
+    assert torch.equal(q(one), q4_row(one, q))
+    assert torch.equal(model.layers[0].mlp.gate_proj(rows), before)  # three rows: the bf16 GEMM
+    h = torch.randn(1, 256, generator=g).bfloat16()
+    assert torch.equal(model._logits(h), q4_row(h, model.lm_head))

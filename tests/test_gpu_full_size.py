@@ -9,11 +9,15 @@
   device-counter decode step captured 64 times in one HIP graph (as the benchmark runs it)
   for B = 1, 8 and 32; every step against ``oracle.from_cache`` over the oracle cache.
 * cfg5: the 24-layer, hidden-2048 decoder with a 32768-token prompt: every swapped layer's
-  attention output against the oracle on the same q/k/v, for the prefill and decode steps.
+  attention output against the oracle on the same q/k/v, for the prefill and decode steps with
+  host counters, and for the graph-replayed decode steps (``bfly_decode_step_qk_norm`` inside the
+  captured step the benchmark times).
 
-Tolerances are the north_star's bf16 bar (2e-2 max-abs, 1e-2 relative L2); for the cfg5
-decoder, whose attention outputs reach several units, the max-abs bar is scaled by the
-output's largest magnitude.
+Tolerances are the north_star's bf16 bar (2e-2 max-abs, 1e-2 relative L2).  The cfg5 decoder's
+attention outputs reach several units, where one bf16 step of the output is 2^-5 = 0.031: there
+the bar is held against the oracle evaluated in float32 (on the same bf16 q/k/v and the same bf16
+summary rows), i.e. the error of the kernel plus the rounding of its own output; the difference
+from the oracle's bf16 output, which adds the oracle's rounding, is printed beside it.
 """
 from __future__ import annotations
 
@@ -175,11 +179,8 @@ def test_cfg5_every_layer_matches_oracle_at_32768(monkeypatch):
         history[layer] = (kh, vh)
         tq, tk = q.shape[2], kh.shape[2]
         lay = _layout(tk, cfg.num_kv_heads, cfg.num_heads // cfg.num_kv_heads, layer)
-        if tq == tk:
-            want = oa.prefill(q.cpu(), kh, vh, layout=lay, W=W)
-        else:
-            want = oa.active(q.cpu(), kh, vh, layout=lay, query_positions=torch.arange(tk - tq, tk), W=W)
-        results.append((layer, tk, *_err(out, want), want.float().abs().max().item()))
+        want, want32 = _oracle_rows(q.cpu(), kh, vh, lay, tq, W)
+        results.append((layer, tk, *_err(out, want32), want.float().abs().max().item(), _err(out, want)[0]))
         return out
 
     monkeypatch.setattr(bf.ButterflyAttentionCore, "__call__", checked)
@@ -194,9 +195,94 @@ def test_cfg5_every_layer_matches_oracle_at_32768(monkeypatch):
         logits = model.forward(tok, caches, pos)
         pos += 1
     assert len(results) == cfg.num_layers * (1 + steps)
-    # The decoder's attention values are not N(0,1): deeper layers reach |o| of several units,
-    # where one bf16 step exceeds 2e-2, so the max-abs bar scales with the output's magnitude.
-    for layer, tk, err, rel, amax in results:
-        assert err <= MAX_ABS * max(1.0, amax) and rel <= REL_L2, (layer, tk, err, rel, amax)
-    print(f"cfg5: {len(results)} layer calls (prefill + {steps} decode steps), worst max_abs="
-          f"{max(r[2] for r in results):.3e} rel_l2={max(r[3] for r in results):.3e}", flush=True)
+    for layer, tk, err, rel, amax, err_bf16 in results:
+        assert err <= MAX_ABS and rel <= REL_L2, (layer, tk, err, rel, amax)
+    print(f"cfg5: {len(results)} layer calls (prefill + {steps} decode steps), worst vs the fp32 oracle "
+          f"max_abs={max(r[2] for r in results):.3e} rel_l2={max(r[3] for r in results):.3e}; vs the oracle's "
+          f"bf16 output max_abs={max(r[5] for r in results):.3e} (largest |o| {max(r[4] for r in results):.2f})",
+          flush=True)
+
+
+def _oracle_rows(q, kh, vh, lay, tq, W):
+    """The oracle's rows for the last ``tq`` positions of ``kh``/``vh``: its bf16 output, and the
+    same evaluated in float32 over the bf16 inputs and the bf16 summary rows (block means
+    rounded as the kernels pool them)."""
+    tk = kh.shape[2]
+    ks = oa.block_mean(kh, seq_len=tk, block_size=128, num_blocks=lay.num_blocks)
+    vs = oa.block_mean(vh, seq_len=tk, block_size=128, num_blocks=lay.num_blocks)
+    if tq == tk:
+        want = oa.prefill(q, kh, vh, layout=lay, W=W)
+        want32 = oa.prefill(q.float(), kh.float(), vh.float(), layout=lay, W=W, k_summary=ks.float(),
+                            v_summary=vs.float())
+    else:
+        qp = torch.arange(tk - tq, tk)
+        want = oa.active(q, kh, vh, layout=lay, query_positions=qp, W=W)
+        want32 = oa.active(q.float(), kh.float(), vh.float(), layout=lay, query_positions=qp, W=W,
+                           k_summary=ks.float(), v_summary=vs.float())
+    return want, want32
+
+
+@pytest.mark.timeout(900)
+def test_cfg5_graph_replayed_steps_match_oracle_at_32768(monkeypatch):
+    """The decode steps the benchmark times: after a 32768-token prompt, every layer's
+    ``bfly_decode_step_qk_norm`` inside the captured greedy step (replayed from one HIP graph,
+    device counters) against the oracle's active row over that layer's full key history."""
+    from butterfly_amd.decoder import Decoder, DecoderConfig
+
+    cfg = DecoderConfig()
+    prompt_len, new_tokens, W = 32768, 6, 64
+    model = Decoder(cfg, seed=5, device="cuda")
+    assert bf.swap_qwen_attention_with_butterfly(model, cfg=bf.compressed_butterfly_config()) == list(range(24))
+    caches = [None] * cfg.num_layers
+    bf.install_compressed_kv_caches(model, caches, block_size=128, local_window_tokens=W,
+                                    max_kv_size=prompt_len + 64, max_chunk_size=prompt_len + 64)
+    prompt_kv, rows, bufs = {}, {l: [] for l in range(cfg.num_layers)}, {}
+    real_call = bf.ButterflyAttentionCore.__call__
+
+    def recording(core, q, k, v, cache=None, qk_norm=None):
+        out = real_call(core, q, k, v, cache, qk_norm=qk_norm)
+        layer = core.layer_idx
+        if q.shape[2] > 1:                                     # the prompt: normed, rotated k and v
+            prompt_kv[layer] = (k.cpu(), v.cpu())
+            return out
+        assert qk_norm is not None, "a device-counter decode step takes the raw q|k|v rows"
+        if layer not in bufs:                                  # the eager first step, before capture
+            bufs[layer] = [torch.empty_like(t) for t in (q, k, v, out)]
+        for b_, t_ in zip(bufs[layer], (q, k, v, out)):
+            b_.copy_(t_)                                       # recorded into the graph as well
+        if not torch.cuda.is_current_stream_capturing():
+            rows[layer].append([t_.cpu() for t_ in bufs[layer]])
+        return out
+
+    monkeypatch.setattr(bf.ButterflyAttentionCore, "__call__", recording)
+    prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=torch.Generator().manual_seed(9)).cuda()
+    logits = model.forward(prompt, caches, 0)
+    torch.cuda.synchronize()
+
+    def on_step(i):
+        for layer in range(cfg.num_layers):
+            rows[layer].append([t_.cpu() for t_ in bufs[layer]])
+        print(f"cfg5 graph replay {i} recorded", flush=True)
+
+    model.greedy_graph_from_logits(logits, prompt_len, new_tokens, caches, on_step=on_step)
+    monkeypatch.undo()
+    steps = new_tokens - 1
+    worst = [0.0, 0.0, 0.0]
+    for layer in range(cfg.num_layers):
+        assert len(rows[layer]) == steps
+        base = model.layers[layer].self_attn.base
+        kh, vh = prompt_kv[layer]
+        for s_, (qr, kr, vr, out) in enumerate(rows[layer]):
+            p = prompt_len + s_
+            # the raw rows normed and rotated by the separate launch (bit-identical to the fused step)
+            qkv = torch.cat([qr.view(-1), kr.view(-1), vr.view(-1)]).view(1, 1, -1).cuda()
+            q, k, v = base.heads(qkv, torch.tensor([p], device="cuda"))
+            kh, vh = torch.cat([kh, k.cpu()], 2), torch.cat([vh, v.cpu()], 2)
+            lay = _layout(p + 1, cfg.num_kv_heads, cfg.num_heads // cfg.num_kv_heads, layer)
+            want, want32 = _oracle_rows(q.cpu(), kh, vh, lay, 1, W)
+            err, rel = _err(out, want32)
+            assert err <= MAX_ABS and rel <= REL_L2, (layer, p, err, rel)
+            worst = [max(worst[0], err), max(worst[1], rel), max(worst[2], _err(out, want)[0])]
+    print(f"cfg5 graph-replayed: {cfg.num_layers} layers x {steps} steps (1 eager + {steps - 1} replays), worst vs "
+          f"the fp32 oracle max_abs={worst[0]:.3e} rel_l2={worst[1]:.3e}; vs its bf16 output {worst[2]:.3e}",
+          flush=True)

@@ -240,41 +240,95 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(AttnArgs a) {
 
 // --------------------------------------------------------------------------------------------
 // fp32 tile kernel: contiguous query ranges, W <= 64, d in {64, 128}, GQA groups of at most 4
-// heads, block_size % 16 == 0, neighbour rows from a table with kcap <= 16.  One 256-thread
+// heads, block_size % 16 == 0, neighbour rows from a table with 1 <= kcap <= 16.  One 256-thread
 // workgroup per (batch, kv head, 16-query tile at positions 16k .. 16k + 15); wave w computes
 // query head w of the group.  The tile's key rows: the window [k0, k0 + 16 nwt) covering
 // [q0 - W + 1, q0 + 15], then one 16-row tile of the routed summary rows of the tile's block in
 // neighbour-row order (slot j = the row's j-th entry; the 16 queries share the block because
-// block_size % 16 == 0).  Each thread requests its share of the K and the V rows together; K goes
-// to LDS first, V stays in registers until the scores are done and then overwrites K in the same
-// LDS buffer (50 KB at d = 128: three workgroups per CU).
-//   * S^T = K Q^T on v_mfma_f32_16x16x4_f32, the key tiles' accumulation chains interleaved.
-//     Lane l: r = l % 16, lane group lg = l / 16.  In the i-th step the lane supplies
-//     K[tile row r][DG lg + i] and Q[q0 + r][DG lg + i] (DG = D / 4) and receives the score of
-//     tile row 4 lg + jj for query q0 + r.  Every tile is computed (no branch joins inside the
-//     unrolled loops, which would copy the accumulators); unused tiles hold copies of valid rows
-//     and are masked.
+// block_size % 16 == 0).
+//   * fp32 products on bf16 MFMA (v_mfma_f32_16x16x32_bf16): every fp32 operand x is split into
+//     three bf16 parts by truncation, x = hi + mid + lo exactly (hi keeps the sign, exponent and
+//     top 7 stored mantissa bits of x, mid those of x - hi, and lo = x - hi - mid has at most 8
+//     significant bits), and a product a b is summed in the fp32 accumulator as the six part
+//     products ah bh + ah bm + am bh + ah bl + am bm + al bh, each exact in fp32 (the three
+//     dropped ones are below 2^-24 of |a b|): the "bf16x6" scheme of Henry, Tang and Heinecke,
+//     "Leveraging the bfloat16 artificial intelligence datatype for higher-precision
+//     computations" (ARITH 2019).  Six 16x16x32 bf16 MFMAs (16 cycles each) replace eight
+//     16x16x4 fp32 ones (32 cycles each).
+//   * Requests, in this order: the block's neighbour-row entries (lane j < 16 of every wave holds
+//     slot j's pool row), Q, the window's K rows tile by tile, then, once the entries are in, the
+//     summary K rows, the window's V rows and the summary V rows.  Loads complete in order: the
+//     scores of a pair of key tiles start when that pair's K parts are in LDS, while the later
+//     rows are still arriving.  V stays in registers until the scores are done and then its parts
+//     overwrite K's in the same LDS buffer (77 KB at d = 128: two workgroups per CU).
+//   * Window rows: when the window lies inside the keys that exist (and, in a ring, does not
+//     wrap), a thread's rows are one run from the window's first row; otherwise each row is
+//     clamped into [wlo, whi] (rows past the window repeat its ends; they are masked).
+//   * S^T = K Q^T: lane l (r = l % 16, lane group lg = l / 16) supplies K[tile row r][d] and
+//     Q[q0 + r][d] for d = lg D/4 + 8 ks + 0..7 in k-step ks and receives the scores of tile rows
+//     4 lg + i for query q0 + r.  Every tile is computed (no branch joins inside the unrolled
+//     loops, which would copy the accumulators); unused tiles hold copies of valid rows and are
+//     masked.
 //   * Masks: window keys [max(p - W + 1, key_lo, 0), min(p, kv_len - 1)]; summary slot j is used
 //     when its neighbour n satisfies 0 <= n < block, n < nsum and (n + 1) BS <= the cut-off
 //     (block-level for one-shot prefill, token-level for active rows).
-//   * Softmax in fp32 over the lane's scores and the four lane groups (xor shuffles 16, 32).
-//   * O^T = V^T P^T, one MFMA per (key tile, jj, d tile e): the lane supplies
-//     V[tile row 4 lg + jj][E r + e] (E = D / 16) and its own probability for that key, and
-//     receives O[q0 + r][DG lg + E jj' + e] (jj' = 0..3).
-// Positions are 32-bit (the host sends only caches below 2^30 rows here).
+//   * Softmax in fp32 over the lane's scores and the four lane groups (xor shuffles 16, 32), the
+//     scale and log2(e) folded into the scores and exp2 on v_exp_f32.
+//   * O^T = V^T P^T over key tile pairs (2 pr, 2 pr + 1): the lane's 8 probabilities are keys
+//     4 lg + 0..3 of both tiles, and its V^T fragment the same keys' values at one d, read from the
+//     row-major V parts by transposing LDS reads (pieces swizzled by row).  Output tile (mt, half)
+//     row r is d = 32 mt + 8 (r / 4) + 4 half + r % 4, so each lane ends with 8 consecutive d of
+//     its query per mt.
+// Positions and ring slots are 32-bit (the host sends only caches and rings below 2^30 rows here).
 constexpr int kF32MaxKcap = 16;
 constexpr int kF32WinTiles = 5;        // (64 - 1 + 15) / 16 + 1
 constexpr int kF32Tiles = kF32WinTiles + 1;
 constexpr int kF32Rows = 16 * kF32Tiles;
 
+// The three bf16 parts (bit patterns, two per dword, element 0 in the low half) of four floats.
+struct Parts4 {
+  uint2 h, m, l;
+};
+__device__ __forceinline__ Parts4 split_parts(f32x4 x) {
+  uint32_t hb[4], mb[4], lb[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hb[i] = __float_as_uint(x[i]) & 0xffff0000u;
+    const float rest = x[i] - __uint_as_float(hb[i]);          // exact
+    mb[i] = __float_as_uint(rest) & 0xffff0000u;
+    lb[i] = __float_as_uint(rest - __uint_as_float(mb[i]));     // exact, low 16 bits zero
+  }
+  auto pk = [](uint32_t e0, uint32_t e1) { return (e0 >> 16) | (e1 & 0xffff0000u); };
+  return {{pk(hb[0], hb[1]), pk(hb[2], hb[3])}, {pk(mb[0], mb[1]), pk(mb[2], mb[3])},
+          {pk(lb[0], lb[1]), pk(lb[2], lb[3])}};
+}
+__device__ __forceinline__ bf16x8 join8(uint2 a, uint2 b) {
+  return __builtin_bit_cast(bf16x8, uint4{a.x, a.y, b.x, b.y});
+}
+// c + a b in the six part products (small terms first)
+__device__ __forceinline__ f32x4 mfma_x6(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x4 c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b[0], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[1], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[2], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[0], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[1], c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], c, 0, 0, 0);
+}
+
 template <int D>
-__global__ void __launch_bounds__(256, 3) attn_f32_tile_kernel(AttnArgs a, int tile0, int ntiles, int per_xcd) {
-  constexpr int DG = D / 4, E = D / 16, KP = D + 4;        // LDS rows padded by 16 bytes
-  constexpr int PER_ROW = D / 4;                            // 16-byte pieces per row
-  constexpr int WIN_PIECES = 16 * kF32WinTiles * PER_ROW;
-  constexpr int STAGE = (kF32Rows * PER_ROW + 255) / 256;   // pieces of K (and of V) per thread
-  static_assert(kF32Rows * PER_ROW % 256 == 0, "every thread stages the same number of pieces");
-  __shared__ __attribute__((aligned(16))) float kvl[kF32Rows * KP];   // K, then V
+__global__ void __launch_bounds__(256, 2) attn_f32_tile_kernel(AttnArgs a, int tile0, int ntiles, int per_xcd) {
+  constexpr int DG = D / 4;                                 // d per lane group
+  constexpr int KP = D + 8;                                 // K part row pitch (bf16; 16-byte pad)
+  constexpr int KSTEPS = D / 32;
+  constexpr int PER_ROW = D / 4;                            // 4-float pieces per row
+  constexpr int RSTEP = 256 / PER_ROW;                      // rows between a thread's pieces
+  constexpr int UPT = 16 / RSTEP;                           // pieces per thread in a 16-row tile
+  constexpr int WIN_STAGE = kF32WinTiles * UPT;             // a thread's window pieces
+  constexpr int STAGE = kF32Tiles * UPT;                    // ... and with the summary tile's
+  constexpr int KPART = kF32Rows * KP, VPART = kF32Rows * D;
+  static_assert(256 % PER_ROW == 0 && 16 % RSTEP == 0, "a thread's pieces are one column, RSTEP rows apart");
+  static_assert(kF32Tiles % 2 == 0, "key tiles are scored in pairs");
+  __shared__ __attribute__((aligned(16))) __bf16 lds[3 * KPART];   // K parts, then V parts
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   // workgroups are dispatched to the 8 XCDs round-robin: XCD x = blockIdx % 8 takes the items
   // x per_xcd .. x per_xcd + per_xcd - 1, consecutive tiles of one (batch, kv head), which share
@@ -293,74 +347,110 @@ __global__ void __launch_bounds__(256, 3) attn_f32_tile_kernel(AttnArgs a, int t
   const bool qok = p >= qlo && p < qhi && w < gsz;
   const int qrow = p >= qlo && p < qhi ? p - qlo : 0;
   const int key_lo = (int)a.key_lo, kv_len = (int)a.kv_len, W = a.W, bs = a.bs;
+  const int ring = (int)a.ring;
   // the workgroup's window: [q0 - W + 1, q0 + 15] clipped to the keys that exist
   const int wlo = max(max(q0 - W + 1, key_lo), 0);
   const int whi = min(q0 + 15, kv_len - 1);
   const int nwt = (W - 1 + 15) / 16 + 1;                    // window tiles
   const int kstart = q0 - 16 * (nwt - 1);
-  const int blk = (int)clamp_block(q0, a);
+  const int blk = min((int)((uint32_t)max(q0, 0) / (uint32_t)bs), (int)a.nblocks - 1);
   const int hq_i = kvh * gsz + (w < gsz ? w : 0);           // a wave past the group repeats head 0
   const float* kb = reinterpret_cast<const float*>(a.k) + (bi * a.hkv + kvh) * a.kv_rows * D;
   const float* vb = reinterpret_cast<const float*>(a.v) + (bi * a.hkv + kvh) * a.kv_rows * D;
   const float* ksb = reinterpret_cast<const float*>(a.ks) + (bi * a.hkv + kvh) * a.pool_rows * D;
   const float* vsb = reinterpret_cast<const float*>(a.vs) + (bi * a.hkv + kvh) * a.pool_rows * D;
-  // summary slot j's pool row, or -1
-  auto slot_row = [&](int j) -> int {
-    if (j >= a.kcap) return -1;
-    const int n = a.nbr[(int64_t)blk * a.kcap + j];
-    return n >= 0 && n < blk && n < a.nsum ? n : -1;
-  };
+
+  // the block's neighbour-row entry of slot lane % 16 (the host sends kcap >= 1)
+  const int nb_raw = a.nbr[(int64_t)blk * a.kcap + min(lane & 15, a.kcap - 1)];
   const float* qp = reinterpret_cast<const float*>(a.q) + ((bi * a.hq + hq_i) * a.tq + qrow) * D + DG * lg;
   f32x4 qv[DG / 4];
 #pragma unroll
   for (int c = 0; c < DG / 4; ++c) qv[c] = *reinterpret_cast<const f32x4*>(qp + 4 * c);
-  // pieces 0 .. WIN_STAGE - 1 of every thread are window rows, the rest summary rows
-  constexpr int WIN_STAGE = WIN_PIECES / 256;
-  static_assert(WIN_PIECES % 256 == 0, "window pieces split evenly over the threads");
+
+  // a thread's pieces: column c4 of rows row0 + RSTEP u (u < WIN_STAGE: window row kstart + that;
+  // then summary slot row0 + RSTEP (u - WIN_STAGE)); LDS row row0 + RSTEP u either way
+  const int c4 = tid % PER_ROW, row0 = tid / PER_ROW;
+  int woff[WIN_STAGE];   // the window pieces' rows among the head's K/V rows
+  const bool run = kstart >= wlo && kstart + 16 * kF32WinTiles - 1 <= whi &&
+                   (ring == 0 || (int)((uint32_t)kstart % (uint32_t)ring) + 16 * kF32WinTiles <= ring);
+  if (run) {
+    const int base = ring ? (int)((uint32_t)kstart % (uint32_t)ring) : kstart - key_lo;
+#pragma unroll
+    for (int u = 0; u < WIN_STAGE; ++u) woff[u] = base + row0 + RSTEP * u;
+  } else {
+    const int last = (int)min(a.kv_rows - 1, (int64_t)INT32_MAX);
+#pragma unroll
+    for (int u = 0; u < WIN_STAGE; ++u) {
+      const int pos = min(max(kstart + row0 + RSTEP * u, wlo), whi);   // >= 0: wlo >= 0, whi >= 0
+      const int ro = ring ? (int)((uint32_t)pos % (uint32_t)ring) : pos - key_lo;
+      woff[u] = min(max(ro, 0), last);
+    }
+  }
   f32x4 kx[STAGE], vx[STAGE];
 #pragma unroll
-  for (int u = 0; u < WIN_STAGE; ++u) {
-    const int idx = tid + 256 * u;
-    const int row = idx / PER_ROW, c4 = idx - row * PER_ROW;
-    const int pos = min(max(kstart + row, wlo), whi);     // rows past the window repeat its ends
-    const int64_t off = (a.ring ? posmod(pos, a.ring) : pos - key_lo) * D + 4 * c4;
-    kx[u] = *reinterpret_cast<const f32x4*>(kb + off);
-    vx[u] = *reinterpret_cast<const f32x4*>(vb + off);
-  }
+  for (int u = 0; u < WIN_STAGE; ++u) kx[u] = *reinterpret_cast<const f32x4*>(kb + (int64_t)woff[u] * D + 4 * c4);
+  // nothing below moves above the window requests: the first use of the entries waits for them
+  __builtin_amdgcn_sched_barrier(0);
+  // lane j < 16 of every wave: slot j's pool row, or -1 where the slot is unused (j >= kcap, no
+  // neighbour, not an earlier block, or not summarised yet)
+  const int nb_lane = (lane & 15) < a.kcap && nb_raw >= 0 && nb_raw < blk && nb_raw < a.nsum ? nb_raw : -1;
+  // the summary pieces' pool rows (the entries were requested first: this waits for them alone);
+  // unused slots read pool row 0 and are masked
+  int soff[STAGE - WIN_STAGE];
 #pragma unroll
-  for (int u = WIN_STAGE; u < STAGE; ++u) {
-    const int idx = tid + 256 * u - WIN_PIECES;
-    const int row = idx / PER_ROW, c4 = idx - row * PER_ROW;
-    const int n = slot_row(row);
-    const int64_t off = (int64_t)(n < 0 ? 0 : n) * D + 4 * c4;   // unused slots read pool row 0
-    kx[u] = *reinterpret_cast<const f32x4*>(ksb + off);
-    vx[u] = *reinterpret_cast<const f32x4*>(vsb + off);
-  }
+  for (int u = WIN_STAGE; u < STAGE; ++u) soff[u - WIN_STAGE] = max(__shfl(nb_lane, row0 + RSTEP * (u - WIN_STAGE)), 0);
 #pragma unroll
-  for (int u = 0; u < STAGE; ++u) {
-    const int idx = tid + 256 * u;
-    const int row = idx / PER_ROW, c4 = idx - row * PER_ROW;
-    *reinterpret_cast<f32x4*>(kvl + row * KP + 4 * c4) = kx[u];
-  }
+  for (int u = WIN_STAGE; u < STAGE; ++u)
+    kx[u] = *reinterpret_cast<const f32x4*>(ksb + (int64_t)soff[u - WIN_STAGE] * D + 4 * c4);
+#pragma unroll
+  for (int u = 0; u < WIN_STAGE; ++u) vx[u] = *reinterpret_cast<const f32x4*>(vb + (int64_t)woff[u] * D + 4 * c4);
+#pragma unroll
+  for (int u = WIN_STAGE; u < STAGE; ++u)
+    vx[u] = *reinterpret_cast<const f32x4*>(vsb + (int64_t)soff[u - WIN_STAGE] * D + 4 * c4);
+  // every request is out before the first wait for data (Q's split below)
+  __builtin_amdgcn_sched_barrier(0);
   // this lane's summary slots 4 lg + jj
   int sn[4];
 #pragma unroll
-  for (int jj = 0; jj < 4; ++jj) sn[jj] = slot_row(4 * lg + jj);
+  for (int jj = 0; jj < 4; ++jj) sn[jj] = __shfl(nb_lane, 4 * lg + jj);
   const int cut = max(a.token_cutoff ? p - W + 1 : blk * bs - W + 1, 0);
   const int klo = max(max(p - W + 1, key_lo), 0), khi = min(p, kv_len - 1);
-  __syncthreads();   // K rows in LDS
+  const float sl2 = a.scale * 1.4426950408889634f;          // scale * log2(e)
+
+  // Q's parts in MFMA B-operand form: k-step ks holds d = DG lg + 8 ks + 0..7
+  bf16x8 qf[KSTEPS][3];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) {
+    const Parts4 x0 = split_parts(qv[2 * ks]), x1 = split_parts(qv[2 * ks + 1]);
+    qf[ks][0] = join8(x0.h, x1.h);
+    qf[ks][1] = join8(x0.m, x1.m);
+    qf[ks][2] = join8(x0.l, x1.l);
+  }
 
   f32x4 c[kF32Tiles];
 #pragma unroll
   for (int t = 0; t < kF32Tiles; ++t) c[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < DG; i += 4) {
+  for (int t0 = 0; t0 < kF32Tiles; t0 += 2) {
 #pragma unroll
-    for (int t = 0; t < kF32Tiles; ++t) {
-      const f32x4 k4 = *reinterpret_cast<const f32x4*>(kvl + (16 * t + r) * KP + DG * lg + i);
-      const f32x4 q4 = qv[i / 4];
+    for (int u = t0 * UPT; u < (t0 + 2) * UPT; ++u) {
+      const Parts4 x = split_parts(kx[u]);
+      const int off = (row0 + RSTEP * u) * KP + 4 * c4;
+      *reinterpret_cast<uint2*>(lds + off) = x.h;
+      *reinterpret_cast<uint2*>(lds + KPART + off) = x.m;
+      *reinterpret_cast<uint2*>(lds + 2 * KPART + off) = x.l;
+    }
+    __syncthreads();   // K parts of tiles t0, t0 + 1 in LDS
 #pragma unroll
-      for (int x = 0; x < 4; ++x) c[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[x], q4[x], c[t], 0, 0, 0);
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+#pragma unroll
+      for (int t = t0; t < t0 + 2; ++t) {
+        const int off = (16 * t + r) * KP + DG * lg + 8 * ks;
+        const bf16x8 kf[3] = {*reinterpret_cast<const bf16x8*>(lds + off),
+                              *reinterpret_cast<const bf16x8*>(lds + KPART + off),
+                              *reinterpret_cast<const bf16x8*>(lds + 2 * KPART + off)};
+        c[t] = mfma_x6(kf, qf[ks], c[t]);
+      }
     }
   }
   float sc[kF32Tiles][4];
@@ -376,7 +466,7 @@ __global__ void __launch_bounds__(256, 3) attn_f32_tile_kernel(AttnArgs a, int t
       } else {
         ok = sn[jj] >= 0 && (sn[jj] + 1) * bs <= cut;
       }
-      sc[t][jj] = ok ? c[t][jj] * a.scale : -INFINITY;
+      sc[t][jj] = ok ? c[t][jj] * sl2 : -INFINITY;
       m = fmaxf(m, sc[t][jj]);
     }
   m = fmaxf(m, __shfl_xor(m, 16));
@@ -387,47 +477,64 @@ __global__ void __launch_bounds__(256, 3) attn_f32_tile_kernel(AttnArgs a, int t
   for (int t = 0; t < kF32Tiles; ++t)
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-      sc[t][jj] = expf(sc[t][jj] - m);
+      sc[t][jj] = __builtin_amdgcn_exp2f(sc[t][jj] - m);   // exp2(-inf) = 0
       l += sc[t][jj];
     }
   l += __shfl_xor(l, 16);
   l += __shfl_xor(l, 32);
+  // P's parts in MFMA B-operand form: pair pr holds keys 4 lg + 0..3 of tiles 2 pr and 2 pr + 1
+  bf16x8 pf[kF32Tiles / 2][3];
+#pragma unroll
+  for (int pr = 0; pr < kF32Tiles / 2; ++pr) {
+    const Parts4 x0 = split_parts(f32x4{sc[2 * pr][0], sc[2 * pr][1], sc[2 * pr][2], sc[2 * pr][3]});
+    const Parts4 x1 = split_parts(f32x4{sc[2 * pr + 1][0], sc[2 * pr + 1][1], sc[2 * pr + 1][2], sc[2 * pr + 1][3]});
+    pf[pr][0] = join8(x0.h, x1.h);
+    pf[pr][1] = join8(x0.m, x1.m);
+    pf[pr][2] = join8(x0.l, x1.l);
+  }
 
   __syncthreads();   // every wave is done with K
 #pragma unroll
   for (int u = 0; u < STAGE; ++u) {
-    const int idx = tid + 256 * u;
-    const int row = idx / PER_ROW, c4 = idx - row * PER_ROW;
-    *reinterpret_cast<f32x4*>(kvl + row * KP + 4 * c4) = vx[u];
+    const Parts4 x = split_parts(vx[u]);
+    const int row = row0 + RSTEP * u;
+    const int off = row * D + (c4 ^ (2 * vrow_swizzle<D>(row))) * 4;
+    *reinterpret_cast<uint2*>(lds + off) = x.h;
+    *reinterpret_cast<uint2*>(lds + VPART + off) = x.m;
+    *reinterpret_cast<uint2*>(lds + 2 * VPART + off) = x.l;
   }
-  __syncthreads();   // V rows in LDS
+  __syncthreads();   // V parts in LDS
 
-  f32x4 acc[E];
+  const float inv = 1.f / fmaxf(l, 1e-9f);
+  float* op = reinterpret_cast<float*>(a.out) + ((bi * a.hq + hq_i) * a.tq + qrow) * D + 8 * lg;
 #pragma unroll
-  for (int e = 0; e < E; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < D / 32; ++mt) {
+    f32x4 o[2];
 #pragma unroll
-  for (int t = 0; t < kF32Tiles; ++t) {
+    for (int half = 0; half < 2; ++half) {
+      // lane (lg, r) reads d 32 mt + 8 (r & 3) + 4 half + 0..3 of key row 4 lg + (r >> 2) of
+      // each tile: lane r of the group receives d row r's four keys 4 lg + 0..3
+      const int unit = mt * 8 + (r & 3) * 2 + half;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const float* vp = kvl + (16 * t + 4 * lg + jj) * KP + E * r;
+      for (int pr = 0; pr < kF32Tiles / 2; ++pr) {
+        const int ra = 32 * pr + 4 * lg + (r >> 2), rb = ra + 16;
+        const int oa = ra * D + (unit ^ (2 * vrow_swizzle<D>(ra))) * 4;
+        const int ob = rb * D + (unit ^ (2 * vrow_swizzle<D>(rb))) * 4;
+        bf16x8 vf[3];
 #pragma unroll
-      for (int e = 0; e < E; e += 4) {
-        const f32x4 v4 = *reinterpret_cast<const f32x4*>(vp + e);
-#pragma unroll
-        for (int x = 0; x < 4; ++x) acc[e + x] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[x], sc[t][jj], acc[e + x], 0, 0, 0);
+        for (int pt = 0; pt < 3; ++pt)
+          vf[pt] = __builtin_shufflevector(read_tr(lds + pt * VPART + oa), read_tr(lds + pt * VPART + ob), 0, 1, 2,
+                                           3, 4, 5, 6, 7);
+        acc = mfma_x6(vf, pf[pr], acc);
       }
+      o[half] = acc;
     }
-  }
-  if (qok) {
-    // acc[e][jj'] is O[q0 + r][DG lg + E jj' + e]
-    const float inv = 1.f / fmaxf(l, 1e-9f);
-    float* op = reinterpret_cast<float*>(a.out) + ((bi * a.hq + hq_i) * a.tq + qrow) * D + DG * lg;
-#pragma unroll
-    for (int jp = 0; jp < 4; ++jp)
-#pragma unroll
-      for (int e = 0; e < E; e += 4)
-        *reinterpret_cast<f32x4*>(op + E * jp + e) =
-            f32x4{acc[e][jp] * inv, acc[e + 1][jp] * inv, acc[e + 2][jp] * inv, acc[e + 3][jp] * inv};
+    // o[half][i] is O[q0 + r][32 mt + 8 lg + 4 half + i]
+    if (qok) {
+      *reinterpret_cast<f32x4*>(op + 32 * mt) = f32x4{o[0][0] * inv, o[0][1] * inv, o[0][2] * inv, o[0][3] * inv};
+      *reinterpret_cast<f32x4*>(op + 32 * mt + 4) = f32x4{o[1][0] * inv, o[1][1] * inv, o[1][2] * inv, o[1][3] * inv};
+    }
   }
 }
 
@@ -1114,8 +1221,9 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
     }
   } else if (dtype == BFLY_DTYPE_F32 && contiguous && a.nbr != nullptr && a.W <= 64 && a.bs % 16 == 0 &&
              a.hq / a.hkv <= 4 &&
-             (a.d == 64 || a.d == 128) && a.kcap <= kF32MaxKcap && a.kv_len + 2 * kF32Rows < (1 << 30) &&
-             a.nblocks * (int64_t)a.bs < (1 << 30) && a.q_pos0 + a.tq < (1 << 30) && a.pool_rows > 0) {
+             (a.d == 64 || a.d == 128) && a.kcap >= 1 && a.kcap <= kF32MaxKcap &&
+             a.kv_len + 2 * kF32Rows < (1 << 30) && a.ring < (1 << 30) && a.nblocks * (int64_t)a.bs < (1 << 30) &&
+             a.q_pos0 >= 0 && a.q_pos0 + a.tq < (1 << 30) && a.pool_rows > 0) {
     const int64_t tile0 = floordiv(a.q_pos0, 16);
     const int64_t ntiles = floordiv(a.q_pos0 + a.tq - 1, 16) - tile0 + 1;
     const int64_t items = ntiles * a.batch * a.hkv;

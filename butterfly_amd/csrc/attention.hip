@@ -613,11 +613,16 @@ struct MfmaArgs {
 struct ChunkArgs {
   const void* q;
   void* out;
+  const void* k;          // the chunk's own keys and values, [batch x kv heads, tq, d]
+  const void* v;
   int tq, qlo, qhi, key_lo, kv_len, nsum, nblocks, c_first, nchunks;
   bfly_topology_t topo;
 };
 struct ChunkBatch {
   int rows_per_chunk;     // grid rows of one chunk (batch x kv heads x head parts)
+  int nch;                // chunks in the batch
+  int from_inputs;        // 1: every chunk starts on a page boundary; pages of the batch's own
+                          // tokens come from the chunk inputs (else every page from the ring)
   ChunkArgs c[kMaxUpdateParts];
 };
 struct NoBatch {};
@@ -806,6 +811,43 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
       const uint4 x = *reinterpret_cast<const uint4*>(base + (int64_t)(v ? rowp(r) : 0) * D + pc * 8);
       return v ? x : make_uint4(0, 0, 0, 0);
     };
+    if constexpr (kBatch) {
+      // A streaming batch whose chunks all start on a page boundary reads its own tokens (the
+      // pages from its first chunk's on) from the chunk inputs: the cache update copies to the
+      // ring only the tokens later steps read there.  Such a page lies in one chunk.
+      if (cb.from_inputs && p0 >= cb.c[0].qlo) {
+        // the chunk holding p0: selects over the slots (workgroup-uniform)
+        const __bf16* kc = reinterpret_cast<const __bf16*>(cb.c[0].k);
+        const __bf16* vc = reinterpret_cast<const __bf16*>(cb.c[0].v);
+        int lo = cb.c[0].qlo, len = cb.c[0].tq;
+#pragma unroll
+        for (int j = 1; j < kMaxUpdateParts; ++j) {
+          const bool in = j < cb.nch && p0 >= cb.c[j].qlo;
+          kc = in ? reinterpret_cast<const __bf16*>(cb.c[j].k) : kc;
+          vc = in ? reinterpret_cast<const __bf16*>(cb.c[j].v) : vc;
+          lo = in ? cb.c[j].qlo : lo;
+          len = in ? cb.c[j].tq : len;
+        }
+        // rows past the chunk's end are past kv_len (the attended chunk's end), so invalid
+        const int64_t rb = (int64_t)bh * len + (p0 - lo);
+        auto ldc = [&](const __bf16* base, int r, int pc) {
+          const bool v = ok(p0 + r);
+          const uint4 x = *reinterpret_cast<const uint4*>(base + (rb + (v ? r : 0)) * D + pc * 8);
+          return v ? x : make_uint4(0, 0, 0, 0);
+        };
+#pragma unroll
+        for (int it = 0; it < C::KLD; ++it) {
+          const int i = tid + it * NTHR;
+          kst[it] = ldc(kc, i / C::PIECES, i % C::PIECES);
+        }
+#pragma unroll
+        for (int it = 0; it < C::KLD; ++it) {
+          const int i = tid + it * NTHR;
+          vst[it] = ldc(vc, i / C::PIECES, i % C::PIECES);
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int it = 0; it < C::KLD; ++it) {
       const int i = tid + it * NTHR;
@@ -1197,7 +1239,7 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
     BFLY_CHECK_ARG(groups * nparts <= 65535, "%s: grid too large", what);
     dim3 grid((unsigned)nseg, (unsigned)(groups * nparts));
     if (upd != nullptr) {
-      const int64_t ux = update_x(upd->n_blocks, upd->step, upd->d, 8);
+      const int64_t ux = update_x(upd->n_blocks, upd->step - upd->append_from, upd->d, 8);
       m.upd = *upd;
       m.attn_y = (int)grid.y;
       m.upd_x = (int)ux;
@@ -1255,22 +1297,31 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
 // bfly_stream_chunks builds them for a launch of its own; they differ only in the query range,
 // q / out and the cache state.  Optionally with a cache update on extra grid rows.  The grid
 // shape follows launch_attention's rules for the whole batch.
-static int launch_attention_batch(const AttnArgs* ch, int n, hipStream_t stream, const char* what,
+static int launch_attention_batch(const AttnArgs* ch, const void* const* kin, const void* const* vin, int n,
+                                  bool from_inputs, hipStream_t stream, const char* what,
                                   const UpdateJob* upd = nullptr, int64_t upd_rows = 0) {
   BFLY_CHECK_ARG(n >= 1 && n <= kMaxUpdateParts, "%s: batch of %d chunks", what, n);
   const AttnArgs& a = ch[0];
   ChunkBatch cb{};
+  cb.nch = n;
+  cb.from_inputs = from_inputs ? 1 : 0;
   int64_t nch_max = 0;
   for (int j = 0; j < n; ++j) {
     const AttnArgs& c = ch[j];
-    BFLY_CHECK_ARG(aligned16(c.q) && aligned16(c.out), "%s: tensor pointers must be 16-byte aligned", what);
+    BFLY_CHECK_ARG(aligned16(c.q) && aligned16(c.out) && aligned16(kin[j]) && aligned16(vin[j]),
+                   "%s: tensor pointers must be 16-byte aligned", what);
     BFLY_CHECK_ARG(c.tq > 0 && c.nbr == nullptr && c.qpos == nullptr, "%s: chunk %d arguments", what, j);
+    // consecutive chunks: chunk j's keys are positions [q_pos0, q_pos0 + tq), the next one's follow
+    BFLY_CHECK_ARG(j == 0 || c.q_pos0 == ch[j - 1].q_pos0 + ch[j - 1].tq, "%s: chunk %d not consecutive", what, j);
+    BFLY_CHECK_ARG(!from_inputs || c.q_pos0 % kPage == 0, "%s: chunk %d off the page grid", what, j);
     const int64_t cf = floordiv(c.q_pos0, kPage);
     const int64_t nc = floordiv(c.q_pos0 + c.tq - 1, kPage) - cf + 1;
     nch_max = nc > nch_max ? nc : nch_max;
     ChunkArgs& k = cb.c[j];
     k.q = c.q;
     k.out = c.out;
+    k.k = kin[j];
+    k.v = vin[j];
     k.tq = (int)c.tq;
     k.qlo = (int)c.q_pos0;
     k.qhi = (int)(c.q_pos0 + c.tq);
@@ -1303,7 +1354,7 @@ static int launch_attention_batch(const AttnArgs* ch, int n, hipStream_t stream,
   m.token_cutoff = a.token_cutoff;
   dim3 grid((unsigned)nseg, (unsigned)(groups * nparts * n));
   if (upd != nullptr) {
-    const int64_t ux = update_x(upd->n_blocks, upd->step, upd->d, 8);
+    const int64_t ux = update_x(upd->n_blocks, upd->step - upd->append_from, upd->d, 8);
     m.upd = *upd;
     m.attn_y = (int)grid.y;
     m.upd_x = (int)ux;
@@ -1524,6 +1575,7 @@ extern "C" int bfly_stream_chunks(int64_t n_chunks, const void* const* q, const 
     UpdateJob job{};
     StreamCounters end{};
     bool overflow = false;   // the last chunk exhausted the pool: its update runs, its attention not
+    bool from_inputs = false;   // the attention reads the batch's own tokens from the chunk inputs
     int stop_rc = BFLY_OK;   // the chunk after the batch does not fit (its error)
   };
   const int64_t budget = (ring_capacity - 2 * kPage) / 2;
@@ -1577,6 +1629,14 @@ extern "C" int bfly_stream_chunks(int64_t n_chunks, const void* const* q, const 
     bt.job.step = bt.total;
     bt.job.n_blocks = (int)blocks;
     bt.job.nparts = (int)bt.count;
+    // When every chunk of the batch starts on a page boundary, its attention reads the batch's
+    // own tokens from the chunk inputs and only the tokens in the tail the batch leaves are
+    // copied to the ring: every later read of the ring (pooling, attention windows, the cache's
+    // views) lies in a later tail, which starts no earlier.
+    bt.from_inputs = true;
+    for (int64_t j = 0; j < bt.count; ++j) bt.from_inputs = bt.from_inputs && bt.args[j].q_pos0 % kPage == 0;
+    const int64_t keep_from = st.offset - st.tail - bt.job.offset;
+    bt.job.append_from = !bt.from_inputs || keep_from < 0 ? 0 : (keep_from > bt.total ? bt.total : keep_from);
     return BFLY_OK;
   };
   auto launch_update = [&](const UpdateJob& j) -> int { return launch_update_job(j, rows, stream); };
@@ -1602,10 +1662,12 @@ extern "C" int bfly_stream_chunks(int64_t n_chunks, const void* const* q, const 
       nxt.stop_rc = cur.stop_rc;
     }
     if (nxt.count > 0 && cur.total + nxt.total + 2 * kPage <= ring_capacity) {
-      rc = launch_attention_batch(cur.args, (int)cur.count, stream, "bfly_stream_chunks", &nxt.job, rows);
+      rc = launch_attention_batch(cur.args, cur.job.k_part, cur.job.v_part, (int)cur.count, cur.from_inputs,
+                                  stream, "bfly_stream_chunks", &nxt.job, rows);
       if (rc) return rc;
     } else {
-      rc = launch_attention_batch(cur.args, (int)cur.count, stream, "bfly_stream_chunks");
+      rc = launch_attention_batch(cur.args, cur.job.k_part, cur.job.v_part, (int)cur.count, cur.from_inputs,
+                                  stream, "bfly_stream_chunks");
       if (rc) return rc;
       if (nxt.count > 0) {
         rc = launch_update(nxt.job);

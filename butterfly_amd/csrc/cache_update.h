@@ -105,6 +105,10 @@ struct UpdateJob {
   const void* k_part[kMaxUpdateParts];
   const void* v_part[kMaxUpdateParts];
   int64_t part_end[kMaxUpdateParts];
+  // new tokens t < append_from are not copied to the ring (the streaming loop: tokens below the
+  // tail that the update leaves, which no later step reads; its attention reads the batch's own
+  // tokens from the chunk inputs)
+  int64_t append_from;
 };
 
 // The part of an update's input that holds new token t (< step): its buffer (K or V), first
@@ -159,7 +163,7 @@ __device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx
     const int lpr = d / VEC, tpw = 256 / lpr;
     const int c = t % lpr;
     if (t / lpr >= tpw) return;
-    const int64_t wg_tok0 = (bx - u.n_blocks) * tpw * kAppendRounds;
+    const int64_t wg_tok0 = u.append_from + (bx - u.n_blocks) * tpw * kAppendRounds;
     const int64_t tok0 = wg_tok0 + t / lpr;
     if (tok0 >= u.step) return;
     const int64_t wg_last = min(wg_tok0 + (int64_t)tpw * kAppendRounds, u.step) - 1;
@@ -226,7 +230,7 @@ __device__ __forceinline__ void cache_update_body(const UpdateJob& u, int64_t bx
 int launch_update_job(const UpdateJob& u, int64_t rows, hipStream_t stream);
 
 // Workgroups along x of an update with a 16-byte row split (VEC elements per
-// 16 bytes): the due blocks, then the append workgroups.
+// 16 bytes): the due blocks, then the append workgroups (step: the tokens copied).
 inline int64_t update_x(int64_t n_blocks, int64_t step, int head_dim, int vec) {
   const int tpw = 256 / (head_dim / vec) * kAppendRounds;
   return n_blocks + (step + tpw - 1) / tpw;

@@ -64,8 +64,9 @@ int launch_update_job(const UpdateJob& u, int64_t rows, hipStream_t stream) {
   BFLY_CHECK_ARG(u.n_blocks == 0 || (u.first_pos >= u.offset + u.step - u.ring &&
                                      u.first_pos + (int64_t)u.n_blocks * u.bs <= u.offset + u.step),
                  "update job: due blocks outside the tail after the append");
-  if (u.step == 0 && u.n_blocks == 0) return BFLY_OK;
-  const int64_t ux = update_x(u.n_blocks, u.step, u.d, 8);
+  BFLY_CHECK_ARG(u.append_from >= 0 && u.append_from <= u.step, "update job: append_from outside the step");
+  if (u.step == u.append_from && u.n_blocks == 0) return BFLY_OK;
+  const int64_t ux = update_x(u.n_blocks, u.step - u.append_from, u.d, 8);
   BFLY_CHECK_ARG(ux <= INT32_MAX, "update job: grid too large");
   hipLaunchKernelGGL((cache_update_kernel<__bf16, 8>), dim3((unsigned)ux, (unsigned)rows, 2), dim3(256), 0, stream, u);
   BFLY_CHECK_LAUNCH("cache update job");

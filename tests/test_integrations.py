@@ -237,7 +237,22 @@ def test_native_chunk_loop_equals_per_chunk_calls(b, hq, hkv, d, max_chunk):
     a few chunks (max_chunk_size 512) gives one chunk per launch; larger rings batch several
     chunks per attention launch and per update job (blocks pooled across chunk boundaries
     inside a batch, batches fused with the next batch's update or not)."""
-    layer, lens = 6, [384, 384, 200, 384, 130, 3, 384, 257, 384, 384, 384, 100, 384, 384]
+    _native_loop_matches_per_chunk(b, hq, hkv, d, max_chunk,
+                                   [384, 384, 200, 384, 130, 3, 384, 257, 384, 384, 384, 100, 384, 384])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,hq,hkv,d,max_chunk", [(1, 16, 4, 256, 4096), (2, 8, 2, 128, 2048), (1, 16, 4, 256, 1024)])
+def test_native_chunk_loop_on_the_page_grid_equals_per_chunk_calls(b, hq, hkv, d, max_chunk):
+    """Every chunk a multiple of 64 tokens: the batches read their own tokens from the chunk
+    inputs and copy only the tail they leave to the ring; outputs, counters, tail and pool
+    must still equal the one-call-per-chunk schedule's."""
+    _native_loop_matches_per_chunk(b, hq, hkv, d, max_chunk,
+                                   [384, 384, 256, 448, 64, 384, 128, 384, 384, 320, 384, 384, 192, 384, 384, 384])
+
+
+def _native_loop_matches_per_chunk(b, hq, hkv, d, max_chunk, lens):
+    layer = 6
     total = sum(lens)
     q = _rand(91, (b, hq, total, d), torch.bfloat16).cuda()
     k = _rand(92, (b, hkv, total, d), torch.bfloat16).cuda()

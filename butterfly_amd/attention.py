@@ -17,7 +17,9 @@ Every call runs on the current torch stream; nothing here falls back to CPU.
 from __future__ import annotations
 
 import math
-from typing import Optional
+import os
+import time
+from typing import Any, Dict, Optional
 
 import torch
 
@@ -63,6 +65,26 @@ def _scale(scale: Optional[float], d: int) -> float:
     return float(scale) if scale is not None else 1.0 / math.sqrt(d)
 
 
+# --------------------------------------------------------------------------- profile counters
+# With BNA_COMPRESS_PROFILE=1 in the environment (read at import), every compressor call and
+# every active-row attention waits for its stream and adds its wall time here, and the
+# compressor records the shapes it pooled.  Reference: bna/mlx/attention.py:45-79 (counters,
+# reset, dump) and 1561-1595 (attention time of the active entry).
+_COMPRESS_PROFILE = os.environ.get("BNA_COMPRESS_PROFILE", "0") == "1"
+_compress_stats: Dict[str, Any] = {"calls": 0, "summary_ms": 0.0, "attn_ms": 0.0, "shapes": []}
+
+
+def _compress_profile_reset() -> None:
+    _compress_stats["calls"] = 0
+    _compress_stats["summary_ms"] = 0.0
+    _compress_stats["attn_ms"] = 0.0
+    _compress_stats["shapes"] = []
+
+
+def _compress_profile_dump() -> Dict[str, Any]:
+    return dict(_compress_stats)
+
+
 # --------------------------------------------------------------------------- compressor
 def block_mean_summaries(x: torch.Tensor, *, seq_len: int, block_size: int, num_blocks: int,
                          x2: Optional[torch.Tensor] = None):
@@ -83,10 +105,20 @@ def block_mean_summaries(x: torch.Tensor, *, seq_len: int, block_size: int, num_
             raise ValueError("x2 must match x in shape and dtype")
         x2 = _c(x2)
         out2 = torch.empty_like(out)
+    t0 = time.perf_counter() if _COMPRESS_PROFILE else 0.0
     with _on(x.device):
         _native.call("bfly_block_mean", x.data_ptr(), out.data_ptr(),
                      x2.data_ptr() if x2 is not None else None, out2.data_ptr() if out2 is not None else None,
                      _dtype_code(x), b * h, int(t), d, int(block_size), int(num_blocks), _stream(x))
+        if _COMPRESS_PROFILE:
+            # one launch pools both tensors; each counts as a call, as the reference pools them in two
+            torch.cuda.current_stream(x.device).synchronize()
+            _compress_stats["summary_ms"] += (time.perf_counter() - t0) * 1000.0
+            for xx in (x, x2) if x2 is not None else (x,):
+                _compress_stats["calls"] += 1
+                _compress_stats["shapes"].append({"seq_len": int(seq_len), "block_size": int(block_size),
+                                                  "num_blocks": int(num_blocks), "x_shape": list(xx.shape),
+                                                  "x_dtype": str(xx.dtype)})
     return (out, out2) if x2 is not None else out
 
 
@@ -271,8 +303,12 @@ def compressed_butterfly_attention_active(q: torch.Tensor, k: torch.Tensor, v: t
     q_pos0, qpos_dev = _positions(query_positions, tq, q.device)
     if qpos_dev is None and tq > 0 and (q_pos0 < 0 or q_pos0 + tq > tk):
         raise ValueError("query positions must lie in [0, kv_len)")
+    t0 = time.perf_counter() if _COMPRESS_PROFILE else 0.0
     out = _attend(q, k, v, ksum, vsum, layout=layout, q_pos0=q_pos0, qpos_dev=qpos_dev, ring_capacity=0,
                   tail_start=0, kv_len=tk, summary_count=n, local_window_tokens=local_window_tokens, scale=scale)
+    if _COMPRESS_PROFILE:
+        torch.cuda.current_stream(q.device).synchronize()
+        _compress_stats["attn_ms"] += (time.perf_counter() - t0) * 1000.0
     return out, None
 
 

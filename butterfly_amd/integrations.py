@@ -27,8 +27,9 @@ Every attention call runs a HIP kernel of ``libbutterfly_amd.so``.
 from __future__ import annotations
 
 import time
+import warnings
 from dataclasses import dataclass, field
-from typing import Any, Dict, List, Optional, Sequence, Union
+from typing import Any, Dict, List, Optional, Sequence, Tuple, Union
 
 import torch
 import torch.nn as nn
@@ -36,7 +37,7 @@ import torch.nn as nn
 from .attention import (_attend, _c, _on, _require_cuda, compressed_butterfly_attention,
                         compressed_butterfly_attention_active)
 from .compressed_cache import CompressedKVCache
-from .layout import build_block_butterfly_layout
+from .layout import build_block_butterfly_layout, drop_layouts_for_other_lengths
 
 _RULES = {"xor", "bit_reversal", "benes", "causal_shift", "fixed_stride", "random"}
 _STRATEGIES = {"random", "greedy", "online_insertion", "regular_partition"}
@@ -558,6 +559,30 @@ def get_qwen_full_attention_layer_indices(model) -> List[int]:
     return out
 
 
+# The full-attention layers of Qwen 3.5 (every fourth of 32); bna/integrations/qwen_mlx.py:49
+EXPECTED_QWEN35_FULL_ATTENTION_LAYERS: Tuple[int, ...] = (3, 7, 11, 15, 19, 23, 27, 31)
+
+
+def validate_qwen35_full_attention_layers(model, *, allow_mismatch: bool = False) -> List[int]:
+    """The model's full-attention layers, checked against Qwen 3.5's layout: a different
+    layout raises ``ValueError``, or with ``allow_mismatch`` warns and is returned as found.
+    Reference: bna/integrations/qwen_mlx.py:1862-1877."""
+    discovered = get_qwen_full_attention_layer_indices(model)
+    if tuple(discovered) != EXPECTED_QWEN35_FULL_ATTENTION_LAYERS:
+        message = ("Unexpected Qwen 3.5 full-attention layer layout: "
+                   f"expected={list(EXPECTED_QWEN35_FULL_ATTENTION_LAYERS)} discovered={discovered}")
+        if not allow_mismatch:
+            raise ValueError(message)
+        warnings.warn(message, stacklevel=2)
+    return discovered
+
+
+def _qwen_graph_cache_drop_other_keys(current_T: int) -> int:
+    """The reference's name for evicting cached layouts of other sequence lengths
+    (bna/integrations/qwen_mlx.py:52-81); see ``layout.drop_layouts_for_other_lengths``."""
+    return drop_layouts_for_other_lengths(current_T)
+
+
 def install_compressed_kv_caches(model, prompt_cache: List[Any], *, layer_indices: Optional[Sequence[int]] = None,
                                  block_size: int = 128, local_window_tokens: int = 128,
                                  max_kv_size: Optional[int] = None, max_chunk_size: int = 512) -> List[int]:
@@ -654,8 +679,12 @@ def chunked_prefill(core: ButterflyAttentionCore, chunks, cache: CompressedKVCac
             continue
         outs += got
         i += len(got)
-        run = 64
+        run = _STREAM_RUN
     return outs
+
+
+# chunks per bfly_stream_chunks call after the first (small) run
+_STREAM_RUN = 64
 
 
 def _stream_possible(core: ButterflyAttentionCore, cache, chunk) -> bool:

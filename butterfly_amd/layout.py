@@ -169,3 +169,19 @@ def _build_layout(*, seq_len: int, block_size: int, num_key_value_heads: int, nu
 def clear_layout_cache() -> None:
     _TABLE_CACHE.clear()
     _LAYOUT_CACHE.clear()
+
+
+def drop_layouts_for_other_lengths(current_T: int) -> int:
+    """Evict every cached layout whose sequence length is not ``current_T``; returns how
+    many were dropped.  Chunked prefill builds one layout per live kv_len, so without this
+    the cache holds one entry per chunk; the layers of one chunk, which share a length,
+    keep sharing theirs.  (The neighbour tables behind the layouts are keyed by block count
+    and stay, bounded by their own LRU.)
+
+    Reference: _qwen_graph_cache_drop_other_keys (bna/integrations/qwen_mlx.py:52-81),
+    called per chunk by the harness (scripts/bench_qwen_consumer_mlx.py:650-651).
+    """
+    drop = [key for key in _LAYOUT_CACHE if int(key[0]) != int(current_T)]
+    for key in drop:
+        _LAYOUT_CACHE.pop(key, None)
+    return len(drop)

@@ -114,6 +114,91 @@ def test_full_attention_layers_and_install_default():
         bf.install_compressed_kv_caches(object(), caches)
 
 
+def test_qwen35_full_attention_layout_validation():
+    """validate_qwen35_full_attention_layers (bna/integrations/qwen_mlx.py:1862-1877): the
+    full-attention layers of Qwen 3.5 are every fourth of 32 (3, 7, .., 31)."""
+    assert bf.EXPECTED_QWEN35_FULL_ATTENTION_LAYERS == (3, 7, 11, 15, 19, 23, 27, 31)
+    m = _Model([_Layer(False, True) if i % 4 != 3 else _Layer(True, False) for i in range(32)])
+    assert bf.validate_qwen35_full_attention_layers(m) == [3, 7, 11, 15, 19, 23, 27, 31]
+    odd = _Model([_Layer(False, True), _Layer(True, False), _Layer(False, True), _Layer(True, False)])
+    with pytest.raises(ValueError, match="expected=.*discovered=\\[1, 3\\]"):
+        bf.validate_qwen35_full_attention_layers(odd)
+    with pytest.warns(UserWarning, match="Unexpected Qwen 3.5 full-attention layer layout"):
+        assert bf.validate_qwen35_full_attention_layers(odd, allow_mismatch=True) == [1, 3]
+
+
+def test_layout_cache_drops_other_lengths():
+    """Per-length eviction of cached layouts (bna/integrations/qwen_mlx.py:52-81) over the
+    cache's keys (sequence length first): entries of other lengths go, the current
+    length's stay."""
+    from butterfly_amd import integrations, layout
+    saved = list(layout._LAYOUT_CACHE.items())
+    layout._LAYOUT_CACHE.clear()
+    try:
+        for t, li in ((256, 3), (384, 3), (512, 3), (384, 4)):
+            layout._LAYOUT_CACHE[(t, 128, 2, 4, li, 1, 1, 1, "causal_shift", "cuda:0")] = object()
+        assert integrations._qwen_graph_cache_drop_other_keys(384) == 2
+        assert sorted(k[4] for k in layout._LAYOUT_CACHE) == [3, 4] and all(k[0] == 384 for k in layout._LAYOUT_CACHE)
+        assert bf.drop_layouts_for_other_lengths(384) == 0
+        assert bf.drop_layouts_for_other_lengths(512) == 2 and not layout._LAYOUT_CACHE
+    finally:
+        layout._LAYOUT_CACHE.clear()
+        layout._LAYOUT_CACHE.update(saved)
+
+
+@pytest.mark.gpu
+def test_layout_cache_eviction_keeps_the_current_length_shared():
+    kw = dict(block_size=128, num_key_value_heads=2, num_key_value_groups=4, layer_idx=3, local_window_blocks=1,
+              partner_rule="causal_shift")
+    bf.clear_layout_cache()
+    lays = {t: bf.build_block_butterfly_layout(seq_len=t, **kw) for t in (256, 384, 512)}
+    keep = bf.build_block_butterfly_layout(seq_len=384, **dict(kw, layer_idx=4))
+    assert bf.drop_layouts_for_other_lengths(384) == 2
+    assert bf.build_block_butterfly_layout(seq_len=384, **kw) is lays[384]
+    assert bf.build_block_butterfly_layout(seq_len=384, **dict(kw, layer_idx=4)) is keep
+    rebuilt = bf.build_block_butterfly_layout(seq_len=512, **kw)
+    assert rebuilt is not lays[512] and torch.equal(rebuilt.block_neighbors, lays[512].block_neighbors)
+    bf.clear_layout_cache()
+
+
+def test_compress_profile_counters_reset_and_dump():
+    """The BNA_COMPRESS_PROFILE counters (bna/mlx/attention.py:45-79): reset zeroes them and
+    dump returns a copy of the store."""
+    from butterfly_amd import attention as at
+    at._compress_stats["calls"] = 3
+    at._compress_stats["shapes"].append({"seq_len": 1})
+    d = at._compress_profile_dump()
+    assert d["calls"] == 3 and d is not at._compress_stats
+    at._compress_profile_reset()
+    assert at._compress_profile_dump() == {"calls": 0, "summary_ms": 0.0, "attn_ms": 0.0, "shapes": []}
+
+
+@pytest.mark.gpu
+def test_compress_profile_counts_the_compressor_and_the_active_attention(monkeypatch):
+    """With the profile on, the active entry's compressor (K and V pooled by one launch, two
+    calls as the reference counts them) and its attention add wall time and shapes."""
+    from butterfly_amd import attention as at
+    monkeypatch.setattr(at, "_COMPRESS_PROFILE", True)
+    at._compress_profile_reset()
+    q = _rand(81, (1, 8, 64, 128), torch.bfloat16).cuda()
+    k = _rand(82, (1, 2, 640, 128), torch.bfloat16).cuda()
+    v = _rand(83, (1, 2, 640, 128), torch.bfloat16).cuda()
+    lay = bf.build_block_butterfly_layout(seq_len=640, block_size=128, num_key_value_heads=2, num_key_value_groups=4,
+                                          layer_idx=2, local_window_blocks=1, partner_rule="causal_shift")
+    out, _ = bf.compressed_butterfly_attention_active(q, k, v, layout=lay, query_positions=list(range(576, 640)),
+                                                      local_window_tokens=64)
+    assert torch.isfinite(out.float()).all()
+    d = at._compress_profile_dump()
+    assert d["calls"] == 2 and d["summary_ms"] > 0 and d["attn_ms"] > 0
+    assert d["shapes"] == [{"seq_len": 640, "block_size": 128, "num_blocks": 5, "x_shape": [1, 2, 640, 128],
+                            "x_dtype": "torch.bfloat16"}] * 2
+    monkeypatch.setattr(at, "_COMPRESS_PROFILE", False)
+    bf.compressed_butterfly_attention_active(q, k, v, layout=lay, query_positions=list(range(576, 640)),
+                                             local_window_tokens=64)
+    assert at._compress_profile_dump()["calls"] == 2     # nothing counted with the profile off
+    at._compress_profile_reset()
+
+
 def test_swap_wraps_modules_with_the_attribute_set():
     m = _Model([_Layer(False, True), _Layer(True, False), _Layer(True, False)])
     cfg = bf.compressed_butterfly_config()

@@ -1264,7 +1264,8 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
   } else if (dtype == BFLY_DTYPE_F32 && contiguous && a.nbr != nullptr && a.W <= 64 && a.bs % 16 == 0 &&
              a.hq / a.hkv <= 4 &&
              (a.d == 64 || a.d == 128) && a.kcap >= 1 && a.kcap <= kF32MaxKcap &&
-             a.kv_len + 2 * kF32Rows < (1 << 30) && a.ring < (1 << 30) && a.nblocks * (int64_t)a.bs < (1 << 30) &&
+             a.kv_len + 2 * kF32Rows < (1 << 30) && a.ring < (1 << 30) && a.nblocks >= 1 &&
+             a.nblocks * (int64_t)a.bs < (1 << 30) &&
              a.q_pos0 >= 0 && a.q_pos0 + a.tq < (1 << 30) && a.pool_rows > 0) {
     const int64_t tile0 = floordiv(a.q_pos0, 16);
     const int64_t ntiles = floordiv(a.q_pos0 + a.tq - 1, 16) - tile0 + 1;

@@ -679,12 +679,20 @@ def chunked_prefill(core: ButterflyAttentionCore, chunks, cache: CompressedKVCac
             continue
         outs += got
         i += len(got)
-        run = _STREAM_RUN
+        run = _stream_run(cache, int(chunks[i - 1][0].shape[2]))
     return outs
 
 
-# chunks per bfly_stream_chunks call after the first (small) run
+# chunks per bfly_stream_chunks call after the first (small) run: about 64, rounded up to whole
+# batches of the native loop (its batches hold at most 10 chunks and half the ring minus two pages),
+# so that a call does not end in a small batch, whose attention launch runs alone
 _STREAM_RUN = 64
+_STREAM_BATCH_CAP = 10
+
+
+def _stream_run(cache, chunk_len: int) -> int:
+    per = max(1, min(_STREAM_BATCH_CAP, (int(cache.tail_capacity) - 128) // 2 // max(1, chunk_len)))
+    return per * -(-_STREAM_RUN // per)
 
 
 def _stream_possible(core: ButterflyAttentionCore, cache, chunk) -> bool:

@@ -250,8 +250,9 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(AttnArgs a) {
 //     three bf16 parts by truncation, x = hi + mid + lo exactly (hi keeps the sign, exponent and
 //     top 7 stored mantissa bits of x, mid those of x - hi, and lo = x - hi - mid has at most 8
 //     significant bits), and a product a b is summed in the fp32 accumulator as the six part
-//     products ah bh + ah bm + am bh + ah bl + am bm + al bh, each exact in fp32 (the three
-//     dropped ones are below 2^-24 of |a b|): the "bf16x6" scheme of Henry, Tang and Heinecke,
+//     products ah bh + ah bm + am bh + ah bl + am bm + al bh, each exact in fp32 (of the three
+//     dropped ones, |am bl| and |al bm| are below 2^-21 |a b| and |al bl| below 2^-28 |a b|,
+//     since |am| < 2^-7 |a| and |al| < 2^-14 |a|): the "bf16x6" scheme of Henry, Tang and Heinecke,
 //     "Leveraging the bfloat16 artificial intelligence datatype for higher-precision
 //     computations" (ARITH 2019).  Six 16x16x32 bf16 MFMAs (16 cycles each) replace eight
 //     16x16x4 fp32 ones (32 cycles each).

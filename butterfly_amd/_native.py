@@ -76,6 +76,9 @@ SIGNATURES = {
     "bfly_decode_step_qk_norm": (_int, [_vp, _int, _i64, _int, _int, _int, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64,
                                         _vp, _i64, _int, _int, _int, _int, _int, _int, _int, _f32, _vp, _vp, _vp, _vp,
                                         _i64, _f32, _vp, _vp]),
+    "bfly_decode_step_qk_norm_oproj": (_int, [_vp, _int, _i64, _int, _int, _int, _vp, _vp, _vp, _vp, _i64, _vp, _vp,
+                                              _i64, _vp, _i64, _int, _int, _int, _int, _int, _int, _int, _f32, _vp,
+                                              _vp, _vp, _vp, _i64, _f32, _vp, _vp, _i64, _int, _vp, _vp, _vp]),
     "bfly_cache_append": (_int, [_vp, _vp, _int, _i64, _int, _i64, _int, _vp, _vp, _i64, _i64, _vp]),
     "bfly_cache_compress": (_int, [_vp, _vp, _int, _i64, _int, _int, _i64, _i64, _i64, _int, _vp, _vp,
                                    _i64, _i64, _vp]),
@@ -93,6 +96,8 @@ SIGNATURES = {
     "bfly_add_rms_norm_q4_gemv": (_int, [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _i64, _i64, _int, _vp, _vp]),
     "bfly_add_rms_norm_q4_gemv_silu": (_int, [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _i64, _i64, _int, _i64, _vp,
                                               _vp]),
+    "bfly_add_rms_norm_q4_gemv_silu_parts": (_int, [_vp, _int, _vp, _vp, _f32, _vp, _vp, _vp, _i64, _i64, _int,
+                                                    _i64, _vp, _vp]),
 }
 
 _lib = None

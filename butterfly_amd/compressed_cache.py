@@ -27,9 +27,15 @@ from . import _native
 from .attention import _c, _dtype_code, _on, _stream
 
 # int64 words per counter copy in the device counter array of bfly_decode_step:
-# an 8-word header, then one copy per sequence and eight for the step's route
-# workgroups, so bfly_decode_state_words(1, 1) == 8 + 9 * _DEV_SLOT.
+# an 8-word header, then _dev_copies(n) copies per sequence (n = batch * Hkv
+# sequences: 64 when n <= 16, for the attending workgroups of
+# bfly_decode_step_qk_norm_oproj, else 1) and eight for the step's route
+# workgroups, so bfly_decode_state_words(1, 1) == 8 + (64 + 8) * _DEV_SLOT.
 _DEV_SLOT = 32
+
+
+def _dev_copies(n: int) -> int:
+    return 64 if n <= 16 else 1
 # device error word (state[4]) of a failed step: 1 = tail or pool capacity, 2 = a
 # position past the RoPE tables of the fused q/k norm step
 _DEV_ERR_CAPACITY, _DEV_ERR_ROPE = 1, 2
@@ -137,10 +143,11 @@ class CompressedKVCache:
     @property
     def device_counters(self) -> Optional[torch.Tensor]:
         """The device counter array, or None: word 4 is the error flag; sequence g
-        (= batch * Hkv + kv head) keeps a copy of ``_DEV_SLOT`` words at 8 + _DEV_SLOT*g
-        (and eight more copies follow for the kernel's route workgroups): {offset,
-        tail_size, summary_count, summary_offset} in its first four words (all copies
-        equal), then the kernel's cache of the next step's routed row."""
+        (= batch * Hkv + kv head) of n keeps copies of ``_DEV_SLOT`` words at
+        8 + _DEV_SLOT * (g + n * j), j < _dev_copies(n) (eight more copies follow for the
+        kernel's route workgroups): {offset, tail_size, summary_count, summary_offset} in
+        their first four words (all copies equal), then the kernel's cache of the next
+        step's routed row."""
         return self._dev
 
     def sync(self) -> None:
@@ -239,6 +246,50 @@ class CompressedKVCache:
                      out.data_ptr(), _stream(q))
         self._dev_dirty = True
         return out
+
+    def decode_step_oproj(self, q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, *, layer_idx: int,
+                          local_window_tokens: int, qk_norm, o_proj, partner_rule: str = "causal_shift",
+                          local_window_blocks: int = 1, sink_count: int = 1, partner_count: int = 1,
+                          scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                          parts: Optional[torch.Tensor] = None):
+        """``decode_step`` with ``qk_norm`` and the attention output projection ``o_proj`` (a 4-bit
+        ``QuantLinear`` over the hq * d attention row) in the same launch
+        (``bfly_decode_step_qk_norm_oproj``).  Returns ``(out, parts)``: the attention output
+        [B, Hq, 1, d] and the projection's fp32 partial rows per kv head
+        [Hkv, B, o_proj.out_features], whose ``bf16((p0 + p1) + (p2 + p3))`` is ``o_proj`` of
+        ``out`` bit for bit.  16 query heads over 4 kv heads of 128, batch * 4 <= 16,
+        ``out_features`` a multiple of 32 up to 2048 or of 64 up to 4096."""
+        from .attention import _scale
+
+        if self._dev is None:
+            raise ValueError("call use_device_counters() first")
+        b, hq, tq, d = q.shape
+        hkv = int(keys.shape[1])
+        if tq != 1 or keys.shape[2] != 1 or keys.shape != values.shape:
+            raise ValueError("decode_step_oproj takes one new token per sequence")
+        if tuple(keys.shape[:2]) != tuple(self._ring_k.shape[:2]) or d != self._ring_k.shape[3] or \
+                keys.dtype != self._ring_k.dtype or q.dtype != keys.dtype:
+            raise ValueError("q/keys do not match the cache's batch/head/dim/dtype")
+        rule = _native.RULES.get(str(partner_rule))
+        if rule is None:
+            raise ValueError(f"Unsupported Butterfly partner rule: {partner_rule!r}")
+        qw, kw, cos, sin, eps = qk_norm
+        q, keys, values = _c(q), _c(keys), _c(values)
+        if out is None:
+            out = torch.empty_like(q)
+        n_out = int(o_proj.out_features)
+        if parts is None:
+            parts = torch.empty(hkv, b, n_out, dtype=torch.float32, device=q.device)
+        _native.call("bfly_decode_step_qk_norm_oproj", q.data_ptr(), _dtype_code(q), b, hq, hkv, d,
+                     keys.data_ptr(), values.data_ptr(), self._ring_k.data_ptr(), self._ring_v.data_ptr(),
+                     self.tail_capacity, self._pool_k.data_ptr(), self._pool_v.data_ptr(), self.summary_capacity,
+                     self._dev.data_ptr(), int(layer_idx), rule, int(local_window_blocks), int(sink_count),
+                     int(partner_count), self.block_size, int(local_window_tokens), self.local_window_tokens,
+                     _scale(scale, d), qw.data_ptr(), kw.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                     int(cos.shape[0]), float(eps), o_proj.packed.data_ptr(), o_proj.scale_bias.data_ptr(), n_out,
+                     int(o_proj.group), parts.data_ptr(), out.data_ptr(), _stream(q))
+        self._dev_dirty = True
+        return out, parts
 
     # ------------------------------------------------------------------ update
     def _advance(self, keys: torch.Tensor, values: torch.Tensor):

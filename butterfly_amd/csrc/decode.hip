@@ -38,6 +38,7 @@
 // XCD, so the next step reads it with its counters (an L2 hit) and issues its
 // summary loads together with the window loads instead of after the selection.
 #include "bfly_topology.h"
+#include "q4_piece.h"
 
 namespace bfly {
 
@@ -82,6 +83,35 @@ constexpr int kStRoute = 4;
 constexpr int kRouteWords = 12;
 constexpr int kRouteGroups = 8;
 __device__ __forceinline__ int64_t* dec_slot(int64_t* state, int64_t g) { return state + kStHeader + kStSlot * g; }
+
+// Counter copies per sequence.  A step with the attention output projection fused in
+// (bfly_decode_step_qk_norm_oproj) runs several attending workgroups per sequence, each
+// with its own copy, so a state of at most kOprojMaxSeq sequences keeps kOprojSubs copies
+// per sequence: sequence s owns copies s + nseq * c (c < cps), the route workgroups' eight
+// follow at nseq * cps.  Every kernel advances all copies of its sequences, so the entry
+// points can take turns on one state.
+constexpr int kOprojMaxSeq = 16;
+constexpr int kOprojSubs = 64;
+__host__ __device__ __forceinline__ int dec_copies(int64_t nseq) { return nseq <= kOprojMaxSeq ? kOprojSubs : 1; }
+
+// The advanced counters into copies first + stride * c, c in [c0, c1): thread tid writes
+// copy c0 + tid.  clear: also zero both route-buffer keys (kernels that keep no routed rows).
+__device__ __forceinline__ void dec_put_counters(int64_t* state, int64_t first, int64_t stride, int c0, int c1,
+                                                 int tid, int64_t off, int64_t ts, int64_t sc, int64_t so,
+                                                 bool clear) {
+  const int c = c0 + tid;
+  if (c < c1) {
+    int64_t* slot = dec_slot(state, first + stride * c);
+    slot[kStOffset] = off;
+    slot[kStTail] = ts;
+    slot[kStCount] = sc;
+    slot[kStSumOff] = so;
+    if (clear) {
+      slot[kStRoute] = 0;
+      slot[kStRoute + kRouteWords] = 0;
+    }
+  }
+}
 
 
 struct StepArgs {
@@ -169,6 +199,15 @@ struct DecodeArgs {
   FastDiv bs_div, ring_div, hkv_div;   // MFMA path: block_size, ring capacity, Hkv
   int gsz;                             // MFMA path: hq / hkv
   int nseq;                            // MFMA step path: batch * hkv (attending sequences)
+  int cps;                             // step mode: counter copies per sequence (dec_copies)
+  // fused output projection (bfly_decode_step_qk_norm_oproj): W_o in bfly_q4_gemv's layout
+  // ([o_rows][64] pieces, o_groups (scale, bias) words per row, o_ppg pieces per group as a
+  // shift), o_subs attending workgroups per sequence, fp32 partial rows [hkv][batch][o_rows]
+  const u32x4* ow;
+  const uint32_t* osb;
+  float* opart;
+  int o_rows, o_groups, o_ppg_log2, o_subs;
+  FastDiv nseq_div;
   // MFMA step path, d = 128: when qn_w is set, q and k_new are the raw projection
   // rows and the kernel applies the per-head q/k RMSNorm and rotate-half RoPE at
   // position kv_len - 1 itself (rope_cos / rope_sin: [rope_rows][128] fp32)
@@ -535,15 +574,8 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeArgs a, StepArgs s
     // Each workgroup advances its own counter copy; no workgroup reads another's
     // copy, pool, ring or output within the step, so no atomic or fence is
     // needed: the next launch sees everything at the kernel boundary.
-    if (tid == 0) {
-      int64_t* slot = dec_slot(sa.state, blockIdx.x);
-      slot[kStOffset] = st.kv_len;
-      slot[kStTail] = st.ts1;
-      slot[kStCount] = st.sc1;
-      slot[kStSumOff] = st.so1;
-      slot[kStRoute] = 0;                  // this kernel keeps no routed rows
-      slot[kStRoute + kRouteWords] = 0;
-    }
+    // (this kernel keeps no routed rows: their keys are cleared)
+    dec_put_counters(sa.state, blockIdx.x, gridDim.x, 0, a.cps, tid, st.kv_len, st.ts1, st.sc1, st.so1, true);
   }
 }
 
@@ -721,14 +753,16 @@ __device__ __forceinline__ RouteKey route_key(int kv_len, int ns, const DecodeAr
 }
 
 // Route workgroup r of a step launch (blockIdx.x = r < kRouteGroups, 256
-// threads; its counter copy is nseq + r): it advances its own counter copy
-// like every other workgroup, computes the routed row of the NEXT step (whose
+// threads; nseq here counts the attending copies, sequences x copies per
+// sequence, and its own counter copy is nseq + r): it advances its own counter
+// copy like every other workgroup, computes the routed row of the NEXT step (whose
 // counters are the ones this step writes back) with the same functions and
 // inputs as that step's own dec_state32 + dec_select32, and writes it into the
-// route buffer of that step's kv_len parity in the copies of the sequences of
-// the attending workgroups j with j mod 8 = r (attending workgroup j is blockIdx
-// j + 8 and holds sequences spw*j .. spw*j + spw - 1, so it runs on the same
-// XCD).  It touches no q, cache row or output.  sel / hdr: the caller's LDS.
+// route buffer of that step's kv_len parity in the attending copies j with
+// j mod 8 = r (attending workgroup j is blockIdx j + 8 and reads copies
+// spw*j .. spw*j + spw - 1, so it runs on the same XCD).  Every sequence of a
+// step has the same counters, so one row serves every copy.  It touches no q,
+// cache row or output.  sel / hdr: the caller's LDS.
 __device__ __forceinline__ void dec_route_workgroup(const DecodeArgs& a, const StepArgs& sa, int tid, int64_t nseq,
                                                     int spw, int* sel, int64_t* hdr, int nthreads = 256) {
   const int64_t g0 = blockIdx.x;
@@ -904,9 +938,22 @@ __device__ __forceinline__ void dec_pool32(const DecodeArgs& a, const DecState32
 // the counter read needs no kernel-argument load first.
 // kQkn: the fused q/k norm + RoPE (d = 128, bfly_decode_step_qk_norm); a separate
 // instance with room for its registers, for the batch-1 decoder steps it serves.
-template <int D, bool kStep, bool kQkn = false>
+// kOS > 0 (with kQkn): the attention output projection as well
+// (bfly_decode_step_qk_norm_oproj): o_subs attending workgroups per sequence, each
+// computing the sequence's attention and rows [16 kOS sub, 16 kOS (sub + 1)) of the
+// partial product W_o[:, 512 kvh .. 512 kvh + 511] o_kvh (kOS sets of four rows per
+// wave; GQA groups of four heads of 128:
+// sixteen pieces of W_o's rows per kv head).  A lane's piece arithmetic and the sum
+// over the sixteen lanes of a row of 16 are those of bfly_q4_gemv, whose total over
+// the four kv heads is (p0 + p1) + (p2 + p3), so the partial rows combined in that
+// order (bfly_add_rms_norm_q4_gemv_silu_parts) round to bfly_q4_gemv's output bit for
+// bit.  Every attending workgroup of a sequence appends the new token and pools a due
+// block (the same values), so none reads what another writes in the launch.
+template <int D, bool kStep, bool kQkn = false, int kOS = 0>
 __global__ void __launch_bounds__(256, kQkn ? 1 : (D <= 128 ? 3 : 1))
 decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) {
+  constexpr bool kOproj = kOS > 0;
+  static_assert(!kOproj || (kStep && kQkn && D == 128), "the fused projection rides on the q/k-norm step");
   StepArgs sa = sa_in;
   sa.state = state;
   using T = __bf16;
@@ -934,18 +981,22 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   constexpr bool qkn = kQkn && D == 128;
   constexpr int QP = 136;
   __shared__ __attribute__((aligned(16))) T q_lds[qkn ? 16 * QP : 8];
+  // kOproj: the attention output of the group's four heads (the projection's input slice)
+  __shared__ __attribute__((aligned(16))) T o_lds[kOproj ? 4 * D : 8];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
   // step mode: the route workgroups come first (no argument is needed to tell
-  // them apart), attending workgroup bh is blockIdx bh + kRouteGroups
+  // them apart), attending workgroup j is blockIdx j + kRouteGroups
   if constexpr (kStep) {
     if (blockIdx.x < kRouteGroups) {
-      dec_route_workgroup(a, sa, tid, (int64_t)gridDim.x - kRouteGroups, 1, selw[0], route_hdr);
+      dec_route_workgroup(a, sa, tid, (int64_t)a.nseq * a.cps, 1, selw[0], route_hdr);
       return;
     }
   }
-  const int bh = kStep ? (int)blockIdx.x - kRouteGroups : (int)blockIdx.x;
+  // attending workgroup j: its own counter copy j, sequence bh = j mod nseq and
+  // sub-workgroup j / nseq (kOproj; found after the counters are requested)
+  const int jw = kStep ? (int)blockIdx.x - kRouteGroups : (int)blockIdx.x;
   // step mode: this workgroup's counter copy and both route buffers' headers,
   // requested first (the state pointer needs no argument load); the kv_len
   // parity picks a route buffer below
@@ -958,7 +1009,7 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   uint64_t rsel2[SK] = {};                       // entry of buffer b in bits 32 b (shifted, not indexed:
                                                  // a parity-indexed array would live in LDS)
   if constexpr (kStep) {
-    const int64_t* slot = dec_slot(sa.state, bh);
+    const int64_t* slot = dec_slot(sa.state, jw);
 #pragma unroll
     for (int w = 0; w < 4; ++w) cnt[w] = slot[w];
 #pragma unroll
@@ -976,6 +1027,8 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
     // then overlap instead of following each other
     __builtin_amdgcn_sched_barrier(0);
   }
+  const int sub = kOproj ? (int)a.nseq_div.div((uint32_t)jw) : 0;
+  const int bh = kOproj ? jw - sub * a.nseq : jw;
   const int bi = (int)a.hkv_div.div((uint32_t)bh);
   const int kvh = bh - bi * a.hkv;
   const int gsz = a.gsz;
@@ -1002,6 +1055,21 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   };
   if constexpr (qkn) load_q_raw(0);
   else load_q(0);
+  // kOproj: this workgroup's slice of W_o, requested after the staging loads (their data is
+  // needed first; loads return in order) and used last.  Lane (r4, pc) = (lane / 16,
+  // lane % 16) takes piece 16 kvh + pc of rows 16 kOS sub + 4 kOS wave + 4 s + r4.
+  u32x4 owv[kOproj ? kOS : 1];
+  uint32_t osv[kOproj ? kOS : 1];
+  auto load_oproj = [&]() {
+    const uint32_t piece = 16u * (uint32_t)kvh + (uint32_t)(lane & 15);
+    const uint32_t grp = piece >> a.o_ppg_log2;
+#pragma unroll
+    for (int st4 = 0; st4 < kOS; ++st4) {
+      const uint32_t row = (uint32_t)(16 * kOS * sub + 4 * kOS * wave + 4 * st4 + (lane >> 4));
+      owv[st4] = __builtin_nontemporal_load(a.ow + row * 64u + piece);
+      osv[st4] = a.osb[row * (uint32_t)a.o_groups + grp];
+    }
+  };
 
   const DecState32 st =
       kStep ? dec_advance32(cnt[kStOffset], cnt[kStTail], cnt[kStCount], cnt[kStSumOff], a, sa) : dec_state32<false>(a, sa, bh);
@@ -1103,6 +1171,7 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
       skx[it] = *reinterpret_cast<const uint4*>(pk + (uint32_t)n * D + (i % PIECES) * VEC);
       svx[it] = *reinterpret_cast<const uint4*>(pv + (uint32_t)n * D + (i % PIECES) * VEC);
     }
+    if constexpr (kOproj) load_oproj();
     // append the new token to its ring slot; requested after every staging load so
     // that its wait coincides with theirs (the staging reads it from k_new/v_new)
     if (knew != nullptr && tid < 2 * PIECES && !(qkn && tid < PIECES)) {   // normed k: appended below
@@ -1231,19 +1300,38 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
           w[i] = (__bf16)(o[0][i] * inv);
           w[4 + i] = (__bf16)(o[1][i] * inv);
         }
-        *reinterpret_cast<bf16x8*>(orow + mt * 32 + lg * 8) = w;
+        if (!kOproj || sub == 0) *reinterpret_cast<bf16x8*>(orow + mt * 32 + lg * 8) = w;
+        if constexpr (kOproj) *reinterpret_cast<bf16x8*>(o_lds + head * D + mt * 32 + lg * 8) = w;
       }
     }
   }
-  if constexpr (kStep) {
-    // each workgroup advances its own counter copy (see decode_kernel)
-    if (tid == 0) {
-      int64_t* slot = dec_slot(sa.state, bh);
-      slot[kStOffset] = st.kv_len;
-      slot[kStTail] = st.ts1;
-      slot[kStCount] = st.sc1;
-      slot[kStSumOff] = st.so1;
+  if constexpr (kOproj) {
+    // the partial product of this workgroup's rows over the group's 512 outputs: lane piece
+    // pc covers o_lds[32 pc, 32 pc + 32) (head pc / 4, d from 32 (pc % 4))
+    __syncthreads();
+    const int pc = lane & 15;
+    bf16x8 xr[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xr[c] = *reinterpret_cast<const bf16x8*>(o_lds + pc * 32 + 8 * c);
+    float xq[kQ4PieceCodes], xs;
+    q4_piece_x(xr, true, xq, xs);
+    float* prow = a.opart + ((int64_t)kvh * (a.nseq / a.hkv) + bi) * a.o_rows;
+#pragma unroll
+    for (int st4 = 0; st4 < kOS; ++st4) {
+      float acc = 0.f;
+      acc += q4_piece_dot(owv[st4], osv[st4], xq, xs);
+      acc = q4_row16_sum(acc);
+      if (pc == 0) prow[16 * kOS * sub + 4 * kOS * wave + 4 * st4 + (lane >> 4)] = acc;
     }
+  }
+  if constexpr (kStep) {
+    // each workgroup advances its own counter copy (see decode_kernel); the first
+    // workgroup of a sequence also the copies no attending workgroup of this launch owns
+    if (tid == 0)
+      dec_put_counters(sa.state, bh, a.nseq, sub, sub + 1, 0, st.kv_len, st.ts1, st.sc1, st.so1, false);
+    const int own = kOproj ? a.o_subs : 1;
+    if (sub == 0 && tid >= 1)
+      dec_put_counters(sa.state, bh, a.nseq, own, a.cps, tid - 1, st.kv_len, st.ts1, st.sc1, st.so1, false);
   }
 }
 
@@ -1309,7 +1397,7 @@ decode_split_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in)
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
   if (blockIdx.x < kRouteGroups) {
-    dec_route_workgroup(a, sa, tid, a.nseq, 1, selw[0], reinterpret_cast<int64_t*>(lds));
+    dec_route_workgroup(a, sa, tid, (int64_t)a.nseq * a.cps, 1, selw[0], reinterpret_cast<int64_t*>(lds));
     return;
   }
   const int bh = (int)blockIdx.x - kRouteGroups;
@@ -1563,13 +1651,7 @@ decode_split_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in)
     }
     *reinterpret_cast<bf16x8*>(orow + mt * 32 + lg * 8) = w;
   }
-  if (tid == 0) {
-    int64_t* ws = dec_slot(sa.state, bh);
-    ws[kStOffset] = st.kv_len;
-    ws[kStTail] = st.ts1;
-    ws[kStCount] = st.sc1;
-    ws[kStSumOff] = st.so1;
-  }
+  dec_put_counters(sa.state, bh, a.nseq, 0, a.cps, tid, st.kv_len, st.ts1, st.sc1, st.so1, false);
 }
 
 // Sequences (batch x kv heads) from which the step runs decode_split_kernel: measured on
@@ -1607,6 +1689,15 @@ static void launch_decode(const DecodeArgs& a, const StepArgs& sa, int d, int64_
       m.nseq = (int)grid;
       const int64_t mgrid = kStep ? grid + kRouteGroups : grid;   // step mode: plus the route workgroups
       if constexpr (kStep) {
+        if (a.ow != nullptr) {   // the fused output projection: o_subs attending workgroups per sequence
+          m.nseq_div = FastDiv::make((uint32_t)grid);
+          const dim3 og((unsigned)(grid * a.o_subs + kRouteGroups));
+          if (a.o_rows == 32 * a.o_subs)
+            hipLaunchKernelGGL((decode_mfma_kernel<128, true, true, 2>), og, dim3(256), 0, stream, sa.state, m.q, m, sa);
+          else
+            hipLaunchKernelGGL((decode_mfma_kernel<128, true, true, 4>), og, dim3(256), 0, stream, sa.state, m.q, m, sa);
+          return;
+        }
         const int64_t smin = decode_split_min();
         if (d == 128 && a.qn_w == nullptr && m.gsz <= 16 && smin > 0 && grid >= smin) {
           hipLaunchKernelGGL(decode_split_kernel, dim3((unsigned)mgrid), dim3(256), 0, stream, sa.state, m.q, m, sa);
@@ -1700,14 +1791,16 @@ extern "C" int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int 
 
 extern "C" int64_t bfly_decode_state_words(int64_t batch, int hkv) {
   if (batch <= 0 || hkv <= 0) return 0;
-  return kStHeader + kStSlot * (batch * hkv + kRouteGroups);
+  const int64_t nseq = batch * hkv;
+  return kStHeader + kStSlot * (nseq * dec_copies(nseq) + kRouteGroups);
 }
 
 static int decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim, const void* k_new,
                        const void* v_new, void* ring_k, void* ring_v, int64_t ring_capacity, void* pool_k,
                        void* pool_v, int64_t pool_capacity, int64_t* state, int64_t layer_idx, int partner_rule,
                        int local_window_blocks, int sink_count, int partner_count, int block_size, int window,
-                       int cache_window, float scale, void* out, const DecodeArgs* qkn, hipStream_t stream) {
+                       int cache_window, float scale, void* out, const DecodeArgs* qkn, hipStream_t stream,
+                       const DecodeArgs* oproj = nullptr) {
   BFLY_CHECK_ARG(dtype == BFLY_DTYPE_F32 || dtype == BFLY_DTYPE_BF16, "unsupported dtype %d", dtype);
   BFLY_CHECK_ARG(q && k_new && v_new && ring_k && ring_v && pool_k && pool_v && state && out, "null pointer");
   BFLY_CHECK_ARG(aligned16(q) && aligned16(out) && aligned16(ring_k) && aligned16(ring_v) && aligned16(pool_k) &&
@@ -1735,11 +1828,17 @@ static int decode_step(const void* q, int dtype, int64_t batch, int hq, int hkv,
   a.ring_k = ring_k; a.ring_v = ring_v; a.pool_k = pool_k; a.pool_v = pool_v;
   a.ring = ring_capacity; a.kv_rows = ring_capacity; a.pool_rows = pool_capacity;
   a.hq = hq; a.hkv = hkv; a.bs = block_size; a.W = window; a.CW = cache_window; a.scale = scale;
+  a.cps = dec_copies(batch * hkv);
   if (qkn != nullptr) {
     BFLY_CHECK_ARG(dtype == BFLY_DTYPE_BF16 && head_dim == 128 && decode_on_mfma(a, head_dim, true),
                    "bfly_decode_step_qk_norm: bf16, head_dim 128 and a positive scale only");
     a.qn_w = qkn->qn_w; a.kn_w = qkn->kn_w; a.rope_cos = qkn->rope_cos; a.rope_sin = qkn->rope_sin;
     a.rope_rows = qkn->rope_rows; a.qk_eps = qkn->qk_eps;
+  }
+  if (oproj != nullptr) {
+    a.ow = oproj->ow; a.osb = oproj->osb; a.opart = oproj->opart;
+    a.o_rows = oproj->o_rows; a.o_groups = oproj->o_groups; a.o_ppg_log2 = oproj->o_ppg_log2;
+    a.o_subs = oproj->o_subs;
   }
   StepArgs sa{state, layer_idx, partner_rule, local_window_blocks, sink_count, partner_count};
   if (dtype == BFLY_DTYPE_F32)
@@ -1783,4 +1882,50 @@ extern "C" int bfly_decode_step_qk_norm(const void* q, int dtype, int64_t batch,
   return decode_step(q, dtype, batch, hq, hkv, head_dim, k_new, v_new, ring_k, ring_v, ring_capacity, pool_k, pool_v,
                      pool_capacity, state, layer_idx, partner_rule, local_window_blocks, sink_count, partner_count,
                      block_size, window, cache_window, scale, out, &n, stream);
+}
+
+extern "C" int bfly_decode_step_qk_norm_oproj(
+    const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim, const void* k_new, const void* v_new,
+    void* ring_k, void* ring_v, int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity,
+    int64_t* state, int64_t layer_idx, int partner_rule, int local_window_blocks, int sink_count, int partner_count,
+    int block_size, int window, int cache_window, float scale, const void* q_norm_weight, const void* k_norm_weight,
+    const float* rope_cos, const float* rope_sin, int64_t rope_rows, float eps, const void* o_packed,
+    const void* o_scale_bias, int64_t o_out_features, int o_group, float* o_parts, void* out, hipStream_t stream) {
+  BFLY_CHECK_ARG(q_norm_weight && k_norm_weight && rope_cos && rope_sin && o_packed && o_scale_bias && o_parts,
+                 "null pointer");
+  BFLY_CHECK_ARG(aligned16(q_norm_weight) && aligned16(k_norm_weight) && aligned16(rope_cos) && aligned16(rope_sin) &&
+                     aligned16(o_packed) && aligned16(o_parts) && (reinterpret_cast<uintptr_t>(o_scale_bias) & 3) == 0,
+                 "norm weights, RoPE tables, W_o codes and o_parts must be 16-byte aligned (scales 4-byte)");
+  BFLY_CHECK_ARG(rope_rows > 0 && eps >= 0.f, "bad rope_rows / eps");
+  BFLY_CHECK_ARG(head_dim == 128 && hkv == 4 && hq == 16,
+                 "bfly_decode_step_qk_norm_oproj: 16 query heads over 4 kv heads of 128 (got hq=%d hkv=%d d=%d)", hq,
+                 hkv, head_dim);
+  BFLY_CHECK_ARG(batch > 0 && batch * hkv <= kOprojMaxSeq, "bfly_decode_step_qk_norm_oproj: batch * hkv <= %d",
+                 kOprojMaxSeq);
+  BFLY_CHECK_ARG(o_group >= 32 && o_group <= 2048 && (o_group & (o_group - 1)) == 0,
+                 "o_group=%d must be a power of two in [32, 2048]", o_group);
+  // 32 rows per attending workgroup (two sets of four per wave) while that needs at most
+  // kOprojSubs workgroups per sequence, else 64
+  const bool rows32 = o_out_features % 32 == 0 && o_out_features <= 32 * kOprojSubs;
+  BFLY_CHECK_ARG(o_out_features > 0 && (rows32 || (o_out_features % 64 == 0 && o_out_features <= 64 * kOprojSubs)),
+                 "o_out_features=%lld must be a multiple of 32 up to %d or of 64 up to %d", (long long)o_out_features,
+                 32 * kOprojSubs, 64 * kOprojSubs);
+  DecodeArgs n{};
+  n.qn_w = static_cast<const __bf16*>(q_norm_weight);
+  n.kn_w = static_cast<const __bf16*>(k_norm_weight);
+  n.rope_cos = rope_cos;
+  n.rope_sin = rope_sin;
+  n.rope_rows = rope_rows;
+  n.qk_eps = eps;
+  DecodeArgs o{};
+  o.ow = static_cast<const u32x4*>(o_packed);
+  o.osb = static_cast<const uint32_t*>(o_scale_bias);
+  o.opart = o_parts;
+  o.o_rows = (int)o_out_features;
+  o.o_groups = 2048 / o_group;
+  o.o_ppg_log2 = __builtin_ctz((unsigned)(o_group / kQ4PieceCodes));
+  o.o_subs = (int)(o_out_features / (rows32 ? 32 : 64));
+  return decode_step(q, dtype, batch, hq, hkv, head_dim, k_new, v_new, ring_k, ring_v, ring_capacity, pool_k, pool_v,
+                     pool_capacity, state, layer_idx, partner_rule, local_window_blocks, sink_count, partner_count,
+                     block_size, window, cache_window, scale, out, &n, stream, &o);
 }

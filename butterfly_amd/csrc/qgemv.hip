@@ -13,31 +13,14 @@
 // fp32 throughout; y is rounded once to bf16.  The results equal the product
 // with the fp32 weights code * scale + bias up to the fp32 summation order.
 #include "bfly_common.h"
+#include "q4_piece.h"
 #include "rmsnorm_row.h"
 #include "../../include/butterfly_amd_decoder.h"
 
 namespace bfly {
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int kQ4PieceCodes = 32;      // codes in one 16-byte piece of a row
 constexpr int kQ4MaxPieces = 4;        // pieces per lane: in_features <= 64 * 4 * 32 = 8192
 constexpr int64_t kQ4MaxWaves = 8192;  // grid cap; the waves stride over the row sets
-
-// v summed over the 64 lanes, the total in every lane: halves and rows of 16 by
-// v_permlane32/16_swap, then rotations by 8 and 4 inside each row of 16 and two
-// quad permutations (DPP); no LDS traffic.
-__device__ __forceinline__ float q4_wave_sum(float v) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(b[0]) + __uint_as_float(b[1]);
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));  // row_ror:8
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, false));  // row_ror:4
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));   // quad_perm 2,3,0,1
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
-  return v;
-}
 
 // SiLU(gate) * up with the rounding points of the separate steps: the projection
 // outputs are bf16, SiLU is rounded to bf16, then the product (the formula of
@@ -133,23 +116,7 @@ __device__ __forceinline__ void q4_sets(const Q4Args& a, int lane, int64_t set0,
   }
 
 #pragma unroll
-  for (int j = 0; j < NP; ++j) {
-    const bool valid = lane + 64 * j < pieces;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xq[j][8 * c + e] = valid ? (float)xr[j][c][e] : 0.f;
-  }
-#pragma unroll
-  for (int j = 0; j < NP; ++j) {
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < kQ4PieceCodes; ++i) {
-      s += xq[j][i];
-      if (i & 1) xq[j][i] *= 0.0625f;
-    }
-    xs[j] = s;
-  }
+  for (int j = 0; j < NP; ++j) q4_piece_x(xr[j], lane + 64 * j < pieces, xq[j], xs[j]);
 
   for (int64_t set = set0; set < a.n_sets; set += stride) {
     const int64_t o0 = set * OUTS;
@@ -158,25 +125,7 @@ __device__ __forceinline__ void q4_sets(const Q4Args& a, int lane, int64_t set0,
     for (int r = 0; r < R; ++r) {
       float acc = 0.f;
 #pragma unroll
-      for (int j = 0; j < NP; ++j) {
-        const uint32_t dw[4] = {wv[r][j][0], wv[r][j][1], wv[r][j][2], wv[r][j][3]};
-        float lo_sum = 0.f, hi_sum = 0.f;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          uint32_t lo = dw[t] & 0x0F0F0F0Fu, hi = dw[t] & 0xF0F0F0F0u;
-          // opaque to the combiner, so each byte converts with v_cvt_f32_ubyte{0..3}
-          // instead of a bit-field extract of the unmasked word and a conversion
-          asm volatile("" : "+v"(lo), "+v"(hi));
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            lo_sum += xq[j][8 * t + 2 * b] * (float)((lo >> (8 * b)) & 0xFFu);
-            hi_sum += xq[j][8 * t + 2 * b + 1] * (float)((hi >> (8 * b)) & 0xFFu);
-          }
-        }
-        const float scale = __uint_as_float(sv[r][j] << 16);
-        const float bias = __uint_as_float(sv[r][j] & 0xFFFF0000u);
-        acc += scale * (lo_sum + hi_sum) + bias * xs[j];
-      }
+      for (int j = 0; j < NP; ++j) acc += q4_piece_dot(wv[r][j], sv[r][j], xq[j], xs[j]);
       tot[r] = acc;
     }
     if (set + stride < a.n_sets) load_set(set + stride);
@@ -204,16 +153,19 @@ __global__ void __launch_bounds__(64) q4_gemv_kernel(Q4Args a) {
 // The residual add + RMSNorm of the input row inside the product: NW waves (8 or 12);
 // threads 0..255 form h = x + residual and its normed row exactly as bfly_add_rms_norm does
 // (into LDS; workgroup 0 also writes h), then each of the NW waves runs its sets on that row.
-// in_features = 256 PER.
+// in_features = 256 PER.  kParts: x is not given as a row but as four fp32 partial rows
+// (parts[g * in_features + i]), and x_i = bf16((p0_i + p1_i) + (p2_i + p3_i)) -- the
+// rounding of a product whose four 16-piece partials are combined by q4_wave_sum.
 struct Q4NormArgs {
   const __bf16* x;
   const __bf16* residual;   // or null (then h_out is null: a plain RMSNorm)
   const __bf16* weight;
   __bf16* h_out;
   float eps;
+  const float* parts;       // kParts: the four partial rows
 };
 
-template <int NP, int R, bool kSilu, int PER, int NW>
+template <int NP, int R, bool kSilu, int PER, int NW, bool kParts>
 __global__ void __launch_bounds__(64 * NW) q4_norm_gemv_kernel(Q4Args a, Q4NormArgs nm) {
   static_assert(NW >= 4, "the row is formed by the first 256 threads");
   constexpr int DIM = 256 * PER;
@@ -223,8 +175,27 @@ __global__ void __launch_bounds__(64 * NW) q4_norm_gemv_kernel(Q4Args a, Q4NormA
   const int64_t waves = (int64_t)gridDim.x * NW;
   // the norm's inputs are requested before the weights, so that forming the row waits for them
   // alone and runs while the weights are in flight
-  const RmsRowIn<PER> in = rms_row_load<PER>(nm.x, nm.residual, nm.weight, tid, tid < 256);
+  RmsRowIn<PER> in = rms_row_load<PER, !kParts>(nm.x, nm.residual, nm.weight, tid, tid < 256);
+  f32x4 pp[kParts ? 4 : 1][kParts ? PER / 4 : 1];
+  if constexpr (kParts) {
+    if (tid < 256) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int c = 0; c < PER / 4; ++c)
+          pp[g][c] = *reinterpret_cast<const f32x4*>(nm.parts + (int64_t)g * DIM + (int64_t)tid * PER + 4 * c);
+    }
+  }
   q4_sets<NP, R, kSilu, false>(a, lane, (int64_t)blockIdx.x * NW + wave, waves, reinterpret_cast<const bf16x8*>(xn), [&] {
+    if constexpr (kParts) {
+#pragma unroll
+      for (int c = 0; c < PER / 8; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = 8 * c + e;
+          in.x[c][e] = (__bf16)((pp[0][i / 4][i % 4] + pp[1][i / 4][i % 4]) + (pp[2][i / 4][i % 4] + pp[3][i / 4][i % 4]));
+        }
+    }
     add_rmsnorm_row_from<PER>(in, nm.residual != nullptr, blockIdx.x == 0 ? nm.h_out : nullptr, xn, DIM, nm.eps, tid,
                               tid < 256, part);
     __syncthreads();   // the normed row is in LDS
@@ -263,13 +234,13 @@ void q4_dispatch(Q4Args a, int64_t in_features, int group, hipStream_t stream) {
   }
 }
 
-template <int NP, int R, bool kSilu, int PER, int NW = 8>
+template <int NP, int R, bool kSilu, int PER, int NW = 8, bool kParts = false>
 void q4_norm_launch(Q4Args a, Q4NormArgs nm, hipStream_t stream) {
   constexpr int OUTS = kSilu ? R / 2 : R;
   a.n_sets = (a.n_out + OUTS - 1) / OUTS;
   const int64_t iters = (a.n_sets + kQ4MaxWaves - 1) / kQ4MaxWaves;
   const int64_t waves = (a.n_sets + iters - 1) / iters;
-  hipLaunchKernelGGL((q4_norm_gemv_kernel<NP, R, kSilu, PER, NW>), dim3((unsigned)((waves + NW - 1) / NW)),
+  hipLaunchKernelGGL((q4_norm_gemv_kernel<NP, R, kSilu, PER, NW, kParts>), dim3((unsigned)((waves + NW - 1) / NW)),
                      dim3(64 * NW), 0, stream, a, nm);
 }
 
@@ -278,7 +249,7 @@ void q4_norm_launch(Q4Args a, Q4NormArgs nm, hipStream_t stream) {
 // SiLU form at four rows per set runs 12 waves per workgroup: cfg5's gate|up (3072 sets) is then
 // 256 workgroups, one per CU, where 8 waves gave 384 and half the CUs ran two (7.26 -> 6.35 us,
 // graph-replayed over 24 weight sets; other shapes measured no faster).
-template <bool kSilu>
+template <bool kSilu, bool kParts = false>
 void q4_norm_dispatch(Q4Args a, Q4NormArgs nm, int64_t in_features, int group, hipStream_t stream) {
   a.pieces = (int)(in_features / kQ4PieceCodes);
   a.groups = (int)(in_features / group);
@@ -287,14 +258,14 @@ void q4_norm_dispatch(Q4Args a, Q4NormArgs nm, int64_t in_features, int group, h
   switch (in_features / 256) {
     case 8:
       if (sets4 >= 2048 && kSilu)
-        q4_norm_launch<1, 4, kSilu, 8, 12>(a, nm, stream);
+        q4_norm_launch<1, 4, kSilu, 8, 12, kParts>(a, nm, stream);
       else if (sets4 >= 2048)
-        q4_norm_launch<1, 4, kSilu, 8>(a, nm, stream);
+        q4_norm_launch<1, 4, kSilu, 8, 8, kParts>(a, nm, stream);
       else
-        q4_norm_launch<1, 2, kSilu, 8>(a, nm, stream);
+        q4_norm_launch<1, 2, kSilu, 8, 8, kParts>(a, nm, stream);
       break;
-    case 16: q4_norm_launch<2, 2, kSilu, 16>(a, nm, stream); break;
-    default: q4_norm_launch<3, 2, kSilu, 24>(a, nm, stream); break;
+    case 16: q4_norm_launch<2, 2, kSilu, 16, 8, kParts>(a, nm, stream); break;
+    default: q4_norm_launch<3, 2, kSilu, 24, 8, kParts>(a, nm, stream); break;
   }
 }
 
@@ -390,5 +361,29 @@ extern "C" int bfly_add_rms_norm_q4_gemv_silu(const void* x, const void* residua
   a.up_off = up_row_offset;
   q4_norm_dispatch<true>(a, nm, in_features, group, stream);
   BFLY_CHECK_LAUNCH("bfly_add_rms_norm_q4_gemv_silu");
+  return BFLY_OK;
+}
+
+extern "C" int bfly_add_rms_norm_q4_gemv_silu_parts(const float* x_parts, int n_parts, const void* residual,
+                                                    const void* norm_weight, float eps, void* h_out,
+                                                    const void* packed, const void* scale_bias, int64_t out_features,
+                                                    int64_t in_features, int group, int64_t up_row_offset, void* out,
+                                                    hipStream_t stream) {
+  BFLY_CHECK_ARG(x_parts != nullptr && n_parts == 4, "x_parts: four partial rows (n_parts=%d)", n_parts);
+  BFLY_CHECK_ARG(aligned16(x_parts), "x_parts must be 16-byte aligned");
+  // x is only checked for null / alignment; the partial rows stand in for it
+  int rc = q4_check(x_parts, packed, scale_bias, out_features, in_features, group, out);
+  if (rc) return rc;
+  rc = q4_norm_check(x_parts, residual, norm_weight, h_out, in_features);
+  if (rc) return rc;
+  BFLY_CHECK_ARG(up_row_offset >= out_features, "up_row_offset=%lld overlaps the gate rows",
+                 (long long)up_row_offset);
+  const Q4NormArgs nm{nullptr, static_cast<const __bf16*>(residual), static_cast<const __bf16*>(norm_weight),
+                      static_cast<__bf16*>(h_out), eps, x_parts};
+  Q4Args a = q4_args(x_parts, packed, scale_bias, out_features, out);
+  a.x = nullptr;
+  a.up_off = up_row_offset;
+  q4_norm_dispatch<true, true>(a, nm, in_features, group, stream);
+  BFLY_CHECK_LAUNCH("bfly_add_rms_norm_q4_gemv_silu_parts");
   return BFLY_OK;
 }

@@ -26,8 +26,8 @@ struct RmsRowIn {
 // Thread t < 256 of the participating threads holds elements [t PER, t PER + PER)
 // of the row (dim = 256 PER), 16-byte pieces (PER a multiple of 8, every pointer 16-byte
 // aligned).  Requested apart from the arithmetic, so that a caller can issue them ahead of
-// other loads and not wait for those.
-template <int PER>
+// other loads and not wait for those.  kX false: x is not read (the caller forms in.x).
+template <int PER, bool kX = true>
 __device__ __forceinline__ RmsRowIn<PER> rms_row_load(const __bf16* __restrict__ x, const __bf16* __restrict__ y,
                                                       const __bf16* __restrict__ w, int t, bool active) {
   RmsRowIn<PER> in{};
@@ -35,7 +35,7 @@ __device__ __forceinline__ RmsRowIn<PER> rms_row_load(const __bf16* __restrict__
     const int64_t base = (int64_t)t * PER;
 #pragma unroll
     for (int c = 0; c < PER / 8; ++c) {
-      in.x[c] = *reinterpret_cast<const bf16x8*>(x + base + 8 * c);
+      if constexpr (kX) in.x[c] = *reinterpret_cast<const bf16x8*>(x + base + 8 * c);
       if (y != nullptr) in.y[c] = *reinterpret_cast<const bf16x8*>(y + base + 8 * c);
       in.w[c] = *reinterpret_cast<const bf16x8*>(w + base + 8 * c);
     }

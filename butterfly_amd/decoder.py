@@ -155,6 +155,9 @@ class QuantLinear(nn.Module):
 
 # shape limits of bfly_q4_gemv / bfly_q4_gemv_silu (include/butterfly_amd_decoder.h)
 Q4_PIECE_CODES, Q4_MAX_IN = 32, 8192
+# decode steps of a swapped layer run its output projection in the decode-step launch where
+# the shapes allow (ButterflyAttention.takes_o_proj); False keeps it a launch of its own
+FUSE_O_PROJ = True
 
 
 def _one_row(x: torch.Tensor) -> bool:
@@ -234,6 +237,26 @@ def add_rms_norm_q4_gemv_silu(x: torch.Tensor, residual: Optional[torch.Tensor],
                      gate_up.packed.data_ptr(), gate_up.scale_bias.data_ptr(), f, gate_up.in_features,
                      gate_up.group, f, out.data_ptr(), stream_of(x))
     return (h.view(x.shape) if rr is not None else x), out
+
+
+def add_rms_norm_q4_gemv_silu_parts(x: torch.Tensor, parts: torch.Tensor, weight: torch.Tensor, eps: float,
+                                    gate_up: QuantLinear):
+    """``add_rms_norm_q4_gemv_silu(x, a, ...)`` where the residual branch ``a`` is given as four fp32
+    partial rows ``parts`` [4, 1, hidden] (``a = bf16((p0 + p1) + (p2 + p3))``, the output
+    projection of ``CompressedKVCache.decode_step_oproj``), in one launch of
+    ``bfly_add_rms_norm_q4_gemv_silu_parts``: ``x`` is this layer's residual input, ``h = x + a``."""
+    xr = _row16(x)
+    if parts.dtype != torch.float32 or not parts.is_contiguous() or parts.numel() != 4 * xr.numel() or \
+            parts.data_ptr() % 16:
+        raise ValueError("parts must be a contiguous, 16-byte aligned fp32 [4, 1, hidden] tensor")
+    h = torch.empty_like(xr)
+    f = gate_up.out_features // 2
+    out = torch.empty(*x.shape[:-1], f, dtype=torch.bfloat16, device=x.device)
+    with on(x.device):
+        _native.call("bfly_add_rms_norm_q4_gemv_silu_parts", parts.data_ptr(), 4, xr.data_ptr(), weight.data_ptr(),
+                     float(eps), h.data_ptr(), gate_up.packed.data_ptr(), gate_up.scale_bias.data_ptr(), f,
+                     gate_up.in_features, gate_up.group, f, out.data_ptr(), stream_of(x))
+    return h.view(x.shape), out
 
 
 def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
@@ -454,9 +477,7 @@ class ButterflyAttention(QwenButterflyAttention):
         return (isinstance(rope, RopeTable) and _one_row(x)
                 and self.core.fuses_qk_norm(cache, 1, c.head_dim, x.dtype))
 
-    def forward_qkv_row(self, qkv: torch.Tensor, cache, rope) -> torch.Tensor:
-        """The decode step from the fused projection's raw output row (``base.qkv`` of the
-        normed input; ``takes_qkv_row`` held), through the output projection."""
+    def _qkv_row(self, qkv: torch.Tensor, rope):
         base, c = self.base, self.base.cfg
         row = qkv.view(-1)
         nq, nkv = c.num_heads * c.head_dim, c.num_kv_heads * c.head_dim
@@ -464,7 +485,32 @@ class ButterflyAttention(QwenButterflyAttention):
         k = row[nq:nq + nkv].view(1, c.num_kv_heads, 1, c.head_dim)
         v = row[nq + nkv:].view(1, c.num_kv_heads, 1, c.head_dim)
         qk = (base.q_norm.weight, base.k_norm.weight, rope.cos_tab, rope.sin_tab, base.q_norm.eps)
-        return base.output(self.core(q, k, v, cache, qk_norm=qk))
+        return q, k, v, qk
+
+    def forward_qkv_row(self, qkv: torch.Tensor, cache, rope) -> torch.Tensor:
+        """The decode step from the fused projection's raw output row (``base.qkv`` of the
+        normed input; ``takes_qkv_row`` held), through the output projection."""
+        q, k, v, qk = self._qkv_row(qkv, rope)
+        return self.base.output(self.core(q, k, v, cache, qk_norm=qk))
+
+    def takes_o_proj(self, x: torch.Tensor, cache, rope) -> bool:
+        """Whether this decode step also runs the output projection in its launch
+        (``forward_qkv_row_parts``): a ``takes_qkv_row`` step of 16 query heads over 4 kv heads of
+        128 whose o_proj is a 4-bit layer of 2048 inputs, a power-of-two group and a multiple of 32
+        outputs up to 2048 or of 64 up to 4096 (``bfly_decode_step_qk_norm_oproj``)."""
+        c, o = self.base.cfg, self.base.o_proj
+        n = o.out_features if isinstance(o, QuantLinear) else 0
+        return (FUSE_O_PROJ and c.num_heads == 16 and c.num_kv_heads == 4 and c.head_dim == 128
+                and isinstance(o, QuantLinear) and o.gemv_from_codes and o.in_features == 2048
+                and ((n % 32 == 0 and 0 < n <= 2048) or (n % 64 == 0 and 0 < n <= 4096))
+                and o.group & (o.group - 1) == 0 and self.takes_qkv_row(x, cache, rope))
+
+    def forward_qkv_row_parts(self, qkv: torch.Tensor, cache, rope) -> torch.Tensor:
+        """``forward_qkv_row`` with the output projection inside the decode step
+        (``takes_o_proj`` held): returns its four fp32 partial rows [4, 1, hidden], which
+        ``add_rms_norm_q4_gemv_silu_parts`` combines into the projection's bf16 row."""
+        q, k, v, qk = self._qkv_row(qkv, rope)
+        return self.core.step_oproj(q, k, v, cache, qk, self.base.o_proj)[1]
 
 
 register_butterfly_attention(Attention, ButterflyAttention)
@@ -521,6 +567,13 @@ class DecoderLayer(nn.Module):
                 and norm_q4_fits(x, attn.base.qkv)):
             # a decode step: each norm rides in the launch of the product that consumes it
             x, qkv = add_rms_norm_q4_gemv(x, pending, ln.weight, ln.eps, attn.base.qkv)
+            if (attn.takes_o_proj(x, cache, rope) and norm_q4_fits(x, mlp.gate_up)
+                    and mlp.down_proj.gemv_from_codes):
+                # and the output projection rides in the decode step: its partial rows go
+                # straight into the post-attention norm of the gate|up launch
+                parts = attn.forward_qkv_row_parts(qkv, cache, rope)
+                h, s = add_rms_norm_q4_gemv_silu_parts(x, parts, post.weight, post.eps, mlp.gate_up)
+                return h, mlp.down_proj(s)
             a = attn.forward_qkv_row(qkv, cache, rope)
         else:
             x, n = add_rms_norm(x, pending, ln.weight, ln.eps)

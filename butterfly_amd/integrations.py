@@ -249,6 +249,25 @@ class ButterflyAttentionCore:
                 and cache.step_on_mfma(head_dim, int(self.cfg.compressed_local_window_tokens),
                                        _scale(self.scale, head_dim), dtype))
 
+    def step_oproj(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cache: CompressedKVCache, qk_norm,
+                   o_proj):
+        """A ``fuses_qk_norm`` device step that also applies the 4-bit output projection
+        ``o_proj`` (``CompressedKVCache.decode_step_oproj``); returns the attention output and the
+        projection's fp32 partial rows per kv head [Hkv, B, out_features]."""
+        t0 = _now_ms()
+        _require_cuda(q, k, v)
+        d = int(q.shape[3])
+        if not self.fuses_qk_norm(cache, int(q.shape[2]), d, q.dtype):
+            raise ValueError("step_oproj takes device-counter decode steps of bf16, head_dim 128 rows only")
+        c = self.cfg
+        out, parts = cache.decode_step_oproj(
+            q, k, v, layer_idx=self.layer_idx, local_window_tokens=int(c.compressed_local_window_tokens),
+            qk_norm=qk_norm, o_proj=o_proj, partner_rule=c.block_partner_rule,
+            local_window_blocks=c.block_local_window_blocks, sink_count=c.block_sink_blocks,
+            partner_count=c.block_partner_count, scale=self.scale)
+        self._last = (t0, _now_ms(), None, "block_sparse_compressed_active", _DEVICE_STEP_NOTES, None)
+        return out, parts
+
     def __call__(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                  cache: Optional[CompressedKVCache] = None, qk_norm=None) -> torch.Tensor:
         """``qk_norm`` (see ``CompressedKVCache.decode_step``) hands raw q/k projection rows to

@@ -276,10 +276,12 @@ int bfly_decode(const void* q, int dtype, int64_t batch, int hq, int hkv, int he
                 float scale, void* out, hipStream_t stream);
 
 /*
- * Length in int64 words of the bfly_decode_step counter array for batch*hkv
- * sequences: an 8-word header (word 4: error) and batch*hkv + 8 copies of 32
- * words (one per sequence, eight for the step's route workgroups).  No
- * counterpart in the reference (its counters are host attributes).
+ * Length in int64 words of the bfly_decode_step counter array for n = batch*hkv
+ * sequences: an 8-word header (word 4: error) and n*c + 8 copies of 32 words,
+ * c = 64 copies per sequence when n <= 16 (the attending workgroups of
+ * bfly_decode_step_qk_norm_oproj), else 1; sequence s owns copies s + n*j
+ * (j < c), the step's eight route workgroups the last eight.  No counterpart in
+ * the reference (its counters are host attributes).
  */
 int64_t bfly_decode_state_words(int64_t batch, int hkv);
 
@@ -295,10 +297,11 @@ int64_t bfly_decode_state_words(int64_t batch, int hkv);
  * ceil(kv_len / BS) blocks).  cache_window in [1, 2^20); the ring must hold
  * cache_window + BS rows.
  * state: device int64[bfly_decode_state_words(batch, hkv)]: state[4] is the
- * error word; copy g (32 words at state[8 + 32g ..], g = b*Hkv + kv head, and
- * g = batch*Hkv + 0..7 for the route workgroups) holds {offset, tail_size,
- * summary_count, summary_offset} in words 0..3, advanced by its workgroup (all
- * copies stay equal; initialise every copy), and words 4..31 hold the kernel's
+ * error word; copy g (32 words at state[8 + 32g ..], the copies of sequence
+ * b*Hkv + kv head and the route workgroups' as bfly_decode_state_words lays
+ * them out) holds {offset, tail_size, summary_count, summary_offset} in words
+ * 0..3, advanced by the step (all copies stay equal; initialise every copy; the
+ * host reads copy 0), and words 4..31 hold the kernel's
  * own cache of the next step's routed row (initialise to zero: zero is "none";
  * the kernel uses an entry only when it names the step's kv_len and
  * arguments).  On a capacity
@@ -336,6 +339,35 @@ int bfly_decode_step_qk_norm(const void* q, int dtype, int64_t batch, int hq, in
                              int sink_count, int partner_count, int block_size, int window, int cache_window,
                              float scale, const void* q_norm_weight, const void* k_norm_weight, const float* rope_cos,
                              const float* rope_sin, int64_t rope_rows, float eps, void* out, hipStream_t stream);
+
+/*
+ * Device: bfly_decode_step_qk_norm with the attention output projection of a
+ * decoder layer applied in the same launch, as partial products per kv head:
+ * o_parts[g][b][i] (fp32, [hkv][batch][o_out_features]) = row i of
+ * W_o[:, 512 g .. 512 g + 511] times the attention output of kv head g's four
+ * query heads, W_o in bfly_q4_gemv's 4-bit layout (o_packed / o_scale_bias,
+ * in_features = hq * head_dim = 2048, group o_group: a power of two in [32, 2048]).
+ * The partial rows combined as (p0 + p1) + (p2 + p3) and rounded to bf16 equal
+ * bfly_q4_gemv over `out` bit for bit (bfly_add_rms_norm_q4_gemv_silu_parts takes
+ * them so).  `out` still receives the attention output.  Shapes: 16 query heads
+ * over 4 kv heads of 128, batch * 4 <= 16, o_out_features a multiple of 32 up to
+ * 2048 or of 64 up to 4096 (else BFLY_ERR_INVALID).  The launch runs
+ * o_out_features / 32 (beyond 2048: / 64) workgroups per sequence, each computing
+ * the attention (every one appends the same token and pools the same due block)
+ * and 32 (64) rows of the product.  Replaces
+ * the swapped attention's output projection (bna/integrations/qwen_mlx.py:1295-1792
+ * projects the attention output with the layer's o_proj; qwen_torch.py:1221-1622)
+ * together with bfly_decode_step_qk_norm in one launch.
+ */
+int bfly_decode_step_qk_norm_oproj(const void* q, int dtype, int64_t batch, int hq, int hkv, int head_dim,
+                                   const void* k_new, const void* v_new, void* ring_k, void* ring_v,
+                                   int64_t ring_capacity, void* pool_k, void* pool_v, int64_t pool_capacity,
+                                   int64_t* state, int64_t layer_idx, int partner_rule, int local_window_blocks,
+                                   int sink_count, int partner_count, int block_size, int window, int cache_window,
+                                   float scale, const void* q_norm_weight, const void* k_norm_weight,
+                                   const float* rope_cos, const float* rope_sin, int64_t rope_rows, float eps,
+                                   const void* o_packed, const void* o_scale_bias, int64_t o_out_features,
+                                   int o_group, float* o_parts, void* out, hipStream_t stream);
 
 /*
  * Device: append `step` new tokens at positions [offset, offset+step) of the

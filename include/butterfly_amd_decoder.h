@@ -131,6 +131,20 @@ int bfly_add_rms_norm_q4_gemv_silu(const void* x, const void* residual, const vo
                                    int64_t out_features, int64_t in_features, int group,
                                    int64_t up_row_offset, void* out, hipStream_t stream);
 
+/*
+ * Device: bfly_add_rms_norm_q4_gemv_silu whose input row x is given as n_parts = 4
+ * fp32 partial rows x_parts[g * in_features + i] and formed as
+ * x_i = bf16((p0_i + p1_i) + (p2_i + p3_i)): the o_parts of
+ * bfly_decode_step_qk_norm_oproj (include/butterfly_amd.h), for which x is then
+ * bfly_q4_gemv's output projection of the attention row bit for bit.  x_parts
+ * 16-byte aligned; other limits as bfly_add_rms_norm_q4_gemv_silu.  No counterpart
+ * in the reference's own code.
+ */
+int bfly_add_rms_norm_q4_gemv_silu_parts(const float* x_parts, int n_parts, const void* residual,
+                                         const void* norm_weight, float eps, void* h_out, const void* packed,
+                                         const void* scale_bias, int64_t out_features, int64_t in_features,
+                                         int group, int64_t up_row_offset, void* out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

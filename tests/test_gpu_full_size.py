@@ -225,8 +225,9 @@ def _oracle_rows(q, kh, vh, lay, tq, W):
 @pytest.mark.timeout(900)
 def test_cfg5_graph_replayed_steps_match_oracle_at_32768(monkeypatch):
     """The decode steps the benchmark times: after a 32768-token prompt, every layer's
-    ``bfly_decode_step_qk_norm`` inside the captured greedy step (replayed from one HIP graph,
-    device counters) against the oracle's active row over that layer's full key history."""
+    ``bfly_decode_step_qk_norm_oproj`` inside the captured greedy step (replayed from one HIP
+    graph, device counters) against the oracle's active row over that layer's full key history,
+    and its output projection's partial rows against ``bfly_q4_gemv`` of that row."""
     from butterfly_amd.decoder import Decoder, DecoderConfig
 
     cfg = DecoderConfig()
@@ -238,23 +239,33 @@ def test_cfg5_graph_replayed_steps_match_oracle_at_32768(monkeypatch):
                                     max_kv_size=prompt_len + 64, max_chunk_size=prompt_len + 64)
     prompt_kv, rows, bufs = {}, {l: [] for l in range(cfg.num_layers)}, {}
     real_call = bf.ButterflyAttentionCore.__call__
+    real_step = bf.ButterflyAttentionCore.step_oproj
 
-    def recording(core, q, k, v, cache=None, qk_norm=None):
-        out = real_call(core, q, k, v, cache, qk_norm=qk_norm)
-        layer = core.layer_idx
-        if q.shape[2] > 1:                                     # the prompt: normed, rotated k and v
-            prompt_kv[layer] = (k.cpu(), v.cpu())
-            return out
-        assert qk_norm is not None, "a device-counter decode step takes the raw q|k|v rows"
+    def record(layer, ts):
         if layer not in bufs:                                  # the eager first step, before capture
-            bufs[layer] = [torch.empty_like(t) for t in (q, k, v, out)]
-        for b_, t_ in zip(bufs[layer], (q, k, v, out)):
+            bufs[layer] = [torch.empty_like(t) for t in ts]
+        for b_, t_ in zip(bufs[layer], ts):
             b_.copy_(t_)                                       # recorded into the graph as well
         if not torch.cuda.is_current_stream_capturing():
             rows[layer].append([t_.cpu() for t_ in bufs[layer]])
+
+    def recording(core, q, k, v, cache=None, qk_norm=None):
+        out = real_call(core, q, k, v, cache, qk_norm=qk_norm)
+        if q.shape[2] > 1:                                     # the prompt: normed, rotated k and v
+            prompt_kv[core.layer_idx] = (k.cpu(), v.cpu())
+            return out
+        assert qk_norm is not None, "a device-counter decode step takes the raw q|k|v rows"
+        record(core.layer_idx, (q, k, v, out))
         return out
 
+    def recording_oproj(core, q, k, v, cache, qk_norm, o_proj):
+        # the step with the output projection inside: its attention row and partial rows
+        out, parts = real_step(core, q, k, v, cache, qk_norm, o_proj)
+        record(core.layer_idx, (q, k, v, out, parts))
+        return out, parts
+
     monkeypatch.setattr(bf.ButterflyAttentionCore, "__call__", recording)
+    monkeypatch.setattr(bf.ButterflyAttentionCore, "step_oproj", recording_oproj)
     prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=torch.Generator().manual_seed(9)).cuda()
     logits = model.forward(prompt, caches, 0)
     torch.cuda.synchronize()
@@ -268,11 +279,20 @@ def test_cfg5_graph_replayed_steps_match_oracle_at_32768(monkeypatch):
     monkeypatch.undo()
     steps = new_tokens - 1
     worst = [0.0, 0.0, 0.0]
+    from butterfly_amd.decoder import q4_gemv
+
     for layer in range(cfg.num_layers):
         assert len(rows[layer]) == steps
         base = model.layers[layer].self_attn.base
         kh, vh = prompt_kv[layer]
-        for s_, (qr, kr, vr, out) in enumerate(rows[layer]):
+        for s_, rec in enumerate(rows[layer]):
+            qr, kr, vr, out = rec[:4]
+            # cfg5's shapes take the output projection into the step: its partial rows combine
+            # into bfly_q4_gemv's product of the attention row bit for bit
+            assert len(rec) == 5, "cfg5's decode steps run the output projection inside"
+            pr = rec[4]
+            y = q4_gemv(out.reshape(1, -1).cuda(), base.o_proj).cpu()
+            assert torch.equal(((pr[0] + pr[1]) + (pr[2] + pr[3])).bfloat16(), y.view(pr.shape[1:])), (layer, s_)
             p = prompt_len + s_
             # the raw rows normed and rotated by the separate launch (bit-identical to the fused step)
             qkv = torch.cat([qr.view(-1), kr.view(-1), vr.view(-1)]).view(1, 1, -1).cuda()

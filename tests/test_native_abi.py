@@ -104,12 +104,17 @@ def test_topology_init_matches_oracle(rule):
 
 
 def test_decode_state_words_match_the_host_layout():
-    from butterfly_amd.compressed_cache import _DEV_SLOT
+    from butterfly_amd.compressed_cache import _DEV_SLOT, _dev_copies
 
     lib = _native.lib()
-    assert lib.bfly_decode_state_words(1, 1) == 8 + 9 * _DEV_SLOT     # one sequence + 8 route copies
+    # up to 16 sequences: 64 copies each (the fused output projection's attending workgroups)
+    assert lib.bfly_decode_state_words(1, 1) == 8 + (64 + 8) * _DEV_SLOT
+    assert lib.bfly_decode_state_words(4, 4) == 8 + (16 * 64 + 8) * _DEV_SLOT
+    assert lib.bfly_decode_state_words(17, 1) == 8 + (17 + 8) * _DEV_SLOT    # one copy per sequence beyond
     assert lib.bfly_decode_state_words(32, 2) == 8 + 72 * _DEV_SLOT
     assert lib.bfly_decode_state_words(0, 2) == 0
+    for n in (1, 4, 16, 17, 64):
+        assert lib.bfly_decode_state_words(n, 1) == 8 + (n * _dev_copies(n) + 8) * _DEV_SLOT
 
 
 def test_decode_step_qk_norm_validates_before_launch():
@@ -125,6 +130,37 @@ def test_decode_step_qk_norm_validates_before_launch():
     d64 = base[:5] + (64,) + base[6:]
     assert lib.bfly_decode_step_qk_norm(*d64, 0x2000, 0x2100, 0x2200, 0x2300, *tail) == _native.ERR_INVALID
     assert b"head_dim 128" in lib.bfly_last_error()
+
+
+def test_decode_step_qk_norm_oproj_validates_before_launch():
+    """Fake, never dereferenced addresses: shapes other than 16 query heads over 4 kv heads of
+    128, batches past 16 sequences, bad o_group / o_out_features and missing or misaligned
+    projection buffers are refused before any launch."""
+    lib = _native.lib()
+
+    def call(b=1, hq=16, hkv=4, d=128, o_packed=0x4000, o_sb=0x5000, n_out=2048, group=64, parts=0x6000):
+        head = (256, _native.DTYPE_BF16, b, hq, hkv, d, 512, 768, 1024, 1280, 256, 1536, 1792, 16, 2048, 0, 3, 1,
+                1, 1, 128, 64, 64, 0.088, 0x2000, 0x2100, 0x2200, 0x2300, 64, 1e-6)
+        return lib.bfly_decode_step_qk_norm_oproj(*head, o_packed, o_sb, n_out, group, parts, 0x3000, None)
+
+    for kw, msg in [(dict(hq=8, hkv=2), b"16 query heads"), (dict(d=64), b"16 query heads"),
+                    (dict(b=5), b"<= 16"), (dict(group=48), b"power of two"), (dict(group=16), b"power of two"),
+                    (dict(n_out=2000), b"multiple of 32"), (dict(n_out=64 * 65), b"multiple of 32"),
+                    (dict(parts=None), b"null"), (dict(o_packed=0x4008), b"16-byte"), (dict(o_sb=0x5002), b"16-byte")]:
+        assert call(**kw) == _native.ERR_INVALID, kw
+        assert msg in lib.bfly_last_error(), (kw, lib.bfly_last_error())
+
+
+def test_add_rms_norm_q4_gemv_silu_parts_validates_before_launch():
+    """Four 16-byte aligned partial rows, else refused before a launch (fake addresses)."""
+    lib = _native.lib()
+    tail = (512, 768, 1e-6, 1024, 1280, 1536, 8, 2048, 64, 8, 2048, None)
+    assert lib.bfly_add_rms_norm_q4_gemv_silu_parts(0x1000, 3, *tail) == _native.ERR_INVALID
+    assert b"four partial rows" in lib.bfly_last_error()
+    assert lib.bfly_add_rms_norm_q4_gemv_silu_parts(0x1008, 4, *tail) == _native.ERR_INVALID
+    assert b"16-byte" in lib.bfly_last_error()
+    bad_in = tail[:7] + (3072,) + tail[8:]
+    assert lib.bfly_add_rms_norm_q4_gemv_silu_parts(0x1000, 4, *bad_in) == _native.ERR_INVALID
 
 
 def test_decode_step_checks_the_cache_window_before_launch():

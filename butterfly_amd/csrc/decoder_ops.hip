@@ -13,6 +13,7 @@
 #include <mutex>
 
 #include "bfly_common.h"
+#include "argmax.h"
 #include "rmsnorm_row.h"
 #include "../../include/butterfly_amd_decoder.h"
 
@@ -348,43 +349,6 @@ extern "C" int bfly_silu_mul(const void* gate, const void* up, int64_t rows, int
 
 namespace bfly {
 
-// Greedy selection order of torch.argmax: NaN above every number, then larger
-// values, then the lower index among equals.
-__device__ __forceinline__ bool argmax_better(float v, int64_t i, float bv, int64_t bi) {
-  if (bi < 0) return true;
-  const bool vn = v != v, bn = bv != bv;
-  if (vn != bn) return vn;
-  if (!vn && v != bv) return v > bv;
-  return i < bi;
-}
-
-__device__ __forceinline__ void argmax_combine(float& bv, int64_t& bi, float v, int64_t i) {
-  if (i >= 0 && argmax_better(v, i, bv, bi)) {
-    bv = v;
-    bi = i;
-  }
-}
-
-// Block-wide combine of every thread's (value, index) candidate (256 threads).
-__device__ __forceinline__ void argmax_block(float& bv, int64_t& bi) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const float ov = __shfl_xor(bv, o);
-    const int64_t oi = __shfl_xor(bi, o);
-    argmax_combine(bv, bi, ov, oi);
-  }
-  __shared__ float sv[4];
-  __shared__ int64_t si[4];
-  const int t = threadIdx.x;
-  if ((t & 63) == 0) {
-    sv[t >> 6] = bv;
-    si[t >> 6] = bi;
-  }
-  __syncthreads();
-  if (t == 0)
-    for (int w = 1; w < 4; ++w) argmax_combine(bv, bi, sv[w], si[w]);
-}
-
 // Pass 1: workgroup (p, r) scans elements [p * span, (p + 1) * span) of row r
 // (span a multiple of 8) and leaves its candidate in part_v / part_i [r * parts + p],
 // or, with a single part, the answer in out[r].  Rows that are contiguous with a
@@ -442,7 +406,55 @@ __global__ void __launch_bounds__(256) argmax_final_kernel(const float* __restri
   if (t == 0) out[r] = bi;
 }
 
+// bfly_greedy_advance: the greedy pick over the per-workgroup candidates a product left in
+// its workspace (bfly_add_rms_norm_q4_gemv_argmax), and a decode loop's bookkeeping for the
+// token: token[0], tokens_out[counters[1]] (while below tokens_cap), both counters + 1, and the
+// next step's input row x_next = embed[token] (hidden bf16).  One workgroup.
+__global__ void __launch_bounds__(256) greedy_advance_kernel(const unsigned char* __restrict__ ws,
+                                                             const __bf16* __restrict__ embed, int64_t vocab,
+                                                             int64_t hidden, __bf16* __restrict__ x_next,
+                                                             int64_t* __restrict__ token,
+                                                             int64_t* __restrict__ tokens_out, int64_t tokens_cap,
+                                                             int64_t* __restrict__ counters) {
+  const int t = threadIdx.x;
+  const int64_t g = *reinterpret_cast<const int64_t*>(ws);
+  const float* cv = reinterpret_cast<const float*>(ws + 16);
+  const int64_t* ci = reinterpret_cast<const int64_t*>(ws + 16 + (4 * g + 7) / 8 * 8);
+  float bv = 0.f;
+  int64_t bi = -1;
+  for (int64_t c = t; c < g; c += 256) argmax_combine(bv, bi, cv[c], ci[c]);
+  argmax_block(bv, bi);
+  __shared__ int64_t tok_s;
+  if (t == 0) {
+    tok_s = bi;
+    token[0] = bi;
+    const int64_t col = counters[1];
+    if (col >= 0 && col < tokens_cap) tokens_out[col] = bi;
+    counters[0] += 1;
+    counters[1] += 1;
+  }
+  __syncthreads();
+  const int64_t tk = tok_s;
+  if (tk < 0 || tk >= vocab) return;
+  const uint4* src = reinterpret_cast<const uint4*>(embed + tk * hidden);
+  for (int64_t c = t; c < hidden / 8; c += 256) reinterpret_cast<uint4*>(x_next)[c] = src[c];
+}
+
 }  // namespace bfly
+
+extern "C" int bfly_greedy_advance(const void* workspace, const void* embed, int64_t vocab, int64_t hidden,
+                                   void* x_next, int64_t* token, int64_t* tokens_out, int64_t tokens_cap,
+                                   int64_t* counters, hipStream_t stream) {
+  BFLY_CHECK_ARG(workspace && embed && x_next && token && tokens_out && counters, "null pointer");
+  BFLY_CHECK_ARG(vocab > 0 && hidden > 0 && hidden % 8 == 0 && tokens_cap > 0, "bad shape");
+  BFLY_CHECK_ARG(aligned16(workspace) && aligned16(embed) && aligned16(x_next),
+                 "workspace, embed and x_next must be 16-byte aligned");
+  hipLaunchKernelGGL(bfly::greedy_advance_kernel, dim3(1), dim3(256), 0, stream,
+                     static_cast<const unsigned char*>(workspace), static_cast<const __bf16*>(embed), vocab, hidden,
+                     static_cast<__bf16*>(x_next), token, tokens_out, tokens_cap, counters);
+  BFLY_CHECK_LAUNCH("bfly_greedy_advance");
+  return BFLY_OK;
+}
 
 // The two passes of bfly_argmax_rows over a workspace the caller checked.
 static int argmax_launch(const void* x, int64_t rows, int64_t n, int64_t row_stride, int64_t col_stride,

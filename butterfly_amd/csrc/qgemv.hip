@@ -13,6 +13,7 @@
 // fp32 throughout; y is rounded once to bf16.  The results equal the product
 // with the fp32 weights code * scale + bias up to the fp32 summation order.
 #include "bfly_common.h"
+#include "argmax.h"
 #include "q4_piece.h"
 #include "rmsnorm_row.h"
 #include "../../include/butterfly_amd_decoder.h"
@@ -50,13 +51,17 @@ struct Q4Args {
   int pieces, groups, pieces_per_group;
 };
 
+struct Q4NoSink {
+  __device__ void operator()(int64_t, __bf16) const {}
+};
+
 // The sets of one wave: set0, set0 + stride, ... < n_sets.  form_x() runs after the first
 // set's weights are requested and before x (xsrc, bf16) is read: the fused form computes x
 // there.  kXFirst (x already in memory): x is requested before the weights, so that its
-// pre-sums wait for x alone.
-template <int NP, int R, bool kSilu, bool kXFirst, class XPtr, class FormX>
+// pre-sums wait for x alone.  sink(o, y) sees every output the lane writes.
+template <int NP, int R, bool kSilu, bool kXFirst, class XPtr, class FormX, class Sink = Q4NoSink>
 __device__ __forceinline__ void q4_sets(const Q4Args& a, int lane, int64_t set0, int64_t stride, XPtr xsrc,
-                                        FormX&& form_x) {
+                                        FormX&& form_x, Sink&& sink = Sink{}) {
   const int pieces = a.pieces, groups = a.groups;
   const u32x4* __restrict__ w = a.w;
   const uint32_t* __restrict__ sb = a.sb;
@@ -140,7 +145,11 @@ __device__ __forceinline__ void q4_sets(const Q4Args& a, int lane, int64_t set0,
       }
     }
     const int64_t o = o0 + lane;
-    if (lane < OUTS && o < n_out) a.y[o] = kSilu ? q4_silu_times(mine, mate) : (__bf16)mine;
+    if (lane < OUTS && o < n_out) {
+      const __bf16 yv = kSilu ? q4_silu_times(mine, mate) : (__bf16)mine;
+      a.y[o] = yv;
+      sink(o, yv);
+    }
   }
 }
 
@@ -163,9 +172,12 @@ struct Q4NormArgs {
   __bf16* h_out;
   float eps;
   const float* parts;       // kParts: the four partial rows
+  float* cand_v;            // kArgmax: one greedy candidate per workgroup
+  int64_t* cand_i;
+  int64_t* cand_n;          // kArgmax: the candidate count (the grid), written by workgroup 0
 };
 
-template <int NP, int R, bool kSilu, int PER, int NW, bool kParts>
+template <int NP, int R, bool kSilu, int PER, int NW, bool kParts, bool kArgmax = false>
 __global__ void __launch_bounds__(64 * NW) q4_norm_gemv_kernel(Q4Args a, Q4NormArgs nm) {
   static_assert(NW >= 4, "the row is formed by the first 256 threads");
   constexpr int DIM = 256 * PER;
@@ -173,6 +185,8 @@ __global__ void __launch_bounds__(64 * NW) q4_norm_gemv_kernel(Q4Args a, Q4NormA
   __shared__ float part[4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t waves = (int64_t)gridDim.x * NW;
+  float bv = 0.f;      // kArgmax: this lane's greedy candidate
+  int64_t bi = -1;
   // the norm's inputs are requested before the weights, so that forming the row waits for them
   // alone and runs while the weights are in flight
   RmsRowIn<PER> in = rms_row_load<PER, !kParts>(nm.x, nm.residual, nm.weight, tid, tid < 256);
@@ -199,7 +213,19 @@ __global__ void __launch_bounds__(64 * NW) q4_norm_gemv_kernel(Q4Args a, Q4NormA
     add_rmsnorm_row_from<PER>(in, nm.residual != nullptr, blockIdx.x == 0 ? nm.h_out : nullptr, xn, DIM, nm.eps, tid,
                               tid < 256, part);
     __syncthreads();   // the normed row is in LDS
+  }, [&](int64_t o, __bf16 yv) {
+    if constexpr (kArgmax) argmax_combine(bv, bi, (float)yv, o);
   });
+  if constexpr (kArgmax) {
+    // the workgroup's greedy candidate over the outputs its waves wrote (torch.argmax's order
+    // on the bf16 values), for bfly_greedy_advance
+    argmax_block<NW>(bv, bi);
+    if (tid == 0) {
+      nm.cand_v[blockIdx.x] = bv;
+      nm.cand_i[blockIdx.x] = bi;
+      if (blockIdx.x == 0) *nm.cand_n = gridDim.x;
+    }
+  }
 }
 
 template <int NP, int R, bool kSilu>
@@ -234,14 +260,22 @@ void q4_dispatch(Q4Args a, int64_t in_features, int group, hipStream_t stream) {
   }
 }
 
-template <int NP, int R, bool kSilu, int PER, int NW = 8, bool kParts = false>
+// Workgroups of a normed product's launch (the grid caps the waves at kQ4MaxWaves).
+template <int R, bool kSilu, int NW = 8>
+int64_t q4_norm_grid(int64_t n_out) {
+  constexpr int OUTS = kSilu ? R / 2 : R;
+  const int64_t n_sets = (n_out + OUTS - 1) / OUTS;
+  const int64_t iters = (n_sets + kQ4MaxWaves - 1) / kQ4MaxWaves;
+  const int64_t waves = (n_sets + iters - 1) / iters;
+  return (waves + NW - 1) / NW;
+}
+
+template <int NP, int R, bool kSilu, int PER, int NW = 8, bool kParts = false, bool kArgmax = false>
 void q4_norm_launch(Q4Args a, Q4NormArgs nm, hipStream_t stream) {
   constexpr int OUTS = kSilu ? R / 2 : R;
   a.n_sets = (a.n_out + OUTS - 1) / OUTS;
-  const int64_t iters = (a.n_sets + kQ4MaxWaves - 1) / kQ4MaxWaves;
-  const int64_t waves = (a.n_sets + iters - 1) / iters;
-  hipLaunchKernelGGL((q4_norm_gemv_kernel<NP, R, kSilu, PER, NW, kParts>), dim3((unsigned)((waves + NW - 1) / NW)),
-                     dim3(64 * NW), 0, stream, a, nm);
+  hipLaunchKernelGGL((q4_norm_gemv_kernel<NP, R, kSilu, PER, NW, kParts, kArgmax>),
+                     dim3((unsigned)q4_norm_grid<R, kSilu, NW>(a.n_out)), dim3(64 * NW), 0, stream, a, nm);
 }
 
 // in_features = 256 PER with PER in {8, 16, 24} (one to three pieces per lane; a fourth would
@@ -249,7 +283,7 @@ void q4_norm_launch(Q4Args a, Q4NormArgs nm, hipStream_t stream) {
 // SiLU form at four rows per set runs 12 waves per workgroup: cfg5's gate|up (3072 sets) is then
 // 256 workgroups, one per CU, where 8 waves gave 384 and half the CUs ran two (7.26 -> 6.35 us,
 // graph-replayed over 24 weight sets; other shapes measured no faster).
-template <bool kSilu, bool kParts = false>
+template <bool kSilu, bool kParts = false, bool kArgmax = false>
 void q4_norm_dispatch(Q4Args a, Q4NormArgs nm, int64_t in_features, int group, hipStream_t stream) {
   a.pieces = (int)(in_features / kQ4PieceCodes);
   a.groups = (int)(in_features / group);
@@ -258,15 +292,21 @@ void q4_norm_dispatch(Q4Args a, Q4NormArgs nm, int64_t in_features, int group, h
   switch (in_features / 256) {
     case 8:
       if (sets4 >= 2048 && kSilu)
-        q4_norm_launch<1, 4, kSilu, 8, 12, kParts>(a, nm, stream);
+        q4_norm_launch<1, 4, kSilu, 8, 12, kParts, kArgmax>(a, nm, stream);
       else if (sets4 >= 2048)
-        q4_norm_launch<1, 4, kSilu, 8, 8, kParts>(a, nm, stream);
+        q4_norm_launch<1, 4, kSilu, 8, 8, kParts, kArgmax>(a, nm, stream);
       else
-        q4_norm_launch<1, 2, kSilu, 8, 8, kParts>(a, nm, stream);
+        q4_norm_launch<1, 2, kSilu, 8, 8, kParts, kArgmax>(a, nm, stream);
       break;
-    case 16: q4_norm_launch<2, 2, kSilu, 16, 8, kParts>(a, nm, stream); break;
-    default: q4_norm_launch<3, 2, kSilu, 24, 8, kParts>(a, nm, stream); break;
+    case 16: q4_norm_launch<2, 2, kSilu, 16, 8, kParts, kArgmax>(a, nm, stream); break;
+    default: q4_norm_launch<3, 2, kSilu, 24, 8, kParts, kArgmax>(a, nm, stream); break;
   }
+}
+
+// Workgroups of the plain (no SiLU) normed product q4_norm_dispatch launches: its greedy
+// candidates.
+int64_t q4_norm_plain_grid(int64_t n_out, int64_t in_features) {
+  return in_features == 2048 && (n_out + 3) / 4 >= 2048 ? q4_norm_grid<4, false>(n_out) : q4_norm_grid<2, false>(n_out);
 }
 
 int q4_norm_check(const void* x, const void* residual, const void* weight, void* h_out, int64_t in_features) {
@@ -385,5 +425,39 @@ extern "C" int bfly_add_rms_norm_q4_gemv_silu_parts(const float* x_parts, int n_
   a.up_off = up_row_offset;
   q4_norm_dispatch<true, true>(a, nm, in_features, group, stream);
   BFLY_CHECK_LAUNCH("bfly_add_rms_norm_q4_gemv_silu_parts");
+  return BFLY_OK;
+}
+
+// Workspace of bfly_add_rms_norm_q4_gemv_argmax: int64 count at 0, float values at 16, int64
+// indices at 16 + 4 G rounded up to 8.
+static int64_t q4_argmax_ws_bytes(int64_t g) { return 16 + (4 * g + 7) / 8 * 8 + 8 * g; }
+
+extern "C" int64_t bfly_q4_argmax_workspace_bytes(int64_t out_features, int64_t in_features) {
+  if (out_features <= 0 || in_features <= 0) return 0;
+  return q4_argmax_ws_bytes(q4_norm_plain_grid(out_features, in_features));
+}
+
+extern "C" int bfly_add_rms_norm_q4_gemv_argmax(const void* x, const void* residual, const void* norm_weight, float eps,
+                                                void* h_out, const void* packed, const void* scale_bias,
+                                                int64_t out_features, int64_t in_features, int group, void* out,
+                                                void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  int rc = q4_check(x, packed, scale_bias, out_features, in_features, group, out);
+  if (rc) return rc;
+  rc = q4_norm_check(x, residual, norm_weight, h_out, in_features);
+  if (rc) return rc;
+  const int64_t g = q4_norm_plain_grid(out_features, in_features);
+  BFLY_CHECK_ARG(workspace != nullptr && aligned16(workspace) && workspace_bytes >= q4_argmax_ws_bytes(g),
+                 "workspace: %lld bytes, 16-byte aligned, needed (bfly_q4_argmax_workspace_bytes)",
+                 (long long)q4_argmax_ws_bytes(g));
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  Q4NormArgs nm{static_cast<const __bf16*>(x), static_cast<const __bf16*>(residual),
+                static_cast<const __bf16*>(norm_weight), static_cast<__bf16*>(h_out), eps, nullptr,
+                reinterpret_cast<float*>(ws + 16), reinterpret_cast<int64_t*>(ws + 16 + (4 * g + 7) / 8 * 8)};
+  // the count the candidates are read with: written by the launch's workgroup 0 (no host copy
+  // and no fill node: the call stays capturable)
+  nm.cand_n = reinterpret_cast<int64_t*>(ws);
+  q4_norm_dispatch<false, false, true>(q4_args(x, packed, scale_bias, out_features, out), nm, in_features, group,
+                                       stream);
+  BFLY_CHECK_LAUNCH("bfly_add_rms_norm_q4_gemv_argmax");
   return BFLY_OK;
 }

@@ -158,6 +158,10 @@ Q4_PIECE_CODES, Q4_MAX_IN = 32, 8192
 # decode steps of a swapped layer run its output projection in the decode-step launch where
 # the shapes allow (ButterflyAttention.takes_o_proj); False keeps it a launch of its own
 FUSE_O_PROJ = True
+# graph-replayed greedy steps of one sequence pick the token from the lm_head launch's
+# per-workgroup candidates and advance token, output, counters and the next input in one more
+# launch (GreedyState); False keeps torch's embedding, index_copy and add and the argmax passes
+FUSE_GREEDY = True
 
 
 def _one_row(x: torch.Tensor) -> bool:
@@ -257,6 +261,42 @@ def add_rms_norm_q4_gemv_silu_parts(x: torch.Tensor, parts: torch.Tensor, weight
                      float(eps), h.data_ptr(), gate_up.packed.data_ptr(), gate_up.scale_bias.data_ptr(), f,
                      gate_up.in_features, gate_up.group, f, out.data_ptr(), stream_of(x))
     return h.view(x.shape), out
+
+
+def add_rms_norm_q4_gemv_argmax(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torch.Tensor,
+                                eps: float, layer: QuantLinear, workspace: torch.Tensor) -> torch.Tensor:
+    """``add_rms_norm_q4_gemv(...)[1]`` through ``bfly_add_rms_norm_q4_gemv_argmax``, which also leaves
+    its per-workgroup greedy candidates in ``workspace`` (uint8, ``bfly_q4_argmax_workspace_bytes``
+    bytes) for ``greedy_advance``."""
+    xr = _row16(x)
+    rr = _row16(residual) if residual is not None else None
+    h = torch.empty_like(xr) if rr is not None else None
+    out = torch.empty(*x.shape[:-1], layer.out_features, dtype=torch.bfloat16, device=x.device)
+    with on(x.device):
+        _native.call("bfly_add_rms_norm_q4_gemv_argmax", xr.data_ptr(), rr.data_ptr() if rr is not None else None,
+                     weight.data_ptr(), float(eps), h.data_ptr() if h is not None else None,
+                     layer.packed.data_ptr(), layer.scale_bias.data_ptr(), layer.out_features, layer.in_features,
+                     layer.group, out.data_ptr(), workspace.data_ptr(), workspace.numel(), stream_of(x))
+    return out
+
+
+class GreedyState:
+    """What ``bfly_greedy_advance`` updates after each graph-replayed decode step of one sequence:
+    ``tok`` [1, 1] int64 (the pick), ``out`` [1, n] int64 (picks by column), ``ctr`` int64
+    [position, column], ``x`` [1, 1, hidden] bf16 (the next step's embedded input), and the
+    candidate workspace of ``add_rms_norm_q4_gemv_argmax``."""
+
+    def __init__(self, tok, out, ctr, x, workspace):
+        self.tok, self.out, self.ctr, self.x, self.workspace = tok, out, ctr, x, workspace
+
+
+def greedy_advance(g: GreedyState, embed: torch.Tensor) -> None:
+    """The greedy pick from ``g.workspace`` and the step's bookkeeping in one launch
+    (``bfly_greedy_advance``): ``g.tok``, ``g.out[0, col]``, ``g.ctr`` + 1 and ``g.x = embed[pick]``."""
+    with on(g.x.device):
+        _native.call("bfly_greedy_advance", g.workspace.data_ptr(), embed.data_ptr(), int(embed.shape[0]),
+                     int(embed.shape[1]), g.x.data_ptr(), g.tok.data_ptr(), g.out.data_ptr(), int(g.out.numel()),
+                     g.ctr.data_ptr(), stream_of(g.x))
 
 
 def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
@@ -618,16 +658,23 @@ class Decoder(nn.Module):
             self._rope_tab = tab
         return tab[0][start:need], tab[1][start:need]
 
-    def _last_logits(self, x: torch.Tensor, positions: torch.Tensor, caches: List, rope) -> torch.Tensor:
+    def _last_logits(self, x: torch.Tensor, positions: torch.Tensor, caches: List, rope,
+                     greedy: Optional[GreedyState] = None) -> torch.Tensor:
         """Run every layer over the embedded ``x`` [B, T, hidden]; returns the logits of the last
         position (final RMSNorm, tied lm_head).  On the HIP path each layer's closing residual
         add is folded into the next layer's (or the final) RMSNorm launch, and for one row the
-        final norm rides in the lm_head product's launch."""
+        final norm rides in the lm_head product's launch.  ``greedy``: also pick the token and
+        advance the decode loop's state (``greedy_advance``; one row)."""
         if _hip(x) and x.shape[-1] % 256 == 0:
             m = None
             for layer, cache in zip(self.layers, caches):
                 x, m = layer.forward_split(x, m, positions, cache, rope)
             xl, ml = x[:, -1], (m[:, -1] if m is not None else None)
+            if greedy is not None:
+                lg = add_rms_norm_q4_gemv_argmax(xl, ml, self.norm.weight, self.norm.eps, self.lm_head,
+                                                 greedy.workspace)
+                greedy_advance(greedy, self.embed_tokens)
+                return lg
             if norm_q4_fits(xl, self.lm_head):
                 return add_rms_norm_q4_gemv(xl, ml, self.norm.weight, self.norm.eps, self.lm_head)[1]
             return self._logits(add_rms_norm(xl, ml, self.norm.weight, self.norm.eps)[1])
@@ -685,8 +732,20 @@ class Decoder(nn.Module):
         ctr = torch.tensor([t, 1], dtype=torch.long, device=dev)   # position, output column: one add per step
         pos, step = ctr[0:1], ctr[1:2]
         cos_tab, sin_tab = self._rope_tab
+        greedy = None
+        hid = self.cfg.hidden_size
+        if (FUSE_GREEDY and b == 1 and _hip(self.embed_tokens) and hid in NORM_Q4_DIMS
+                and self.lm_head.gemv_from_codes and self.lm_head.in_features == hid):
+            ws = torch.empty(int(_native.lib().bfly_q4_argmax_workspace_bytes(self.cfg.vocab_size, hid)),
+                             dtype=torch.uint8, device=dev)
+            greedy = GreedyState(tok, out, ctr, F.embedding(tok, self.embed_tokens).contiguous(), ws)
 
         def one_step():
+            if greedy is not None:
+                # the token, its output column, the counters and the next step's input row are
+                # advanced inside the launches after the lm_head
+                self._last_logits(greedy.x, pos, caches, RopeTable(cos_tab, sin_tab, pos), greedy=greedy)
+                return
             x = F.embedding(tok, self.embed_tokens)
             rope = RopeTable(cos_tab, sin_tab, pos)
             lg = self._last_logits(x, pos, caches, rope)

@@ -132,6 +132,34 @@ int bfly_add_rms_norm_q4_gemv_silu(const void* x, const void* residual, const vo
                                    int64_t up_row_offset, void* out, hipStream_t stream);
 
 /*
+ * Device: bfly_add_rms_norm_q4_gemv that also leaves one greedy candidate per workgroup
+ * (the largest bf16 output it wrote, torch.argmax's order: NaN first, then larger, then the
+ * lower index) in `workspace` (bfly_q4_argmax_workspace_bytes bytes, 16-byte aligned; the
+ * launch writes the candidate count too, so nothing needs clearing), for
+ * bfly_greedy_advance.  The decoder's final norm with the lm_head at batch 1; no counterpart
+ * in the reference's own code (its greedy loop takes mx.argmax of the logits).
+ */
+int64_t bfly_q4_argmax_workspace_bytes(int64_t out_features, int64_t in_features);
+int bfly_add_rms_norm_q4_gemv_argmax(const void* x, const void* residual, const void* norm_weight, float eps,
+                                     void* h_out, const void* packed, const void* scale_bias, int64_t out_features,
+                                     int64_t in_features, int group, void* out, void* workspace,
+                                     int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Device: the greedy pick over the candidates bfly_add_rms_norm_q4_gemv_argmax left in
+ * `workspace` (the argmax of its whole output), and a decode loop's bookkeeping in the same
+ * launch: token[0] = the pick, tokens_out[counters[1]] = the pick while counters[1] <
+ * tokens_cap, counters[0] and counters[1] (position, output column) + 1, and the next step's
+ * input row x_next[0 .. hidden) = embed[pick] (bf16 [vocab][hidden], the tied embedding table;
+ * hidden a multiple of 8; embed, x_next 16-byte aligned).  One workgroup; capturable.  Replaces
+ * the reference's greedy step around the model call (argmax, token append, embedding lookup of
+ * the next input); no counterpart in its own code.
+ */
+int bfly_greedy_advance(const void* workspace, const void* embed, int64_t vocab, int64_t hidden, void* x_next,
+                        int64_t* token, int64_t* tokens_out, int64_t tokens_cap, int64_t* counters,
+                        hipStream_t stream);
+
+/*
  * Device: bfly_add_rms_norm_q4_gemv_silu whose input row x is given as n_parts = 4
  * fp32 partial rows x_parts[g * in_features + i] and formed as
  * x_i = bf16((p0_i + p1_i) + (p2_i + p3_i)): the o_parts of

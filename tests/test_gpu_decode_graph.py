@@ -261,6 +261,56 @@ def test_decoder_graph_greedy_equals_eager_greedy(batch, head_dim):
     assert torch.equal(eager, graphed), (eager, graphed)
 
 
+@pytest.mark.parametrize("fuse", [True, False])
+def test_decoder_graph_with_fused_projection_and_greedy_equals_eager(fuse):
+    """cfg5's attention shapes (16 heads over 4 kv heads of 128, hidden 2048) at a small depth:
+    the graphed steps take the decode step with the output projection inside and the greedy
+    pick from the lm_head launch's candidates with the loop's bookkeeping in one launch
+    (fuse=True), or neither; either way the tokens equal the eager loop's (separate launches,
+    torch.argmax over the logits), which holds only if every fused result is bit-identical."""
+    import butterfly_amd.decoder as dec
+
+    cfg = DecoderConfig(vocab_size=4096, hidden_size=2048, num_layers=2, num_heads=16, num_kv_heads=4, head_dim=128,
+                        intermediate_size=1024)
+    model = Decoder(cfg, seed=3)
+    bf.swap_qwen_attention_with_butterfly(model, cfg=bf.compressed_butterfly_config())
+    for layer in model.layers:
+        g = torch.Generator(device="cuda").manual_seed(7)
+        for norm in (layer.self_attn.base.q_norm, layer.self_attn.base.k_norm):
+            norm.weight.data = (1 + 0.3 * torch.randn(128, generator=g, device="cuda")).bfloat16()
+    prompt = torch.randint(0, cfg.vocab_size, (1, 400), generator=torch.Generator().manual_seed(8)).cuda()
+
+    def caches():
+        c = [None] * cfg.num_layers
+        bf.install_compressed_kv_caches(model, c, block_size=128, local_window_tokens=64, max_kv_size=700)
+        return c
+
+    eager = model.greedy(prompt, 150, caches())        # crosses a block end: pooling inside the steps
+    saved = dec.FUSE_O_PROJ, dec.FUSE_GREEDY
+    dec.FUSE_O_PROJ = dec.FUSE_GREEDY = fuse
+    try:
+        calls = {"oproj": 0, "greedy": 0}
+        real, real_adv = bf.ButterflyAttentionCore.step_oproj, dec.greedy_advance
+
+        def counting(core, *a, **k):
+            calls["oproj"] += 1
+            return real(core, *a, **k)
+
+        def counting_adv(*a, **k):
+            calls["greedy"] += 1
+            return real_adv(*a, **k)
+
+        bf.ButterflyAttentionCore.step_oproj = counting
+        dec.greedy_advance = counting_adv
+        graphed = model.greedy_graph(prompt, 150, caches())
+    finally:
+        bf.ButterflyAttentionCore.step_oproj = real
+        dec.greedy_advance = real_adv
+        dec.FUSE_O_PROJ, dec.FUSE_GREEDY = saved
+    assert (calls["oproj"] > 0) == fuse and (calls["greedy"] > 0) == fuse, calls
+    assert torch.equal(eager, graphed), (eager, graphed)
+
+
 def test_default_window_128_with_device_counters_takes_the_host_path():
     """The reference's compressed defaults give a 128-token attention window, beyond the
     device step's 64: with device counters on, a one-token call of the swapped layer's

@@ -129,3 +129,49 @@ def test_add_rms_norm_q4_gemv_silu_equals_two_launches(f, in_f):
     h2, n = add_rms_norm(x, r, w, 1e-6)
     assert torch.equal(h, h2)
     assert torch.equal(s, q4_gemv_silu(n, gate_up))
+
+
+@pytest.mark.parametrize("out_f,tie", [(151936, False), (4096, True), (50000, True), (300, False)])
+def test_argmax_variant_and_greedy_advance(out_f, tie):
+    """``bfly_add_rms_norm_q4_gemv_argmax`` writes the same logits as ``bfly_add_rms_norm_q4_gemv``
+    and leaves candidates whose pick (``bfly_greedy_advance``) is torch.argmax of those logits;
+    with two equal top rows the lower index wins.  The advance also writes the token, its
+    output column, both counters and the next input row (the pick's embedding row)."""
+    from butterfly_amd.decoder import GreedyState, add_rms_norm_q4_gemv, add_rms_norm_q4_gemv_argmax, greedy_advance
+
+    g = torch.Generator().manual_seed(out_f)
+    w = torch.randn(out_f, 2048, generator=g) / 2048 ** 0.5
+    x = torch.randn(1, 2048, generator=g).bfloat16().cuda()
+    r = torch.randn(1, 2048, generator=g).bfloat16().cuda()
+    nw = (1 + 0.1 * torch.randn(2048, generator=g)).bfloat16().cuda()
+    layer = QuantLinear(2048, out_f, group=64, weight=w).cuda()
+    want = add_rms_norm_q4_gemv(x, r, nw, 1e-6, layer)[1]
+    expect = None
+    if tie:
+        # the top row copied to a lower index: identical codes, identical logits, the lower index wins
+        top = int(torch.argmax(want.float()))
+        dup = top // 2 if top > 0 else out_f - 1
+        w[dup] = w[top]
+        layer = QuantLinear(2048, out_f, group=64, weight=w).cuda()
+        want = add_rms_norm_q4_gemv(x, r, nw, 1e-6, layer)[1]
+        assert want[0, dup] == want[0, top]
+        expect = min(dup, top)
+    ws = torch.empty(int(_native.lib().bfly_q4_argmax_workspace_bytes(out_f, 2048)), dtype=torch.uint8,
+                     device="cuda")
+    got = add_rms_norm_q4_gemv_argmax(x, r, nw, 1e-6, layer, ws)
+    assert torch.equal(got, want)
+    embed = torch.randn(out_f, 256, generator=g).bfloat16().cuda()
+    tok = torch.full((1, 1), -5, dtype=torch.long, device="cuda")
+    out = torch.full((1, 6), -1, dtype=torch.long, device="cuda")
+    ctr = torch.tensor([1000, 2], dtype=torch.long, device="cuda")
+    xn = torch.empty(1, 1, 256, dtype=torch.bfloat16, device="cuda")
+    greedy_advance(GreedyState(tok, out, ctr, xn, ws), embed)
+    pick = int(torch.argmax(want.float()))
+    if tie:
+        assert pick == expect
+    assert int(tok) == pick
+    assert out.tolist() == [[-1, -1, pick, -1, -1, -1]] and ctr.tolist() == [1001, 3]
+    assert torch.equal(xn.view(-1), embed[pick])
+    ctr.fill_(6)                                    # a column past the output: nothing written there
+    greedy_advance(GreedyState(tok, out, ctr, xn, ws), embed)
+    assert out.tolist() == [[-1, -1, pick, -1, -1, -1]] and ctr.tolist() == [7, 7]

@@ -950,7 +950,7 @@ __device__ __forceinline__ void dec_pool32(const DecodeArgs& a, const DecState32
 // bit.  Every attending workgroup of a sequence appends the new token and pools a due
 // block (the same values), so none reads what another writes in the launch.
 template <int D, bool kStep, bool kQkn = false, int kOS = 0>
-__global__ void __launch_bounds__(256, kQkn ? 1 : (D <= 128 ? 3 : 1))
+__global__ void __launch_bounds__(kOS > 0 ? 512 : 256, kQkn ? 1 : (D <= 128 ? 3 : 1))
 decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) {
   constexpr bool kOproj = kOS > 0;
   static_assert(!kOproj || (kStep && kQkn && D == 128), "the fused projection rides on the q/k-norm step");
@@ -981,11 +981,48 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   constexpr bool qkn = kQkn && D == 128;
   constexpr int QP = 136;
   __shared__ __attribute__((aligned(16))) T q_lds[qkn ? 16 * QP : 8];
-  // kOproj: the attention output of the group's four heads (the projection's input slice)
+  // kOproj: the attention output of the group's four heads (the projection's input slice), and
+  // the workgroup's slice of W_o ([16 kOS rows][16 pieces] and their scale words)
   __shared__ __attribute__((aligned(16))) T o_lds[kOproj ? 4 * D : 8];
+  __shared__ u32x4 ow_lds[kOproj ? 16 * kOS * 16 : 1];
+  __shared__ uint32_t osb_lds[kOproj ? 16 * kOS * 16 : 1];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
+  if constexpr (kOproj) {
+    // Threads 256..511 only bring the W_o slice into LDS and exit: their loads do not queue
+    // ahead of the attention waves' own (a wave's loads return in order).  An exited wave no
+    // longer counts at a barrier, so the attention waves' staging barrier, which every step
+    // takes before the projection, completes only after these writes.
+    if (tid >= 256) {
+      if (blockIdx.x >= kRouteGroups) {
+        const int t2 = tid - 256;
+        const int jw = (int)blockIdx.x - kRouteGroups;
+        const int sub = (int)a.nseq_div.div((uint32_t)jw);
+        const int bh = jw - sub * a.nseq;
+        const int kvh = bh - (int)a.hkv_div.div((uint32_t)bh) * a.hkv;
+        const uint32_t pc = (uint32_t)(t2 & 15);
+        const uint32_t piece = 16u * (uint32_t)kvh + pc;
+        const uint32_t grp = piece >> a.o_ppg_log2;
+        u32x4 w[kOS];
+        uint32_t sc[kOS];
+#pragma unroll
+        for (int k = 0; k < kOS; ++k) {
+          const uint32_t row = (uint32_t)(16 * kOS * sub + (t2 >> 4) + 16 * k);
+          w[k] = __builtin_nontemporal_load(a.ow + row * 64u + piece);
+          sc[k] = a.osb[row * (uint32_t)a.o_groups + grp];
+        }
+#pragma unroll
+        for (int k = 0; k < kOS; ++k) {
+          const int rl = (t2 >> 4) + 16 * k;
+          ow_lds[rl * 16 + (int)pc] = w[k];
+          osb_lds[rl * 16 + (int)pc] = sc[k];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      }
+      return;
+    }
+  }
   // step mode: the route workgroups come first (no argument is needed to tell
   // them apart), attending workgroup j is blockIdx j + kRouteGroups
   if constexpr (kStep) {
@@ -1055,21 +1092,6 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
   };
   if constexpr (qkn) load_q_raw(0);
   else load_q(0);
-  // kOproj: this workgroup's slice of W_o, requested after the staging loads (their data is
-  // needed first; loads return in order) and used last.  Lane (r4, pc) = (lane / 16,
-  // lane % 16) takes piece 16 kvh + pc of rows 16 kOS sub + 4 kOS wave + 4 s + r4.
-  u32x4 owv[kOproj ? kOS : 1];
-  uint32_t osv[kOproj ? kOS : 1];
-  auto load_oproj = [&]() {
-    const uint32_t piece = 16u * (uint32_t)kvh + (uint32_t)(lane & 15);
-    const uint32_t grp = piece >> a.o_ppg_log2;
-#pragma unroll
-    for (int st4 = 0; st4 < kOS; ++st4) {
-      const uint32_t row = (uint32_t)(16 * kOS * sub + 4 * kOS * wave + 4 * st4 + (lane >> 4));
-      owv[st4] = __builtin_nontemporal_load(a.ow + row * 64u + piece);
-      osv[st4] = a.osb[row * (uint32_t)a.o_groups + grp];
-    }
-  };
 
   const DecState32 st =
       kStep ? dec_advance32(cnt[kStOffset], cnt[kStTail], cnt[kStCount], cnt[kStSumOff], a, sa) : dec_state32<false>(a, sa, bh);
@@ -1171,7 +1193,6 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
       skx[it] = *reinterpret_cast<const uint4*>(pk + (uint32_t)n * D + (i % PIECES) * VEC);
       svx[it] = *reinterpret_cast<const uint4*>(pv + (uint32_t)n * D + (i % PIECES) * VEC);
     }
-    if constexpr (kOproj) load_oproj();
     // append the new token to its ring slot; requested after every staging load so
     // that its wait coincides with theirs (the staging reads it from k_new/v_new)
     if (knew != nullptr && tid < 2 * PIECES && !(qkn && tid < PIECES)) {   // normed k: appended below
@@ -1306,8 +1327,10 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
     }
   }
   if constexpr (kOproj) {
-    // the partial product of this workgroup's rows over the group's 512 outputs: lane piece
-    // pc covers o_lds[32 pc, 32 pc + 32) (head pc / 4, d from 32 (pc % 4))
+    // the partial product of this workgroup's rows over the group's 512 outputs: lane (r4, pc)
+    // = (lane / 16, lane % 16) takes piece pc of local rows 4 kOS wave + 4 s + r4 (W_o's rows
+    // 16 kOS sub + ..., pieces 16 kvh + pc), over o_lds[32 pc, 32 pc + 32) (head pc / 4, d from
+    // 32 (pc % 4))
     __syncthreads();
     const int pc = lane & 15;
     bf16x8 xr[4];
@@ -1318,8 +1341,9 @@ decode_mfma_kernel(int64_t* state, const void* q, DecodeArgs a, StepArgs sa_in) 
     float* prow = a.opart + ((int64_t)kvh * (a.nseq / a.hkv) + bi) * a.o_rows;
 #pragma unroll
     for (int st4 = 0; st4 < kOS; ++st4) {
+      const int rl = 4 * kOS * wave + 4 * st4 + (lane >> 4);
       float acc = 0.f;
-      acc += q4_piece_dot(owv[st4], osv[st4], xq, xs);
+      acc += q4_piece_dot(ow_lds[rl * 16 + pc], osb_lds[rl * 16 + pc], xq, xs);
       acc = q4_row16_sum(acc);
       if (pc == 0) prow[16 * kOS * sub + 4 * kOS * wave + 4 * st4 + (lane >> 4)] = acc;
     }
@@ -1692,10 +1716,11 @@ static void launch_decode(const DecodeArgs& a, const StepArgs& sa, int d, int64_
         if (a.ow != nullptr) {   // the fused output projection: o_subs attending workgroups per sequence
           m.nseq_div = FastDiv::make((uint32_t)grid);
           const dim3 og((unsigned)(grid * a.o_subs + kRouteGroups));
+          // 512 threads: 256 attend, 256 bring the W_o slice into LDS
           if (a.o_rows == 32 * a.o_subs)
-            hipLaunchKernelGGL((decode_mfma_kernel<128, true, true, 2>), og, dim3(256), 0, stream, sa.state, m.q, m, sa);
+            hipLaunchKernelGGL((decode_mfma_kernel<128, true, true, 2>), og, dim3(512), 0, stream, sa.state, m.q, m, sa);
           else
-            hipLaunchKernelGGL((decode_mfma_kernel<128, true, true, 4>), og, dim3(256), 0, stream, sa.state, m.q, m, sa);
+            hipLaunchKernelGGL((decode_mfma_kernel<128, true, true, 4>), og, dim3(512), 0, stream, sa.state, m.q, m, sa);
           return;
         }
         const int64_t smin = decode_split_min();

@@ -101,7 +101,7 @@ SIGNATURES = {
     "bfly_q4_argmax_workspace_bytes": (_i64, [_i64, _i64]),
     "bfly_add_rms_norm_q4_gemv_argmax": (_int, [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _i64, _i64, _int, _vp, _vp,
                                                 _i64, _vp]),
-    "bfly_greedy_advance": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp]),
+    "bfly_greedy_advance": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp]),
 }
 
 _lib = None

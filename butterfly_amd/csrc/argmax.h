@@ -45,4 +45,16 @@ __device__ __forceinline__ void argmax_block(float& bv, int64_t& bi) {
     for (int w = 1; w < NW; ++w) argmax_combine(bv, bi, sv[w], si[w]);
 }
 
+// (value, index) as one 64-bit key that orders like the selection above: the value's bits
+// mapped to an unsigned order (-0 taken as +0, every NaN above every number), then the index
+// reversed, so the larger key is the better candidate and 0 is below every key.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t i) {
+  uint32_t u = __float_as_uint(v);
+  if (u == 0x80000000u) u = 0u;
+  uint32_t hi = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  if (v != v) hi = 0xFFFFFFFFu;
+  return ((uint64_t)hi << 32) | (uint64_t)(0xFFFFFFFFu - i);
+}
+__device__ __forceinline__ int64_t argmax_key_index(uint64_t k) { return (int64_t)(0xFFFFFFFFu - (uint32_t)k); }
+
 }  // namespace bfly

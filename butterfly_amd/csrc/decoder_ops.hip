@@ -407,9 +407,12 @@ __global__ void __launch_bounds__(256) argmax_final_kernel(const float* __restri
 }
 
 // bfly_greedy_advance: the greedy pick over the per-workgroup candidates a product left in
-// its workspace (bfly_add_rms_norm_q4_gemv_argmax), and a decode loop's bookkeeping for the
-// token: token[0], tokens_out[counters[1]] (while below tokens_cap), both counters + 1, and the
-// next step's input row x_next = embed[token] (hidden bf16).  One workgroup.
+// its workspace (bfly_add_rms_norm_q4_gemv_argmax: an int64 count at byte 0, then
+// kGreedyMaxCand 64-bit argmax_key candidates from byte 16), and a decode loop's bookkeeping for
+// the token: token[0], tokens_out[counters[1]] (while below tokens_cap), both counters + 1, and
+// the next step's input row x_next = embed[token] (hidden bf16).  Every slot is requested with
+// the count (slots past it are dropped), so the pick waits for one round trip.  One workgroup.
+constexpr int kGreedyMaxCand = 1024;
 __global__ void __launch_bounds__(256) greedy_advance_kernel(const unsigned char* __restrict__ ws,
                                                              const __bf16* __restrict__ embed, int64_t vocab,
                                                              int64_t hidden, __bf16* __restrict__ x_next,
@@ -418,14 +421,28 @@ __global__ void __launch_bounds__(256) greedy_advance_kernel(const unsigned char
                                                              int64_t* __restrict__ counters) {
   const int t = threadIdx.x;
   const int64_t g = *reinterpret_cast<const int64_t*>(ws);
-  const float* cv = reinterpret_cast<const float*>(ws + 16);
-  const int64_t* ci = reinterpret_cast<const int64_t*>(ws + 16 + (4 * g + 7) / 8 * 8);
-  float bv = 0.f;
-  int64_t bi = -1;
-  for (int64_t c = t; c < g; c += 256) argmax_combine(bv, bi, cv[c], ci[c]);
-  argmax_block(bv, bi);
+  const uint64_t* cand = reinterpret_cast<const uint64_t*>(ws + 16);
+  uint64_t c[kGreedyMaxCand / 256];
+#pragma unroll
+  for (int k = 0; k < kGreedyMaxCand / 256; ++k) c[k] = cand[t + 256 * k];
+  uint64_t best = 0;
+#pragma unroll
+  for (int k = 0; k < kGreedyMaxCand / 256; ++k)
+    if (t + 256 * k < g && c[k] > best) best = c[k];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint64_t ob = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(best >> 32), o) << 32) |
+                        (uint32_t)__shfl_xor((int)(uint32_t)best, o);
+    best = ob > best ? ob : best;
+  }
+  __shared__ uint64_t wb[4];
   __shared__ int64_t tok_s;
+  if ((t & 63) == 0) wb[t >> 6] = best;
+  __syncthreads();
   if (t == 0) {
+#pragma unroll
+    for (int w = 1; w < 4; ++w) best = wb[w] > best ? wb[w] : best;
+    const int64_t bi = best != 0 ? argmax_key_index(best) : -1;
     tok_s = bi;
     token[0] = bi;
     const int64_t col = counters[1];
@@ -437,15 +454,18 @@ __global__ void __launch_bounds__(256) greedy_advance_kernel(const unsigned char
   const int64_t tk = tok_s;
   if (tk < 0 || tk >= vocab) return;
   const uint4* src = reinterpret_cast<const uint4*>(embed + tk * hidden);
-  for (int64_t c = t; c < hidden / 8; c += 256) reinterpret_cast<uint4*>(x_next)[c] = src[c];
+  for (int64_t c8 = t; c8 < hidden / 8; c8 += 256) reinterpret_cast<uint4*>(x_next)[c8] = src[c8];
 }
 
 }  // namespace bfly
 
-extern "C" int bfly_greedy_advance(const void* workspace, const void* embed, int64_t vocab, int64_t hidden,
-                                   void* x_next, int64_t* token, int64_t* tokens_out, int64_t tokens_cap,
-                                   int64_t* counters, hipStream_t stream) {
+extern "C" int bfly_greedy_advance(const void* workspace, int64_t workspace_bytes, const void* embed, int64_t vocab,
+                                   int64_t hidden, void* x_next, int64_t* token, int64_t* tokens_out,
+                                   int64_t tokens_cap, int64_t* counters, hipStream_t stream) {
   BFLY_CHECK_ARG(workspace && embed && x_next && token && tokens_out && counters, "null pointer");
+  BFLY_CHECK_ARG(workspace_bytes >= 16 + 8 * (int64_t)bfly::kGreedyMaxCand,
+                 "workspace_bytes=%lld: the candidate workspace holds %lld bytes (bfly_q4_argmax_workspace_bytes)",
+                 (long long)workspace_bytes, (long long)(16 + 8 * (int64_t)bfly::kGreedyMaxCand));
   BFLY_CHECK_ARG(vocab > 0 && hidden > 0 && hidden % 8 == 0 && tokens_cap > 0, "bad shape");
   BFLY_CHECK_ARG(aligned16(workspace) && aligned16(embed) && aligned16(x_next),
                  "workspace, embed and x_next must be 16-byte aligned");

@@ -165,6 +165,9 @@ __global__ void __launch_bounds__(64) q4_gemv_kernel(Q4Args a) {
 // in_features = 256 PER.  kParts: x is not given as a row but as four fp32 partial rows
 // (parts[g * in_features + i]), and x_i = bf16((p0_i + p1_i) + (p2_i + p3_i)) -- the
 // rounding of a product whose four 16-piece partials are combined by q4_wave_sum.
+// One greedy candidate (argmax_key of the best output) per workgroup.
+constexpr int kQ4MaxCand = (int)(kQ4MaxWaves / 8);   // workgroups of at least 8 waves
+
 struct Q4NormArgs {
   const __bf16* x;
   const __bf16* residual;   // or null (then h_out is null: a plain RMSNorm)
@@ -172,8 +175,7 @@ struct Q4NormArgs {
   __bf16* h_out;
   float eps;
   const float* parts;       // kParts: the four partial rows
-  float* cand_v;            // kArgmax: one greedy candidate per workgroup
-  int64_t* cand_i;
+  uint64_t* cand;           // kArgmax: one greedy candidate key per workgroup
   int64_t* cand_n;          // kArgmax: the candidate count (the grid), written by workgroup 0
 };
 
@@ -185,8 +187,15 @@ __global__ void __launch_bounds__(64 * NW) q4_norm_gemv_kernel(Q4Args a, Q4NormA
   __shared__ float part[4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t waves = (int64_t)gridDim.x * NW;
-  float bv = 0.f;      // kArgmax: this lane's greedy candidate
-  int64_t bi = -1;
+  uint64_t bk = 0;     // kArgmax: this lane's greedy candidate (argmax_key; 0 = none)
+  __shared__ unsigned long long wg_key;
+  __shared__ unsigned int wg_done;
+  if constexpr (kArgmax) {
+    if (tid == 0) {   // ordered before every wave's use by the norm's barriers
+      wg_key = 0;
+      wg_done = 0;
+    }
+  }
   // the norm's inputs are requested before the weights, so that forming the row waits for them
   // alone and runs while the weights are in flight
   RmsRowIn<PER> in = rms_row_load<PER, !kParts>(nm.x, nm.residual, nm.weight, tid, tid < 256);
@@ -214,16 +223,29 @@ __global__ void __launch_bounds__(64 * NW) q4_norm_gemv_kernel(Q4Args a, Q4NormA
                               tid < 256, part);
     __syncthreads();   // the normed row is in LDS
   }, [&](int64_t o, __bf16 yv) {
-    if constexpr (kArgmax) argmax_combine(bv, bi, (float)yv, o);
+    if constexpr (kArgmax) {
+      const uint64_t k = argmax_key((float)yv, (uint32_t)o);
+      bk = k > bk ? k : bk;
+    }
   });
   if constexpr (kArgmax) {
     // the workgroup's greedy candidate over the outputs its waves wrote (torch.argmax's order
     // on the bf16 values), for bfly_greedy_advance
-    argmax_block<NW>(bv, bi);
-    if (tid == 0) {
-      nm.cand_v[blockIdx.x] = bv;
-      nm.cand_i[blockIdx.x] = bi;
-      if (blockIdx.x == 0) *nm.cand_n = gridDim.x;
+    // only lanes 0..3 hold outputs: two steps within the quad; then each wave folds its key
+    // into the workgroup's by an LDS max and counts itself done, and the last one writes the
+    // workgroup's candidate (no barrier: a wave that is done leaves the CU at once)
+#pragma unroll
+    for (int o = 1; o <= 2; o <<= 1) {
+      const uint64_t ok = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(bk >> 32), o) << 32) |
+                          (uint32_t)__shfl_xor((int)(uint32_t)bk, o);
+      bk = ok > bk ? ok : bk;
+    }
+    if (lane == 0) {
+      atomicMax(&wg_key, (unsigned long long)bk);
+      if (atomicAdd(&wg_done, 1u) == (unsigned)NW - 1) {
+        nm.cand[blockIdx.x] = atomicMax(&wg_key, 0ull);   // every wave's key is in
+        if (blockIdx.x == 0) *nm.cand_n = gridDim.x;
+      }
     }
   }
 }
@@ -428,13 +450,14 @@ extern "C" int bfly_add_rms_norm_q4_gemv_silu_parts(const float* x_parts, int n_
   return BFLY_OK;
 }
 
-// Workspace of bfly_add_rms_norm_q4_gemv_argmax: int64 count at 0, float values at 16, int64
-// indices at 16 + 4 G rounded up to 8.
-static int64_t q4_argmax_ws_bytes(int64_t g) { return 16 + (4 * g + 7) / 8 * 8 + 8 * g; }
+// Workspace of bfly_add_rms_norm_q4_gemv_argmax: the int64 candidate count at 0 and
+// kQ4MaxCand 64-bit candidate keys from byte 16 (one per workgroup), so a reader can request
+// every slot together with the count (bfly_greedy_advance).
+constexpr int64_t kQ4ArgmaxWsBytes = 16 + 8 * (int64_t)kQ4MaxCand;
 
 extern "C" int64_t bfly_q4_argmax_workspace_bytes(int64_t out_features, int64_t in_features) {
   if (out_features <= 0 || in_features <= 0) return 0;
-  return q4_argmax_ws_bytes(q4_norm_plain_grid(out_features, in_features));
+  return kQ4ArgmaxWsBytes;
 }
 
 extern "C" int bfly_add_rms_norm_q4_gemv_argmax(const void* x, const void* residual, const void* norm_weight, float eps,
@@ -445,14 +468,15 @@ extern "C" int bfly_add_rms_norm_q4_gemv_argmax(const void* x, const void* resid
   if (rc) return rc;
   rc = q4_norm_check(x, residual, norm_weight, h_out, in_features);
   if (rc) return rc;
-  const int64_t g = q4_norm_plain_grid(out_features, in_features);
-  BFLY_CHECK_ARG(workspace != nullptr && aligned16(workspace) && workspace_bytes >= q4_argmax_ws_bytes(g),
+  BFLY_CHECK_ARG(out_features < INT32_MAX, "out_features=%lld: rows are kept as int32", (long long)out_features);
+  BFLY_CHECK_ARG(q4_norm_plain_grid(out_features, in_features) <= kQ4MaxCand, "too many workgroups");
+  BFLY_CHECK_ARG(workspace != nullptr && aligned16(workspace) && workspace_bytes >= kQ4ArgmaxWsBytes,
                  "workspace: %lld bytes, 16-byte aligned, needed (bfly_q4_argmax_workspace_bytes)",
-                 (long long)q4_argmax_ws_bytes(g));
+                 (long long)kQ4ArgmaxWsBytes);
   unsigned char* ws = static_cast<unsigned char*>(workspace);
   Q4NormArgs nm{static_cast<const __bf16*>(x), static_cast<const __bf16*>(residual),
                 static_cast<const __bf16*>(norm_weight), static_cast<__bf16*>(h_out), eps, nullptr,
-                reinterpret_cast<float*>(ws + 16), reinterpret_cast<int64_t*>(ws + 16 + (4 * g + 7) / 8 * 8)};
+                reinterpret_cast<uint64_t*>(ws + 16)};
   // the count the candidates are read with: written by the launch's workgroup 0 (no host copy
   // and no fill node: the call stays capturable)
   nm.cand_n = reinterpret_cast<int64_t*>(ws);

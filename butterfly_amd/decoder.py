@@ -294,7 +294,8 @@ def greedy_advance(g: GreedyState, embed: torch.Tensor) -> None:
     """The greedy pick from ``g.workspace`` and the step's bookkeeping in one launch
     (``bfly_greedy_advance``): ``g.tok``, ``g.out[0, col]``, ``g.ctr`` + 1 and ``g.x = embed[pick]``."""
     with on(g.x.device):
-        _native.call("bfly_greedy_advance", g.workspace.data_ptr(), embed.data_ptr(), int(embed.shape[0]),
+        _native.call("bfly_greedy_advance", g.workspace.data_ptr(), g.workspace.numel(), embed.data_ptr(),
+                     int(embed.shape[0]),
                      int(embed.shape[1]), g.x.data_ptr(), g.tok.data_ptr(), g.out.data_ptr(), int(g.out.numel()),
                      g.ctr.data_ptr(), stream_of(g.x))
 

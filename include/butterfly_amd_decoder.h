@@ -132,11 +132,11 @@ int bfly_add_rms_norm_q4_gemv_silu(const void* x, const void* residual, const vo
                                    int64_t up_row_offset, void* out, hipStream_t stream);
 
 /*
- * Device: bfly_add_rms_norm_q4_gemv that also leaves one greedy candidate per workgroup
- * (the largest bf16 output it wrote, torch.argmax's order: NaN first, then larger, then the
- * lower index) in `workspace` (bfly_q4_argmax_workspace_bytes bytes, 16-byte aligned; the
- * launch writes the candidate count too, so nothing needs clearing), for
- * bfly_greedy_advance.  The decoder's final norm with the lm_head at batch 1; no counterpart
+ * Device: bfly_add_rms_norm_q4_gemv that also leaves one greedy candidate per workgroup (the
+ * largest bf16 output its waves wrote, torch.argmax's order: NaN first, then larger, then the
+ * lower index, as one 64-bit key) in `workspace` (bfly_q4_argmax_workspace_bytes bytes,
+ * 16-byte aligned: an int64 count, then up to 1024 keys from byte 16; the launch writes the
+ * count too, so nothing needs clearing), for bfly_greedy_advance.  out_features < 2^31.  The decoder's final norm with the lm_head at batch 1; no counterpart
  * in the reference's own code (its greedy loop takes mx.argmax of the logits).
  */
 int64_t bfly_q4_argmax_workspace_bytes(int64_t out_features, int64_t in_features);
@@ -155,9 +155,9 @@ int bfly_add_rms_norm_q4_gemv_argmax(const void* x, const void* residual, const 
  * the reference's greedy step around the model call (argmax, token append, embedding lookup of
  * the next input); no counterpart in its own code.
  */
-int bfly_greedy_advance(const void* workspace, const void* embed, int64_t vocab, int64_t hidden, void* x_next,
-                        int64_t* token, int64_t* tokens_out, int64_t tokens_cap, int64_t* counters,
-                        hipStream_t stream);
+int bfly_greedy_advance(const void* workspace, int64_t workspace_bytes, const void* embed, int64_t vocab,
+                        int64_t hidden, void* x_next, int64_t* token, int64_t* tokens_out, int64_t tokens_cap,
+                        int64_t* counters, hipStream_t stream);
 
 /*
  * Device: bfly_add_rms_norm_q4_gemv_silu whose input row x is given as n_parts = 4

@@ -168,18 +168,21 @@ def test_greedy_entry_points_validate_before_launch():
     (fake addresses)."""
     lib = _native.lib()
     need = lib.bfly_q4_argmax_workspace_bytes(151936, 2048)
-    # the lm_head's 37984 sets of four rows: 7597 waves of 8 per workgroup = 950 candidates
-    assert need == 16 + 4 * 950 + 8 * 950 and lib.bfly_q4_argmax_workspace_bytes(0, 2048) == 0
+    # an int64 count and 1024 candidate keys, one per workgroup, whatever the grid (the lm_head's: 950)
+    assert need == 16 + 8 * 1024 and lib.bfly_q4_argmax_workspace_bytes(0, 2048) == 0
     head = (256, 512, 768, 1e-6, 1024, 1280, 1536, 151936, 2048, 64, 2048)
     assert lib.bfly_add_rms_norm_q4_gemv_argmax(*head, 0x8000, need - 1, None) == _native.ERR_INVALID
     assert b"workspace" in lib.bfly_last_error()
     assert lib.bfly_add_rms_norm_q4_gemv_argmax(*head, 0x8008, need, None) == _native.ERR_INVALID
-    assert lib.bfly_greedy_advance(0x1000, 0x2000, 100, 2044, 0x3000, 0x4000, 0x5000, 8, 0x6000, None) == \
+    adv = lib.bfly_greedy_advance
+    assert adv(0x1000, need, 0x2000, 100, 2044, 0x3000, 0x4000, 0x5000, 8, 0x6000, None) == \
         _native.ERR_INVALID                                      # hidden not a multiple of 8
-    assert lib.bfly_greedy_advance(0x1000, 0x2008, 100, 2048, 0x3000, 0x4000, 0x5000, 8, 0x6000, None) == \
+    assert adv(0x1000, need, 0x2008, 100, 2048, 0x3000, 0x4000, 0x5000, 8, 0x6000, None) == \
         _native.ERR_INVALID                                      # embed misaligned
-    assert lib.bfly_greedy_advance(None, 0x2000, 100, 2048, 0x3000, 0x4000, 0x5000, 8, 0x6000, None) == \
-        _native.ERR_INVALID
+    assert adv(None, need, 0x2000, 100, 2048, 0x3000, 0x4000, 0x5000, 8, 0x6000, None) == _native.ERR_INVALID
+    assert adv(0x1000, need - 8, 0x2000, 100, 2048, 0x3000, 0x4000, 0x5000, 8, 0x6000, None) == \
+        _native.ERR_INVALID                                      # a workspace short of the 1024 slots
+    assert b"workspace_bytes" in lib.bfly_last_error()
 
 
 def test_decode_step_checks_the_cache_window_before_launch():

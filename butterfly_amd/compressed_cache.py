@@ -274,12 +274,28 @@ class CompressedKVCache:
         if rule is None:
             raise ValueError(f"Unsupported Butterfly partner rule: {partner_rule!r}")
         qw, kw, cos, sin, eps = qk_norm
+        dev = self._ring_k.device
+        if q.device != dev or keys.device != dev or values.device != dev:
+            raise ValueError(f"decode_step_oproj tensors must be on the cache's device {dev}")
+        if cos.dtype != torch.float32 or cos.shape != sin.shape or cos.dim() != 2 or cos.shape[-1] != d or \
+                not cos.is_contiguous() or not sin.is_contiguous() or cos.device != dev or sin.device != dev:
+            raise ValueError("rope tables must be contiguous fp32 [rows, head_dim] on the cache's device")
+        for w in (qw, kw):
+            if w.dtype != torch.bfloat16 or tuple(w.shape) != (d,) or not w.is_contiguous() or w.device != dev:
+                raise ValueError("q/k norm weights must be contiguous bf16 [head_dim] on the cache's device")
+        n_out = int(o_proj.out_features)
+        if int(o_proj.in_features) != hq * d or o_proj.packed.device != dev or o_proj.scale_bias.device != dev \
+                or not o_proj.packed.is_contiguous() or not o_proj.scale_bias.is_contiguous():
+            raise ValueError(f"o_proj must be a 4-bit layer of hq * head_dim = {hq * d} inputs on the cache's "
+                             f"device (contiguous codes and scales)")
         q, keys, values = _c(q), _c(keys), _c(values)
         if out is None:
             out = torch.empty_like(q)
-        n_out = int(o_proj.out_features)
         if parts is None:
             parts = torch.empty(hkv, b, n_out, dtype=torch.float32, device=q.device)
+        elif (parts.dtype != torch.float32 or tuple(parts.shape) != (hkv, b, n_out) or not parts.is_contiguous()
+              or parts.device != dev):
+            raise ValueError(f"parts must be a contiguous fp32 [{hkv}, {b}, {n_out}] tensor on the cache's device")
         _native.call("bfly_decode_step_qk_norm_oproj", q.data_ptr(), _dtype_code(q), b, hq, hkv, d,
                      keys.data_ptr(), values.data_ptr(), self._ring_k.data_ptr(), self._ring_v.data_ptr(),
                      self.tail_capacity, self._pool_k.data_ptr(), self._pool_v.data_ptr(), self.summary_capacity,

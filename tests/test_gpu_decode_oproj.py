@@ -151,6 +151,11 @@ def test_oproj_step_refuses_other_shapes():
     odd = QuantLinear(2048, 2040, generator=g, device="cuda")                 # not a multiple of 32
     with pytest.raises(ValueError, match="multiple of 32"):
         core.step_oproj(*raw, ca, qk, odd)
+    with pytest.raises(ValueError, match="2048 inputs"):                    # in_features other than hq * d
+        core.step_oproj(*raw, ca, qk, QuantLinear(1024, 2048, generator=g, device="cuda"))
+    with pytest.raises(ValueError, match="parts"):
+        ca.decode_step_oproj(*raw, layer_idx=0, local_window_tokens=64, qk_norm=qk, o_proj=attn.o_proj,
+                             parts=torch.empty(4, 1, 2048, dtype=torch.bfloat16, device="cuda"))   # wrong dtype
     ca.use_device_counters(False)
     with pytest.raises(ValueError):
         core.step_oproj(*raw, ca, qk, attn.o_proj)

@@ -86,6 +86,40 @@ def test_oproj_step_equals_step_then_q4_gemv(hidden, layer_idx, cache_window):
     assert torch.equal(sa.pool_k, sb.pool_k) and torch.equal(sa.pool_v, sb.pool_v)
 
 
+def test_oproj_step_batch_of_three():
+    """Three sequences (12 of the 16 a state of 64 copies per sequence holds): every batch row's
+    partial rows combine into bfly_q4_gemv's product of its own attention row."""
+    cfg = DecoderConfig(vocab_size=256, hidden_size=2048, num_layers=1, num_heads=16, num_kv_heads=4,
+                        head_dim=128, intermediate_size=512)
+    g = torch.Generator(device="cuda").manual_seed(21)
+    attn = Attention(cfg, generator=g, device="cuda")
+    cos, sin = rope_cos_sin(torch.arange(1024, device="cuda"), 128, cfg.rope_theta)
+    qk = (attn.q_norm.weight, attn.k_norm.weight, cos.contiguous(), sin.contiguous(), attn.q_norm.eps)
+    k = torch.randn(3, 4, 600, 128, generator=g, device="cuda").bfloat16()
+    caches = []
+    for _ in range(2):
+        c = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=1000)
+        c.update_and_fetch(k, k.flip(2))
+        c.use_device_counters()
+        caches.append(c)
+    ca, cb = caches
+    core = bf.ButterflyAttentionCore(bf.compressed_butterfly_config(), 6)
+    for step in range(140):
+        q = torch.randn(3, 16, 1, 128, generator=g, device="cuda").bfloat16()
+        kn = torch.randn(3, 4, 1, 128, generator=g, device="cuda").bfloat16()
+        vn = torch.randn(3, 4, 1, 128, generator=g, device="cuda").bfloat16()
+        oa = core(q, kn, vn, ca, qk_norm=qk)
+        ob, parts = core.step_oproj(q, kn, vn, cb, qk, attn.o_proj)
+        assert parts.shape == (4, 3, 2048)
+        assert torch.equal(oa, ob), step
+        for b in range(3):
+            y = q4_gemv(oa[b].reshape(1, 1, -1), attn.o_proj).view(1, 2048)
+            assert torch.equal(_combined(parts[:, b:b + 1]), y), (step, b)
+    ca.sync()
+    cb.sync()
+    assert ca.offset == cb.offset == 740
+
+
 def test_entry_points_take_turns_on_one_cache():
     """Steps with and without the projection alternate on one cache (runs of 1, 2 and 5 across
     block ends): every step's attention output equals that of a cache stepped without it, and

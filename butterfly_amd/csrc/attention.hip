@@ -681,10 +681,28 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
   }
 
   int yrow = (int)blockIdx.y;
+  int seg = xcd_remap(blockIdx.x, gridDim.x);
   if constexpr (kBatch) {
-    // this workgroup's chunk: its queries, output and cache state
-    const int zc = yrow / cb.rows_per_chunk;
-    yrow -= zc * cb.rows_per_chunk;
+    // this workgroup's chunk (zc), row (batch x kv head x head part) and segment.  Workgroups
+    // go to the 8 XCDs round-robin by linear id; when they divide evenly, each XCD takes a
+    // contiguous run of the order (row, chunk, segment), so that a segment and the one before
+    // it, whose last page is its halo, mostly share an L2 (the first segment of a chunk takes
+    // its halo from the previous chunk's last).
+    const int nsg = (int)gridDim.x, rpc = cb.rows_per_chunk;
+    const int total = rpc * cb.nch * nsg;
+    int zc;
+    if (total % 8 == 0) {
+      const int lin = (int)blockIdx.y * nsg + (int)blockIdx.x;
+      const int ord = (lin & 7) * (total >> 3) + (lin >> 3);
+      yrow = ord / (cb.nch * nsg);
+      const int rem = ord - yrow * cb.nch * nsg;
+      zc = rem / nsg;
+      seg = rem - zc * nsg;
+    } else {
+      zc = yrow / rpc;
+      yrow -= zc * rpc;
+      seg = (int)blockIdx.x;
+    }
     const ChunkArgs& ck = cb.c[zc];
     a.q = ck.q;
     a.out = ck.out;
@@ -709,7 +727,6 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
   // parity hpar (the wave takes heads hlo + hpar, hlo + hpar + 2, ...)
   const int qwave = kWaveHead ? (wave & 3) : wave;
   const int hpar = kWaveHead ? (wave >> 2) : 0;
-  const int seg = xcd_remap(blockIdx.x, gridDim.x);
   // small grids split a GQA group's heads over workgroups of hper heads each
   const int gsz = a.hq / a.hkv;
   const int nparts = (gsz + hper - 1) / hper;
@@ -1178,10 +1195,9 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
   }
 }
 
-// upd (optional, bf16 MFMA path only): a cache update to run in the same
-// launch on extra grid rows (see attn_mfma_kernel's kUpd).
-static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, const char* what,
-                            const UpdateJob* upd = nullptr, int64_t upd_rows = 0) {
+// One attention launch: the MFMA kernel where its conditions hold, else the fp32 tile kernel
+// or the generic one.
+static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, const char* what) {
   BFLY_CHECK_ARG(aligned16(a.q) && aligned16(a.out) && aligned16(a.k) && aligned16(a.v) && aligned16(a.ks) &&
                      aligned16(a.vs),
                  "%s: tensor pointers must be 16-byte aligned", what);
@@ -1194,7 +1210,6 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
                        a.nblocks < INT32_MAX && a.kv_rows < INT32_MAX && a.pool_rows < INT32_MAX;
   if (a.tq == 0) return BFLY_OK;
   BFLY_CHECK_ARG(mfma_ok || a.nbr != nullptr, "%s: neighbour rows from the topology need the MFMA path", what);
-  BFLY_CHECK_ARG(mfma_ok || upd == nullptr, "%s: a fused cache update needs the MFMA path", what);
   if (mfma_ok) {
     const int64_t c_first = floordiv(a.q_pos0, kPage);
     const int64_t c_last = floordiv(a.q_pos0 + a.tq - 1, kPage);
@@ -1239,28 +1254,10 @@ static int launch_attention(const AttnArgs& a, int dtype, hipStream_t stream, co
     const int nparts = (gsz + hper - 1) / hper;
     BFLY_CHECK_ARG(groups * nparts <= 65535, "%s: grid too large", what);
     dim3 grid((unsigned)nseg, (unsigned)(groups * nparts));
-    if (upd != nullptr) {
-      const int64_t ux = update_x(upd->n_blocks, upd->step - upd->append_from, upd->d, 8);
-      m.upd = *upd;
-      m.attn_y = (int)grid.y;
-      m.upd_x = (int)ux;
-      m.upd_rows = (int)upd_rows;
-      m.upd_wgs = ux * upd_rows * 2;   // work items; a d = 256 workgroup (512 threads) runs two
-      const int64_t per_wg = a.d == 256 ? MfmaCfg<256>::NTHR / 256 : 1;
-      const int64_t extra = ((m.upd_wgs + per_wg - 1) / per_wg + nseg - 1) / nseg;
-      BFLY_CHECK_ARG(ux <= INT32_MAX && upd_rows <= 65535 && grid.y + extra <= 65535, "%s: grid too large", what);
-      grid.y += (unsigned)extra;
-      switch (a.d) {
-        case 64: hipLaunchKernelGGL((attn_mfma_kernel<64, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
-        case 128: hipLaunchKernelGGL((attn_mfma_kernel<128, true>), grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
-        default: hipLaunchKernelGGL((attn_mfma_kernel<256, true>), grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
-      }
-    } else {
-      switch (a.d) {
-        case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
-        case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
-        default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
-      }
+    switch (a.d) {
+      case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
+      case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(256), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
+      default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, (int)c_first, (int)nchunks, hper, NoBatch{}); break;
     }
   } else if (dtype == BFLY_DTYPE_F32 && contiguous && a.nbr != nullptr && a.W <= 64 && a.bs % 16 == 0 &&
              a.hq / a.hkv <= 4 &&

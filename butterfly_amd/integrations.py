@@ -698,20 +698,24 @@ def chunked_prefill(core: ButterflyAttentionCore, chunks, cache: CompressedKVCac
             continue
         outs += got
         i += len(got)
-        run = _stream_run(cache, int(chunks[i - 1][0].shape[2]))
+        run = _stream_run(cache, int(chunks[i - 1][0].shape[2]), run)
     return outs
 
 
-# chunks per bfly_stream_chunks call after the first (small) run: about 64, rounded up to whole
-# batches of the native loop (its batches hold at most 10 chunks and half the ring minus two pages),
-# so that a call does not end in a small batch, whose attention launch runs alone
-_STREAM_RUN = 64
+# Chunks per bfly_stream_chunks call: a first run of 8, then each run about 1.5 times the one
+# before, in whole batches of the native loop (its batches hold at most 10 chunks and half the ring
+# minus two pages), up to 256.  The host prepares a run (about 2 us per chunk) in less time than
+# the GPU takes for the one before it (about 3 us per chunk), so the GPU is not left waiting
+# between calls, and a call rarely ends in a small batch, whose attention launch runs alone.
+_STREAM_GROWTH = 1.5
+_STREAM_RUN_MAX = 256
 _STREAM_BATCH_CAP = 10
 
 
-def _stream_run(cache, chunk_len: int) -> int:
+def _stream_run(cache, chunk_len: int, prev: int) -> int:
     per = max(1, min(_STREAM_BATCH_CAP, (int(cache.tail_capacity) - 128) // 2 // max(1, chunk_len)))
-    return per * -(-_STREAM_RUN // per)
+    want = min(_STREAM_RUN_MAX, max(int(prev * _STREAM_GROWTH), per))
+    return per * -(-want // per)
 
 
 def _stream_possible(core: ButterflyAttentionCore, cache, chunk) -> bool:
@@ -740,17 +744,27 @@ def _stream_chunks(core: ButterflyAttentionCore, chunks, start: int, run: int,
     q0, k0, _ = chunks[start]
     b, hq, _, d = (int(x) for x in q0.shape)
     hkv = int(k0.shape[1])
-    qs, ks, vs = [], [], []
+    # One pass over the chunks, each tensor's attributes read once (the host's cost per chunk
+    # is what keeps the GPU fed): pointers, lengths, and the tensors themselves only where a
+    # chunk needed a contiguous copy (kept alive until the launches are enqueued).
+    qp, kp, vp, lens_l, copies = [], [], [], [], []
     bf16 = torch.bfloat16
     for qc, kc, vc in chunks[start:start + run]:
-        n = qc.shape[2]
-        if (n <= 2 or qc.shape != (b, hq, n, d) or kc.shape != (b, hkv, n, d) or vc.shape != kc.shape
+        sq = qc.shape
+        n = sq[2]
+        if (n <= 2 or sq != (b, hq, n, d) or kc.shape != (b, hkv, n, d) or vc.shape != (b, hkv, n, d)
                 or qc.dtype != bf16 or kc.dtype != bf16 or vc.dtype != bf16 or not qc.is_cuda):
             break
-        qs.append(_c(qc))
-        ks.append(_c(kc))
-        vs.append(_c(vc))
-    if not qs:
+        pq, pk, pv = qc.data_ptr(), kc.data_ptr(), vc.data_ptr()
+        if (pq | pk | pv) & 15 or not (qc.is_contiguous() and kc.is_contiguous() and vc.is_contiguous()):
+            qc, kc, vc = _c(qc), _c(kc), _c(vc)
+            copies.append((qc, kc, vc))
+            pq, pk, pv = qc.data_ptr(), kc.data_ptr(), vc.data_ptr()
+        qp.append(pq)
+        kp.append(pk)
+        vp.append(pv)
+        lens_l.append(n)
+    if not qp:
         return None
     cache.sync()
     cache._apply_realign()
@@ -759,20 +773,24 @@ def _stream_chunks(core: ButterflyAttentionCore, chunks, start: int, run: int,
         raise ValueError("keys do not match the cache's batch/head/dim/dtype")
     # outputs: consecutive 16-byte aligned ranges of one allocation (chunks of one length: one
     # [m, b, hq, n, d] tensor unbound into its rows, which costs the host far less per chunk)
-    m = len(qs)
-    n0 = int(qs[0].shape[2])
-    if all(int(q.shape[2]) == n0 for q in qs):
-        outs = list(torch.empty((m, b, hq, n0, d), dtype=torch.bfloat16, device=q0.device).unbind(0))
+    m = len(qp)
+    n0 = lens_l[0]
+    per = b * hq * d
+    if all(n == n0 for n in lens_l):
+        big = torch.empty((m, b, hq, n0, d), dtype=torch.bfloat16, device=q0.device)
+        outs = list(big.unbind(0))
+        base, step = big.data_ptr(), per * n0 * 2
+        op = [base + i * step for i in range(m)]
     else:
-        sizes = [q.numel() for q in qs]
         starts, off = [], 0
-        for n in sizes:
+        for n in lens_l:
             starts.append(off)
-            off += (n + 7) // 8 * 8
+            off += (per * n + 7) // 8 * 8
         flat = torch.empty(off, dtype=torch.bfloat16, device=q0.device)
-        outs = [flat[s:s + n].view(q.shape) for s, n, q in zip(starts, sizes, qs)]
-    ptrs = lambda ts: (C.c_void_p * m)(*[t.data_ptr() for t in ts])
-    lens = (C.c_int64 * m)(*[int(q.shape[2]) for q in qs])
+        outs = [flat[s0:s0 + per * n].view(b, hq, n, d) for s0, n in zip(starts, lens_l)]
+        op = [o.data_ptr() for o in outs]
+    ptrs = lambda xs: (C.c_void_p * m)(*xs)
+    lens = (C.c_int64 * m)(*lens_l)
     counters = (C.c_int64 * 4)(cache.offset, cache.tail_size, cache.summary_count, cache.summary_offset)
     done = C.c_int64(0)
     c = core.cfg
@@ -781,7 +799,7 @@ def _stream_chunks(core: ButterflyAttentionCore, chunks, start: int, run: int,
     t0 = _now_ms()
     with _on(q0.device):
         rc = _native.lib().bfly_stream_chunks(
-            m, ptrs(qs), ptrs(ks), ptrs(vs), ptrs(outs), lens, _dtype_code(q0), b, hq, hkv, d, ring_k.data_ptr(),
+            m, ptrs(qp), ptrs(kp), ptrs(vp), ptrs(op), lens, _dtype_code(q0), b, hq, hkv, d, ring_k.data_ptr(),
             ring_v.data_ptr(), cache.tail_capacity, pool_k.data_ptr(), pool_v.data_ptr(), cache.summary_capacity,
             counters, int(cache.local_window_tokens), core.layer_idx, rule, int(c.block_local_window_blocks),
             int(c.block_sink_blocks), int(c.block_partner_count), cache.block_size, w, _scale(core.scale, d),
@@ -792,6 +810,6 @@ def _stream_chunks(core: ButterflyAttentionCore, chunks, start: int, run: int,
     _native.check(rc, "bfly_stream_chunks")
     lay = core.layout(cache.offset, hkv, hq // hkv, q0.device)
     core._last = (t0, _now_ms(), None, "block_sparse_compressed_active",
-                  {"seq_len": cache.offset, "q_len": int(qs[-1].shape[2]), "block_sparse_active_mode": True,
+                  {"seq_len": cache.offset, "q_len": lens_l[-1], "block_sparse_active_mode": True,
                    "native_chunk_loop": m}, lay)     # chunks of the last native call
     return outs

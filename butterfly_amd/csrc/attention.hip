@@ -556,6 +556,11 @@ struct MfmaCfg {
   // and take the two heads of a pair), so a wave holds one head's Q, S and O and two waves fit
   // per SIMD; smaller d: 256 threads, each wave runs a head pair over its 16 query rows
   static constexpr bool kWaveHead = D == 256;
+  // d = 256: the two staged pages sit at fixed rows, the chunk's halo (page c - 1) at 0..63 and
+  // its own page at 64..127, so every tile a wave reads is at a constant offset from a few
+  // per-lane bases (the offsets fold into the LDS instructions); a segment of several chunks
+  // shifts the page it keeps between the halves.  Smaller d keep pages at rows (page & 1) * 64.
+  static constexpr bool kFixedPages = D == 256;
   static constexpr int NTHR = kWaveHead ? 512 : 256;
   static constexpr int KP = D + 8;                 // bf16 per K row (pad 16 B)
   static constexpr int KSTEPS = D / 32;            // MFMA k-steps over head_dim
@@ -720,6 +725,7 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
 
   constexpr int NTHR = C::NTHR, NWAVES = NTHR / 64;
   constexpr bool kWaveHead = C::kWaveHead;
+  constexpr bool kFixed = C::kFixedPages;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int lg = lane >> 4, lq = lane & 15;
@@ -877,8 +883,9 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
       vst[it] = ld(vbase, i / C::PIECES, i % C::PIECES);
     }
   };
-  auto store_page = [&](int pg) {
-    const int sbase = (pg & 1) * kPage;
+  // page pg into rows half * 64.. (kFixed) or (pg & 1) * 64..
+  auto store_page = [&](int pg, int half) {
+    const int sbase = (kFixed ? half : (pg & 1)) * kPage;
 #pragma unroll
     for (int it = 0; it < C::KLD; ++it) {
       const int i = tid + it * NTHR;
@@ -1005,15 +1012,58 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
   if constexpr (kWaveHead) build_rows();
   fetch_page(dir > 0 ? cbeg - 1 : cend - 1);
   if constexpr (!kWaveHead) build_rows();
-  store_page(dir > 0 ? cbeg - 1 : cend - 1);
+  // (kFixed: walking forwards, the first page is the first chunk's halo; backwards, its own page)
+  store_page(dir > 0 ? cbeg - 1 : cend - 1, dir > 0 ? 0 : 1);
   fetch_page(new_page(cfirst));
   __syncthreads();   // s_nbr visible
   fetch_sum(cfirst);
 
   __bf16* ohead0 = reinterpret_cast<__bf16*>(a.out) + ((int64_t)bi * a.hq + (int64_t)kvh * gsz) * a.tq * D;
+  // kFixed: per-lane bases (elements) of the fragments a wave reads.  K: row 16 qwave + lq of
+  // the window tiles (tile t adds 16 t rows), row 128 + lq of the summary tile, at d
+  // lg * D / 4.  V (transposing reads): rows 16 qwave + 4 lg + (lq >> 2) and 128 + ..., at the
+  // 8-byte unit mt * 8 + (lq & 3) * 2 + half XOR the rows' swizzle ((lq >> 2) & 3) * 8, which is
+  // vr[mt & 3] + (mt >> 2) * 128 + half * 4 elements.
+  int klane = 0, ksum = 0, vlane[4] = {0, 0, 0, 0}, vsum[4] = {0, 0, 0, 0};
+  if constexpr (kFixed) {
+    klane = (16 * qwave + lq) * C::KP + lg * (D / 4);
+    ksum = (kRing + lq) * C::KP + lg * (D / 4);
+    const int x = (lq >> 2) & 3;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int vr = (r ^ x) * 32 + (lq & 3) * 8;
+      vlane[r] = (16 * qwave + 4 * lg + (lq >> 2)) * D + vr;
+      vsum[r] = (kRing + 4 * lg + (lq >> 2)) * D + vr;
+    }
+  }
 
   for (int c = cfirst; c != cstop; c += dir) {
-    store_page(new_page(c));
+    if constexpr (kFixed) {
+      // the page this chunk shares with the previous one moves to its place: forwards the old
+      // own page becomes the halo (rows 64.. -> 0..), backwards the old halo the own page
+      if (c != cfirst) {
+        const int src = dir > 0 ? kPage : 0, dst = kPage - src;
+        // (a native vector type: arrays of HIP's uint4 struct stay in scratch memory)
+        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+        u32x4 kx[C::KLD], vx[C::KLD];
+#pragma unroll
+        for (int it = 0; it < C::KLD; ++it) {
+          const int i = tid + it * NTHR;
+          const int r = i / C::PIECES, pc = i % C::PIECES;
+          kx[it] = *reinterpret_cast<const u32x4*>(Ks + (src + r) * C::KP + pc * 8);
+          vx[it] = *reinterpret_cast<const u32x4*>(Vs + (src + r) * D + pc * 8);   // same swizzle 64 rows on
+        }
+#pragma unroll
+        for (int it = 0; it < C::KLD; ++it) {
+          const int i = tid + it * NTHR;
+          const int r = i / C::PIECES, pc = i % C::PIECES;
+          *reinterpret_cast<u32x4*>(Ks + (dst + r) * C::KP + pc * 8) = kx[it];
+          *reinterpret_cast<u32x4*>(Vs + (dst + r) * D + pc * 8) = vx[it];
+        }
+        __syncthreads();   // every copy read before the new page lands on its source rows
+      }
+    }
+    store_page(new_page(c), dir > 0 ? 1 : 0);
     store_sum();
     __syncthreads();
     if (c + dir != cstop) {
@@ -1046,7 +1096,7 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
     }
     int slot[6];
 #pragma unroll
-    for (int t = 0; t < 5; ++t) slot[t] = (pw - kPage + 16 * t) & (kRing - 1);
+    for (int t = 0; t < 5; ++t) slot[t] = kFixed ? 16 * (qwave + t) : (pw - kPage + 16 * t) & (kRing - 1);
     slot[5] = kRing;
 
     // softmax of one head's 24 scores (already masked to -inf) -> bf16 P, 1/l
@@ -1095,7 +1145,9 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
             bf16x8 kf[C::KSTEPS];
   #pragma unroll
             for (int ks = 0; ks < C::KSTEPS; ++ks)
-              kf[ks] = *reinterpret_cast<const bf16x8*>(Ks + (slot[t] + lq) * C::KP + lg * (D / 4) + 8 * ks);
+              kf[ks] = *reinterpret_cast<const bf16x8*>(
+                  kFixed ? Ks + (t < 5 ? klane + 16 * t * C::KP : ksum) + 8 * ks
+                         : Ks + (slot[t] + lq) * C::KP + lg * (D / 4) + 8 * ks);
             f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
   #pragma unroll
             for (int ks = 0; ks < C::KSTEPS; ++ks) {
@@ -1144,8 +1196,15 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
   #pragma unroll
                 for (int pr = 0; pr < 3; ++pr) {
                   const int ra = slot[2 * pr] + 4 * lg + (lq >> 2), rb = slot[2 * pr + 1] + 4 * lg + (lq >> 2);
-                  const bf16x4 va = read_tr(Vs + ra * D + (unit ^ (2 * C::vswz(ra))) * 4);
-                  const bf16x4 vb = read_tr(Vs + rb * D + (unit ^ (2 * C::vswz(rb))) * 4);
+                  // kFixed: rows 16 (qwave + t) + 4 lg + (lq >> 2) (t < 5) or 128 + ..., whose
+                  // swizzle is the lane's (lq >> 2) & 3; unit ^ that swizzle is then
+                  // ((mt ^ x) * 8 + low bits) with x = (lq >> 2) & 3, i.e. vr[mt & 3] + (mt >> 2) * 128
+                  const int tail = (mt >> 2) * 128 + half * 4;
+                  const int ta = 2 * pr, tb = 2 * pr + 1;
+                  const bf16x4 va = read_tr(kFixed ? Vs + vlane[mt & 3] + 16 * ta * D + tail
+                                                   : Vs + ra * D + (unit ^ (2 * C::vswz(ra))) * 4);
+                  const bf16x4 vb = read_tr(kFixed ? Vs + (tb < 5 ? vlane[mt & 3] + 16 * tb * D : vsum[mt & 3]) + tail
+                                                   : Vs + rb * D + (unit ^ (2 * C::vswz(rb))) * 4);
                   vf[pr] = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
                 }
                 f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};

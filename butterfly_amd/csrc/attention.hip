@@ -812,7 +812,8 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
 
   // ---- register staging of one page (K rows and V row pairs) and of the routed summaries
   uint4 kst[C::KLD], vst[C::KLD];
-  auto fetch_page = [&](int pg) {
+  // (into kst / vst, or the given registers)
+  auto fetch_page_to = [&](int pg, uint4 (&kst)[C::KLD], uint4 (&vst)[C::KLD]) {
     const int p0 = pg * kPage;
     // row of position p0 (+ r): linear, or ring slot (ring >= kPage, so one wrap at most)
     int r0 = 0;
@@ -883,8 +884,9 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
       vst[it] = ld(vbase, i / C::PIECES, i % C::PIECES);
     }
   };
+  auto fetch_page = [&](int pg) { fetch_page_to(pg, kst, vst); };
   // page pg into rows half * 64.. (kFixed) or (pg & 1) * 64..
-  auto store_page = [&](int pg, int half) {
+  auto store_page_from = [&](int pg, int half, const uint4 (&kst)[C::KLD], const uint4 (&vst)[C::KLD]) {
     const int sbase = (kFixed ? half : (pg & 1)) * kPage;
 #pragma unroll
     for (int it = 0; it < C::KLD; ++it) {
@@ -899,6 +901,7 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
       *reinterpret_cast<uint4*>(Vs + r * D + (pc ^ C::vswz(r)) * 8) = vst[it];
     }
   };
+  auto store_page = [&](int pg, int half) { store_page_from(pg, half, kst, vst); };
 
   uint4 skst[C::SLD], svst[C::SLD];
   int scn[C::SLD], scb[C::SLD];
@@ -1007,14 +1010,21 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
     for (int u = 0; u < kQPipe; ++u)
       if (hlo + u < hhi) load_q(u, cfirst, hlo + u);
   }
-  // d <= 128: the rows are built while the first page is in flight; at d = 256 the rows'
-  // registers would join the page's (spills), so they come first
-  if constexpr (kWaveHead) build_rows();
-  fetch_page(dir > 0 ? cbeg - 1 : cend - 1);
-  if constexpr (!kWaveHead) build_rows();
-  // (kFixed: walking forwards, the first page is the first chunk's halo; backwards, its own page)
-  store_page(dir > 0 ? cbeg - 1 : cend - 1, dir > 0 ? 0 : 1);
-  fetch_page(new_page(cfirst));
+  if constexpr (kFixed) {
+    // both pages of the first chunk requested together, then the rows built while they are in
+    // flight (walking forwards, the first page is the chunk's halo; backwards, its own page)
+    uint4 k0[C::KLD], v0[C::KLD];
+    fetch_page_to(dir > 0 ? cbeg - 1 : cend - 1, k0, v0);
+    fetch_page(new_page(cfirst));
+    build_rows();
+    store_page_from(dir > 0 ? cbeg - 1 : cend - 1, dir > 0 ? 0 : 1, k0, v0);
+  } else {
+    // the rows are built while the first page is in flight
+    fetch_page(dir > 0 ? cbeg - 1 : cend - 1);
+    build_rows();
+    store_page(dir > 0 ? cbeg - 1 : cend - 1, 0);
+    fetch_page(new_page(cfirst));
+  }
   __syncthreads();   // s_nbr visible
   fetch_sum(cfirst);
 

@@ -26,6 +26,7 @@ Every attention call runs a HIP kernel of ``libbutterfly_amd.so``.
 """
 from __future__ import annotations
 
+import gc
 import time
 import warnings
 from dataclasses import dataclass, field
@@ -683,22 +684,33 @@ def chunked_prefill(core: ButterflyAttentionCore, chunks, cache: CompressedKVCac
     kernels and arguments, with the per-chunk bookkeeping in C++; a small first run
     so the GPU starts while the host prepares the next) whenever the configuration
     allows it; a chunk the loop does not cover goes through ``core``.
+
+    Python's cyclic garbage collector is paused for the loop (and resumed as it was): the
+    loop makes a few objects per chunk (output views, pointer arrays), none of them cyclic,
+    and each collection they would set off (several per stream, tens of microseconds each)
+    holds the host while the GPU drains its queue.
     """
     chunks = list(chunks)
     if not chunks:
         return []
-    outs = [core(*chunks[0], cache)]
-    i, native, run = 1, True, 8
-    while i < len(chunks):
-        got = _stream_chunks(core, chunks, i, run, cache) if native else None
-        if got is None:
-            native = native and _stream_possible(core, cache, chunks[i])
-            outs.append(core(*chunks[i], cache))
-            i += 1
-            continue
-        outs += got
-        i += len(got)
-        run = _stream_run(cache, int(chunks[i - 1][0].shape[2]), run)
+    collecting = gc.isenabled()
+    gc.disable()
+    try:
+        outs = [core(*chunks[0], cache)]
+        i, native, run = 1, True, 8
+        while i < len(chunks):
+            got = _stream_chunks(core, chunks, i, run, cache) if native else None
+            if got is None:
+                native = native and _stream_possible(core, cache, chunks[i])
+                outs.append(core(*chunks[i], cache))
+                i += 1
+                continue
+            outs += got
+            i += len(got)
+            run = _stream_run(cache, int(chunks[i - 1][0].shape[2]), run)
+    finally:
+        if collecting:
+            gc.enable()
     return outs
 
 

@@ -294,6 +294,34 @@ def test_chunked_prefill_then_decode_through_core(dtype):
     assert core.last_profile.notes["stage_count"] == tp.width((total + 127) // 128)
 
 
+def test_chunked_prefill_pauses_the_cyclic_collector_and_restores_it():
+    """chunked_prefill runs its loop with Python's cyclic GC paused and leaves it as it found
+    it, also when a chunk raises (a stand-in core and cache: no native loop, CPU only)."""
+    import gc
+    seen = []
+
+    def core(q, k, v, cache):
+        seen.append(gc.isenabled())
+        if q.shape[2] == 3:
+            raise RuntimeError("planted")
+        return q
+
+    chunks = [tuple(torch.zeros(1, 1, n, 4) for _ in range(3)) for n in (5, 4, 6)]
+    was = gc.isenabled()
+    try:
+        for enabled in (True, False):
+            gc.enable() if enabled else gc.disable()
+            seen.clear()
+            outs = bf.chunked_prefill(core, chunks, object())
+            assert [o.shape[2] for o in outs] == [5, 4, 6] and seen == [False] * 3
+            assert gc.isenabled() == enabled
+            with pytest.raises(RuntimeError, match="planted"):
+                bf.chunked_prefill(core, chunks + [tuple(torch.zeros(1, 1, 3, 4) for _ in range(3))], object())
+            assert gc.isenabled() == enabled
+    finally:
+        gc.enable() if was else gc.disable()
+
+
 @pytest.mark.gpu
 def test_stock_decode_fallback_is_dense_over_the_tail():
     dtype, d, b, hq, hkv, T = torch.bfloat16, 128, 2, 8, 2, 1000

@@ -98,6 +98,10 @@ CASES = [
     (1, 16, 2, 2048, 128, 128, 17, 4, torch.bfloat16),
     (1, 2, 1, 1500, 64, 128, 64, 5, torch.bfloat16),
     (1, 16, 4, 3000, 256, 128, 64, 6, torch.bfloat16),
+    # d = 256 with two / four chunks per workgroup segment: the kept page moves between the LDS
+    # halves from chunk to chunk, forwards in even segments and backwards in odd ones
+    (2, 16, 4, 8192, 256, 128, 64, 5, torch.bfloat16),
+    (2, 16, 4, 16384, 256, 128, 64, 7, torch.bfloat16),
     (1, 8, 2, 4096, 128, 128, 100, 3, torch.bfloat16),   # W > 64: generic kernel
     (1, 8, 2, 999, 96, 32, 33, 2, torch.bfloat16),      # d=96, BS<64: generic kernel
     (1, 2, 2, 18, 8, 4, 4, 2, torch.float32),           # reference test shape

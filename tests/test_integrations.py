@@ -355,11 +355,13 @@ def test_native_chunk_loop_equals_per_chunk_calls(b, hq, hkv, d, max_chunk):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("b,hq,hkv,d,max_chunk", [(1, 16, 4, 256, 4096), (2, 8, 2, 128, 2048), (1, 16, 4, 256, 1024)])
+@pytest.mark.parametrize("b,hq,hkv,d,max_chunk", [(1, 16, 4, 256, 4096), (2, 8, 2, 128, 2048), (1, 16, 4, 256, 1024),
+                                                   (4, 16, 8, 256, 4096)])
 def test_native_chunk_loop_on_the_page_grid_equals_per_chunk_calls(b, hq, hkv, d, max_chunk):
     """Every chunk a multiple of 64 tokens: the batches read their own tokens from the chunk
     inputs and copy only the tail they leave to the ring; outputs, counters, tail and pool
-    must still equal the one-call-per-chunk schedule's."""
+    must still equal the one-call-per-chunk schedule's.  At batch 4 with 8 kv heads the d = 256
+    batches hold two chunks per workgroup segment (the LDS page shift inside a batched launch)."""
     _native_loop_matches_per_chunk(b, hq, hkv, d, max_chunk,
                                    [384, 384, 256, 448, 64, 384, 128, 384, 384, 320, 384, 384, 192, 384, 384, 384])
 

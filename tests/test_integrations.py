@@ -395,6 +395,34 @@ def _native_loop_matches_per_chunk(b, hq, hkv, d, max_chunk, lens):
 
 
 @pytest.mark.gpu
+def test_native_chunk_loop_takes_non_contiguous_chunks():
+    """Chunks given as strided views (slices of the whole sequence along its length) go through
+    the native loop as contiguous copies: outputs and cache equal those of contiguous chunks."""
+    b, hq, hkv, d, layer = 1, 16, 4, 256, 3
+    lens = [384, 384, 320, 384, 200, 384, 384]
+    total = sum(lens)
+    q = _rand(71, (b, hq, total, d), torch.bfloat16).cuda()
+    k = _rand(72, (b, hkv, total, d), torch.bfloat16).cuda()
+    v = _rand(73, (b, hkv, total, d), torch.bfloat16).cuda()
+    runs = []
+    for contiguous in (True, False):
+        chunks, pos = [], 0
+        for n in lens:
+            views = tuple(t[:, :, pos:pos + n] for t in (q, k, v))
+            assert not any(x.is_contiguous() for x in views)
+            chunks.append(tuple(x.contiguous() for x in views) if contiguous else views)
+            pos += n
+        core = bf.ButterflyAttentionCore(bf.compressed_butterfly_config(), layer)
+        cache = bf.CompressedKVCache(block_size=128, local_window_tokens=64, max_kv_size=total, max_chunk_size=4096)
+        runs.append((core, cache, bf.chunked_prefill(core, chunks, cache)))
+    (ca, a, oa_), (cb, bb, ob) = runs
+    assert ca.last_profile.notes.get("native_chunk_loop", 0) > 0 and cb.last_profile.notes.get("native_chunk_loop", 0) > 0
+    for x, y in zip(oa_, ob):
+        assert torch.equal(x, y)
+    assert torch.equal(a.k_summary, bb.k_summary) and torch.equal(a.keys, bb.keys)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("max_chunk", [512, 2048])     # 2048: the pool runs out inside a batch
 def test_native_chunk_loop_capacity_error_matches_per_chunk_calls(max_chunk):
     b, hq, hkv, d, layer = 1, 8, 2, 128, 2

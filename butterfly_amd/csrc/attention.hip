@@ -649,7 +649,7 @@ struct NoBatch {};
 // workgroups that run the NEXT chunk's cache update (append + pooling) while
 // the attention workgroups run this chunk; the host fuses only when the update
 // writes no ring slot or pool row that this chunk's attention reads.
-template <int D, bool kUpd = false, bool kBatch = false>
+template <int D, bool kUpd = false, bool kBatch = false, bool kSplitD = false>
 __global__ void __launch_bounds__(MfmaCfg<D>::NTHR, D <= 128 || MfmaCfg<D>::kWaveHead ? 2 : 1)
 attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, int nchunks_in, int hper,
                  std::conditional_t<kBatch, ChunkBatch, NoBatch> cb) {
@@ -1003,6 +1003,14 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
     }
   };
 
+  // Split d (kSplitD; d = 256, a segment of one chunk and four query heads, as in the batched
+  // streaming launches): each wave first scores its two heads (hlo + hpar, hlo + 2 + hpar) and forms their P
+  // and 1/l; once every wave is done with K, the waves of a pair (same rows, hpar 0 and 1) trade
+  // their P and 1/l through the K rows, and each computes PV and the output for all four heads
+  // on its half of d (hpar): every V fragment read then feeds four heads instead of one.  Each
+  // output element is the same MFMA chain over the same operands as in the head-per-wave form.
+  // (kSplitD: the host launches it only for segments of one chunk and workgroups of four heads)
+  static_assert(!kSplitD || kWaveHead, "split d is the d = 256 form");
   if constexpr (kWaveHead) {
     if (hlo + hpar < hhi) load_q(0, cfirst, hlo + hpar);
   } else {
@@ -1076,7 +1084,7 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
     store_page(new_page(c), dir > 0 ? 1 : 0);
     store_sum();
     __syncthreads();
-    if (c + dir != cstop) {
+    if (!kSplitD && c + dir != cstop) {
       fetch_page(new_page(c + dir));
       fetch_sum(c + dir);
     }
@@ -1129,7 +1137,121 @@ attn_mfma_kernel(AttnArgs a_in, MfmaArgs m_in, int seg_chunks, int c_first_in, i
       inv = __builtin_amdgcn_rcpf(fmaxf(lsum, 1e-30f));
     };
 
-    for (int hb = hlo; hb < hhi; hb += kQPipe) {
+    if constexpr (kSplitD) {
+      {
+        bf16x8 pa[2][3];
+        float inva[2] = {0.f, 0.f};
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+          if (!wave_active) continue;
+          f32x4 st[6];
+#pragma unroll
+          for (int t = 0; t < 6; ++t) {
+            bf16x8 kf[C::KSTEPS];
+#pragma unroll
+            for (int ks = 0; ks < C::KSTEPS; ++ks)
+              kf[ks] = *reinterpret_cast<const bf16x8*>(Ks + (t < 5 ? klane + 16 * t * C::KP : ksum) + 8 * ks);
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < C::KSTEPS; ++ks)
+              acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qbuf[0][ks], acc, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) st[t][i] = ok[t][i] ? acc[i] : -INFINITY;
+          }
+          refill_q(0, c, hlo + 2 * it + hpar);   // the second head's Q, loaded during the first's softmax
+          softmax(st, pa[it], inva[it]);
+        }
+        __syncthreads();   // every wave is done with K: its rows take the exchange
+        // [wave pair slot qwave * 2 + hpar][it][pr][lane] P pieces, then [slot][it][lane] 1/l
+        constexpr int kXP = 8 * 2 * 3 * 64 * 16;
+        static_assert(kXP + 8 * 2 * 64 * 4 <= C::K_BYTES, "the exchange fits the K rows");
+        bf16x8* xp = reinterpret_cast<bf16x8*>(smem);
+        float* xi = reinterpret_cast<float*>(smem + kXP);
+        const int me = qwave * 2 + hpar, mate = qwave * 2 + (hpar ^ 1);
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+#pragma unroll
+          for (int pr = 0; pr < 3; ++pr) xp[((me * 2 + it) * 3 + pr) * 64 + lane] = pa[it][pr];
+          xi[(me * 2 + it) * 64 + lane] = inva[it];
+        }
+        __syncthreads();   // both waves of every pair have published
+        if (wave_active) {
+          // this wave's half of d: tiles mt = 4 hpar .. 4 hpar + 3, i.e. the V bases plus hpar * 128
+          int vlh[4], vsh[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            vlh[r] = vlane[r] + hpar * 128;
+            vsh[r] = vsum[r] + hpar * 128;
+          }
+          const bool lo8 = lq < 8;
+          const int pA = pw + (lq & 7), pB = pA + 8;
+          const bool okA = pA >= m.qlo && pA < m.qhi, okB = pB >= m.qlo && pB < m.qhi;
+          __bf16* oA = ohead0 + (int64_t)(okA ? pA - m.qlo : 0) * D;
+          __bf16* oB = ohead0 + (int64_t)(okB ? pB - m.qlo : 0) * D;
+          const int64_t hstride = (int64_t)a.tq * D;
+          // two passes of a head pair: (hlo + 2 it + hpar, own) and (hlo + 2 it + (hpar ^ 1), mate's)
+#pragma unroll
+          for (int it = 0; it < 2; ++it) {
+            bf16x8 pf[2][3];
+            float inv[2];
+#pragma unroll
+            for (int pr = 0; pr < 3; ++pr) {
+              pf[0][pr] = pa[it][pr];
+              pf[1][pr] = xp[((mate * 2 + it) * 3 + pr) * 64 + lane];
+            }
+            inv[0] = inva[it];
+            inv[1] = xi[(mate * 2 + it) * 64 + lane];
+            const int64_t ho[2] = {(hlo + 2 * it + hpar) * hstride, (hlo + 2 * it + (hpar ^ 1)) * hstride};
+#pragma unroll
+            for (int mpi = 0; mpi < 2; ++mpi) {
+              bf16x8 w[2][2];
+#pragma unroll
+              for (int sub = 0; sub < 2; ++sub) {
+                const int r = 2 * mpi + sub;   // mt & 3 (mt = 4 hpar + r)
+                f32x4 o[2][2];
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                  bf16x8 vf[3];
+#pragma unroll
+                  for (int pr = 0; pr < 3; ++pr) {
+                    const int ta = 2 * pr, tb = 2 * pr + 1;
+                    const bf16x4 va = read_tr(Vs + vlh[r] + 16 * ta * D + half * 4);
+                    const bf16x4 vb = read_tr(Vs + (tb < 5 ? vlh[r] + 16 * tb * D : vsh[r]) + half * 4);
+                    vf[pr] = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
+                  }
+#pragma unroll
+                  for (int jh = 0; jh < 2; ++jh) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int pr = 0; pr < 3; ++pr)
+                      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[pr], pf[jh][pr], acc, 0, 0, 0);
+                    o[jh][half] = acc;
+                  }
+                }
+#pragma unroll
+                for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+                  for (int i = 0; i < 4; ++i) {
+                    w[jh][sub][i] = (__bf16)(o[jh][0][i] * inv[jh]);
+                    w[jh][sub][4 + i] = (__bf16)(o[jh][1][i] * inv[jh]);
+                  }
+              }
+              // whole 128-byte lines per store, as in the head-per-wave form (mp = 2 hpar + mpi)
+              const int dA = (4 * hpar + 2 * mpi + (lo8 ? 0 : 1)) * 32 + lg * 8;
+#pragma unroll
+              for (int jh = 0; jh < 2; ++jh) {
+                const bf16x8 x = xchg8(lo8 ? w[jh][1] : w[jh][0]);
+                const bf16x8 sa = lo8 ? w[jh][0] : x, sb = lo8 ? x : w[jh][1];
+                if (okA) __builtin_nontemporal_store(sa, reinterpret_cast<bf16x8*>(oA + ho[jh] + dA));
+                if (okB) __builtin_nontemporal_store(sb, reinterpret_cast<bf16x8*>(oB + ho[jh] + dA));
+              }
+            }
+          }
+        }
+        break;   // the segment's only chunk (no page or Q is carried over)
+      }
+    }
+    for (int hb = hlo; hb < hhi && !kSplitD; hb += kQPipe) {
 #pragma unroll
       for (int pp = 0; pp < kQPipe / 2; ++pp) {
         // kWaveHead: this wave's head of the pair alone, in Q slot 0
@@ -1413,6 +1535,8 @@ static int launch_attention_batch(const AttnArgs* ch, const void* const* kin, co
   const int hper = hq_per >= 2 ? (hq_per + 1) & ~1 : 1;
   const int nparts = (gsz + hper - 1) / hper;
   cb.rows_per_chunk = (int)(groups * nparts);
+  // d = 256 workgroups of one chunk and four heads: the split-d form of the kernel
+  const bool splitd = a.d == 256 && seg == 1 && hper == 4 && gsz % 4 == 0;
   BFLY_CHECK_ARG(nseg <= INT32_MAX && groups * nparts * n <= 65535, "%s: grid too large", what);
   MfmaArgs m{};
   m.ring = (int)a.ring;
@@ -1435,13 +1559,23 @@ static int launch_attention_batch(const AttnArgs* ch, const void* const* kin, co
     switch (a.d) {
       case 64: hipLaunchKernelGGL((attn_mfma_kernel<64, true, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
       case 128: hipLaunchKernelGGL((attn_mfma_kernel<128, true, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
-      default: hipLaunchKernelGGL((attn_mfma_kernel<256, true, true>), grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, 0, 0, hper, cb); break;
+      default:
+        if (splitd)
+          hipLaunchKernelGGL((attn_mfma_kernel<256, true, true, true>), grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, 0, 0, hper, cb);
+        else
+          hipLaunchKernelGGL((attn_mfma_kernel<256, true, true>), grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, 0, 0, hper, cb);
+        break;
     }
   } else {
     switch (a.d) {
       case 64: hipLaunchKernelGGL((attn_mfma_kernel<64, false, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
       case 128: hipLaunchKernelGGL((attn_mfma_kernel<128, false, true>), grid, dim3(256), 0, stream, a, m, seg, 0, 0, hper, cb); break;
-      default: hipLaunchKernelGGL((attn_mfma_kernel<256, false, true>), grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, 0, 0, hper, cb); break;
+      default:
+        if (splitd)
+          hipLaunchKernelGGL((attn_mfma_kernel<256, false, true, true>), grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, 0, 0, hper, cb);
+        else
+          hipLaunchKernelGGL((attn_mfma_kernel<256, false, true>), grid, dim3(MfmaCfg<256>::NTHR), 0, stream, a, m, seg, 0, 0, hper, cb);
+        break;
     }
   }
   BFLY_CHECK_LAUNCH(what);

@@ -714,12 +714,14 @@ def chunked_prefill(core: ButterflyAttentionCore, chunks, cache: CompressedKVCac
     return outs
 
 
-# Chunks per bfly_stream_chunks call: a first run of 8, then each run about 1.5 times the one
+# Chunks per bfly_stream_chunks call: a first run of 8, then each run about 1.3 times the one
 # before, in whole batches of the native loop (its batches hold at most 10 chunks and half the ring
-# minus two pages), up to 256.  The host prepares a run (about 2 us per chunk) in less time than
-# the GPU takes for the one before it (about 3 us per chunk), so the GPU is not left waiting
-# between calls, and a call rarely ends in a small batch, whose attention launch runs alone.
-_STREAM_GROWTH = 1.5
+# minus two pages), up to 256.  The host prepares a call's chunks (about 2 us each) before its first
+# launch, while the GPU works through the call before (about 3 us per chunk, of which about 2 are
+# still queued when that call returns); a run 1.3 times the last is ready before that queue drains,
+# where 1.5 times left the GPU waiting at every call boundary.  A call rarely ends in a small batch,
+# whose attention launch runs alone.
+_STREAM_GROWTH = 1.3
 _STREAM_RUN_MAX = 256
 _STREAM_BATCH_CAP = 10
 
@@ -783,24 +785,28 @@ def _stream_chunks(core: ButterflyAttentionCore, chunks, start: int, run: int,
     ring_k, ring_v, pool_k, pool_v = cache._ring_k, cache._ring_v, cache._pool_k, cache._pool_v
     if tuple(ring_k.shape[:2]) != (b, hkv) or ring_k.shape[3] != d or ring_k.dtype != torch.bfloat16:
         raise ValueError("keys do not match the cache's batch/head/dim/dtype")
-    # outputs: consecutive 16-byte aligned ranges of one allocation (chunks of one length: one
-    # [m, b, hq, n, d] tensor unbound into its rows, which costs the host far less per chunk)
+    # outputs: the leading run of chunks of one length as one [m1, b, hq, n, d] tensor unbound into
+    # its rows (far cheaper for the host per chunk than a view each), the rest (a stream's short
+    # last chunk, ragged lengths) as 16-byte aligned ranges of a second allocation
     m = len(qp)
     n0 = lens_l[0]
+    m1 = 1
+    while m1 < m and lens_l[m1] == n0:
+        m1 += 1
     per = b * hq * d
-    if all(n == n0 for n in lens_l):
-        big = torch.empty((m, b, hq, n0, d), dtype=torch.bfloat16, device=q0.device)
-        outs = list(big.unbind(0))
-        base, step = big.data_ptr(), per * n0 * 2
-        op = [base + i * step for i in range(m)]
-    else:
+    big = torch.empty((m1, b, hq, n0, d), dtype=torch.bfloat16, device=q0.device)
+    outs = list(big.unbind(0))
+    base, step = big.data_ptr(), per * n0 * 2
+    op = [base + i * step for i in range(m1)]
+    if m1 < m:
         starts, off = [], 0
-        for n in lens_l:
+        for n in lens_l[m1:]:
             starts.append(off)
             off += (per * n + 7) // 8 * 8
         flat = torch.empty(off, dtype=torch.bfloat16, device=q0.device)
-        outs = [flat[s0:s0 + per * n].view(b, hq, n, d) for s0, n in zip(starts, lens_l)]
-        op = [o.data_ptr() for o in outs]
+        rest = [flat[s0:s0 + per * n].view(b, hq, n, d) for s0, n in zip(starts, lens_l[m1:])]
+        outs += rest
+        op += [o.data_ptr() for o in rest]
     ptrs = lambda xs: (C.c_void_p * m)(*xs)
     lens = (C.c_int64 * m)(*lens_l)
     counters = (C.c_int64 * 4)(cache.offset, cache.tail_size, cache.summary_count, cache.summary_offset)

@@ -84,10 +84,18 @@ class CompressedKVCache:
         # compressed_cache.py:69-92 (same capacity formulas)
         self.tail_capacity = self.local_window_tokens + 2 * self.max_chunk_size + 2 * self.block_size
         self.summary_capacity = (self.max_kv_size // self.block_size + 4) if self.max_kv_size is not None else 2048
-        self._ring_k = torch.zeros((b, h, self.tail_capacity, d), dtype=dtype, device=device)
-        self._ring_v = torch.zeros_like(self._ring_k)
-        self._pool_k = torch.zeros((b, h, self.summary_capacity, d), dtype=dtype, device=device)
-        self._pool_v = torch.zeros_like(self._pool_k)
+        # the two rings and the two pools as views of one zeroed allocation (one allocation and one
+        # fill instead of four of each, on the path of a stream's first chunk); each view starts on a
+        # 256-element boundary
+        shapes = [(b, h, self.tail_capacity, d)] * 2 + [(b, h, self.summary_capacity, d)] * 2
+        sizes = [b * h * n * d for _, _, n, d in shapes]
+        starts, off = [], 0
+        for n in sizes:
+            starts.append(off)
+            off += -(-n // 256) * 256
+        flat = torch.zeros(off, dtype=dtype, device=device)
+        self._ring_k, self._ring_v, self._pool_k, self._pool_v = (
+            flat[s:s + n].view(shape) for s, n, shape in zip(starts, sizes, shapes))
 
     def _apply_realign(self) -> None:
         if self._realign and self._ring_k is not None:

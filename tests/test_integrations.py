@@ -322,6 +322,36 @@ def test_chunked_prefill_pauses_the_cyclic_collector_and_restores_it():
         gc.enable() if was else gc.disable()
 
 
+def test_native_call_sizes_grow_in_whole_batches():
+    """Chunks per bfly_stream_chunks call after the first run: whole batches of the native loop
+    (at most ten chunks, and half the ring minus two pages), about 1.3 times the run before, at
+    least one batch, at most 256 chunks rounded up to a whole batch."""
+    from types import SimpleNamespace
+
+    from butterfly_amd.integrations import _stream_run
+
+    def schedule(tail_capacity, chunk_len, first=8, total=682):
+        cache = SimpleNamespace(tail_capacity=tail_capacity)
+        runs, run, done = [], first, 0
+        while done < total:
+            runs.append(min(run, total - done))
+            done += runs[-1]
+            run = _stream_run(cache, chunk_len, run)
+        return runs
+
+    # cfg4: a ring of 8512 rows and chunks of 384 -> batches of ten
+    assert schedule(8512, 384) == [8, 10, 20, 30, 40, 60, 80, 110, 150, 174]
+    cache = SimpleNamespace(tail_capacity=8512)
+    assert _stream_run(cache, 384, 200) == 260 and _stream_run(cache, 384, 260) == 260
+    # a ring of 1344 rows (max_chunk_size 512): one chunk of 384 per batch, growth alone
+    assert schedule(1344, 384, total=60) == [8, 10, 13, 16, 13]
+    # batches bounded by the ring, not the cap of ten: (8512 - 128) // 2 // 1000 = 4 chunks
+    runs = schedule(8512, 1000, total=300)
+    assert all(r % 4 == 0 for r in runs[1:-1]) and runs[1] == 12
+    # a chunk longer than half the ring still makes progress, one chunk per batch
+    assert _stream_run(SimpleNamespace(tail_capacity=1344), 4096, 8) == 10
+
+
 @pytest.mark.gpu
 def test_stock_decode_fallback_is_dense_over_the_tail():
     dtype, d, b, hq, hkv, T = torch.bfloat16, 128, 2, 8, 2, 1000
